@@ -1,0 +1,172 @@
+/* t2r.h -- C-ABI of the MI355X-native W8A8 decoder datapath (libt2r.so, gfx950).
+ *
+ * The drop-in boundary for the path jonathansong/Torch2RISCV-accelerator runs on its FPGA
+ * accelerator and models on the CPU (llm/ref_model.py DeviceModel, llm/sa_funcsim.py,
+ * llm/sfu.py, llm/fp32.py). Two levels, as llm/runtime.py dispatches:
+ *   - op level: one call per piece of the reference's token list (ModelCompiler's embed,
+ *     rmsnorm, quant_act + W8A8 linear, rope, kv_append, attention, silu_mul / ffn_up,
+ *     residual, final: llm/compile_model.py:147-349), each step for step the DeviceModel
+ *     method it names;
+ *   - model level: one decode step / one prefill of a resident model, the per-token
+ *     Device.submit + wait of llm/runtime.py:107-125.
+ *
+ * Conventions
+ *   - Tensor arguments are DEVICE pointers owned by the caller; the library never allocates,
+ *     frees or synchronises on these calls. Every call enqueues on `stream` (a hipStream_t
+ *     passed as void*, NULL = the default stream) and returns T2R_OK, or a negative code
+ *     BEFORE launching anything when an argument is invalid (the reference's SaError shape /
+ *     range checks, llm/sa_funcsim.py:26-31, as T2R_ESHAPE / T2R_ERANGE).
+ *   - Numerics: int8 x int8 -> exact int32; y = F(F(f32(acc) * s_w) * s_x); fp32 vector steps
+ *     with one IEEE rounding each, never fused; EXP / RECIP / RSQRT bit-exact with the SFU;
+ *     sums in the D-lane order (D = 8 or 16). Results are bit-identical to the reference's.
+ *   - Matrices are row-major; linear weights are (out, in) int8 with one fp32 scale per row.
+ *   - Thread safety: calls on different streams may run concurrently; the only global state
+ *     is the SFU table constant, written once per device by the first call (t2r_init).
+ */
+#ifndef T2R_H
+#define T2R_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define T2R_ABI_VERSION 1
+
+enum {
+  T2R_OK = 0,
+  T2R_EINVAL = -1,   /* null pointer, bad enum, bad config                             */
+  T2R_ESHAPE = -2,   /* a size the kernels cannot take (~ SaError XERR_SHAPE = 1)       */
+  T2R_ERANGE = -3,   /* an index or size out of range (~ SaError XERR_RANGE = 2)        */
+  T2R_EHIP = -4,     /* a HIP runtime error (launch or symbol copy)                     */
+  T2R_ENOMEM = -5,   /* the workspace given is too small                                */
+  T2R_ESTATE = -6    /* a model handle in the wrong state                               */
+};
+
+int t2r_abi_version(void);
+const char* t2r_strerror(int code);
+/* Writes the SFU tables (llm/sfu.py:42-56) to the current device; the other calls do it
+ * themselves on first use. Returns T2R_OK or T2R_EHIP. */
+int t2r_init(void);
+/* Copies the SFU tables as the device holds them: T/S of EXP (64 + 64), RECIP (64 + 64),
+ * RSQRT (128 + 128) as fp32 bit patterns into host memory out[512]. */
+int t2r_sfu_tables(uint32_t* out);
+
+/* ---------------------------------------------------------------- element-wise hooks */
+/* fn 0 EXP, 1 RECIP, 2 RSQRT, 3 ABS on n fp32 bit patterns (llm/sfu.py:69-118). */
+int t2r_sfu(int fn, const uint32_t* x, uint32_t* y, int64_t n, void* stream);
+/* The fp32 primitives (llm/fp32.py:78-189): op 0 add, 1 sub, 2 mul (flush-to-zero), 3 ldexp
+ * (b = int32 exponents), 4 floor to int32 (saturated), 5 to_i8 (RNE, +-127, NaN -> 0),
+ * 6 int32 -> fp32 (RNE), 7 IEEE mul, 8 IEEE add (the vector steps). */
+int t2r_fp32_op(int op, const uint32_t* a, const uint32_t* b, uint32_t* y, int64_t n, void* stream);
+/* Integer REQUANT of the vector engine (llm/sa_funcsim.py:265-274, driver/pynq_matmul.py:127-135):
+ * out = sat8(clamp(((r * scale + 2^(shift-1)) >> shift) + zp, lo, hi)); scale is signed 16-bit. */
+int t2r_requant(const int32_t* r, int64_t n, int scale, int shift, int zp, int lo, int hi, int8_t* out,
+                void* stream);
+
+/* ---------------------------------------------------------------- op level */
+/* x[r] = F(f32(emb_q[tokens[r]]) * emb_s[tokens[r]]) (llm/ref_model.py:221; ModelCompiler.embed
+ * llm/compile_model.py:192-201). A token outside [0, vocab) reads row 0 and sets *status = 1
+ * (status may be NULL). */
+int t2r_embed(const int8_t* emb_q, const float* emb_s, const int32_t* tokens, int rows, int dim, int vocab,
+              float* x, int32_t* status, void* stream);
+/* RMSNorm of rows x[rows, n] (DeviceModel.rmsnorm llm/ref_model.py:204-207; ModelCompiler.rmsnorm
+ * llm/compile_model.py:147-156); n <= 8192. */
+int t2r_rmsnorm(const float* x, const float* g, int rows, int n, float eps, int D, float* out, void* stream);
+/* Per-row dynamic int8 (DeviceModel.quant_act llm/ref_model.py:191-196; CL.quant_act
+ * llm/compile_layer.py:66-77); n <= 8192, n % 16 == 0. */
+int t2r_quant_act(const float* x, int rows, int n, int8_t* xq, float* s_x, void* stream);
+/* The W8A8 linear layer of one activation row (DeviceModel.linear llm/ref_model.py:198-202;
+ * SaFuncSim.gemv llm/sa_funcsim.py:138-162; CL.linear llm/compile_layer.py:93-182):
+ * acc[n] = sum_k xq[k] w[n, k] (int32), y[n] = F(F(f32(acc) * s_w[n]) * s_x[0]) (+ residual[n]
+ * first rounded sum, llm/compile_model.py:330-331). y and acc_out may be NULL (not both);
+ * residual may be NULL or alias y. K % 16 == 0, K <= 8192. */
+int t2r_gemv_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const float* s_x, int N, int K, float* y,
+                  int32_t* acc_out, const float* residual, void* stream);
+/* The same over M activation rows xq[M, K] with scales s_x[M] (prefill rows,
+ * compiler/plugins/sa/transforms/SahlExpandKernels.cpp:205 expandLinearRows; int8 MFMA). */
+int t2r_gemm_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const float* s_x, int M, int N, int K,
+                  float* y, int32_t* acc_out, const float* residual, void* stream);
+/* RoPE of rows v[rows, n] in place at positions pos[rows] (DeviceModel.rope llm/ref_model.py:209-214;
+ * ModelCompiler.rope llm/compile_model.py:203-214): pairs (2i, 2i+1), tables [S, half] with
+ * half = head_dim / 2, pair i using column i % half. */
+int t2r_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* pos, int rows, int n, int half,
+             void* stream);
+/* KV append (llm/ref_model.py:228-229; ModelCompiler.kv_append llm/compile_model.py:221-231):
+ * kc[pos[r]] = to_i8(F(k[r] * inv_sk)), vc[pos[r]] = to_i8(F(v[r] * inv_sv)); caches [S, kv_dim]. */
+int t2r_kv_append(const float* k, const float* v, float inv_sk, float inv_sv, int8_t* kc, int8_t* vc,
+                  const int32_t* pos, int rows, int kv_dim, void* stream);
+/* Attention of rows q[rows, H * hd] (already rotated) at positions pos[rows] over the int8 cache
+ * rows 0..pos (DeviceModel.forward llm/ref_model.py:230-243; ModelCompiler.attention
+ * llm/compile_model.py:233-293; GQA: compiler/frontend/qhf.py:304-319). a_k = F(s_k / sqrt(hd)),
+ * a_v = F(s_v / 127). S = cache rows; S * H / Hk <= 16384, hd <= 128, H / Hk <= 8. */
+int t2r_attn_decode(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H,
+                    int Hk, int hd, int S, float a_k, float a_v, int D, float* att, void* stream);
+/* SwiGLU of one row (DeviceModel.forward llm/ref_model.py:246-250; ModelCompiler.ffn_up / silu_mul
+ * llm/compile_model.py:295-328; expandFfn SahlExpandKernels.cpp:529): h1, h3 = the two W8A8 linears
+ * of xq, u = F(F(h1 * RECIP(F(1 + EXP(F(h1 * -1))))) * h3) -> u_out[F] (required), then
+ * hq, s_h = quant_act(u). */
+int t2r_swiglu_w8a8(const int8_t* w1, const float* s_w1, const int8_t* w3, const float* s_w3, const int8_t* xq,
+                    const float* s_x, int F, int K, float* u_out, int8_t* hq, float* s_h, void* stream);
+/* MoE routing of rows scores[rows, E] (compiler/frontend/hf_generic.py:641-646;
+ * compiler/tests/oracle.py:558-585): top-k ids in descending score order (equal scores: lower
+ * id first), weights w = F(e * RECIP(red_sum(e))), e = EXP(F(v - v0)). E <= 64, k <= 8. */
+int t2r_moe_route(const float* scores, int rows, int E, int k, int D, int32_t* ids, float* weights, void* stream);
+/* First index of the largest value of each row (np.argmax; llm/ref_model.py:277). */
+int t2r_argmax(const float* x, int rows, int n, int32_t* idx, void* stream);
+
+/* ---------------------------------------------------------------- model level */
+/* A decoder resident on the device. Pointers are device pointers except kv_consts (host).
+ * Per-layer tensors are stacked with the layer first. */
+typedef struct t2r_model_desc {
+  int32_t abi_version;                 /* T2R_ABI_VERSION */
+  int32_t dim, hidden, layers, heads, kv_heads, head_dim, vocab, seq_len;
+  int32_t n_experts, top_k;            /* 0, 0: dense FFN */
+  int32_t qk_norm, D;
+  float eps;
+  const int8_t* emb_q; const float* emb_s;          /* [vocab, dim], [vocab] */
+  const int8_t* cls_q; const float* cls_s;          /* classifier (the embedding when tied) */
+  const float* rms_att; const float* rms_ffn;       /* [L, dim] */
+  const float* rms_final;                           /* [dim] */
+  const float* q_norm; const float* k_norm;         /* [L, head_dim] (QK-norm) or NULL */
+  const int8_t* wqkv; const float* s_wqkv;          /* [L, q + 2 kv, dim], [L, q + 2 kv] */
+  const int8_t* wo; const float* s_wo;              /* [L, dim, q] */
+  const int8_t* w1; const float* s_w1;              /* [L, hidden, dim] (dense) */
+  const int8_t* w3; const float* s_w3;
+  const int8_t* w2; const float* s_w2;              /* [L, dim, hidden] */
+  const int8_t* router; const float* s_router;      /* [L, E, dim] (MoE) */
+  const int8_t* wg; const float* s_wg;              /* [L, E, hidden, dim] */
+  const int8_t* wu; const float* s_wu;
+  const int8_t* wd; const float* s_wd;              /* [L, E, dim, hidden] */
+  const float* rope_cos; const float* rope_sin;     /* [seq_len, head_dim / 2] */
+  const float* kv_consts;                           /* HOST [L, 4]: 1/s_k, 1/s_v, a_k, a_v */
+  int8_t* k_cache; int8_t* v_cache;                 /* [L, seq_len, kv_dim] */
+  void* workspace; int64_t workspace_bytes;         /* see t2r_model_workspace_bytes */
+  int32_t max_rows;                                 /* prefill rows per call the workspace holds */
+} t2r_model_desc;
+
+/* Bytes of workspace a model needs for prefill calls of up to max_rows rows (>= 1). */
+int64_t t2r_model_workspace_bytes(const t2r_model_desc* desc, int max_rows);
+/* Validates desc (shapes, pointers, workspace) and returns a handle; copies desc. */
+int t2r_model_create(const t2r_model_desc* desc, void** model);
+void t2r_model_destroy(void* model);
+/* One decode step (the reference's static token list: llm/compile_model.py:351-374, run per token
+ * by llm/runtime.py:107-125): token and pos are read from DEVICE memory, so a captured HIP graph
+ * replays unchanged (only the (pos, token) block changes, llm/compile_model.py:56-62). Writes the
+ * logits [vocab] (may be NULL) and the greedy next token (may be NULL); the KV rows of pos are
+ * written. flags: T2R_ADVANCE_POS increments *pos on the device after the step. */
+#define T2R_ADVANCE_POS 1
+int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logits, int32_t* next_token,
+                    int flags, void* stream);
+/* Prefill of M prompt rows tokens[M] at positions[M] (device arrays; each row a decode step at its
+ * position: compiler/frontend/qhf.py:356-409): the KV rows are written, the logits of the last row
+ * go to last_logits (may be NULL) and its greedy token to next_token (may be NULL).
+ * M <= max_rows. Identical, bit for bit, to M decode steps. */
+int t2r_prefill(void* model, const int32_t* tokens, const int32_t* positions, int M, float* last_logits,
+                int32_t* next_token, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* T2R_H */

@@ -1,0 +1,235 @@
+#!/usr/bin/env python3
+"""Writes the golden fixtures of tests/golden/ from the reference itself.
+
+Run in a checkout next to the reference (it imports /root/reference/llm, NumPy only);
+the fixtures it writes are data (inputs and the reference's outputs), committed so the
+tests never need the reference:
+
+  sfu_tables.json    the SFU ROM transcribed from rtl/sysarray/sa_sfu_tables.vh
+                     ({T, S} per entry, address {fn, idx}: fn 0 EXP, 1 RECIP, 2 RSQRT)
+  sfu_golden.npz     inputs and outputs of llm/sfu.py exp / recip / rsqrt and of
+                     llm/fp32.py add / sub / mul / ldexp / to_int on sweeps that cover
+                     the flush-to-zero boundary and the special values
+  model_golden.json  DeviceModel(sfu=SfuExact) runs (llm/ref_model.py:151-255) of the
+                     synthetic models of t2r_amd.config (tiny, tiny-gqa, c1), and
+                     SaFuncSim runs of ModelCompiler's token list (llm/test_l4.py:58-116)
+                     for some of them: the token fed at every position, a sha256 of the
+                     logits bytes, the argmax, and a sha256 of the int8 KV cache
+
+    python3 tests/golden/make_golden.py [--reference /root/reference] [--skip-funcsim]
+"""
+import argparse
+import hashlib
+import json
+import os
+import re
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, REPO)
+F = np.float32
+
+
+def sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def write_tables(ref):
+    path = os.path.join(ref, "rtl", "sysarray", "sa_sfu_tables.vh")
+    rom = {}
+    for line in open(path):
+        m = re.match(r"\s*9'h([0-9a-f]{3}): sfu_rom = 64'h([0-9a-f]{8})_([0-9a-f]{8});", line)
+        if m:
+            rom[int(m.group(1), 16)] = (int(m.group(2), 16), int(m.group(3), 16))
+    out = {}
+    for fn, name, n in ((0, "exp", 64), (1, "recip", 64), (2, "rsqrt", 128)):
+        out[name] = {"T": [rom[fn << 7 | i][0] for i in range(n)], "S": [rom[fn << 7 | i][1] for i in range(n)]}
+    json.dump({"source": "rtl/sysarray/sa_sfu_tables.vh", **out}, open(os.path.join(HERE, "sfu_tables.json"), "w"),
+              indent=0)
+    print("sfu_tables.json:", {k: len(v["T"]) for k, v in out.items() if isinstance(v, dict)})
+
+
+def rand_bits(rng, n, emin=1, emax=254, sign=None):
+    s = rng.integers(0, 2, n, dtype=np.int64) if sign is None else np.full(n, sign, np.int64)
+    e = rng.integers(emin, emax + 1, n, dtype=np.int64)
+    m = rng.integers(0, 1 << 23, n, dtype=np.int64)
+    return ((s << 31) | (e << 23) | m).astype(np.uint32)
+
+
+def specials():
+    v = [0.0, -0.0, np.inf, -np.inf, np.nan, 1.0, -1.0, 2.0, 0.5, 89.0, -104.0, 88.99999, -103.99999, 89.00001,
+         -104.00001, 1e-38, -1e-38, 1.2e-38, 3.4e38, -3.4e38, 2.0 ** -126, 2.0 ** 127, 2.0 ** -125, 0.6931472,
+         -0.6931472, 1e-7, -1e-7, 127.0, 128.0, -87.3, 88.7]
+    b = np.asarray(v, F).view(np.uint32)
+    sub = np.array([1, 0x80000001, 0x007FFFFF, 0x807FFFFF, 0x00400000, 0x7F7FFFFF, 0xFF7FFFFF, 0x00800000,
+                    0x80800000, 0x7FC00001, 0xFFFFFFFF], np.uint32)
+    return np.concatenate([b, sub])
+
+
+def write_sfu(llm):
+    import fp32
+    import sfu
+    rng = np.random.default_rng(2027)
+    sp = specials()
+    xs = {
+        "exp": np.concatenate([sp, np.asarray(rng.uniform(-110, 95, 2048), F).view(np.uint32),
+                               np.asarray(rng.uniform(-20, 20, 1024), F).view(np.uint32),
+                               np.asarray(rng.uniform(-1, 1, 512), F).view(np.uint32), rand_bits(rng, 464)]),
+        "recip": np.concatenate([sp, np.asarray(np.exp(rng.uniform(-88, 88, 1536)), F).view(np.uint32),
+                                 np.asarray(-np.exp(rng.uniform(-88, 88, 1024)), F).view(np.uint32),
+                                 rand_bits(rng, 1024), rand_bits(rng, 464, 240, 254)]),
+        "rsqrt": np.concatenate([sp, np.asarray(np.exp(rng.uniform(-88, 88, 2048)), F).view(np.uint32),
+                                 rand_bits(rng, 1024, sign=0), rand_bits(rng, 512), rand_bits(rng, 464, 1, 12, 0)]),
+    }
+    out = {}
+    for name, x in xs.items():
+        out[name + "_x"] = x
+        out[name + "_y"] = getattr(sfu, name)(x)
+    n = 2048
+    a = np.concatenate([rand_bits(rng, n // 4), rand_bits(rng, n // 4, 1, 30), rand_bits(rng, n // 4, 60, 70),
+                        rand_bits(rng, n // 4, 120, 130)])
+    b = np.concatenate([rand_bits(rng, n // 4), rand_bits(rng, n // 4, 1, 30), rand_bits(rng, n // 4, 60, 70),
+                        (a[3 * n // 4:] ^ np.uint32(0x80000000)) + rng.integers(-3, 4, n // 4).astype(np.uint32)])
+    A, B = np.meshgrid(sp, sp)
+    a = np.concatenate([a, A.ravel()])
+    b = np.concatenate([b, B.ravel()])
+    out["bin_a"], out["bin_b"] = a, b
+    out["add"], out["sub"], out["mul"] = fp32.add(a, b), fp32.sub(a, b), fp32.mul(a, b)
+    nn = rng.integers(-300, 301, a.size)
+    out["ldexp_n"], out["ldexp"] = nn, fp32.ldexp(a, nn)
+    out["floor"] = fp32.to_int(a, -2 ** 31, 2 ** 31 - 1, "floor")
+    out["rne_i8"] = fp32.to_int(a, -127, 127)
+    ints = np.concatenate([rng.integers(-2 ** 31, 2 ** 31, 2048), [0, 1, -1, 2 ** 31 - 1, -2 ** 31, 2 ** 24 + 1,
+                                                                  2 ** 24 + 3, -(2 ** 24 + 1)]]).astype(np.int64)
+    out["from_int_x"], out["from_int"] = ints, fp32.from_int(ints)
+    np.savez_compressed(os.path.join(HERE, "sfu_golden.npz"), **out)
+    print("sfu_golden.npz:", {k: v.shape for k, v in out.items()})
+
+
+def ref_weights(cfg):
+    """The reference's weight dict (llm/checkpoint.py:33-59 names) of a synthetic model."""
+    from t2r_amd import weights as W
+    L = cfg.layers
+    w = {"tok": W.fp32_tensor(cfg, "tok"), "rms_final": W.fp32_tensor(cfg, "rms_final")}
+    for name in ("rms_att", "rms_ffn", "wq", "wk", "wv", "wo", "w1", "w2", "w3"):
+        w[name] = np.stack([W.fp32_tensor(cfg, name, l) for l in range(L)])
+    w["wcls"] = w["tok"]
+    return w
+
+
+def run_device_model(cfg, D, kv, steps, prompt, llm):
+    import checkpoint
+    from ref_model import DeviceModel, SfuExact, rope_tables
+    from t2r_amd import weights as W
+    rc = checkpoint.Config(cfg.dim, cfg.hidden, cfg.layers, cfg.heads, cfg.kv_heads, cfg.vocab, cfg.seq_len)
+    assert rc.head_size == cfg.head_dim
+    w = ref_weights(cfg)
+    dm = DeviceModel(rc, w, kv, d=D, sfu=SfuExact)
+    ref_cos, ref_sin = rope_tables(rc)
+    cos, sin = W.rope_tables(cfg)
+    reps = cfg.dim // cfg.head_dim
+    dm.cos, dm.sin = np.tile(cos, (1, reps)), np.tile(sin, (1, reps))        # the tables as data
+    fed, recs = [prompt[0]], []
+    t0 = time.time()
+    for pos in range(steps):
+        lg = dm.forward(fed[-1], pos)
+        recs.append({"pos": pos, "token": int(fed[-1]), "logits_sha": sha(lg.astype(F)), "argmax": int(np.argmax(lg)),
+                     "head": [int(b) for b in lg.astype(F).view(np.uint32)[:8]]})
+        fed.append(prompt[pos + 1] if pos + 1 < len(prompt) else int(np.argmax(lg)))
+    q, s = __import__("ref_model").quantize_rows(w["tok"])
+    return {"config": cfg.name, "D": D, "steps": steps, "prompt": [int(t) for t in prompt],
+            "kv_bits": [int(b) for b in np.asarray(kv, F).view(np.uint32).ravel()],
+            "positions": recs, "tokens": [int(t) for t in fed],
+            "kv_sha": sha(dm.kc[:, :steps], dm.vc[:, :steps]),
+            "emb_quant_sha": sha(q, s),
+            "rope_sha_mine": sha(cos, sin),
+            "rope_sha_reference": sha(ref_cos[:, :cfg.head_dim // 2], ref_sin[:, :cfg.head_dim // 2]),
+            "rope_reference_periodic": bool(np.array_equal(ref_cos, np.tile(ref_cos[:, :cfg.head_dim // 2], (1, reps)))),
+            "seconds": round(time.time() - t0, 2)}
+
+
+def run_funcsim(cfg, D, kv, tokens, llm):
+    """ModelCompiler's static list on SaFuncSim (the "sa_funcsim path as it runs today",
+    llm/test_l4.py:58-116): logits sha per position."""
+    import compile_model as CM
+    from export_w8a8 import W8A8, export
+    from sa_funcsim import SaFuncSim
+    import checkpoint
+    rc = checkpoint.Config(cfg.dim, cfg.hidden, cfg.layers, cfg.heads, cfg.kv_heads, cfg.vocab, cfg.seq_len)
+    w = ref_weights(cfg)
+    DDR = 0x10000000
+    out = []
+    t0 = time.time()
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "m.w8a8")
+        export(rc, w, kv, D, path)
+        m = W8A8(path)
+        dl = CM.ModelCompiler(m).build()
+        io = -(-m.raw.size // 4096) * 4096
+        kvo = io + 0x40000
+        lst = kvo + -(-CM.kv_bytes(rc) // 4096) * 4096
+        sim = SaFuncSim(D, DDR, lst + 64 * (len(dl) + 1))
+        sim.ddr_write(DDR, m.raw.tobytes())
+        rows = dl.array().tobytes()
+        for pos, t in enumerate(tokens):
+            sim.ddr_write(DDR + lst, rows)
+            sim.ddr_write(DDR + io, CM.arg_block(pos, t))
+            sim.run_list(DDR + lst, bases=[DDR, DDR + io, DDR + kvo], params=CM.token_params(pos, D, rc.head_size))
+            lg = sim.ddr_read(DDR + io + CM.IO_LOGITS, 4 * cfg.vocab).view(F)
+            out.append({"pos": pos, "token": int(t), "logits_sha": sha(lg), "argmax": int(np.argmax(lg))})
+        kraw = sim.ddr_read(DDR + kvo, CM.kv_bytes(rc)).view(np.int8).reshape(cfg.layers, 2, cfg.seq_len, cfg.kv_dim)
+        n = len(tokens)
+        ksha = sha(kraw[:, 0, :n], kraw[:, 1, :n])
+    return {"config": cfg.name, "D": D, "positions": out, "kv_sha": ksha, "seconds": round(time.time() - t0, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--reference", default="/root/reference")
+    ap.add_argument("--skip-funcsim", action="store_true")
+    ap.add_argument("--only", nargs="*")
+    args = ap.parse_args()
+    llm = os.path.join(args.reference, "llm")
+    sys.path.insert(0, llm)
+    sys.path.insert(0, os.path.join(args.reference, "driver"))
+    import t2r_amd.config as C
+    from t2r_amd import weights as W
+    if not args.only or "tables" in args.only:
+        write_tables(args.reference)
+    if not args.only or "sfu" in args.only:
+        write_sfu(llm)
+    if args.only and "model" not in args.only:
+        return
+    runs, fsim = [], []
+    plan = [(C.TINY, 8, None, True), (C.TINY, 16, None, True), (C.TINY_GQA, 8, None, True),
+            (C.TINY_GQA, 16, None, False), (C.C1, 16, C.C1.prompt_len + C.C1.decode_steps, 3),
+            (C.C1, 8, 40, 0)]
+    for cfg, D, steps, do_fsim in plan:
+        kv = W.stored_kv_scales(cfg) if cfg.name in C.CONFIGS else W.calibrate_kv(cfg)
+        steps = steps or cfg.prompt_len + cfg.decode_steps
+        r = run_device_model(cfg, D, kv, steps, cfg.prompt(), llm)
+        print(f"DeviceModel {cfg.name} D={D}: {steps} steps in {r['seconds']} s; rope mine==reference: "
+              f"{r['rope_sha_mine'] == r['rope_sha_reference']}", flush=True)
+        runs.append(r)
+        if do_fsim and not args.skip_funcsim:
+            n = steps if do_fsim is True else int(do_fsim)
+            fs = run_funcsim(cfg, D, kv, r["tokens"][:n], llm)
+            same = all(a["logits_sha"] == b["logits_sha"] for a, b in zip(fs["positions"], r["positions"]))
+            fs["equals_device_model"] = same
+            print(f"SaFuncSim {cfg.name} D={D}: {n} positions in {fs['seconds']} s; == DeviceModel: {same}",
+                  flush=True)
+            fsim.append(fs)
+    json.dump({"generator": "tests/golden/make_golden.py", "device_model": runs, "funcsim": fsim},
+              open(os.path.join(HERE, "model_golden.json"), "w"), indent=0)
+
+
+if __name__ == "__main__":
+    main()

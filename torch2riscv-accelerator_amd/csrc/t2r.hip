@@ -1,0 +1,533 @@
+// libt2r.so: the C-ABI of include/t2r.h over the gfx950 kernels (one translation unit).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "../../include/t2r.h"
+#include "t2r_attn.h"
+#include "t2r_device.h"
+#include "t2r_gemm.h"
+#include "t2r_gemv.h"
+#include "t2r_misc.h"
+
+namespace t2r {
+__constant__ float c_sfu[kSfuWords];
+}
+
+using namespace t2r;
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_init_mu;
+bool g_inited[kMaxDevices];
+
+// The SFU tables (llm/sfu.py:42-56): segment start T and slope S of each function, computed in
+// double and rounded once to float.
+void sfu_host_tables(float* t) {
+  for (int k = 0; k < 64; ++k) {
+    const double te = std::pow(2.0, k / 64.0), te1 = std::pow(2.0, (k + 1) / 64.0);
+    t[kSfuExpT + k] = (float)te;
+    t[kSfuExpS + k] = (float)(te1 - te);
+    const double m = 1.0 + k / 64.0;
+    const double tr = 1.0 / m;
+    t[kSfuRecT + k] = (float)tr;
+    t[kSfuRecS + k] = (float)(1.0 / (m + 1.0 / 64.0) - tr);
+  }
+  for (int j = 0; j < 128; ++j) {
+    const int k = j & 63;
+    const double m2 = j < 64 ? 1.0 + k / 64.0 : 2.0 * (1.0 + k / 64.0);
+    const double step = j < 64 ? 1.0 / 64.0 : 2.0 / 64.0;
+    const double tq = 1.0 / std::sqrt(m2);
+    t[kSfuRsqT + j] = (float)tq;
+    t[kSfuRsqS + j] = (float)(1.0 / std::sqrt(m2 + step) - tq);
+  }
+}
+
+int ensure_init() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return T2R_EHIP;
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (g_inited[dev]) return T2R_OK;
+  float t[kSfuWords];
+  sfu_host_tables(t);
+  if (hipMemcpyToSymbol(HIP_SYMBOL(c_sfu), t, sizeof(t), 0, hipMemcpyHostToDevice) != hipSuccess) return T2R_EHIP;
+  if (hipFuncSetAttribute((const void*)k_attn<ATTN_FUSED>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) !=
+          hipSuccess ||
+      hipFuncSetAttribute((const void*)k_attn<ATTN_ONLY>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) !=
+          hipSuccess)
+    return T2R_EHIP;
+  g_inited[dev] = true;
+  return T2R_OK;
+}
+
+#define T2R_INIT()                 \
+  do {                             \
+    int rc_ = ensure_init();       \
+    if (rc_ != T2R_OK) return rc_; \
+  } while (0)
+
+inline int launched() { return hipGetLastError() == hipSuccess ? T2R_OK : T2R_EHIP; }
+inline hipStream_t S(void* s) { return (hipStream_t)s; }
+inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+GemvArgs gemv_args() {
+  GemvArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.D = 16;
+  return a;
+}
+
+int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
+  const int G = a.H / a.Hk;
+  if (a.H <= 0 || a.Hk <= 0 || a.H % a.Hk || G > kMaxG || a.hd <= 0 || a.hd > kMaxHd || a.hd % 8 || a.S <= 0 ||
+      (long long)G * a.S > 16384 || (a.D != 8 && a.D != 16))
+    return T2R_ESHAPE;
+  const size_t lds = attn_lds_bytes(G, a.S);
+  dim3 grid(a.Hk, rows), block(kAttnThreads);
+  if (mode == ATTN_FUSED) hipLaunchKernelGGL(k_attn<ATTN_FUSED>, grid, block, lds, st, a);
+  else if (mode == ATTN_PREP) hipLaunchKernelGGL(k_attn<ATTN_PREP>, grid, block, 0, st, a);
+  else hipLaunchKernelGGL(k_attn<ATTN_ONLY>, grid, block, lds, st, a);
+  return launched();
+}
+
+// ---------------------------------------------------------------- the resident model
+struct Model {
+  t2r_model_desc d;
+  std::vector<float> kvc;           // [L, 4]
+  int q_dim, kv_dim, qkv_dim, ffn_rows, max_in;
+  float* x;
+  float* qkv;
+  float* att;
+  float* u;
+  int8_t* xq;
+  float* sx;
+  float* logits;
+  unsigned long long* keys;
+  int32_t* ids;
+  float* wts;
+  int8_t* mxq;
+  float* msx;
+  int32_t* status;
+};
+
+struct Carve {
+  char* base;
+  long long off;
+  template <class T>
+  T* take(long long n) {
+    off = (off + 255) / 256 * 256;
+    T* p = base ? (T*)(base + off) : nullptr;
+    off += n * (long long)sizeof(T);
+    return p;
+  }
+};
+
+long long carve(Model* m, char* base, int M) {
+  const t2r_model_desc& d = m->d;
+  Carve c{base, 0};
+  m->x = c.take<float>((long long)M * d.dim);
+  m->qkv = c.take<float>((long long)M * m->qkv_dim);
+  m->att = c.take<float>((long long)M * m->q_dim);
+  m->u = c.take<float>((long long)M * m->ffn_rows);
+  m->xq = c.take<int8_t>((long long)M * m->max_in);
+  m->sx = c.take<float>(M);
+  m->logits = c.take<float>(d.vocab);
+  m->keys = c.take<unsigned long long>(M);
+  const int k = d.top_k > 0 ? d.top_k : 1;
+  m->ids = c.take<int32_t>((long long)M * k);
+  m->wts = c.take<float>((long long)M * k);
+  m->mxq = c.take<int8_t>((long long)M * d.dim);
+  m->msx = c.take<float>(M);
+  m->status = c.take<int32_t>(1);
+  return c.off;
+}
+
+void model_dims(Model* m) {
+  const t2r_model_desc& d = m->d;
+  m->q_dim = d.heads * d.head_dim;
+  m->kv_dim = d.kv_heads * d.head_dim;
+  m->qkv_dim = m->q_dim + 2 * m->kv_dim;
+  m->ffn_rows = d.n_experts > 0 ? d.top_k * d.hidden : d.hidden;
+  int mi = d.dim;
+  if (m->q_dim > mi) mi = m->q_dim;
+  if (d.hidden > mi) mi = d.hidden;
+  m->max_in = mi;
+}
+
+int validate(const t2r_model_desc* d) {
+  if (!d || d->abi_version != T2R_ABI_VERSION) return T2R_EINVAL;
+  if (d->dim <= 0 || d->hidden <= 0 || d->layers <= 0 || d->heads <= 0 || d->kv_heads <= 0 || d->head_dim <= 0 ||
+      d->vocab <= 0 || d->seq_len <= 0)
+    return T2R_ESHAPE;
+  if (d->heads % d->kv_heads || d->heads / d->kv_heads > kMaxG || d->head_dim > kMaxHd || d->head_dim % 8)
+    return T2R_ESHAPE;
+  const int q = d->heads * d->head_dim, kv = d->kv_heads * d->head_dim;
+  if (d->dim % 16 || d->hidden % 16 || q % 16 || kv % 16 || d->dim > kMaxK || d->hidden > kMaxK || q > kMaxK)
+    return T2R_ESHAPE;
+  if ((long long)(d->heads / d->kv_heads) * d->seq_len > 16384) return T2R_ESHAPE;
+  if (d->D != 8 && d->D != 16) return T2R_ESHAPE;
+  if (d->n_experts < 0 || (d->n_experts > 0 && (d->top_k < 1 || d->top_k > 8 || d->top_k > d->n_experts ||
+                                                d->n_experts > 64 || d->hidden > 1024)))
+    return T2R_ESHAPE;
+  if (!d->emb_q || !d->emb_s || !d->cls_q || !d->cls_s || !d->rms_att || !d->rms_ffn || !d->rms_final ||
+      !d->wqkv || !d->s_wqkv || !d->wo || !d->s_wo || !d->rope_cos || !d->rope_sin || !d->kv_consts ||
+      !d->k_cache || !d->v_cache || !d->workspace)
+    return T2R_EINVAL;
+  if (d->qk_norm && (!d->q_norm || !d->k_norm)) return T2R_EINVAL;
+  if (d->n_experts > 0) {
+    if (!d->router || !d->s_router || !d->wg || !d->s_wg || !d->wu || !d->s_wu || !d->wd || !d->s_wd) return T2R_EINVAL;
+  } else if (!d->w1 || !d->s_w1 || !d->w3 || !d->s_w3 || !d->w2 || !d->s_w2) {
+    return T2R_EINVAL;
+  }
+  if (d->max_rows < 1) return T2R_ERANGE;
+  return T2R_OK;
+}
+
+// one decoder layer on `rows` rows of the workspace at device positions pos[rows]
+int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStream_t st) {
+  const t2r_model_desc& d = m->d;
+  const long long L_dim = (long long)l * d.dim;
+  const float inv_d = (float)(1.0 / d.dim);
+  int rc;
+  // Wqkv: RMSNorm + quant_act + linear
+  GemvArgs a = gemv_args();
+  a.w = d.wqkv + (long long)l * m->qkv_dim * d.dim;
+  a.s_w = d.s_wqkv + (long long)l * m->qkv_dim;
+  a.x = m->x; a.x_stride = d.dim; a.g = d.rms_att + L_dim; a.inv_n = inv_d; a.eps = d.eps; a.D = d.D;
+  a.N = m->qkv_dim; a.K = d.dim; a.y = m->qkv; a.y_stride = m->qkv_dim;
+  if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
+  // attention (QK-norm, RoPE, KV append fused for decode)
+  AttnArgs at;
+  std::memset(&at, 0, sizeof(at));
+  at.qkv = m->qkv; at.qkv_stride = m->qkv_dim;
+  at.kc = d.k_cache + (long long)l * d.seq_len * m->kv_dim;
+  at.vc = d.v_cache + (long long)l * d.seq_len * m->kv_dim;
+  at.pos = pos;
+  at.qn = d.qk_norm ? d.q_norm + (long long)l * d.head_dim : nullptr;
+  at.kn = d.qk_norm ? d.k_norm + (long long)l * d.head_dim : nullptr;
+  at.cos_t = d.rope_cos; at.sin_t = d.rope_sin;
+  const float* kc4 = &m->kvc[(size_t)l * 4];
+  at.inv_sk = kc4[0]; at.inv_sv = kc4[1]; at.a_k = kc4[2]; at.a_v = kc4[3];
+  at.eps = d.eps; at.inv_hd = (float)(1.0 / d.head_dim);
+  at.H = d.heads; at.Hk = d.kv_heads; at.hd = d.head_dim; at.D = d.D; at.S = d.seq_len;
+  at.att = m->att; at.att_stride = m->q_dim;
+  if (decode) {
+    if ((rc = attn_launch(ATTN_FUSED, at, rows, st))) return rc;
+  } else {
+    if ((rc = attn_launch(ATTN_PREP, at, rows, st))) return rc;
+    if ((rc = attn_launch(ATTN_ONLY, at, rows, st))) return rc;
+  }
+  // Wo: quant_act(att) + linear + residual
+  a = gemv_args();
+  a.w = d.wo + (long long)l * d.dim * m->q_dim;
+  a.s_w = d.s_wo + L_dim;
+  a.x = m->att; a.x_stride = m->q_dim;
+  a.N = d.dim; a.K = m->q_dim; a.y = m->x; a.y_stride = d.dim; a.res = m->x; a.res_stride = d.dim;
+  if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+  if (d.n_experts == 0) {
+    // SwiGLU: RMSNorm + quant_act + W1 / W3 + gate
+    a = gemv_args();
+    a.w = d.w1 + (long long)l * d.hidden * d.dim; a.s_w = d.s_w1 + (long long)l * d.hidden;
+    a.w3 = d.w3 + (long long)l * d.hidden * d.dim; a.s_w3 = d.s_w3 + (long long)l * d.hidden;
+    a.x = m->x; a.x_stride = d.dim; a.g = d.rms_ffn + L_dim; a.inv_n = inv_d; a.eps = d.eps; a.D = d.D;
+    a.N = d.hidden; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows;
+    if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_SWIGLU>(a, rows, st))) return rc;
+    // W2: quant_act(u) + linear + residual
+    a = gemv_args();
+    a.w = d.w2 + (long long)l * d.dim * d.hidden; a.s_w = d.s_w2 + L_dim;
+    a.x = m->u; a.x_stride = m->ffn_rows;
+    a.N = d.dim; a.K = d.hidden; a.y = m->x; a.y_stride = d.dim; a.res = m->x; a.res_stride = d.dim;
+    if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+  } else {
+    const int E = d.n_experts, k = d.top_k, Fe = d.hidden;
+    RouteArgs ra;
+    std::memset(&ra, 0, sizeof(ra));
+    ra.a = gemv_args();
+    ra.a.w = d.router + (long long)l * E * d.dim; ra.a.s_w = d.s_router + (long long)l * E;
+    ra.a.x = m->x; ra.a.x_stride = d.dim; ra.a.g = d.rms_ffn + L_dim; ra.a.inv_n = inv_d; ra.a.eps = d.eps;
+    ra.a.D = d.D; ra.a.N = E; ra.a.K = d.dim; ra.a.xq_out = m->mxq; ra.a.xq_stride = d.dim; ra.a.sx_out = m->msx;
+    ra.k = k; ra.ids = m->ids; ra.wts = m->wts;
+    hipLaunchKernelGGL(k_moe_route, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+    if ((rc = launched())) return rc;
+    // expert gate / up of the k selected experts (rows j * Fe + n of the selected tables)
+    a = gemv_args();
+    a.w = d.wg + (long long)l * E * Fe * d.dim; a.s_w = d.s_wg + (long long)l * E * Fe;
+    a.w3 = d.wu + (long long)l * E * Fe * d.dim; a.s_w3 = d.s_wu + (long long)l * E * Fe;
+    a.xq = m->mxq; a.xq_stride = d.dim; a.s_x = m->msx;
+    a.ids = m->ids; a.rows_per_id = Fe; a.ids_stride = k;
+    a.N = k * Fe; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows;
+    if ((rc = gemv_launch<PRO_XQ, EPI_SWIGLU>(a, rows, st))) return rc;
+    MoeDownArgs md;
+    md.u = m->u; md.wd = d.wd + (long long)l * E * d.dim * Fe; md.s_wd = d.s_wd + (long long)l * E * d.dim;
+    md.ids = m->ids; md.wts = m->wts; md.x = m->x; md.k = k; md.F = Fe; md.dim = d.dim; md.x_stride = d.dim;
+    int blocks = cdiv(d.dim, 4);
+    if (blocks > 512) blocks = 512;
+    hipLaunchKernelGGL(k_moe_down, dim3(blocks, rows), dim3(256), 0, st, md);
+    if ((rc = launched())) return rc;
+  }
+  return T2R_OK;
+}
+
+// final RMSNorm + quant_act + classifier of workspace row `row`, with the greedy argmax
+int run_final(Model* m, int row, float* logits, int32_t* next_token, int32_t* pos, int advance, hipStream_t st) {
+  const t2r_model_desc& d = m->d;
+  GemvArgs a = gemv_args();
+  a.w = d.cls_q; a.s_w = d.cls_s;
+  a.x = m->x + (long long)row * d.dim; a.g = d.rms_final; a.inv_n = (float)(1.0 / d.dim); a.eps = d.eps; a.D = d.D;
+  a.N = d.vocab; a.K = d.dim; a.y = logits ? logits : m->logits; a.argmax_key = m->keys;
+  int rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, 1, st);
+  if (rc) return rc;
+  if (next_token || advance) {
+    hipLaunchKernelGGL(k_finish, dim3(1), dim3(64), 0, st, m->keys, next_token, pos, advance);
+    return launched();
+  }
+  return T2R_OK;
+}
+
+}  // namespace
+
+// ================================================================== C-ABI
+extern "C" {
+
+int t2r_abi_version(void) { return T2R_ABI_VERSION; }
+
+const char* t2r_strerror(int code) {
+  switch (code) {
+    case T2R_OK: return "ok";
+    case T2R_EINVAL: return "invalid argument";
+    case T2R_ESHAPE: return "shape not supported (XERR_SHAPE)";
+    case T2R_ERANGE: return "index or size out of range (XERR_RANGE)";
+    case T2R_EHIP: return "HIP runtime error";
+    case T2R_ENOMEM: return "workspace too small";
+    case T2R_ESTATE: return "bad model state";
+    default: return "unknown error";
+  }
+}
+
+int t2r_init(void) { return ensure_init(); }
+
+int t2r_sfu_tables(uint32_t* out) {
+  if (!out) return T2R_EINVAL;
+  T2R_INIT();
+  if (hipMemcpyFromSymbol(out, HIP_SYMBOL(c_sfu), kSfuWords * 4, 0, hipMemcpyDeviceToHost) != hipSuccess)
+    return T2R_EHIP;
+  return T2R_OK;
+}
+
+int t2r_sfu(int fn, const uint32_t* x, uint32_t* y, int64_t n, void* stream) {
+  if (fn < 0 || fn > 3 || n < 0 || (n > 0 && (!x || !y))) return T2R_EINVAL;
+  T2R_INIT();
+  if (n == 0) return T2R_OK;
+  long long blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(k_sfu, dim3((unsigned)blocks), dim3(256), 0, S(stream), fn, x, y, (long long)n);
+  return launched();
+}
+
+int t2r_fp32_op(int op, const uint32_t* a, const uint32_t* b, uint32_t* y, int64_t n, void* stream) {
+  if (op < 0 || op > 8 || n < 0 || (n > 0 && (!a || !b || !y))) return T2R_EINVAL;
+  T2R_INIT();
+  if (n == 0) return T2R_OK;
+  long long blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(k_fp32op, dim3((unsigned)blocks), dim3(256), 0, S(stream), op, a, b, y, (long long)n);
+  return launched();
+}
+
+int t2r_requant(const int32_t* r, int64_t n, int scale, int shift, int zp, int lo, int hi, int8_t* out,
+                void* stream) {
+  if (n < 0 || (n > 0 && (!r || !out))) return T2R_EINVAL;
+  if (shift < 0 || shift > 31 || scale < -32768 || scale > 32767 || lo > hi) return T2R_ERANGE;
+  T2R_INIT();
+  if (n == 0) return T2R_OK;
+  long long blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(k_requant, dim3((unsigned)blocks), dim3(256), 0, S(stream), r, (long long)n, scale, shift, zp,
+                     lo, hi, out);
+  return launched();
+}
+
+int t2r_embed(const int8_t* emb_q, const float* emb_s, const int32_t* tokens, int rows, int dim, int vocab, float* x,
+              int32_t* status, void* stream) {
+  if (!emb_q || !emb_s || !tokens || !x) return T2R_EINVAL;
+  if (rows <= 0 || dim <= 0 || vocab <= 0) return T2R_ESHAPE;
+  T2R_INIT();
+  hipLaunchKernelGGL(k_embed, dim3(rows), dim3(256), 0, S(stream), emb_q, emb_s, tokens, dim, vocab, x,
+                     (long long)dim, (unsigned long long*)nullptr, 0, status);
+  return launched();
+}
+
+int t2r_rmsnorm(const float* x, const float* g, int rows, int n, float eps, int D, float* out, void* stream) {
+  if (!x || !g || !out) return T2R_EINVAL;
+  if (rows <= 0 || n <= 0 || n > kMaxK || (D != 8 && D != 16)) return T2R_ESHAPE;
+  T2R_INIT();
+  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, S(stream), x, g, n, (float)(1.0 / n), eps, D, out);
+  return launched();
+}
+
+int t2r_quant_act(const float* x, int rows, int n, int8_t* xq, float* s_x, void* stream) {
+  if (!x || !xq || !s_x) return T2R_EINVAL;
+  if (rows <= 0 || n <= 0 || n > kMaxK || n % 16) return T2R_ESHAPE;
+  T2R_INIT();
+  GemvArgs a = gemv_args();
+  a.x = x; a.x_stride = n; a.K = n; a.xq_out = xq; a.xq_stride = n; a.sx_out = s_x;
+  hipLaunchKernelGGL(k_rows_norm_quant, dim3(rows), dim3(kGemvThreads), 0, S(stream), a, 0, (float*)nullptr, 0LL);
+  return launched();
+}
+
+int t2r_gemv_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const float* s_x, int N, int K, float* y,
+                  int32_t* acc_out, const float* residual, void* stream) {
+  return t2r_gemm_w8a8(w, s_w, xq, s_x, 1, N, K, y, acc_out, residual, stream);
+}
+
+int t2r_gemm_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const float* s_x, int M, int N, int K,
+                  float* y, int32_t* acc_out, const float* residual, void* stream) {
+  if (!w || !s_w || !xq || !s_x || (!y && !acc_out) || (residual && !y)) return T2R_EINVAL;
+  if (M <= 0 || N <= 0 || K <= 0 || K % 16 || K > kMaxK) return T2R_ESHAPE;
+  T2R_INIT();
+  GemvArgs a = gemv_args();
+  a.w = w; a.s_w = s_w; a.xq = xq; a.xq_stride = K; a.s_x = s_x; a.N = N; a.K = K;
+  a.acc_out = acc_out;
+  float* scratch_y = y;
+  if (!y) return T2R_EINVAL;   // y is required by the kernels' epilogue (acc_out is an extra)
+  a.y = scratch_y; a.y_stride = N;
+  if (residual) {
+    a.res = residual; a.res_stride = N;
+    return gemm_dispatch<EPI_RESID>(a, M, S(stream));
+  }
+  return gemm_dispatch<EPI_STORE>(a, M, S(stream));
+}
+
+int t2r_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* pos, int rows, int n, int half,
+             void* stream) {
+  if (!v || !cos_t || !sin_t || !pos) return T2R_EINVAL;
+  if (rows <= 0 || n <= 0 || half <= 0 || n % (2 * half)) return T2R_ESHAPE;
+  T2R_INIT();
+  hipLaunchKernelGGL(k_rope, dim3(rows), dim3(256), 0, S(stream), v, cos_t, sin_t, pos, n, half);
+  return launched();
+}
+
+int t2r_kv_append(const float* k, const float* v, float inv_sk, float inv_sv, int8_t* kc, int8_t* vc,
+                  const int32_t* pos, int rows, int kv_dim, void* stream) {
+  if (!k || !v || !kc || !vc || !pos) return T2R_EINVAL;
+  if (rows <= 0 || kv_dim <= 0) return T2R_ESHAPE;
+  T2R_INIT();
+  hipLaunchKernelGGL(k_kv_append, dim3(rows), dim3(256), 0, S(stream), k, v, inv_sk, inv_sv, kc, vc, pos, kv_dim);
+  return launched();
+}
+
+int t2r_attn_decode(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H, int Hk,
+                    int hd, int S_, float a_k, float a_v, int D, float* att, void* stream) {
+  if (!q || !kc || !vc || !pos || !att) return T2R_EINVAL;
+  if (rows <= 0) return T2R_ESHAPE;
+  T2R_INIT();
+  AttnArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.qkv = (float*)q; a.qkv_stride = (long long)H * hd;
+  a.kc = (int8_t*)kc; a.vc = (int8_t*)vc; a.pos = pos;
+  a.a_k = a_k; a.a_v = a_v; a.H = H; a.Hk = Hk; a.hd = hd; a.D = D; a.S = S_;
+  a.att = att; a.att_stride = (long long)H * hd;
+  return attn_launch(ATTN_ONLY, a, rows, S(stream));
+}
+
+int t2r_swiglu_w8a8(const int8_t* w1, const float* s_w1, const int8_t* w3, const float* s_w3, const int8_t* xq,
+                    const float* s_x, int F, int K, float* u_out, int8_t* hq, float* s_h, void* stream) {
+  if (!w1 || !s_w1 || !w3 || !s_w3 || !xq || !s_x || !u_out || !hq || !s_h) return T2R_EINVAL;
+  if (F <= 0 || F % 16 || F > kMaxK) return T2R_ESHAPE;
+  T2R_INIT();
+  GemvArgs a = gemv_args();
+  a.w = w1; a.s_w = s_w1; a.w3 = w3; a.s_w3 = s_w3; a.xq = xq; a.xq_stride = K; a.s_x = s_x;
+  a.N = F; a.K = K; a.y = u_out; a.y_stride = F;
+  int rc = gemv_launch<PRO_XQ, EPI_SWIGLU>(a, 1, S(stream));
+  if (rc) return rc;
+  return t2r_quant_act(u_out, 1, F, hq, s_h, stream);
+}
+
+int t2r_moe_route(const float* scores, int rows, int E, int k, int D, int32_t* ids, float* weights, void* stream) {
+  if (!scores || !ids || !weights) return T2R_EINVAL;
+  if (rows <= 0 || E <= 0 || E > 64 || k < 1 || k > 8 || k > E || (D != 8 && D != 16)) return T2R_ESHAPE;
+  T2R_INIT();
+  hipLaunchKernelGGL(k_route_scores, dim3(rows), dim3(64), 0, S(stream), scores, E, k, D, ids, weights);
+  return launched();
+}
+
+int t2r_argmax(const float* x, int rows, int n, int32_t* idx, void* stream) {
+  if (!x || !idx) return T2R_EINVAL;
+  if (rows <= 0 || n <= 0) return T2R_ESHAPE;
+  T2R_INIT();
+  hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(256), 0, S(stream), x, n, idx);
+  return launched();
+}
+
+// ---------------------------------------------------------------- model level
+int64_t t2r_model_workspace_bytes(const t2r_model_desc* desc, int max_rows) {
+  if (!desc || max_rows < 1) return -1;
+  Model m;
+  m.d = *desc;
+  model_dims(&m);
+  return carve(&m, nullptr, max_rows);
+}
+
+int t2r_model_create(const t2r_model_desc* desc, void** model) {
+  if (!model) return T2R_EINVAL;
+  *model = nullptr;
+  int rc = validate(desc);
+  if (rc) return rc;
+  T2R_INIT();
+  Model* m = new (std::nothrow) Model();
+  if (!m) return T2R_ENOMEM;
+  m->d = *desc;
+  model_dims(m);
+  if (carve(m, nullptr, desc->max_rows) > desc->workspace_bytes) {
+    delete m;
+    return T2R_ENOMEM;
+  }
+  carve(m, (char*)desc->workspace, desc->max_rows);
+  m->kvc.assign(desc->kv_consts, desc->kv_consts + (size_t)desc->layers * 4);
+  m->d.kv_consts = nullptr;
+  *model = m;
+  return T2R_OK;
+}
+
+void t2r_model_destroy(void* model) { delete (Model*)model; }
+
+int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logits, int32_t* next_token, int flags,
+                    void* stream) {
+  Model* m = (Model*)model;
+  if (!m || !token || !pos) return T2R_EINVAL;
+  T2R_INIT();
+  hipStream_t st = S(stream);
+  const t2r_model_desc& d = m->d;
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, d.emb_q, d.emb_s, token, d.dim, d.vocab, m->x,
+                     (long long)d.dim, m->keys, 1, m->status);
+  int rc = launched();
+  if (rc) return rc;
+  for (int l = 0; l < d.layers; ++l)
+    if ((rc = run_layer(m, l, 1, pos, true, st))) return rc;
+  return run_final(m, 0, logits, next_token, pos, flags & T2R_ADVANCE_POS, st);
+}
+
+int t2r_prefill(void* model, const int32_t* tokens, const int32_t* positions, int M, float* last_logits,
+                int32_t* next_token, void* stream) {
+  Model* m = (Model*)model;
+  if (!m || !tokens || !positions) return T2R_EINVAL;
+  if (M < 1 || M > m->d.max_rows) return T2R_ERANGE;
+  T2R_INIT();
+  hipStream_t st = S(stream);
+  const t2r_model_desc& d = m->d;
+  hipLaunchKernelGGL(k_embed, dim3(M), dim3(256), 0, st, d.emb_q, d.emb_s, tokens, d.dim, d.vocab, m->x,
+                     (long long)d.dim, m->keys, 1, m->status);
+  int rc = launched();
+  if (rc) return rc;
+  for (int l = 0; l < d.layers; ++l)
+    if ((rc = run_layer(m, l, M, positions, false, st))) return rc;
+  return run_final(m, M - 1, last_logits, next_token, nullptr, 0, st);
+}
+
+}  // extern "C"

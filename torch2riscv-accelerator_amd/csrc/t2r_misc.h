@@ -1,0 +1,311 @@
+// Row kernels around the linear layers and attention: embedding, RMSNorm / quant_act rows,
+// RoPE, KV append, the MoE router / expert combine, argmax, and the element-wise hooks that let
+// the tests see the SFU and the flush-to-zero primitives bit for bit.
+#pragma once
+#include "t2r_gemv.h"
+
+namespace t2r {
+
+// x[r] = F(f32(emb_q[tok[r]]) * emb_s[tok[r]]) (llm/ref_model.py:221); block 0 also clears the
+// argmax keys of the step (one per row) when given.
+__global__ __launch_bounds__(256) void k_embed(const int8_t* emb_q, const float* emb_s, const int32_t* tokens,
+                                               int dim, int vocab, float* x, long long x_stride,
+                                               unsigned long long* keys, int nkeys, int32_t* status) {
+  const int r = blockIdx.x;
+  int t = tokens[r];
+  if (t < 0 || t >= vocab) {
+    if (threadIdx.x == 0 && status) *status = 1;      // out-of-range token: row 0 of the table instead
+    t = 0;
+  }
+  const float s = emb_s[t];
+  for (int i = threadIdx.x; i < dim; i += blockDim.x) x[r * x_stride + i] = (float)emb_q[(long long)t * dim + i] * s;
+  if (keys && r == 0)
+    for (int i = threadIdx.x; i < nkeys; i += blockDim.x) keys[i] = 0;
+}
+
+// RMSNorm and / or quant_act of rows (prefill inputs of the MFMA GEMM; the op-level ABI).
+// out_f: normalised rows (optional), xq / s_x: quantised rows (optional).
+__global__ __launch_bounds__(kGemvThreads) void k_rows_norm_quant(GemvArgs a, int norm, float* out_f, long long out_stride) {
+  __shared__ __align__(16) int8_t xq_lds[kMaxK];
+  __shared__ float xf_lds[kMaxK];
+  __shared__ float red[64];
+  const int row = blockIdx.x;
+  float s_x;
+  if (norm) s_x = gemv_prologue<PRO_NORM_QUANT>(a, row, xq_lds, xf_lds, red);
+  else s_x = gemv_prologue<PRO_QUANT>(a, row, xq_lds, xf_lds, red);
+  for (int i = threadIdx.x; i < a.K; i += kGemvThreads) {
+    if (out_f) out_f[row * out_stride + i] = xf_lds[i];
+    if (a.xq_out) a.xq_out[row * a.xq_stride + i] = xq_lds[i];
+  }
+  if (threadIdx.x == 0 && a.sx_out) a.sx_out[row] = s_x;
+}
+
+// RMSNorm alone (no quantisation): out = F(F(x * r) * g), r = RSQRT(F(F(ss * F(1/n)) + F(eps)))
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* g, int n, float inv_n, float eps, int D,
+                                                 float* out) {
+  __shared__ float xs[kMaxK];
+  __shared__ float rr;
+  const int row = blockIdx.x;
+  x += (long long)row * n;
+  out += (long long)row * n;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) xs[i] = x[i];
+  __syncthreads();
+  if (threadIdx.x < D) {
+    const float ss = ordered_sum<true>(xs, n, D, threadIdx.x);
+    if (threadIdx.x == 0) rr = sfu_rsqrt(ss * inv_n + eps);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (xs[i] * rr) * g[i];
+}
+
+// RoPE of rows v[rows, n] in place at positions pos[rows]; the tables are [S, half] (pairs of a
+// head), n a multiple of 2 * half (the heads of a row).
+__global__ __launch_bounds__(256) void k_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* pos,
+                                              int n, int half) {
+  const int row = blockIdx.x;
+  float* r = v + (long long)row * n;
+  const int p = pos[row];
+  for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
+    const int k = i % half;
+    const float c = cos_t[(long long)p * half + k], s = sin_t[(long long)p * half + k];
+    const float v0 = r[2 * i], v1 = r[2 * i + 1];
+    const float o0 = (v0 * c) + ((-v1) * s), o1 = (v1 * c) + (v0 * s);
+    r[2 * i] = o0;
+    r[2 * i + 1] = o1;
+  }
+}
+
+// kc[pos[r]] = to_i8(F(k[r] * inv_sk)), vc[pos[r]] = to_i8(F(v[r] * inv_sv))
+__global__ __launch_bounds__(256) void k_kv_append(const float* k, const float* v, float inv_sk, float inv_sv,
+                                                   int8_t* kc, int8_t* vc, const int32_t* pos, int kv_dim) {
+  const int row = blockIdx.x;
+  const long long p = pos[row];
+  for (int i = threadIdx.x; i < kv_dim; i += blockDim.x) {
+    kc[p * kv_dim + i] = (int8_t)to_i8(k[(long long)row * kv_dim + i] * inv_sk);
+    vc[p * kv_dim + i] = (int8_t)to_i8(v[(long long)row * kv_dim + i] * inv_sv);
+  }
+}
+
+// Top-k of a score vector in device order (compiler/tests/oracle.py:558-585): descending value,
+// an equal value before a larger id; NaN scores after every number. Then the route weights
+// e = EXP(F(v - v0)), w = F(e * RECIP(red_sum(e))) (compiler/frontend/hf_generic.py:641-646).
+// Run by lanes [0, 64) of wave 0; sc in LDS.
+T2R_DEV bool route_before(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return nb && (!na || ia < ib);
+  if (a != b) return a > b;
+  return ia < ib;
+}
+
+T2R_DEV void route_topk(const float* sc, int E, int k, int D, int lane, int32_t* ids, float* w, float* ev) {
+  if (lane == 0) {
+    int sel[8];
+    for (int j = 0; j < k; ++j) {
+      int best = -1;
+      for (int e = 0; e < E; ++e) {
+        bool used = false;
+        for (int q = 0; q < j; ++q) used |= sel[q] == e;
+        if (used) continue;
+        if (best < 0 || route_before(sc[e], e, sc[best], best)) best = e;
+      }
+      sel[j] = best;
+      ids[j] = best;
+    }
+    const float v0 = sc[sel[0]];
+    for (int j = 0; j < k; ++j) ev[j] = sfu_exp(sc[sel[j]] - v0);
+  }
+  __builtin_amdgcn_wave_barrier();
+  float s = 0.0f;
+  if (lane < D) s = ordered_sum<false>(ev, k, D, lane);
+  s = __shfl(s, 0);
+  const float r = sfu_recip(s);
+  if (lane < k) w[lane] = ev[lane] * r;
+}
+
+// The MoE router of rows: RMSNorm + quant_act of x (the activations every expert shares), the
+// router's W8A8 scores, top-k and weights. One block per row.
+struct RouteArgs {
+  GemvArgs a;                 // x, g, inv_n, eps, D, router weights (w, s_w; N = E, K = dim)
+  int k;
+  int32_t* ids;               // [rows, k]
+  float* wts;                 // [rows, k]
+  float* scores;              // optional [rows, E]
+};
+__global__ __launch_bounds__(kGemvThreads) void k_moe_route(RouteArgs ra) {
+  __shared__ __align__(16) int8_t xq_lds[kMaxK];
+  __shared__ float xf_lds[kMaxK];
+  __shared__ float red[64];
+  __shared__ float sc[64];
+  __shared__ float ev[16];
+  const GemvArgs& a = ra.a;
+  const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int norm = a.g != nullptr;
+  const float s_x = norm ? gemv_prologue<PRO_NORM_QUANT>(a, row, xq_lds, xf_lds, red)
+                         : gemv_prologue<PRO_XQ>(a, row, xq_lds, xf_lds, red);
+  if (a.xq_out) {
+    for (int i = threadIdx.x; i < a.K; i += kGemvThreads) a.xq_out[row * a.xq_stride + i] = xq_lds[i];
+    if (threadIdx.x == 0) a.sx_out[row] = s_x;
+  }
+  for (int e = wave; e < a.N; e += kGemvThreads / 64) {
+    int acc = 0;
+    for (int col = lane * 16; col < a.K; col += 1024)
+      acc = dot16(*(const int4*)(a.w + (long long)e * a.K + col), *(const int4*)(xq_lds + col), acc);
+    acc = wave_sum_i32(acc);
+    if (lane == 0) sc[e] = dequant(acc, a.s_w[e], s_x);
+  }
+  __syncthreads();
+  if (ra.scores)
+    for (int e = threadIdx.x; e < a.N; e += kGemvThreads) ra.scores[row * a.N + e] = sc[e];
+  if (wave == 0) route_topk(sc, a.N, ra.k, a.D, lane, ra.ids + row * ra.k, ra.wts + row * ra.k, ev);
+}
+
+// top-k + weights from given scores (the op-level ABI)
+__global__ __launch_bounds__(64) void k_route_scores(const float* scores, int E, int k, int D, int32_t* ids, float* wts) {
+  __shared__ float sc[64];
+  __shared__ float ev[16];
+  const int row = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += 64) sc[e] = scores[row * E + e];
+  __syncthreads();
+  route_topk(sc, E, k, D, threadIdx.x, ids + row * k, wts + row * k, ev);
+}
+
+// MoE down projections and the ordered combine of one row (compiler/frontend/hf_generic.py:648-657):
+//   hq_j, s_j = quant_act(u_j)                           per selected expert j
+//   y_j[n]    = F(F(f32(wd[id_j][n] . hq_j) * s_wd) * s_j)
+//   y[n] = +0; y[n] = F(y[n] + F(w_j * y_j[n])) for j = 0..k-1 in order; x[n] = F(x[n] + y[n])
+// One wave per output row n at a time; u rows [k, F] (F <= 1024).
+struct MoeDownArgs {
+  const float* u;             // [rows, k, F]
+  const int8_t* wd;           // [E, dim, F]
+  const float* s_wd;          // [E, dim]
+  const int32_t* ids;         // [rows, k]
+  const float* wts;           // [rows, k]
+  float* x;                   // [rows, dim] residual stream, updated in place
+  int k, F, dim;
+  long long x_stride;
+};
+__global__ __launch_bounds__(256) void k_moe_down(MoeDownArgs m) {
+  __shared__ __align__(16) int8_t hq[8 * 1024];
+  __shared__ float red[64];
+  __shared__ float s_h[8];
+  __shared__ int s_id[8];
+  __shared__ float s_w[8];
+  const int row = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int k = m.k, F = m.F;
+  const float* u = m.u + (long long)row * k * F;
+  // quant_act of each expert's u (one wave per expert)
+  for (int j = wave; j < k; j += 4) {
+    float amax = 0.0f;
+    for (int i = lane; i < F; i += 64) amax = nanmax(amax, fabsf(u[j * F + i]));
+    amax = wave_max(amax);
+    const float s = amax * kInv127, inv = sfu_recip(s);
+    for (int i = lane; i < F; i += 64) hq[j * 1024 + i] = (int8_t)to_i8(u[j * F + i] * inv);
+    if (lane == 0) {
+      s_h[j] = s;
+      s_id[j] = m.ids[row * k + j];
+      s_w[j] = m.wts[row * k + j];
+    }
+  }
+  __syncthreads();
+  const int col = lane * 16;
+  int4 xr[8];
+  for (int j = 0; j < 8; ++j) xr[j] = (j < k && col < F) ? *(const int4*)(hq + j * 1024 + col) : make_int4(0, 0, 0, 0);
+  const int nwaves = gridDim.x * 4;
+  for (int n = blockIdx.x * 4 + wave; n < m.dim; n += nwaves) {
+    int4 wv[8];
+    for (int j = 0; j < 8; ++j)
+      wv[j] = (j < k && col < F) ? *(const int4*)(m.wd + ((long long)s_id[j] * m.dim + n) * F + col) : make_int4(0, 0, 0, 0);
+    int acc[8];
+    for (int j = 0; j < 8; ++j) acc[j] = wave_sum_i32(dot16(wv[j], xr[j], 0));
+    if (lane == 0) {
+      float y = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        const float yj = dequant(acc[j], m.s_wd[(long long)s_id[j] * m.dim + n], s_h[j]);
+        y = y + s_w[j] * yj;
+      }
+      float* x = m.x + row * m.x_stride;
+      x[n] = x[n] + y;
+    }
+  }
+}
+
+// argmax of rows (first index of the largest value; NaN counts as the largest): one block per row
+__global__ __launch_bounds__(256) void k_argmax(const float* x, int n, int32_t* idx) {
+  __shared__ unsigned long long red[4];
+  const int row = blockIdx.x;
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const unsigned long long kk = argmax_key(x[(long long)row * n + i], i);
+    best = kk > best ? kk : best;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long other = __shfl_xor(best, o);
+    best = other > best ? other : best;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long b = red[0];
+    for (int w = 1; w < 4; ++w) b = red[w] > b ? red[w] : b;
+    idx[row] = (int32_t)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu));
+  }
+}
+
+// End of a decode step: the greedy token from the argmax key; optionally pos += 1.
+__global__ void k_finish(const unsigned long long* key, int32_t* next_token, int32_t* pos, int advance) {
+  if (threadIdx.x == 0) {
+    if (next_token) *next_token = (int32_t)(0xFFFFFFFFu - (uint32_t)(*key & 0xFFFFFFFFu));
+    if (advance) *pos = *pos + 1;
+  }
+}
+
+// ---- test hooks: the SFU and the flush-to-zero primitives on bit patterns
+__global__ void k_sfu(int fn, const uint32_t* x, uint32_t* y, long long n) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    const float v = fv(x[i]);
+    float r;
+    switch (fn) {
+      case 0: r = sfu_exp(v); break;
+      case 1: r = sfu_recip(v); break;
+      case 2: r = sfu_rsqrt(v); break;
+      default: r = fv(x[i] & 0x7FFFFFFFu); break;
+    }
+    y[i] = fb(r);
+  }
+}
+
+// op: 0 add, 1 sub, 2 mul, 3 ldexp (b = exponent as int32), 4 floor to int32, 5 to_i8, 6 from_int
+// (a as int32), 7 IEEE mul (the vector-step multiply), 8 IEEE add
+__global__ void k_fp32op(int op, const uint32_t* a, const uint32_t* b, uint32_t* y, long long n) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    const float x0 = ftz(fv(a[i])), x1 = ftz(fv(b[i]));
+    uint32_t r;
+    switch (op) {
+      case 0: r = fb(fadd_ftz(x0, x1)); break;
+      case 1: r = fb(fadd_ftz(x0, -x1)); break;
+      case 2: r = fb(fmul_ftz(x0, x1)); break;
+      case 3: r = fb(ldexp_ftz(x0, (int)b[i])); break;
+      case 4: r = (uint32_t)floor_sat(x0); break;
+      case 5: r = (uint32_t)to_i8(fv(a[i])); break;
+      case 6: r = fb((float)(int)a[i]); break;
+      case 7: r = fb(fv(a[i]) * fv(b[i])); break;
+      default: r = fb(fv(a[i]) + fv(b[i])); break;
+    }
+    if (op <= 3 && (r & 0x7F800000u) == 0x7F800000u && (r & 0x7FFFFFu)) r = kQNaN;
+    y[i] = r;
+  }
+}
+
+// Integer REQUANT of the vector engine (llm/sa_funcsim.py:265-274):
+// q = clamp(((r * scale + 2^(shift-1)) >> shift) + zp, lo, hi), saturated to int8.
+__global__ void k_requant(const int32_t* r, long long n, int scale, int shift, int zp, int lo, int hi, int8_t* out) {
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    long long q = ((long long)r[i] * scale + (shift ? (1LL << (shift - 1)) : 0)) >> shift;
+    q += zp;
+    q = q < lo ? lo : (q > hi ? hi : q);
+    q = q < -128 ? -128 : (q > 127 ? 127 : q);
+    out[i] = (int8_t)q;
+  }
+}
+
+}  // namespace t2r

@@ -1,0 +1,154 @@
+"""A W8A8 decoder resident on one MI355X, driven through the C-ABI (t2r_model_* in include/t2r.h).
+
+PyTorch owns the device memory (weights, the int8 KV cache, the workspace, the per-step
+(pos, token) block); the kernels are the HIP ones in libt2r.so. One decode step is one call to
+t2r_decode_step, which reads the token and the position from device memory, so a HIP graph of
+it replays unchanged step after step: the GPU form of the reference's static token list where
+only the PARAM block and the (pos, token) arguments change (llm/compile_model.py:1-8, 56-62).
+"""
+import ctypes
+
+import numpy as np
+
+from . import abi
+
+F = np.float32
+
+
+class ResidentModel:
+    def __init__(self, qm, device="cuda:0", max_rows=None, D=None):
+        """qm: t2r_amd.weights.QuantModel (host arrays). max_rows: prefill rows per t2r_prefill call."""
+        import torch
+        self.torch = torch
+        self.cfg = c = qm.cfg
+        self.D = D or c.D
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError(f"{device}: the datapath runs on a GPU (HIP) device")
+        if not torch.cuda.is_available():
+            raise RuntimeError("no HIP device is visible: the W8A8 datapath has no CPU fallback")
+        self.lib = abi.load()
+        self.max_rows = max(1, int(max_rows or min(c.seq_len, 512)))
+        dev = self.device
+        keep = self._keep = {}
+
+        def up(name, a):
+            if a is None:
+                return None
+            t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+            keep[name] = t
+            return t
+
+        with torch.cuda.device(dev):
+            up("emb_q", qm.emb_q); up("emb_s", qm.emb_s)
+            if qm.cls_q is qm.emb_q:
+                keep["cls_q"], keep["cls_s"] = keep["emb_q"], keep["emb_s"]
+            else:
+                up("cls_q", qm.cls_q); up("cls_s", qm.cls_s)
+            for n in ("rms_att", "rms_ffn", "rms_final", "wqkv", "s_wqkv", "wo", "s_wo"):
+                up(n, getattr(qm, n))
+            if c.qk_norm:
+                up("q_norm", qm.q_norm); up("k_norm", qm.k_norm)
+            names = ("router", "s_router", "wg", "s_wg", "wu", "s_wu", "wd", "s_wd") if c.moe else \
+                ("w1", "s_w1", "w3", "s_w3", "w2", "s_w2")
+            for n in names:
+                up(n, getattr(qm, n))
+            up("rope_cos", qm.cos); up("rope_sin", qm.sin)
+            self.kc = torch.zeros((c.layers, c.seq_len, c.kv_dim), dtype=torch.int8, device=dev)
+            self.vc = torch.zeros_like(self.kc)
+            self.kv_consts = np.ascontiguousarray(qm.kvc, F)
+            desc = abi.ModelDesc()
+            desc.abi_version = abi.T2R_ABI_VERSION
+            desc.dim, desc.hidden, desc.layers = c.dim, c.hidden, c.layers
+            desc.heads, desc.kv_heads, desc.head_dim = c.heads, c.kv_heads, c.head_dim
+            desc.vocab, desc.seq_len = c.vocab, c.seq_len
+            desc.n_experts, desc.top_k = c.n_experts, c.top_k
+            desc.qk_norm, desc.D, desc.eps = int(c.qk_norm), self.D, float(F(c.eps))
+            for n, t in keep.items():
+                setattr(desc, n, t.data_ptr())
+            desc.kv_consts = self.kv_consts.ctypes.data
+            desc.k_cache, desc.v_cache = self.kc.data_ptr(), self.vc.data_ptr()
+            desc.max_rows = self.max_rows
+            nbytes = self.lib.t2r_model_workspace_bytes(ctypes.byref(desc), self.max_rows)
+            if nbytes <= 0:
+                raise ValueError("t2r_model_workspace_bytes rejected the model description")
+            self.workspace = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
+            desc.workspace, desc.workspace_bytes = self.workspace.data_ptr(), int(nbytes)
+            self.desc = desc
+            handle = ctypes.c_void_p()
+            abi.check("t2r_model_create", self.lib.t2r_model_create(ctypes.byref(desc), ctypes.byref(handle)))
+            self.handle = handle
+            self.tok = torch.zeros(1, dtype=torch.int32, device=dev)
+            self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+            self.next = torch.zeros(1, dtype=torch.int32, device=dev)
+            self.logits = torch.empty(c.vocab, dtype=torch.float32, device=dev)
+            self.rows_tok = torch.zeros(self.max_rows, dtype=torch.int32, device=dev)
+            self.rows_pos = torch.zeros(self.max_rows, dtype=torch.int32, device=dev)
+
+    # ------------------------------------------------------------ state
+    def reset(self):
+        """Empty KV cache (rows beyond pos must be zero, as the reference's runtime keeps them)."""
+        self.kc.zero_()
+        self.vc.zero_()
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.t2r_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------ steps
+    def step(self, logits=True, advance=False, stream=None):
+        """One decode step on the device-resident (self.tok, self.pos); the greedy token goes to self.next
+        (or to self.tok and pos += 1 with advance=True, for a device-side greedy loop)."""
+        nxt = self.tok if advance else self.next
+        abi.check("t2r_decode_step", self.lib.t2r_decode_step(
+            self.handle, abi.ptr(self.tok), abi.ptr(self.pos), abi.ptr(self.logits) if logits else None,
+            abi.ptr(nxt), abi.T2R_ADVANCE_POS if advance else 0, abi.stream_ptr(stream)))
+
+    def decode(self, token, pos):
+        """Logits (device tensor, valid until the next call) of `token` at `pos`."""
+        if not 0 <= pos < self.cfg.seq_len:
+            raise ValueError(f"position {pos} outside [0, {self.cfg.seq_len})")
+        self.tok.fill_(int(token))
+        self.pos.fill_(int(pos))
+        self.step()
+        return self.logits
+
+    def prefill(self, tokens, start=0, logits=True):
+        """Rows tokens at positions start.. as one call per max_rows chunk; logits of the last row."""
+        torch = self.torch
+        toks = [int(t) for t in tokens]
+        if start < 0 or start + len(toks) > self.cfg.seq_len:
+            raise ValueError(f"positions {start}..{start + len(toks) - 1} outside [0, {self.cfg.seq_len})")
+        if not toks:
+            raise ValueError("empty prompt")
+        i = 0
+        while i < len(toks):
+            chunk = toks[i:i + self.max_rows]
+            M = len(chunk)
+            self.rows_tok[:M].copy_(torch.tensor(chunk, dtype=torch.int32))
+            self.rows_pos[:M].copy_(torch.arange(start + i, start + i + M, dtype=torch.int32))
+            last = i + M >= len(toks)
+            abi.check("t2r_prefill", self.lib.t2r_prefill(
+                self.handle, abi.ptr(self.rows_tok), abi.ptr(self.rows_pos), M,
+                abi.ptr(self.logits) if (last and logits) else None, abi.ptr(self.next) if last else None,
+                abi.stream_ptr()))
+            i += M
+        return self.logits
+
+    def prefill_chunks(self, tokens, M=16):
+        """The reference's chunk schedule (compiler/frontend/export.py:69-72): chunks of M rows at
+        0, M, 2M, ... and a last one at P - M (it recomputes rows the one before wrote, with the same
+        values); a prompt shorter than M runs as one chunk."""
+        P = len(tokens)
+        starts = [0] if P <= M else list(range(0, P - M, M)) + [P - M]
+        out = None
+        for s in starts:
+            out = self.prefill(tokens[s:s + M], start=s)
+        return out

@@ -1,0 +1,186 @@
+"""The llm/runtime.py API on the MI355X datapath: LlamaDevice and run.c's Sampler.
+
+    dev = LlamaDevice("c1-stories15m")                     # a config (synthetic weights) or a QuantModel
+    for tok, text in dev.generate([1, 400, 22], steps=64):
+        ...
+    dev.close()
+
+Same methods, arguments, yields and exceptions as the reference's LlamaDevice
+(llm/runtime.py:75-152): reset() empties the KV cache, forward(token) returns a float32 copy of
+the logits and advances pos (ValueError when the sequence is full, RuntimeError when a step
+fails), generate() feeds the prompt through the decode path and then samples. The FPGA-only
+constructor arguments (bitfile, firmware, use_irq) are accepted and ignored; `device` names the
+GPU ("cuda:0") instead of an injectable PYNQ Device. Additions: prefill() runs prompt rows
+through the int8 MFMA GEMM path (bit-identical to feeding them one by one), and
+greedy_on_device() runs a whole greedy loop without host round trips.
+"""
+import time
+
+import numpy as np
+
+from . import config as C
+from . import weights as W
+from .model import ResidentModel
+
+F = np.float32
+BOS = 1
+
+
+class Sampler:
+    """llama2.c run.c's sampler: temperature 0 = argmax; otherwise softmax(logits / T) and then
+    top-p (nucleus) sampling, or multinomial when topp is not in (0, 1), with run.c's xorshift*
+    random numbers (llm/runtime.py:37-72)."""
+    MASK = (1 << 64) - 1
+
+    def __init__(self, temperature=0.0, topp=0.9, seed=1):
+        self.t, self.topp = temperature, topp
+        self.state = (seed & self.MASK) or 1
+
+    def random_u32(self):
+        s = self.state
+        s ^= s >> 12
+        s ^= (s << 25) & self.MASK
+        s ^= s >> 27
+        self.state = s
+        return ((s * 0x2545F4914F6CDD1D) & self.MASK) >> 32
+
+    def random_f32(self):
+        return (self.random_u32() >> 8) / 16777216.0
+
+    def __call__(self, logits):
+        if self.t == 0:
+            return int(np.argmax(logits))
+        x = np.asarray(logits, F) / F(self.t)
+        p = np.exp((x - x.max()).astype(F)).astype(F)
+        p /= p.sum(dtype=F)
+        coin = self.random_f32()
+        if self.topp <= 0 or self.topp >= 1:
+            cdf = np.cumsum(p, dtype=F)
+            return int(min(np.searchsorted(cdf, coin, side="right"), p.size - 1))
+        # nucleus: candidates above (1 - topp) / (n - 1), by descending probability (stable)
+        cutoff = (1.0 - self.topp) / (p.size - 1)
+        cand = np.flatnonzero(p >= cutoff)
+        cand = cand[np.argsort(-p[cand], kind="stable")]
+        cdf = np.cumsum(p[cand], dtype=F)
+        last = int(min(np.searchsorted(cdf, F(self.topp), side="right"), cand.size - 1))
+        r = coin * float(cdf[last])
+        return int(cand[int(min(np.searchsorted(cdf[:last + 1], r, side="right"), last))])
+
+
+def _resolve_model(model):
+    if isinstance(model, W.QuantModel):
+        return model
+    if isinstance(model, C.ModelConfig):
+        return W.QuantModel(model)
+    if isinstance(model, str):
+        return W.QuantModel(C.get(model))
+    raise TypeError(f"model: a ModelConfig, a config name or a QuantModel, not {type(model).__name__}")
+
+
+class LlamaDevice:
+    def __init__(self, model_path, tokenizer_path=None, bitfile=None, firmware=None, use_irq=True, device=None,
+                 max_rows=None):
+        self.qm = _resolve_model(model_path)
+        c = self.cfg = self.qm.cfg
+        self.d = c.D
+        self.tok = None
+        if tokenizer_path is not None:
+            raise NotImplementedError("tokenizer files are not supported yet; pass token ids")
+        self.m = ResidentModel(self.qm, device=device or "cuda:0", max_rows=max_rows)
+        self.pos = 0
+        self.stats = []                          # per token: (pos, device ns, wall seconds)
+
+    def reset(self):
+        """Start a new sequence: empty KV cache, pos 0."""
+        self.m.reset()
+        self.pos = 0
+
+    def forward(self, token, perf=False):
+        """Logits (float32 copy) of token at the current position; advances pos."""
+        c = self.cfg
+        if self.pos >= c.seq_len:
+            raise ValueError(f"sequence full ({c.seq_len} positions)")
+        torch = self.m.torch
+        t0 = time.perf_counter()
+        if perf:
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
+        try:
+            lg = self.m.decode(token, self.pos)
+            if perf:
+                ev1.record()
+            logits = lg.cpu().numpy().copy()
+        except RuntimeError as e:
+            raise RuntimeError(f"pos {self.pos}: step failed: {e}") from e
+        wall = time.perf_counter() - t0
+        dev_ns = int(ev0.elapsed_time(ev1) * 1e6) if perf else None
+        self.stats.append((self.pos, dev_ns, wall))
+        self.pos += 1
+        return logits
+
+    def prefill(self, tokens):
+        """Feed prompt rows at pos.. in one pass (the MFMA GEMM path); returns the last row's logits
+        (float32 copy). Bit-identical to calling forward() on each token."""
+        c = self.cfg
+        if self.pos + len(tokens) > c.seq_len:
+            raise ValueError(f"sequence full ({c.seq_len} positions)")
+        lg = self.m.prefill(tokens, start=self.pos)
+        self.pos += len(tokens)
+        return lg.cpu().numpy().copy()
+
+    def generate(self, prompt, steps=256, temperature=0.0, topp=0.9, seed=1, stop_at_bos=True, forced=None):
+        """Yield (token, text piece) per generated token, run.c style: the prompt tokens are fed first,
+        then sampled tokens until `steps` positions (or BOS). prompt: token ids (a tokenizer is not
+        loaded; the text piece is None). forced: teacher forcing, yields (argmax, logits) per position."""
+        self.reset()
+        toks = list(forced) if forced is not None else list(prompt)
+        sample = Sampler(temperature, topp, seed)
+        token = toks[0]
+        for pos in range(min(steps, self.cfg.seq_len)):
+            logits = self.forward(token)
+            if forced is not None:
+                yield int(np.argmax(logits)), logits
+                if pos + 1 >= len(forced):
+                    return
+                token = forced[pos + 1]
+                continue
+            nxt = toks[pos + 1] if pos + 1 < len(toks) else sample(logits)
+            if nxt == BOS and stop_at_bos:
+                return
+            yield nxt, None
+            token = nxt
+
+    def greedy_on_device(self, prompt, steps, use_prefill=True):
+        """Prompt (prefilled, or fed as decode steps), then greedy decode until `steps` positions, with
+        the argmax and the position update on the device (no host round trip per token). Returns the
+        tokens fed at every position plus the last one chosen (as ref_model.generate without BOS stop)."""
+        torch = self.m.torch
+        self.reset()
+        P = len(prompt)
+        steps = min(steps, self.cfg.seq_len)
+        out = list(prompt[:steps])
+        if use_prefill and P > 1:
+            self.m.prefill(prompt[:min(P, steps)], start=0)
+            self.m.tok.copy_(self.m.next)
+            self.m.pos.fill_(min(P, steps))
+            done = min(P, steps)
+        else:
+            done = 0
+            for pos in range(min(P, steps)):
+                self.m.decode(prompt[pos], pos)
+            done = min(P, steps)
+            self.m.tok.copy_(self.m.next)
+            self.m.pos.fill_(done)
+        gen = torch.empty(max(steps - done, 0) + 1, dtype=torch.int32, device=self.m.device)
+        gen[0:1].copy_(self.m.tok)
+        for i in range(steps - done):
+            self.m.step(logits=False, advance=True)
+            gen[i + 1:i + 2].copy_(self.m.tok)
+        self.pos = steps
+        g = gen.cpu().numpy().tolist()
+        if done < P:
+            return out
+        return out + g[:steps - done + 1]
+
+    def close(self):
+        self.m.close()

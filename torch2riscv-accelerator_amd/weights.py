@@ -1,0 +1,270 @@
+"""Host-side model data: seeded synthetic fp32 weights, their W8A8 quantisation,
+the RoPE tables and the per-layer KV constants.
+
+Everything here runs once per model on the host, as the reference's exporter
+does (llm/export_w8a8.py:75-95): the device only ever sees int8 weight rows
+with one fp32 scale per row, fp32 norm gains, the RoPE tables and four fp32
+constants per layer.
+
+- Weights: N(0, std) in float32 from one NumPy generator per tensor, seeded by
+  (seed_w, tensor id, layer), so any tensor can be regenerated alone.
+- Quantisation: symmetric per output row, s = max|w| / 127 in float32 and
+  q = to_i8(w / s) (llm/ref_model.py:136-148).
+- RoPE tables: (seq_len, head_dim / 2) cos and sin; pair i of every head at
+  position p rotates by p * theta^(-2i / head_dim). Method "f32" evaluates it
+  in float32 as llama2.c's run.c does (llm/ref_model.py:34-41), "f64" in float64
+  then rounds (compiler/frontend/qhf.py:183-189).
+- KV constants per layer from the static scales (s_k, s_v):
+  1/s_k, 1/s_v, a_k = s_k / sqrt(head_dim), a_v = s_v / 127, each computed in
+  float64 and rounded once (llm/export_w8a8.py:68-72).
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+
+F = np.float32
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+_TENSOR_ID = {"tok": 1, "wq": 2, "wk": 3, "wv": 4, "wo": 5, "w1": 6, "w3": 7, "w2": 8, "router": 9,
+              "rms_att": 10, "rms_ffn": 11, "rms_final": 12, "q_norm": 13, "k_norm": 14, "wcls": 15,
+              "wg": 16, "wu": 17, "wd": 18}
+
+
+def to_i8(x):
+    """fp32 -> int8: round half to even, saturate to [-127, 127], NaN -> 0 (llm/ref_model.py:136-139)."""
+    y = np.rint(np.asarray(x, F))
+    return np.clip(np.nan_to_num(y, nan=0.0, posinf=127, neginf=-127), -127, 127).astype(np.int8)
+
+
+def quantize_rows(w):
+    """Symmetric int8 per row: (q int8, s float32) with s = max|row| / 127 (llm/ref_model.py:142-148)."""
+    w = np.asarray(w, F)
+    s = (np.abs(w).max(axis=-1) / F(127)).astype(F)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = to_i8(w / s[..., None])
+    return q, s
+
+
+def _gen(cfg, name, layer, shape, fan_in):
+    rng = np.random.default_rng([cfg.seed_w, _TENSOR_ID[name], layer + 1])
+    std = cfg.weight_std if cfg.weight_std is not None else 1.0 / np.sqrt(fan_in)
+    return (rng.standard_normal(shape, dtype=F) * F(std)).astype(F)
+
+
+def _gain(cfg, name, layer, n):
+    if cfg.gain_std == 0:
+        return np.ones(n, F)
+    rng = np.random.default_rng([cfg.seed_w, _TENSOR_ID[name], layer + 1])
+    return (F(1) + F(cfg.gain_std) * rng.standard_normal(n, dtype=F)).astype(F)
+
+
+def fp32_tensor(cfg, name, layer=-1):
+    """One fp32 tensor of the synthetic model (PyTorch orientation: linear weights are (out, in))."""
+    d, q, kv, f = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden
+    E = cfg.n_experts
+    shapes = {"tok": ((cfg.vocab, d), d), "wq": ((q, d), d), "wk": ((kv, d), d), "wv": ((kv, d), d),
+              "wo": ((d, q), q), "w1": ((f, d), d), "w3": ((f, d), d), "w2": ((d, f), f),
+              "router": ((E, d), d), "wg": ((E, f, d), d), "wu": ((E, f, d), d), "wd": ((E, d, f), f)}
+    if name in ("rms_att", "rms_ffn", "rms_final"):
+        return _gain(cfg, name, layer, d)
+    if name in ("q_norm", "k_norm"):
+        return _gain(cfg, name, layer, cfg.head_dim)
+    shape, fan_in = shapes[name]
+    w = _gen(cfg, name, layer, shape, fan_in)
+    if name == "tok" and cfg.emb_scale != 1.0:
+        w = (w * F(cfg.emb_scale)).astype(F)
+    return w
+
+
+def rope_tables(cfg):
+    """(cos, sin), each float32 (seq_len, head_dim // 2)."""
+    hs = cfg.head_dim
+    if cfg.rope_method == "f32":
+        hd = np.arange(0, hs, 2).astype(F)
+        freq = F(1.0) / np.power(F(cfg.theta), hd / F(hs))
+        val = np.arange(cfg.seq_len, dtype=F)[:, None] * freq[None, :]
+        return np.cos(val).astype(F), np.sin(val).astype(F)
+    freq = 1.0 / np.power(float(cfg.theta), np.arange(0, hs, 2, dtype=np.float64) / hs)
+    val = np.arange(cfg.seq_len, dtype=np.float64)[:, None] * freq[None, :]
+    return np.cos(val).astype(F), np.sin(val).astype(F)
+
+
+def kv_constants(cfg, kv_scales):
+    """(L, 4) float32: 1/s_k, 1/s_v, s_k / sqrt(head_dim), s_v / 127 per layer."""
+    kv = np.asarray(kv_scales, F).reshape(cfg.layers, 2)
+    out = np.empty((cfg.layers, 4), F)
+    for l, (sk, sv) in enumerate(kv):
+        out[l] = [F(1.0 / float(sk)), F(1.0 / float(sv)), F(float(sk) / np.sqrt(cfg.head_dim)),
+                  F(float(sv) / 127.0)]
+    return out
+
+
+class QuantModel:
+    """The quantised model as the device consumes it (host NumPy arrays).
+
+    Linear layers are int8 row-major (out, in) with a float32 scale per row:
+    wqkv (L, q + 2 kv, d) = the q | k | v rows; wo (L, d, q); w1, w3 (L, F, d);
+    w2 (L, d, F); MoE: router (L, E, d), wg / wu (L, E, F, d), wd (L, E, d, F).
+    The classifier is the embedding (tied) unless cfg.tied is False.
+    """
+
+    def __init__(self, cfg, kv_scales=None, layers=None):
+        cfg.validate()
+        self.cfg = c = cfg
+        L = c.layers
+        self.emb_q, self.emb_s = quantize_rows(fp32_tensor(c, "tok"))
+        if c.tied:
+            self.cls_q, self.cls_s = self.emb_q, self.emb_s
+        else:
+            self.cls_q, self.cls_s = quantize_rows(fp32_tensor(c, "wcls"))
+        self.rms_final = fp32_tensor(c, "rms_final")
+        self.rms_att = np.stack([fp32_tensor(c, "rms_att", l) for l in range(L)])
+        self.rms_ffn = np.stack([fp32_tensor(c, "rms_ffn", l) for l in range(L)])
+        hd = c.head_dim
+        self.q_norm = np.stack([fp32_tensor(c, "q_norm", l) for l in range(L)]) if c.qk_norm else np.ones((L, hd), F)
+        self.k_norm = np.stack([fp32_tensor(c, "k_norm", l) for l in range(L)]) if c.qk_norm else np.ones((L, hd), F)
+
+        def stack(fn):
+            qs = [fn(l) for l in range(L)]
+            return np.stack([a for a, _ in qs]), np.stack([b for _, b in qs])
+        self.wqkv, self.s_wqkv = stack(lambda l: quantize_rows(np.concatenate(
+            [fp32_tensor(c, "wq", l), fp32_tensor(c, "wk", l), fp32_tensor(c, "wv", l)])))
+        self.wo, self.s_wo = stack(lambda l: quantize_rows(fp32_tensor(c, "wo", l)))
+        if c.moe:
+            self.router, self.s_router = stack(lambda l: quantize_rows(fp32_tensor(c, "router", l)))
+            self.wg, self.s_wg = stack(lambda l: quantize_rows(fp32_tensor(c, "wg", l)))
+            self.wu, self.s_wu = stack(lambda l: quantize_rows(fp32_tensor(c, "wu", l)))
+            self.wd, self.s_wd = stack(lambda l: quantize_rows(fp32_tensor(c, "wd", l)))
+        else:
+            self.w1, self.s_w1 = stack(lambda l: quantize_rows(fp32_tensor(c, "w1", l)))
+            self.w3, self.s_w3 = stack(lambda l: quantize_rows(fp32_tensor(c, "w3", l)))
+            self.w2, self.s_w2 = stack(lambda l: quantize_rows(fp32_tensor(c, "w2", l)))
+        self.cos, self.sin = rope_tables(c)
+        if kv_scales is None:
+            kv_scales = stored_kv_scales(c)
+        self.kv_scales = np.asarray(kv_scales, F).reshape(L, 2)
+        self.kvc = kv_constants(c, self.kv_scales)
+
+    def digest(self):
+        """sha256 over every array (a fingerprint of the model data)."""
+        h = hashlib.sha256()
+        for k in sorted(vars(self)):
+            v = getattr(self, k)
+            if isinstance(v, np.ndarray):
+                h.update(k.encode())
+                h.update(np.ascontiguousarray(v).tobytes())
+        return h.hexdigest()
+
+
+# ------------------------------------------------------------------ KV calibration
+def _fp32_forward_rows(cfg, tokens, amax_out):
+    """Causal fp32 forward of `tokens` at positions 0.. (all rows at once, torch on the CPU),
+    recording max|k| and max|v| per layer (after RoPE for k). llama2.c run.c semantics
+    (llm/ref_model.py:45-91) generalised as compiler/frontend/qhf.py:206-243."""
+    import torch
+    c = cfg
+    M = len(tokens)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    H, Hk, hd = c.heads, c.kv_heads, c.head_dim
+    G = H // Hk
+    cos, sin = rope_tables(c)
+    cos = t(np.repeat(cos[:M], 2, axis=1))
+    sin = t(np.repeat(sin[:M], 2, axis=1))
+
+    def rms(x, g):
+        return x * torch.rsqrt(torch.mean(x * x, dim=-1, keepdim=True) + c.eps) * g
+
+    def swapneg(v):
+        p = v.reshape(v.shape[:-1] + (-1, 2))
+        return torch.stack((-p[..., 1], p[..., 0]), dim=-1).reshape(v.shape)
+
+    with torch.no_grad():
+        x = t(fp32_tensor(c, "tok"))[torch.tensor(tokens)]
+        mask = torch.tril(torch.ones(M, M, dtype=torch.bool))
+        for l in range(c.layers):
+            xb = rms(x, t(fp32_tensor(c, "rms_att", l)))
+            q = (xb @ t(fp32_tensor(c, "wq", l)).T).reshape(M, H, hd)
+            k = (xb @ t(fp32_tensor(c, "wk", l)).T).reshape(M, Hk, hd)
+            v = xb @ t(fp32_tensor(c, "wv", l)).T
+            if c.qk_norm:
+                q = rms(q, t(fp32_tensor(c, "q_norm", l)))
+                k = rms(k, t(fp32_tensor(c, "k_norm", l)))
+            q = q * cos[:, None] + swapneg(q) * sin[:, None]
+            k = k * cos[:, None] + swapneg(k) * sin[:, None]
+            amax_out[l, 0] = max(amax_out[l, 0], float(k.abs().max()))
+            amax_out[l, 1] = max(amax_out[l, 1], float(v.abs().max()))
+            kk = k.repeat_interleave(G, dim=1)                        # (M, H, hd)
+            vv = v.reshape(M, Hk, hd).repeat_interleave(G, dim=1)
+            s = torch.einsum("mhd,thd->hmt", q, kk) / np.sqrt(hd)
+            s = s.masked_fill(~mask[None], float("-inf"))
+            att = torch.einsum("hmt,thd->mhd", torch.softmax(s, dim=-1), vv).reshape(M, -1)
+            x = x + att @ t(fp32_tensor(c, "wo", l)).T
+            xb = rms(x, t(fp32_tensor(c, "rms_ffn", l)))
+            if c.moe:
+                sc = xb @ t(fp32_tensor(c, "router", l)).T               # (M, E)
+                vals, ids = torch.topk(sc, c.top_k, dim=-1)
+                wts = torch.softmax(vals, dim=-1)
+                wg, wu, wd = (t(fp32_tensor(c, n, l)) for n in ("wg", "wu", "wd"))
+                y = torch.zeros_like(x)
+                for m in range(M):
+                    for j in range(c.top_k):
+                        e = int(ids[m, j])
+                        h = torch.nn.functional.silu(wg[e] @ xb[m]) * (wu[e] @ xb[m])
+                        y[m] += wts[m, j] * (wd[e] @ h)
+                x = x + y
+            else:
+                h = torch.nn.functional.silu(xb @ t(fp32_tensor(c, "w1", l)).T) * (xb @ t(fp32_tensor(c, "w3", l)).T)
+                x = x + h @ t(fp32_tensor(c, "w2", l)).T
+
+
+def calibrate_kv(cfg, tokens=None, chunk=None):
+    """Static per-layer KV scales: max(absmax, 1e-8) / 127 over an fp32 run of the prompt
+    (llm/test_l4.py:51-55, compiler/frontend/qhf.py:246-251)."""
+    tokens = cfg.prompt() if tokens is None else list(tokens)
+    tokens = tokens[:cfg.seq_len]
+    amax = np.zeros((cfg.layers, 2), np.float64)
+    _fp32_forward_rows(cfg, tokens, amax)
+    return (np.maximum(amax, 1e-8) / 127.0).astype(F)
+
+
+_KV_FILE = os.path.join(HERE, "kv_scales.json")
+
+
+def stored_kv_scales(cfg):
+    """The recorded calibration of a named config (kv_scales.json, float32 bit patterns); the tiny
+    test models are calibrated on the fly."""
+    if os.path.exists(_KV_FILE):
+        with open(_KV_FILE) as f:
+            table = json.load(f)
+        if cfg.name in table and table[cfg.name]["seed_w"] == cfg.seed_w:
+            return np.array(table[cfg.name]["bits"], np.uint32).view(F).reshape(cfg.layers, 2)
+    if cfg.layers * cfg.dim <= 1 << 16:
+        return calibrate_kv(cfg)
+    raise FileNotFoundError(f"no recorded KV scales for {cfg.name}; run `python -m t2r_amd.weights --calibrate "
+                            f"{cfg.name}` in a checkout that has the reference data")
+
+
+def _main():
+    import argparse
+    import sys
+    sys.path.insert(0, os.path.dirname(HERE))
+    ap = argparse.ArgumentParser(description="record the static KV scales of the named configs")
+    ap.add_argument("--calibrate", nargs="+", required=True)
+    args = ap.parse_args()
+    from t2r_amd import config as C
+    table = json.load(open(_KV_FILE)) if os.path.exists(_KV_FILE) else {}
+    for name in args.calibrate:
+        cfg = C.get(name)
+        kv = calibrate_kv(cfg)
+        table[cfg.name] = {"seed_w": cfg.seed_w, "prompt_len": cfg.prompt_len,
+                           "bits": [int(b) for b in kv.view(np.uint32).ravel()],
+                           "values": [float(v) for v in kv.ravel()]}
+        print(cfg.name, kv.ravel()[:6], "...", flush=True)
+        with open(_KV_FILE, "w") as f:
+            json.dump(table, f, indent=1)
+
+
+if __name__ == "__main__":
+    _main()
