@@ -90,17 +90,19 @@ int t2r_gemm_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const flo
                   float* y, int32_t* acc_out, const float* residual, void* stream);
 /* RoPE of rows v[rows, n] in place at positions pos[rows] (DeviceModel.rope llm/ref_model.py:209-214;
  * ModelCompiler.rope llm/compile_model.py:203-214): pairs (2i, 2i+1), tables [S, half] with
- * half = head_dim / 2, pair i using column i % half. */
-int t2r_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* pos, int rows, int n, int half,
+ * half = head_dim / 2, pair i using column i % half. A row whose position is outside [0, S) is
+ * left unchanged. */
+int t2r_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* pos, int rows, int n, int half, int S,
              void* stream);
 /* KV append (llm/ref_model.py:228-229; ModelCompiler.kv_append llm/compile_model.py:221-231):
- * kc[pos[r]] = to_i8(F(k[r] * inv_sk)), vc[pos[r]] = to_i8(F(v[r] * inv_sv)); caches [S, kv_dim]. */
+ * kc[pos[r]] = to_i8(F(k[r] * inv_sk)), vc[pos[r]] = to_i8(F(v[r] * inv_sv)); caches [S, kv_dim].
+ * A row whose position is outside [0, S) is not written. */
 int t2r_kv_append(const float* k, const float* v, float inv_sk, float inv_sv, int8_t* kc, int8_t* vc,
-                  const int32_t* pos, int rows, int kv_dim, void* stream);
+                  const int32_t* pos, int rows, int kv_dim, int S, void* stream);
 /* Attention of rows q[rows, H * hd] (already rotated) at positions pos[rows] over the int8 cache
  * rows 0..pos (DeviceModel.forward llm/ref_model.py:230-243; ModelCompiler.attention
  * llm/compile_model.py:233-293; GQA: compiler/frontend/qhf.py:304-319). a_k = F(s_k / sqrt(hd)),
- * a_v = F(s_v / 127). S = cache rows; S * H / Hk <= 16384, hd <= 128, H / Hk <= 8. */
+ * a_v = F(s_v / 127). S = cache rows; S * H / Hk <= 8192, hd <= 128, H / Hk <= 8. */
 int t2r_attn_decode(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H,
                     int Hk, int hd, int S, float a_k, float a_v, int D, float* att, void* stream);
 /* SwiGLU of one row (DeviceModel.forward llm/ref_model.py:246-250; ModelCompiler.ffn_up / silu_mul

@@ -1,0 +1,139 @@
+"""Model-level parity of the HIP datapath: decode steps and prefills through t2r_decode_step /
+t2r_prefill against the reference's own runs (DeviceModel and SaFuncSim fixtures) and against
+the CPU restatement for the generalised shapes (q_dim != dim, QK-norm, MoE). Bit-exact logits,
+greedy tokens and int8 KV cache."""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return json.load(open(os.path.join(GOLD, "model_golden.json")))
+
+
+def resident(cfg, kv=None, D=None, max_rows=None):
+    from t2r_amd import weights as W
+    from t2r_amd.model import ResidentModel
+    qm = W.QuantModel(cfg, kv_scales=kv)
+    return qm, ResidentModel(qm, D=D, max_rows=max_rows)
+
+
+def kv_host(rm, n):
+    return rm.kc[:, :n].cpu().numpy(), rm.vc[:, :n].cpu().numpy()
+
+
+@pytest.mark.parametrize("idx", range(6))
+def test_decode_equals_reference_runs(gold, idx):
+    """Every step's logits (sha256 of the bytes), the greedy token and the KV cache of the reference's
+    DeviceModel(SfuExact) runs; for c1-stories15m D=16 that is the whole config-1 run (32-token prompt,
+    128 greedy steps), which SaFuncSim reproduces on its first positions (the fixture checks that)."""
+    import t2r_amd.config as C
+    run = gold["device_model"][idx]
+    cfg = C.get(run["config"])
+    kv = np.array(run["kv_bits"], np.uint32).view(F).reshape(cfg.layers, 2)
+    qm, rm = resident(cfg, kv, D=run["D"])
+    print(f"{cfg.name} D={run['D']}: {run['steps']} steps", flush=True)
+    for rec in run["positions"]:
+        lg = rm.decode(rec["token"], rec["pos"]).cpu().numpy()
+        assert sha(lg) == rec["logits_sha"], f"{cfg.name} D={run['D']} pos {rec['pos']}: logits differ"
+        assert int(np.argmax(lg)) == rec["argmax"]
+        assert int(rm.next.item()) == rec["argmax"]                         # the device-side argmax
+    assert sha(*kv_host(rm, run["steps"])) == run["kv_sha"]
+    rm.close()
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen", "tiny-moe", "tiny-gqa"])
+def test_generalised_decode_vs_oracle(name):
+    import t2r_amd.config as C
+    from oracle import OracleModel
+    cfg = C.get(name)
+    qm, rm = resident(cfg)
+    om = OracleModel(qm)
+    toks = cfg.prompt()
+    seq = list(toks)
+    for pos in range(cfg.prompt_len + cfg.decode_steps):
+        t = seq[pos]
+        want = om.forward(t, pos)
+        got = rm.decode(t, pos).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{name} pos {pos}"
+        if pos + 1 >= len(seq):
+            seq.append(int(np.argmax(want)))
+    n = len(seq) - 1
+    kc, vc = kv_host(rm, n)
+    assert np.array_equal(kc, om.kc[:, :n]) and np.array_equal(vc, om.vc[:, :n])
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny-qwen", "tiny-moe", "c1-stories15m"])
+def test_prefill_equals_decode(name):
+    """A prompt through t2r_prefill (all rows at once, and the reference's 16-row chunk schedule with
+    its overlapping last chunk) gives the decode-only logits and KV cache bit for bit."""
+    import t2r_amd.config as C
+    cfg = C.get(name)
+    qm, rm = resident(cfg, max_rows=64)
+    toks = cfg.prompt() if cfg.prompt_len >= 8 else (cfg.prompt() * 8)[:min(cfg.seq_len, 20)]
+    P = len(toks)
+    for p, t in enumerate(toks):
+        dec = rm.decode(t, p).cpu().numpy()
+    kd = kv_host(rm, P)
+    rm.reset()
+    pre = rm.prefill(toks).cpu().numpy()
+    assert sha(pre) == sha(dec)
+    kp = kv_host(rm, P)
+    assert np.array_equal(kp[0], kd[0]) and np.array_equal(kp[1], kd[1])
+    if P > 8:
+        rm.reset()
+        ch = rm.prefill_chunks(toks, M=8).cpu().numpy()
+        assert sha(ch) == sha(dec)
+        kc = kv_host(rm, P)
+        assert np.array_equal(kc[0], kd[0]) and np.array_equal(kc[1], kd[1])
+
+
+def test_greedy_on_device_c1(gold):
+    """The config-1 run as LlamaDevice.greedy_on_device does it (prefill, then argmax and pos += 1 on the
+    device, no host round trip): the same 160 tokens as the reference's run."""
+    import t2r_amd.config as C
+    from t2r_amd.runtime import LlamaDevice
+    run = next(r for r in gold["device_model"] if r["config"] == "c1-stories15m" and r["D"] == 16)
+    cfg = C.get(run["config"])
+    kv = np.array(run["kv_bits"], np.uint32).view(F).reshape(cfg.layers, 2)
+    from t2r_amd import weights as W
+    dev = LlamaDevice(W.QuantModel(cfg, kv_scales=kv), max_rows=64)
+    toks = dev.greedy_on_device(run["prompt"], run["steps"])
+    assert toks == run["tokens"]
+    assert sha(*kv_host(dev.m, run["steps"])) == run["kv_sha"]
+    dev.close()
+
+
+def test_llamadevice_api():
+    """forward() / generate() / reset() and the errors of llm/runtime.py:107-148."""
+    import t2r_amd.config as C
+    from t2r_amd.runtime import LlamaDevice
+    dev = LlamaDevice(C.TINY)
+    out = list(dev.generate([5, 6, 7], steps=10, stop_at_bos=False))
+    assert len(out) == 10 and all(isinstance(t, int) for t, _ in out)
+    again = list(dev.generate([5, 6, 7], steps=10, stop_at_bos=False))
+    assert again == out                                                      # reset() restores the state
+    dev.reset()
+    for _ in range(C.TINY.seq_len):
+        dev.forward(3)
+    with pytest.raises(ValueError):
+        dev.forward(3)
+    forced = list(dev.generate(None, steps=6, forced=[1, 2, 3, 4]))
+    assert len(forced) == 4 and forced[0][1].shape == (C.TINY.vocab,)
+    dev.close()

@@ -1,0 +1,266 @@
+"""Pins the CPU restatement (oracle/) before it is trusted as the checker of the HIP path.
+
+Each check is one the restatement could fail by a plausible mistake: the reference's own
+outputs (golden vectors written by tests/golden/make_golden.py from llm/sfu.py, llm/fp32.py,
+DeviceModel and SaFuncSim), the SFU ROM of the RTL, the literal known-answer tests of
+llm/test_fp32.py, IEEE binary32 where it coincides with the flush-to-zero rule, and closed forms.
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import t2r_amd.config as C
+from oracle import OracleModel
+from oracle import numerics as N
+from t2r_amd import weights as W
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLD = os.path.join(HERE, "golden")
+F = np.float32
+
+
+def sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+@pytest.fixture(scope="module")
+def sfu_gold():
+    return np.load(os.path.join(GOLD, "sfu_golden.npz"))
+
+
+@pytest.fixture(scope="module")
+def model_gold():
+    return json.load(open(os.path.join(GOLD, "model_golden.json")))
+
+
+# ------------------------------------------------------------------ fp32 primitives
+def test_sfu_tables_equal_rtl_rom():
+    rom = json.load(open(os.path.join(GOLD, "sfu_tables.json")))
+    mine = N.sfu_tables()
+    for name in ("exp", "recip", "rsqrt"):
+        assert np.array_equal(mine[name][0], np.array(rom[name]["T"], np.uint32)), name
+        assert np.array_equal(mine[name][1], np.array(rom[name]["S"], np.uint32)), name
+
+
+@pytest.mark.parametrize("name", ["exp", "recip", "rsqrt"])
+def test_sfu_equals_reference_outputs(sfu_gold, name):
+    fn = {"exp": N.sfu_exp_bits, "recip": N.sfu_recip_bits, "rsqrt": N.sfu_rsqrt_bits}[name]
+    x, y = sfu_gold[name + "_x"], sfu_gold[name + "_y"]
+    got = fn(x)
+    bad = np.flatnonzero(got != y)
+    assert bad.size == 0, [(hex(x[i]), hex(got[i]), hex(y[i])) for i in bad[:5]]
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul"])
+def test_fp32_binops_equal_reference(sfu_gold, op):
+    a, b = sfu_gold["bin_a"], sfu_gold["bin_b"]
+    assert np.array_equal(getattr(N, op)(a, b), sfu_gold[op])
+
+
+def test_fp32_conversions_equal_reference(sfu_gold):
+    a = sfu_gold["bin_a"]
+    assert np.array_equal(N.ldexp(a, sfu_gold["ldexp_n"]), sfu_gold["ldexp"])
+    assert np.array_equal(N.to_int(a, -2 ** 31, 2 ** 31 - 1, "floor"), sfu_gold["floor"])
+    assert np.array_equal(N.to_int(a, -127, 127), sfu_gold["rne_i8"])
+    assert np.array_equal(N.from_int(sfu_gold["from_int_x"]), sfu_gold["from_int"])
+
+
+def _rand_bits(rng, n, emin=1, emax=254):
+    s = rng.integers(0, 2, n, dtype=np.int64)
+    e = rng.integers(emin, emax + 1, n, dtype=np.int64)
+    m = rng.integers(0, 1 << 23, n, dtype=np.int64)
+    return ((s << 31) | (e << 23) | m).astype(np.uint32)
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul"])
+def test_fp32_binops_equal_ieee_where_comparable(op):
+    """IEEE binary32 (NumPy float32) and the FTZ rule agree on normal / infinite results
+    (llm/test_fp32.py:51-68)."""
+    rng = np.random.default_rng(3)
+    for emin, emax in ((1, 254), (100, 110), (120, 130)):
+        a, b = _rand_bits(rng, 50_000, emin, emax), _rand_bits(rng, 50_000, emin, emax)
+        with np.errstate(all="ignore"):
+            fa, fb = N.val(a), N.val(b)
+            ref = {"add": fa + fb, "sub": fa - fb, "mul": fa * fb}[op].astype(F).view(np.uint32)
+        e = (ref >> 23) & 0xFF
+        m = ((e != 0) | ((ref & 0x7FFFFFFF) == 0)) & ~np.isnan(N.val(ref))
+        assert np.array_equal(getattr(N, op)(a, b)[m], ref[m])
+
+
+def test_fp32_literal_kats():
+    """llm/test_fp32.py:79-105, as literal values."""
+    tiny = N.bits(F(2.0 ** -70))
+    r = N.mul(np.repeat(tiny, 2), N.bits(np.array([2.0 ** -70, -2.0 ** -70], F)))
+    assert list(r) == [0, 0x80000000]                                       # underflow -> +-0
+    r = N.add(np.array([0x00000001, 0x807FFFFF], np.uint32), N.bits(np.array([1.0, 1.0], F)))
+    assert list(r) == [0x3F800000, 0x3F800000]                              # subnormal input = 0
+    r = N.sub(N.bits(np.array([1.5 * 2.0 ** -126], F)), N.bits(np.array([2.0 ** -126], F)))
+    assert list(r) == [0]                                                   # 2^-127 flushes
+    assert list(N.add(N.bits(np.array([3.0, -0.0], F)), N.bits(np.array([-3.0, -0.0], F)))) == [0, 0x80000000]
+    ints = np.array([0, 1, -1, 2 ** 31 - 1, -2 ** 31, 2 ** 24 + 1, 2 ** 24 + 3, -(2 ** 24 + 1)])
+    assert np.array_equal(N.from_int(ints), ints.astype(F).view(np.uint32))
+    assert list(N.to_int(N.bits(np.array([np.nan, np.inf, -np.inf], F)), -127, 127)) == [0, 127, -127]
+    halves = np.arange(-300, 300) * 0.5
+    assert np.array_equal(N.to_int(N.bits(halves.astype(F)), -127, 127), np.clip(np.rint(halves), -127, 127))
+
+
+def test_sfu_accuracy_and_specials():
+    """Accuracy bounds and special values of llm/test_fp32.py:108-132."""
+    rng = np.random.default_rng(3)
+    xs = {"exp": np.concatenate([rng.uniform(-104, 89, 100_000), rng.uniform(-20, 20, 100_000)]),
+          "recip": np.concatenate([np.exp(rng.uniform(-85, 85, 100_000)), -np.exp(rng.uniform(-85, 85, 100_000))]),
+          "rsqrt": np.exp(rng.uniform(-85, 85, 200_000))}
+    ref = {"exp": np.exp, "recip": lambda x: 1 / x, "rsqrt": lambda x: 1 / np.sqrt(x)}
+    target = {"exp": 3e-5, "recip": 2e-7, "rsqrt": 5e-7}
+    fns = {"exp": N.sfu_exp_bits, "recip": N.sfu_recip_bits, "rsqrt": N.sfu_rsqrt_bits}
+    for name, x in xs.items():
+        b = N.bits(x.astype(F))
+        xf = N.val(b).astype(np.float64)
+        got = N.val(fns[name](b)).astype(np.float64)
+        want = ref[name](xf)
+        m = (np.abs(want) >= 2.0 ** -125) & (np.abs(want) < 2.0 ** 127)
+        assert (np.abs(got[m] - want[m]) / np.abs(want[m])).max() <= target[name], name
+    sp = N.bits(np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 89.0, -104.0, -1.0], F))
+    e, r, q = N.sfu_exp_bits(sp), N.sfu_recip_bits(sp), N.sfu_rsqrt_bits(sp)
+    assert list(e[:7]) == [N.QNAN, N.PINF, 0, 0x3F800000, 0x3F800000, N.PINF, 0]
+    assert abs(float(N.val(e[7])) - np.exp(-1)) < 1e-5
+    assert list(r[:5]) == [N.QNAN, 0, 0x80000000, N.PINF, N.NINF]
+    assert [int(v) for v in q[:5]] + [int(q[7])] == [N.QNAN, 0, N.QNAN, N.PINF, N.PINF, N.QNAN]
+    assert N.sfu_exp_bits(N.bits(F(0.0)))[()] == 0x3F800000                # exp(0) = 1 exactly
+    assert N.sfu_recip_bits(N.bits(F(1.0)))[()] == 0x3F800000              # recip(1) = 1 exactly
+
+
+# ------------------------------------------------------------------ vector primitives
+def test_to_i8_ties_and_saturation():
+    x = np.array([0.5, 1.5, 2.5, -0.5, -1.5, 126.5, 127.5, -127.5, 1e9, -1e9, np.nan, np.inf, -np.inf, -0.0], F)
+    assert list(N.to_i8(x)) == [0, 2, 2, 0, -2, 126, 127, -127, 127, -127, 0, 127, -127, 0]
+
+
+def test_red_sum_order():
+    """The lane order: with D = 4 and values chosen so that any other association rounds
+    differently, the sum is ((v0 + v4) + v8) per lane then (l0 + l1) + (l2 + l3)."""
+    v = np.array([1.0, 2.0 ** 24, 3.0, 1.0, 2.0 ** 24, 1.0, -2.0 ** 24, 1.0, 1.0, -2.0 ** 24, 2.0 ** 24, 1.0], F)
+    lanes = [F(F(v[l] + v[4 + l]) + v[8 + l]) for l in range(4)]
+    want = F(F(lanes[0] + lanes[1]) + F(lanes[2] + lanes[3]))
+    assert N.red_sum(v, 4) == want
+    assert want != F(np.sum(v.astype(np.float64)))                          # order matters here
+    seq = F(0)
+    for t in v:
+        seq = F(seq + t)
+    assert want != seq
+    # exact integers: any order gives the exact sum
+    rng = np.random.default_rng(5)
+    ints = rng.integers(-1000, 1000, 777).astype(F)
+    for D in (8, 16):
+        assert N.red_sum(ints, D) == F(ints.astype(np.int64).sum())
+        assert N.red_sum(np.zeros(0, F), D) == 0
+
+
+def test_quant_act_zero_row_and_scale():
+    xq, s = N.quant_act(np.zeros((2, 32), F))
+    assert not xq.any() and not s.any()
+    x = np.linspace(-3, 5, 64).astype(F)
+    xq, s = N.quant_act(x)
+    assert s == F(F(5.0) * F(1 / 127)) and xq.max() == 127
+
+
+def test_topk_ties_and_nan():
+    s = np.array([1.0, 3.0, 3.0, np.nan, -1.0, 3.0, 2.0], F)
+    assert list(N.topk_desc(s, 5)) == [1, 2, 5, 6, 0]
+    rng = np.random.default_rng(9)
+    for _ in range(200):
+        v = rng.integers(-3, 4, 12).astype(F)
+        k = int(rng.integers(1, 9))
+        want = sorted(range(12), key=lambda i: (-v[i], i))[:k]               # brute force
+        assert list(N.topk_desc(v, k)) == want
+
+
+def test_requant_closed_form():
+    r = np.array([1000, -1000, 7, -7, 2 ** 20, -2 ** 20, 0])
+    # ((r * 3 + 8) >> 4) + 5, clamp [-100, 120], int8
+    assert list(N.requant_int(r, 3, 4, 5, -100, 120)) == [120, -100, 6, 4, 120, -100, 5]
+    assert list(N.requant_int(np.array([-300, 300]), 1, 0, 0, -2 ** 31, 2 ** 31 - 1)) == [-128, 127]
+
+
+# ------------------------------------------------------------------ the decoder
+def _golden_model(run):
+    cfg = C.get(run["config"])
+    kv = np.array(run["kv_bits"], np.uint32).view(F).reshape(cfg.layers, 2)
+    return cfg, W.QuantModel(cfg, kv_scales=kv)
+
+
+def test_rope_tables_method(model_gold):
+    for run in model_gold["device_model"]:
+        cfg = C.get(run["config"])
+        cos, sin = W.rope_tables(cfg)
+        assert run["rope_sha_mine"] == run["rope_sha_reference"]           # the f32 method = ref_model.rope_tables
+        assert sha(cos, sin) == run["rope_sha_mine"], f"{cfg.name}: tables differ on this platform"
+
+
+def test_quantisation_equals_reference(model_gold):
+    for run in model_gold["device_model"]:
+        _, qm = _golden_model(run)
+        assert sha(qm.emb_q, qm.emb_s) == run["emb_quant_sha"]
+
+
+@pytest.mark.parametrize("idx", range(6))
+def test_oracle_equals_device_model(model_gold, idx):
+    """Every logit of every step, the greedy tokens and the int8 KV cache equal DeviceModel(SfuExact)
+    (and SaFuncSim where the fixture ran it: tests/golden/model_golden.json "funcsim")."""
+    run = model_gold["device_model"][idx]
+    cfg, qm = _golden_model(run)
+    om = OracleModel(qm, D=run["D"])
+    for rec in run["positions"]:
+        lg = om.forward(rec["token"], rec["pos"])
+        assert sha(lg) == rec["logits_sha"], f"{cfg.name} D={run['D']} pos {rec['pos']}"
+        assert int(np.argmax(lg)) == rec["argmax"]
+    assert sha(om.kc[:, :run["steps"]], om.vc[:, :run["steps"]]) == run["kv_sha"]
+
+
+def test_funcsim_fixture_consistent(model_gold):
+    """The fixture's SaFuncSim runs (the reference's "sa_funcsim path as it runs today") agree with its
+    DeviceModel runs position by position, so the DeviceModel goldens pin both."""
+    dm = {(r["config"], r["D"]): r for r in model_gold["device_model"]}
+    assert model_gold["funcsim"]
+    for fs in model_gold["funcsim"]:
+        ref = dm[(fs["config"], fs["D"])]
+        assert fs["equals_device_model"]
+        for a, b in zip(fs["positions"], ref["positions"]):
+            assert a["logits_sha"] == b["logits_sha"] and a["token"] == b["token"]
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny-qwen", "tiny-moe"])
+def test_oracle_prefill_equals_decode(name):
+    cfg = C.get(name)
+    qm = W.QuantModel(cfg)
+    om = OracleModel(qm)
+    toks = cfg.prompt()
+    for p, t in enumerate(toks):
+        dec = om.forward(t, p)
+    kc, vc = om.kc.copy(), om.vc.copy()
+    om.reset()
+    pre = om.prefill(toks)
+    assert sha(pre) == sha(dec)
+    assert np.array_equal(om.kc, kc) and np.array_equal(om.vc, vc)
+
+
+def test_moe_one_expert_collapses_to_dense():
+    """Top-1 of a single expert: e = EXP(0) = 1, w = 1 * RECIP(1) = 1, y = F(+0 + F(1 * y0)), i.e. the
+    dense SwiGLU FFN with the expert's tables (closed form of compiler/frontend/hf_generic.py:641-657)."""
+    moe = C.TINY_MOE.with_(n_experts=1, top_k=1)
+    qm = W.QuantModel(moe)
+    dense = C.TINY_MOE.with_(n_experts=0, top_k=0)
+    qd = W.QuantModel(dense, kv_scales=qm.kv_scales)
+    qd.w1, qd.s_w1 = qm.wg[:, 0], qm.s_wg[:, 0]
+    qd.w3, qd.s_w3 = qm.wu[:, 0], qm.s_wu[:, 0]
+    qd.w2, qd.s_w2 = qm.wd[:, 0], qm.s_wd[:, 0]
+    a, b = OracleModel(qm), OracleModel(qd)
+    for p, t in enumerate(moe.prompt()):
+        la, lb = a.forward(t, p), b.forward(t, p)
+        assert sha(la) == sha(lb)

@@ -56,8 +56,8 @@ _SIGS = {
     "t2r_quant_act": (c_int, [P, c_int, c_int, P, P, P]),
     "t2r_gemv_w8a8": (c_int, [P, P, P, P, c_int, c_int, P, P, P, P]),
     "t2r_gemm_w8a8": (c_int, [P, P, P, P, c_int, c_int, c_int, P, P, P, P]),
-    "t2r_rope": (c_int, [P, P, P, P, c_int, c_int, c_int, P]),
-    "t2r_kv_append": (c_int, [P, P, c_float, c_float, P, P, P, c_int, c_int, P]),
+    "t2r_rope": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "t2r_kv_append": (c_int, [P, P, c_float, c_float, P, P, P, c_int, c_int, c_int, P]),
     "t2r_attn_decode": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int, P, P]),
     "t2r_swiglu_w8a8": (c_int, [P, P, P, P, P, P, c_int, c_int, P, P, P, P]),
     "t2r_moe_route": (c_int, [P, c_int, c_int, c_int, c_int, P, P, P]),

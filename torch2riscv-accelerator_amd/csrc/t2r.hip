@@ -57,11 +57,6 @@ int ensure_init() {
   float t[kSfuWords];
   sfu_host_tables(t);
   if (hipMemcpyToSymbol(HIP_SYMBOL(c_sfu), t, sizeof(t), 0, hipMemcpyHostToDevice) != hipSuccess) return T2R_EHIP;
-  if (hipFuncSetAttribute((const void*)k_attn<ATTN_FUSED>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) !=
-          hipSuccess ||
-      hipFuncSetAttribute((const void*)k_attn<ATTN_ONLY>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) !=
-          hipSuccess)
-    return T2R_EHIP;
   g_inited[dev] = true;
   return T2R_OK;
 }
@@ -86,7 +81,7 @@ GemvArgs gemv_args() {
 int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   const int G = a.H / a.Hk;
   if (a.H <= 0 || a.Hk <= 0 || a.H % a.Hk || G > kMaxG || a.hd <= 0 || a.hd > kMaxHd || a.hd % 8 || a.S <= 0 ||
-      (long long)G * a.S > 16384 || (a.D != 8 && a.D != 16))
+      (long long)G * a.S > kMaxGS || (a.D != 8 && a.D != 16))
     return T2R_ESHAPE;
   const size_t lds = attn_lds_bytes(G, a.S);
   dim3 grid(a.Hk, rows), block(kAttnThreads);
@@ -170,7 +165,7 @@ int validate(const t2r_model_desc* d) {
   const int q = d->heads * d->head_dim, kv = d->kv_heads * d->head_dim;
   if (d->dim % 16 || d->hidden % 16 || q % 16 || kv % 16 || d->dim > kMaxK || d->hidden > kMaxK || q > kMaxK)
     return T2R_ESHAPE;
-  if ((long long)(d->heads / d->kv_heads) * d->seq_len > 16384) return T2R_ESHAPE;
+  if ((long long)(d->heads / d->kv_heads) * d->seq_len > kMaxGS) return T2R_ESHAPE;
   if (d->D != 8 && d->D != 16) return T2R_ESHAPE;
   if (d->n_experts < 0 || (d->n_experts > 0 && (d->top_k < 1 || d->top_k > 8 || d->top_k > d->n_experts ||
                                                 d->n_experts > 64 || d->hidden > 1024)))
@@ -404,21 +399,21 @@ int t2r_gemm_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const flo
   return gemm_dispatch<EPI_STORE>(a, M, S(stream));
 }
 
-int t2r_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* pos, int rows, int n, int half,
+int t2r_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* pos, int rows, int n, int half, int S_,
              void* stream) {
   if (!v || !cos_t || !sin_t || !pos) return T2R_EINVAL;
-  if (rows <= 0 || n <= 0 || half <= 0 || n % (2 * half)) return T2R_ESHAPE;
+  if (rows <= 0 || n <= 0 || half <= 0 || n % (2 * half) || S_ <= 0) return T2R_ESHAPE;
   T2R_INIT();
-  hipLaunchKernelGGL(k_rope, dim3(rows), dim3(256), 0, S(stream), v, cos_t, sin_t, pos, n, half);
+  hipLaunchKernelGGL(k_rope, dim3(rows), dim3(256), 0, S(stream), v, cos_t, sin_t, pos, n, half, S_);
   return launched();
 }
 
 int t2r_kv_append(const float* k, const float* v, float inv_sk, float inv_sv, int8_t* kc, int8_t* vc,
-                  const int32_t* pos, int rows, int kv_dim, void* stream) {
+                  const int32_t* pos, int rows, int kv_dim, int S_, void* stream) {
   if (!k || !v || !kc || !vc || !pos) return T2R_EINVAL;
-  if (rows <= 0 || kv_dim <= 0) return T2R_ESHAPE;
+  if (rows <= 0 || kv_dim <= 0 || S_ <= 0) return T2R_ESHAPE;
   T2R_INIT();
-  hipLaunchKernelGGL(k_kv_append, dim3(rows), dim3(256), 0, S(stream), k, v, inv_sk, inv_sv, kc, vc, pos, kv_dim);
+  hipLaunchKernelGGL(k_kv_append, dim3(rows), dim3(256), 0, S(stream), k, v, inv_sk, inv_sv, kc, vc, pos, kv_dim, S_);
   return launched();
 }
 

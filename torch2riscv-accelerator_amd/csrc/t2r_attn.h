@@ -23,6 +23,7 @@ enum { ATTN_FUSED = 0, ATTN_PREP = 1, ATTN_ONLY = 2 };
 constexpr int kAttnThreads = 256;
 constexpr int kMaxG = 8;
 constexpr int kMaxHd = 128;
+constexpr int kMaxGS = 8192;          // G * S scores in LDS (32 KB), with the int8 probabilities 40 KB
 
 struct AttnArgs {
   float* qkv;                // rows of [q | k | v] projections (stride qkv_stride)
@@ -95,6 +96,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
   const int hd = a.hd, G = a.H / a.Hk, S = a.S;
   const int q_dim = a.H * hd, kv_dim = a.Hk * hd;
   const int pos = a.pos[row];
+  if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
   const int T = pos + 1;
   float* qkv = a.qkv + row * a.qkv_stride;
 

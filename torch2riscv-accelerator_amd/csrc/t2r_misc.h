@@ -61,10 +61,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* g,
 // RoPE of rows v[rows, n] in place at positions pos[rows]; the tables are [S, half] (pairs of a
 // head), n a multiple of 2 * half (the heads of a row).
 __global__ __launch_bounds__(256) void k_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* pos,
-                                              int n, int half) {
+                                              int n, int half, int S) {
   const int row = blockIdx.x;
   float* r = v + (long long)row * n;
   const int p = pos[row];
+  if (p < 0 || p >= S) return;
   for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
     const int k = i % half;
     const float c = cos_t[(long long)p * half + k], s = sin_t[(long long)p * half + k];
@@ -77,9 +78,10 @@ __global__ __launch_bounds__(256) void k_rope(float* v, const float* cos_t, cons
 
 // kc[pos[r]] = to_i8(F(k[r] * inv_sk)), vc[pos[r]] = to_i8(F(v[r] * inv_sv))
 __global__ __launch_bounds__(256) void k_kv_append(const float* k, const float* v, float inv_sk, float inv_sv,
-                                                   int8_t* kc, int8_t* vc, const int32_t* pos, int kv_dim) {
+                                                   int8_t* kc, int8_t* vc, const int32_t* pos, int kv_dim, int S) {
   const int row = blockIdx.x;
   const long long p = pos[row];
+  if (p < 0 || p >= S) return;
   for (int i = threadIdx.x; i < kv_dim; i += blockDim.x) {
     kc[p * kv_dim + i] = (int8_t)to_i8(k[(long long)row * kv_dim + i] * inv_sk);
     vc[p * kv_dim + i] = (int8_t)to_i8(v[(long long)row * kv_dim + i] * inv_sv);
