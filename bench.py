@@ -1,0 +1,235 @@
+#!/usr/bin/env python3
+"""Measures the W8A8 decoder datapath on one MI355X (BASELINE.json metric: decode & prefill tok/s at
+batch 1; W8A8 GEMV % of HBM peak) and prints ONE JSON line.
+
+Workload: the Llama-3.2-1B-shaped config (the one the metric's GEMV and
+MFMA roofline fractions are quoted on): synthetic N(0, 0.02) weights quantised to int8, the
+seeded 512-token prompt prefilled, then greedy decode at batch 1. A step is one decode token;
+`value` is decode tokens/s over exactly --steps steps with everything resident in HBM.
+
+    python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--config c4-llama3.2-1b]
+
+Extra fields: prefill tok/s (the 512-row prompt in one t2r_prefill), per-kernel-class HIP-event
+durations from the timed region, the roofline of the dominant kernel (the fused SwiGLU GEMV:
+RMSNorm + quant + W1/W3 + SiLU gate), and the CPU baseline (the bit-exact NumPy restatement in
+oracle/, timed on a bounded sample on this host).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA, published
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(cfg):
+    """Algorithmic bytes of one launch of each decode kernel class (weights int8 + fp32 row scales
+    + fp32 inputs / outputs / gains): what the launch must move, once."""
+    d, q, kv, F, V = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden, cfg.vocab
+    return {
+        "qkv": (q + 2 * kv) * d + 4 * (q + 2 * kv) + 4 * d + 4 * d + 4 * (q + 2 * kv),
+        "wo": d * q + 4 * d + 4 * q + 4 * d + 4 * d,
+        "ffn_up": 2 * F * d + 2 * 4 * F + 4 * d + 4 * d + 4 * F,
+        "ffn_down": d * F + 4 * d + 4 * F + 4 * d + 4 * d,
+        "cls": V * d + 4 * V + 4 * d + 4 * d + 4 * V,
+    }
+
+
+def cpu_baseline(qm, prompt, seconds):
+    """The oracle (NumPy restatement, bit-exact with the reference) decoding on this host's cores."""
+    import numpy as np
+    from oracle import OracleModel
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        cores = 1
+    om = OracleModel(qm)
+    P = 8
+    om.prefill(prompt[:P])
+    tok = prompt[P]
+    om.forward(tok, P)                                 # untimed: converts the weights to the matmul layout
+    om.reset()
+    om.prefill(prompt[:P])
+    n, t0 = 0, time.perf_counter()
+    logits = []
+    while time.perf_counter() - t0 < seconds and n < 64:
+        lg = om.forward(tok, P + n)
+        logits.append(lg)
+        tok = int(np.argmax(lg))
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": int(cores), "kind": "port",
+            "sample": f"{n} greedy decode steps at positions {P}..{P + n - 1} after an {P}-token prefill "
+                      f"({dt:.1f} s)"}, logits
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", default="c4-llama3.2-1b")
+    ap.add_argument("--prefill-reps", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="time eager decode steps instead of a HIP graph")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the datapath runs on a single "
+              f"MI355X; DESIGN.md describes how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import t2r_amd.config as C
+    from t2r_amd import weights as W
+    from t2r_amd.model import ResidentModel
+    cfg = C.get(args.config)
+    t0 = time.time()
+    qm = W.QuantModel(cfg)
+    log(f"{cfg.name}: weights generated and quantised in {time.time() - t0:.1f} s")
+    prompt = cfg.prompt()
+    P = len(prompt)
+    rm = ResidentModel(qm, device="cuda:0", max_rows=P)
+    sync = torch.cuda.synchronize
+
+    # ---- prefill tok/s: the whole prompt in one call
+    times = []
+    for r in range(args.prefill_reps + 1):
+        rm.reset()
+        sync()
+        t = time.perf_counter()
+        rm.prefill(prompt)
+        sync()
+        times.append(time.perf_counter() - t)
+    prefill_s = float(np.median(times[1:])) if len(times) > 1 else times[0]
+    log(f"prefill {P} rows: {prefill_s * 1e3:.2f} ms ({P / prefill_s:.0f} tok/s)")
+    after_prompt = rm.next.clone()
+
+    # ---- decode: greedy on the device, batch 1, positions P .. P + steps.
+    steps = min(args.steps, cfg.seq_len - P)
+    warm = min(args.warmup, steps)
+
+    def rewind():
+        rm.tok.copy_(after_prompt)
+        rm.pos.fill_(P)
+
+    # (1) eager steps with HIP events around every kernel class: the per-class breakdown
+    rewind()
+    for _ in range(warm):
+        rm.step(logits=False, advance=True)
+    rewind()
+    rm.profile(max_launches=steps * (cfg.layers * 6 + 4))
+    sync()
+    t = time.perf_counter()
+    for _ in range(steps):
+        rm.step(logits=False, advance=True)
+    sync()
+    eager_dt = time.perf_counter() - t
+    prof = rm.profile_read()
+    rm.profile(kinds=())
+    log(f"decode eager: {eager_dt / steps * 1e3:.3f} ms/token ({steps / eager_dt:.1f} tok/s)")
+
+    # (2) the timed region of `value`: one HIP graph of all `steps` decode steps (launch-free)
+    dom_ms = None
+    graph = None
+    if not args.no_graph:
+        try:
+            rewind()
+            graph = rm.capture_decode(steps)
+            graph.replay()                                  # warm-up replay
+            sync()
+        except Exception as e:                              # capture not available: eager timing only
+            log(f"HIP graph capture failed ({e}); timing eager steps")
+            graph = None
+    if graph is not None:
+        rewind()
+        sync()
+        t = time.perf_counter()
+        graph.replay()
+        sync()
+        dt = time.perf_counter() - t
+        mode = "hip-graph"
+    else:
+        dt, mode = eager_dt, "eager"
+    tok_s = steps / dt
+    log(f"decode {mode}: {steps} steps, {dt / steps * 1e3:.3f} ms/token ({tok_s:.1f} tok/s)")
+
+    nbytes = gemv_bytes(cfg)
+    classes = {}
+    gemv_b = gemv_t = 0.0
+    for k, ts in prof.items():
+        avg = sum(ts) / len(ts)
+        rec = {"launches": len(ts), "avg_us": round(avg * 1e3, 3), "total_ms": round(sum(ts), 3)}
+        if k in nbytes and not cfg.moe:
+            rec["bytes_per_launch"] = nbytes[k]
+            rec["GBps"] = round(nbytes[k] / (avg * 1e-3) / 1e9, 1)
+            gemv_b += nbytes[k] * len(ts)
+            gemv_t += sum(ts) * 1e-3
+        classes[k] = rec
+    dom = classes.get("ffn_up", {})
+    if dom_ms:                                              # from the timed region itself
+        dom = {"launches": len(dom_ms), "avg_us": round(sum(dom_ms) / len(dom_ms) * 1e3, 3),
+               "GBps": round(nbytes["ffn_up"] / (sum(dom_ms) / len(dom_ms) * 1e-3) / 1e9, 1)}
+    achieved = dom.get("GBps")
+    out = {
+        "metric": "decode & prefill tok/s at batch 1; W8A8 GEMV % of HBM peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": round(dt / steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (N(0, 0.02) random weights, per-row int8; seeded uniform prompt ids)",
+        "config": {"workload": f"{cfg.name}: decode at batch 1 after a {P}-token prefill", "model": cfg.name,
+                   "global_batch": 1, "seq_len": cfg.seq_len, "prompt": P, "decode_steps": steps,
+                   "parallelism": "none (1 GPU)"},
+        "prefill_tok_s": round(P / prefill_s, 1),
+        "prefill_ms": round(prefill_s * 1e3, 3),
+        "kernels": classes,
+        "gemv_all_GBps": round(gemv_b / gemv_t / 1e9, 1) if gemv_t else None,
+        "gemv_all_frac": round(gemv_b / gemv_t / 1e9 / HBM_PEAK_GBS, 4) if gemv_t else None,
+        "decode_mode": mode,
+        "eager_tok_s": round(steps / eager_dt, 2),
+        "roofline": {"kernel": "k_gemv<PRO_NORM_QUANT, EPI_SWIGLU> (fused SwiGLU decode GEMV)", "bound": "hbm",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+                     "bytes_per_launch": nbytes["ffn_up"], "avg_us": dom.get("avg_us"),
+                     "launches": dom.get("launches"), "traffic": None},
+    }
+
+    # ---- CPU baseline (+ a bit-exactness spot check of the same positions on the GPU)
+    if not args.no_cpu_baseline:
+        cb, cpu_logits = cpu_baseline(qm, prompt, args.cpu_seconds)
+        out["cpu_baseline"] = cb
+        rm.reset()
+        rm.prefill(prompt[:8])
+        tok = prompt[8]
+        same = True
+        for i, lg in enumerate(cpu_logits[:4]):
+            g = rm.decode(tok, 8 + i).cpu().numpy()
+            same &= bool(np.array_equal(g.view(np.uint32), lg.view(np.uint32)))
+            tok = int(np.argmax(lg))
+        out["parity_spot_check"] = {"positions": min(4, len(cpu_logits)), "bit_exact": same}
+        log(f"cpu baseline: {cb['value']} tok/s on {cb['cores']} cores; GPU == CPU logits: {same}")
+    rm.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

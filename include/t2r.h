@@ -102,7 +102,7 @@ int t2r_kv_append(const float* k, const float* v, float inv_sk, float inv_sv, in
 /* Attention of rows q[rows, H * hd] (already rotated) at positions pos[rows] over the int8 cache
  * rows 0..pos (DeviceModel.forward llm/ref_model.py:230-243; ModelCompiler.attention
  * llm/compile_model.py:233-293; GQA: compiler/frontend/qhf.py:304-319). a_k = F(s_k / sqrt(hd)),
- * a_v = F(s_v / 127). S = cache rows; S * H / Hk <= 8192, hd <= 128, H / Hk <= 8. */
+ * a_v = F(s_v / 127). S = cache rows <= 8192, hd <= 128 and a multiple of 8. */
 int t2r_attn_decode(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H,
                     int Hk, int hd, int S, float a_k, float a_v, int D, float* att, void* stream);
 /* SwiGLU of one row (DeviceModel.forward llm/ref_model.py:246-250; ModelCompiler.ffn_up / silu_mul
@@ -167,6 +167,27 @@ int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logi
  * M <= max_rows. Identical, bit for bit, to M decode steps. */
 int t2r_prefill(void* model, const int32_t* tokens, const int32_t* positions, int M, float* last_logits,
                 int32_t* next_token, void* stream);
+
+/* Kernel timing of a resident model with HIP events on the launch stream (the GPU counterpart of
+ * the reference's event counters and per-list cycle counts: rtl/sysarray/sa_perf.v,
+ * driver/pynq_matmul.py:969-981, 1029-1066). t2r_model_profile creates 2 * max_launches events
+ * (set-up time, not the hot path) and, for the kernel classes in mask (1 << T2R_PROF_*), records
+ * one event before and one after every launch of later decode / prefill calls, until the pool is
+ * full; mask 0 frees the pool. t2r_model_profile_read waits for the recorded events and returns
+ * the number of launches recorded (kinds[i], ms[i] for the first max of them), then empties the
+ * record. Returns a negative code on error. */
+enum {
+  T2R_PROF_QKV = 0,        /* RMSNorm + quant + Wqkv GEMV                        */
+  T2R_PROF_ATTN = 1,       /* QK-norm, RoPE, KV append, attention                */
+  T2R_PROF_WO = 2,         /* quant + Wo GEMV + residual                         */
+  T2R_PROF_FFN_UP = 3,     /* RMSNorm + quant + W1 / W3 GEMV + SiLU gate (MoE: expert gate / up) */
+  T2R_PROF_FFN_DOWN = 4,   /* quant + W2 GEMV + residual (MoE: expert down + combine) */
+  T2R_PROF_CLS = 5,        /* final RMSNorm + quant + classifier GEMV + argmax   */
+  T2R_PROF_ROUTE = 6,      /* MoE router + top-k                                 */
+  T2R_PROF_OTHER = 7       /* embedding, step end                                */
+};
+int t2r_model_profile(void* model, int mask, int max_launches);
+int t2r_model_profile_read(void* model, int32_t* kinds, float* ms, int max);
 
 #ifdef __cplusplus
 }

@@ -79,15 +79,22 @@ GemvArgs gemv_args() {
 }
 
 int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
-  const int G = a.H / a.Hk;
-  if (a.H <= 0 || a.Hk <= 0 || a.H % a.Hk || G > kMaxG || a.hd <= 0 || a.hd > kMaxHd || a.hd % 8 || a.S <= 0 ||
-      (long long)G * a.S > kMaxGS || (a.D != 8 && a.D != 16))
+  if (a.H <= 0 || a.Hk <= 0 || a.H % a.Hk || a.hd <= 0 || a.hd > kMaxHd || a.hd % 8 || a.S <= 0 || a.S > kMaxS ||
+      (a.D != 8 && a.D != 16))
     return T2R_ESHAPE;
-  const size_t lds = attn_lds_bytes(G, a.S);
-  dim3 grid(a.Hk, rows), block(kAttnThreads);
-  if (mode == ATTN_FUSED) hipLaunchKernelGGL(k_attn<ATTN_FUSED>, grid, block, lds, st, a);
-  else if (mode == ATTN_PREP) hipLaunchKernelGGL(k_attn<ATTN_PREP>, grid, block, 0, st, a);
-  else hipLaunchKernelGGL(k_attn<ATTN_ONLY>, grid, block, lds, st, a);
+  const size_t lds = mode == ATTN_PREP ? 0 : attn_lds_bytes(a.S, a.D);
+  dim3 grid(a.H, rows), block(kAttnThreads);
+  const bool c16 = a.hd % 16 == 0;
+  if (mode == ATTN_FUSED) {
+    if (c16) hipLaunchKernelGGL((k_attn<ATTN_FUSED, 16>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((k_attn<ATTN_FUSED, 8>), grid, block, lds, st, a);
+  } else if (mode == ATTN_PREP) {
+    if (c16) hipLaunchKernelGGL((k_attn<ATTN_PREP, 16>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((k_attn<ATTN_PREP, 8>), grid, block, lds, st, a);
+  } else {
+    if (c16) hipLaunchKernelGGL((k_attn<ATTN_ONLY, 16>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((k_attn<ATTN_ONLY, 8>), grid, block, lds, st, a);
+  }
   return launched();
 }
 
@@ -109,7 +116,36 @@ struct Model {
   int8_t* mxq;
   float* msx;
   int32_t* status;
+  // kernel timing (t2r_model_profile)
+  int prof_mask = 0;
+  std::vector<hipEvent_t> ev;
+  std::vector<int32_t> ev_kind;
+  int ev_used = 0;
 };
+
+// events around the launches of one kernel class
+struct ProfScope {
+  Model* m;
+  hipStream_t st;
+  bool on;
+  ProfScope(Model* m_, int kind, hipStream_t s) : m(m_), st(s), on(false) {
+    if ((m->prof_mask >> kind) & 1 && m->ev_used + 2 <= (int)m->ev.size()) {
+      on = hipEventRecord(m->ev[m->ev_used], st) == hipSuccess;
+      if (on) m->ev_kind[m->ev_used / 2] = kind;
+    }
+  }
+  ~ProfScope() {
+    if (on && hipEventRecord(m->ev[m->ev_used + 1], st) == hipSuccess) m->ev_used += 2;
+  }
+};
+
+void free_events(Model* m) {
+  for (hipEvent_t e : m->ev) (void)hipEventDestroy(e);
+  m->ev.clear();
+  m->ev_kind.clear();
+  m->ev_used = 0;
+  m->prof_mask = 0;
+}
 
 struct Carve {
   char* base;
@@ -165,7 +201,7 @@ int validate(const t2r_model_desc* d) {
   const int q = d->heads * d->head_dim, kv = d->kv_heads * d->head_dim;
   if (d->dim % 16 || d->hidden % 16 || q % 16 || kv % 16 || d->dim > kMaxK || d->hidden > kMaxK || q > kMaxK)
     return T2R_ESHAPE;
-  if ((long long)(d->heads / d->kv_heads) * d->seq_len > kMaxGS) return T2R_ESHAPE;
+  if (d->seq_len > kMaxS) return T2R_ESHAPE;
   if (d->D != 8 && d->D != 16) return T2R_ESHAPE;
   if (d->n_experts < 0 || (d->n_experts > 0 && (d->top_k < 1 || d->top_k > 8 || d->top_k > d->n_experts ||
                                                 d->n_experts > 64 || d->hidden > 1024)))
@@ -196,7 +232,10 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
   a.s_w = d.s_wqkv + (long long)l * m->qkv_dim;
   a.x = m->x; a.x_stride = d.dim; a.g = d.rms_att + L_dim; a.inv_n = inv_d; a.eps = d.eps; a.D = d.D;
   a.N = m->qkv_dim; a.K = d.dim; a.y = m->qkv; a.y_stride = m->qkv_dim;
-  if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
+  {
+    ProfScope p(m, T2R_PROF_QKV, st);
+    if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
+  }
   // attention (QK-norm, RoPE, KV append fused for decode)
   AttnArgs at;
   std::memset(&at, 0, sizeof(at));
@@ -212,11 +251,14 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
   at.eps = d.eps; at.inv_hd = (float)(1.0 / d.head_dim);
   at.H = d.heads; at.Hk = d.kv_heads; at.hd = d.head_dim; at.D = d.D; at.S = d.seq_len;
   at.att = m->att; at.att_stride = m->q_dim;
-  if (decode) {
-    if ((rc = attn_launch(ATTN_FUSED, at, rows, st))) return rc;
-  } else {
-    if ((rc = attn_launch(ATTN_PREP, at, rows, st))) return rc;
-    if ((rc = attn_launch(ATTN_ONLY, at, rows, st))) return rc;
+  {
+    ProfScope p(m, T2R_PROF_ATTN, st);
+    if (decode) {
+      if ((rc = attn_launch(ATTN_FUSED, at, rows, st))) return rc;
+    } else {
+      if ((rc = attn_launch(ATTN_PREP, at, rows, st))) return rc;
+      if ((rc = attn_launch(ATTN_ONLY, at, rows, st))) return rc;
+    }
   }
   // Wo: quant_act(att) + linear + residual
   a = gemv_args();
@@ -224,7 +266,10 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
   a.s_w = d.s_wo + L_dim;
   a.x = m->att; a.x_stride = m->q_dim;
   a.N = d.dim; a.K = m->q_dim; a.y = m->x; a.y_stride = d.dim; a.res = m->x; a.res_stride = d.dim;
-  if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+  {
+    ProfScope p(m, T2R_PROF_WO, st);
+    if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+  }
   if (d.n_experts == 0) {
     // SwiGLU: RMSNorm + quant_act + W1 / W3 + gate
     a = gemv_args();
@@ -232,13 +277,19 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
     a.w3 = d.w3 + (long long)l * d.hidden * d.dim; a.s_w3 = d.s_w3 + (long long)l * d.hidden;
     a.x = m->x; a.x_stride = d.dim; a.g = d.rms_ffn + L_dim; a.inv_n = inv_d; a.eps = d.eps; a.D = d.D;
     a.N = d.hidden; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows;
-    if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_SWIGLU>(a, rows, st))) return rc;
+    {
+      ProfScope p(m, T2R_PROF_FFN_UP, st);
+      if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_SWIGLU>(a, rows, st))) return rc;
+    }
     // W2: quant_act(u) + linear + residual
     a = gemv_args();
     a.w = d.w2 + (long long)l * d.dim * d.hidden; a.s_w = d.s_w2 + L_dim;
     a.x = m->u; a.x_stride = m->ffn_rows;
     a.N = d.dim; a.K = d.hidden; a.y = m->x; a.y_stride = d.dim; a.res = m->x; a.res_stride = d.dim;
-    if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+    {
+      ProfScope p(m, T2R_PROF_FFN_DOWN, st);
+      if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+    }
   } else {
     const int E = d.n_experts, k = d.top_k, Fe = d.hidden;
     RouteArgs ra;
@@ -248,8 +299,11 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
     ra.a.x = m->x; ra.a.x_stride = d.dim; ra.a.g = d.rms_ffn + L_dim; ra.a.inv_n = inv_d; ra.a.eps = d.eps;
     ra.a.D = d.D; ra.a.N = E; ra.a.K = d.dim; ra.a.xq_out = m->mxq; ra.a.xq_stride = d.dim; ra.a.sx_out = m->msx;
     ra.k = k; ra.ids = m->ids; ra.wts = m->wts;
-    hipLaunchKernelGGL(k_moe_route, dim3(rows), dim3(kGemvThreads), 0, st, ra);
-    if ((rc = launched())) return rc;
+    {
+      ProfScope p(m, T2R_PROF_ROUTE, st);
+      hipLaunchKernelGGL(k_moe_route, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+      if ((rc = launched())) return rc;
+    }
     // expert gate / up of the k selected experts (rows j * Fe + n of the selected tables)
     a = gemv_args();
     a.w = d.wg + (long long)l * E * Fe * d.dim; a.s_w = d.s_wg + (long long)l * E * Fe;
@@ -257,14 +311,20 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
     a.xq = m->mxq; a.xq_stride = d.dim; a.s_x = m->msx;
     a.ids = m->ids; a.rows_per_id = Fe; a.ids_stride = k;
     a.N = k * Fe; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows;
-    if ((rc = gemv_launch<PRO_XQ, EPI_SWIGLU>(a, rows, st))) return rc;
+    {
+      ProfScope p(m, T2R_PROF_FFN_UP, st);
+      if ((rc = gemv_launch<PRO_XQ, EPI_SWIGLU>(a, rows, st))) return rc;
+    }
     MoeDownArgs md;
     md.u = m->u; md.wd = d.wd + (long long)l * E * d.dim * Fe; md.s_wd = d.s_wd + (long long)l * E * d.dim;
     md.ids = m->ids; md.wts = m->wts; md.x = m->x; md.k = k; md.F = Fe; md.dim = d.dim; md.x_stride = d.dim;
     int blocks = cdiv(d.dim, 4);
     if (blocks > 512) blocks = 512;
-    hipLaunchKernelGGL(k_moe_down, dim3(blocks, rows), dim3(256), 0, st, md);
-    if ((rc = launched())) return rc;
+    {
+      ProfScope p(m, T2R_PROF_FFN_DOWN, st);
+      hipLaunchKernelGGL(k_moe_down, dim3(blocks, rows), dim3(256), 0, st, md);
+      if ((rc = launched())) return rc;
+    }
   }
   return T2R_OK;
 }
@@ -276,7 +336,11 @@ int run_final(Model* m, int row, float* logits, int32_t* next_token, int32_t* po
   a.w = d.cls_q; a.s_w = d.cls_s;
   a.x = m->x + (long long)row * d.dim; a.g = d.rms_final; a.inv_n = (float)(1.0 / d.dim); a.eps = d.eps; a.D = d.D;
   a.N = d.vocab; a.K = d.dim; a.y = logits ? logits : m->logits; a.argmax_key = m->keys;
-  int rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, 1, st);
+  int rc;
+  {
+    ProfScope p(m, T2R_PROF_CLS, st);
+    rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, 1, st);
+  }
   if (rc) return rc;
   if (next_token || advance) {
     hipLaunchKernelGGL(k_finish, dim3(1), dim3(64), 0, st, m->keys, next_token, pos, advance);
@@ -490,7 +554,42 @@ int t2r_model_create(const t2r_model_desc* desc, void** model) {
   return T2R_OK;
 }
 
-void t2r_model_destroy(void* model) { delete (Model*)model; }
+void t2r_model_destroy(void* model) {
+  Model* m = (Model*)model;
+  if (!m) return;
+  free_events(m);
+  delete m;
+}
+
+int t2r_model_profile(void* model, int mask, int max_launches) {
+  Model* m = (Model*)model;
+  if (!m || mask < 0 || max_launches < 0 || (mask && max_launches == 0)) return T2R_EINVAL;
+  free_events(m);
+  if (!mask) return T2R_OK;
+  m->ev.resize((size_t)2 * max_launches);
+  m->ev_kind.assign((size_t)max_launches, -1);
+  for (auto& e : m->ev)
+    if (hipEventCreate(&e) != hipSuccess) {
+      e = nullptr;
+      free_events(m);
+      return T2R_EHIP;
+    }
+  m->prof_mask = mask;
+  return T2R_OK;
+}
+
+int t2r_model_profile_read(void* model, int32_t* kinds, float* ms, int max) {
+  Model* m = (Model*)model;
+  if (!m || max < 0 || (max > 0 && (!kinds || !ms))) return T2R_EINVAL;
+  const int n = m->ev_used / 2;
+  if (n > 0 && hipEventSynchronize(m->ev[m->ev_used - 1]) != hipSuccess) return T2R_EHIP;
+  for (int i = 0; i < n && i < max; ++i) {
+    kinds[i] = m->ev_kind[i];
+    if (hipEventElapsedTime(&ms[i], m->ev[2 * i], m->ev[2 * i + 1]) != hipSuccess) return T2R_EHIP;
+  }
+  m->ev_used = 0;
+  return n;
+}
 
 int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logits, int32_t* next_token, int flags,
                     void* stream) {
@@ -499,9 +598,13 @@ int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logi
   T2R_INIT();
   hipStream_t st = S(stream);
   const t2r_model_desc& d = m->d;
-  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, d.emb_q, d.emb_s, token, d.dim, d.vocab, m->x,
-                     (long long)d.dim, m->keys, 1, m->status);
-  int rc = launched();
+  int rc;
+  {
+    ProfScope p(m, T2R_PROF_OTHER, st);
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, d.emb_q, d.emb_s, token, d.dim, d.vocab, m->x,
+                       (long long)d.dim, m->keys, 1, m->status);
+    rc = launched();
+  }
   if (rc) return rc;
   for (int l = 0; l < d.layers; ++l)
     if ((rc = run_layer(m, l, 1, pos, true, st))) return rc;

@@ -1,29 +1,32 @@
-// Attention over the int8 KV cache, one workgroup per (KV head, query row): the KV head's G
-// query heads share every K / V row it reads (grouped-query attention).
+// Attention over the int8 KV cache, one 512-thread workgroup per (query head, query row).
 //
-// Per query head h (llm/ref_model.py:230-243; QK-norm and q_dim != dim as
+// Per query head h with KV head g = h / G (llm/ref_model.py:230-243; QK-norm and q_dim != dim as
 // compiler/frontend/qhf.py:304-353):
 //   qq, s_q = quant_act(q_h)                                  int8 q per head
 //   sc[t]   = F(F(f32(sum_j K[t, j] qq[j]) * s_q) * a_k)       exact int32 dot products
 //   m = max(sc); e = EXP(F(sc - m)); r = RECIP(red_sum(e))     red_sum in the D-lane order
 //   pq[t]   = to_i8(F(F(e[t] * r) * 127))                      int8 probabilities
-//   att_h   = F(f32(sum_t pq[t] V[t, :]) * a_v)                exact int32 P.V
+//   att_h   = F(f32(sum_t pq[t] V[t, :]) * a_v)                exact int32 P.V (any summation order)
 // The stages before it, per row at its position (llm/ref_model.py:224-229):
 //   k, q: per-head RMSNorm (QK-norm models), RoPE on the interleaved pairs
 //   kc[pos] = to_i8(F(k * (1/s_k))), vc[pos] = to_i8(F(v * (1/s_v)))
-// Modes: ATTN_FUSED (decode: the stages, then attention; the new row is used from LDS),
-// ATTN_PREP (prefill: the stages for every row, q rotated in place), ATTN_ONLY (prefill:
-// attention of rows whose q is rotated and whose KV rows are all in the cache).
+// Every workgroup of a KV head's group computes that head's new row (identical bits); the first
+// one of the group writes it to the cache, and each uses it from LDS, so no workgroup reads a
+// row another one writes.
+// Modes: ATTN_FUSED (decode: the stages, then attention), ATTN_PREP (prefill: the stages for every
+// row, q rotated in place), ATTN_ONLY (prefill: attention of rows whose q is rotated and whose KV
+// rows are all in the cache).
 #pragma once
 #include "t2r_device.h"
 
 namespace t2r {
 
 enum { ATTN_FUSED = 0, ATTN_PREP = 1, ATTN_ONLY = 2 };
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 512;
+constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kMaxG = 8;
 constexpr int kMaxHd = 128;
-constexpr int kMaxGS = 8192;          // G * S scores in LDS (32 KB), with the int8 probabilities 40 KB
+constexpr int kMaxS = 8192;           // cache rows: scores and int8 probabilities in LDS (40 KB)
 
 struct AttnArgs {
   float* qkv;                // rows of [q | k | v] projections (stride qkv_stride)
@@ -41,8 +44,7 @@ struct AttnArgs {
   long long att_stride;
 };
 
-// RMSNorm (optional) and RoPE of one head vector v[0..hd) in LDS, by the threads of one wave
-// (wave-local: lanes l < hd / 2 rotate pair l; D lanes run the ordered sum).
+// RMSNorm (optional) and RoPE of one head vector v[0..hd) in LDS, by one wave.
 T2R_DEV void head_norm_rope(float* v, const float* gain, const AttnArgs& a, int pos, int lane) {
   const int hd = a.hd;
   if (gain != nullptr) {
@@ -63,53 +65,69 @@ T2R_DEV void head_norm_rope(float* v, const float* gain, const AttnArgs& a, int 
   }
   const float* cs = a.cos_t + (long long)pos * (hd / 2);
   const float* sn = a.sin_t + (long long)pos * (hd / 2);
-  float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
-  const int i0 = lane, i1 = lane + 64;
-  if (i0 < hd / 2) {
-    const float v0 = v[2 * i0], v1 = v[2 * i0 + 1], c = cs[i0], s = sn[i0];
-    o0 = (v0 * c) + ((-v1) * s);
-    o1 = (v1 * c) + (v0 * s);
-  }
-  if (i1 < hd / 2) {
-    const float v0 = v[2 * i1], v1 = v[2 * i1 + 1], c = cs[i1], s = sn[i1];
-    o2 = (v0 * c) + ((-v1) * s);
-    o3 = (v1 * c) + (v0 * s);
+  float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k = 0; k < 2; ++k) {
+    const int i = lane + 64 * k;
+    if (i < hd / 2) {
+      const float v0 = v[2 * i], v1 = v[2 * i + 1], c = cs[i], s = sn[i];
+      o[2 * k] = (v0 * c) + ((-v1) * s);
+      o[2 * k + 1] = (v1 * c) + (v0 * s);
+    }
   }
   __builtin_amdgcn_wave_barrier();
-  if (i0 < hd / 2) { v[2 * i0] = o0; v[2 * i0 + 1] = o1; }
-  if (i1 < hd / 2) { v[2 * i1] = o2; v[2 * i1 + 1] = o3; }
+  for (int k = 0; k < 2; ++k) {
+    const int i = lane + 64 * k;
+    if (i < hd / 2) {
+      v[2 * i] = o[2 * k];
+      v[2 * i + 1] = o[2 * k + 1];
+    }
+  }
   __builtin_amdgcn_wave_barrier();
 }
 
-template <int MODE>
-__global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
-  extern __shared__ __align__(16) float dyn[];   // [G * S] scores / exps, then P.V partial sums
-  __shared__ float s_q[kMaxG][kMaxHd];
-  __shared__ float s_k[kMaxHd], s_v[kMaxHd];
-  __shared__ int s_qq[kMaxG][kMaxHd / 4];
-  __shared__ int s_kq[kMaxHd / 4], s_vq[kMaxHd / 4];
-  __shared__ float s_sq[kMaxG], s_m[kMaxG], s_r[kMaxG];
-  __shared__ float red[64];
+// 8 or 16 int8 of a cache row as int32 words (hd % 16 == 0: one 16-byte load)
+template <int CB>
+T2R_DEV void load_chunk(const int8_t* p, int* w) {
+  if (CB == 16) {
+    const int4 v = *(const int4*)p;
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else {
+    const int2 v = *(const int2*)p;
+    w[0] = v.x; w[1] = v.y;
+  }
+}
 
-  const int g = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+T2R_DEV int sext8(int w, int b) { return (int)(int8_t)((w >> (8 * b)) & 0xFF); }
+
+// CB: bytes per cache-row chunk a thread handles (16 when hd % 16 == 0, else 8)
+template <int MODE, int CB>
+__global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
+  extern __shared__ __align__(16) float dyn[];   // sc[S] scores / exps, then pq[S] int8
+  __shared__ float s_q[kMaxHd], s_k[kMaxHd], s_v[kMaxHd];
+  __shared__ int s_qq[kMaxHd / 4], s_kq[kMaxHd / 4], s_vq[kMaxHd / 4];
+  __shared__ int part[kAttnWaves][kMaxHd];
+  __shared__ float red[64];
+  __shared__ float s_sq, s_r;
+
+  const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int hd = a.hd, G = a.H / a.Hk, S = a.S;
+  const int hd = a.hd, G = a.H / a.Hk, S = a.S, g = h / G;
   const int q_dim = a.H * hd, kv_dim = a.Hk * hd;
   const int pos = a.pos[row];
   if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
   const int T = pos + 1;
   float* qkv = a.qkv + row * a.qkv_stride;
+  constexpr int CW = CB / 4;                     // int32 words per chunk
 
-  // ---- the row's k / v: norm, RoPE, int8, append to the cache
-  if (MODE != ATTN_ONLY) {
-    for (int j = tid; j < hd; j += kAttnThreads) {
+  // ---- the row's k / v (wave 0) and this head's q (wave 1): norm, RoPE; k / v to int8
+  if (MODE != ATTN_ONLY && wave == 0) {
+    for (int j = lane; j < hd; j += 64) {
       s_k[j] = qkv[q_dim + g * hd + j];
       s_v[j] = qkv[q_dim + kv_dim + g * hd + j];
     }
-    __syncthreads();
-    if (wave == 0) head_norm_rope(s_k, a.kn, a, pos, lane);
-    __syncthreads();
-    for (int j = tid; j < hd / 4; j += kAttnThreads) {
+    __builtin_amdgcn_wave_barrier();
+    head_norm_rope(s_k, a.kn, a, pos, lane);
+    for (int j = lane; j < hd / 4; j += 64) {
       int k4[4], v4[4];
       for (int b = 0; b < 4; ++b) {
         k4[b] = to_i8(s_k[4 * j + b] * a.inv_sk);
@@ -118,128 +136,143 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
       const int kw = pack_i8x4(k4[0], k4[1], k4[2], k4[3]), vw = pack_i8x4(v4[0], v4[1], v4[2], v4[3]);
       s_kq[j] = kw;
       s_vq[j] = vw;
-      *(int*)(a.kc + (long long)pos * kv_dim + g * hd + 4 * j) = kw;
-      *(int*)(a.vc + (long long)pos * kv_dim + g * hd + 4 * j) = vw;
+      if (h % G == 0) {
+        *(int*)(a.kc + (long long)pos * kv_dim + g * hd + 4 * j) = kw;
+        *(int*)(a.vc + (long long)pos * kv_dim + g * hd + 4 * j) = vw;
+      }
     }
   }
-  // ---- the group's query heads
-  for (int i = tid; i < G * hd; i += kAttnThreads) s_q[i / hd][i % hd] = qkv[(g * G + i / hd) * hd + i % hd];
-  __syncthreads();
-  if (MODE != ATTN_ONLY) {
-    for (int hh = wave; hh < G; hh += kAttnThreads / 64) head_norm_rope(s_q[hh], a.qn, a, pos, lane);
-    __syncthreads();
+  if (wave == 1) {
+    for (int j = lane; j < hd; j += 64) s_q[j] = qkv[h * hd + j];
+    __builtin_amdgcn_wave_barrier();
+    if (MODE != ATTN_ONLY) head_norm_rope(s_q, a.qn, a, pos, lane);
     if (MODE == ATTN_PREP) {
-      for (int i = tid; i < G * hd; i += kAttnThreads) qkv[(g * G + i / hd) * hd + i % hd] = s_q[i / hd][i % hd];
-      return;
+      for (int j = lane; j < hd; j += 64) qkv[h * hd + j] = s_q[j];
+    } else {
+      // quant_act of the head
+      float m = 0.0f;
+      for (int j = lane; j < hd; j += 64) m = nanmax(m, fabsf(s_q[j]));
+      m = wave_max(m);
+      const float sq = m * kInv127;
+      const float inv = sfu_recip(sq);
+      for (int j = lane; j < hd / 4; j += 64)
+        s_qq[j] = pack_i8x4(to_i8(s_q[4 * j] * inv), to_i8(s_q[4 * j + 1] * inv), to_i8(s_q[4 * j + 2] * inv),
+                            to_i8(s_q[4 * j + 3] * inv));
+      if (lane == 0) s_sq = sq;
     }
   }
-  // quant_act per head (one wave per head)
-  for (int hh = wave; hh < G; hh += kAttnThreads / 64) {
-    float m = 0.0f;
-    for (int j = lane; j < hd; j += 64) m = nanmax(m, fabsf(s_q[hh][j]));
-    m = wave_max(m);
-    const float sq = m * kInv127;
-    const float inv = sfu_recip(sq);
-    for (int j = lane; j < hd / 4; j += 64) {
-      const float* q = &s_q[hh][4 * j];
-      s_qq[hh][j] = pack_i8x4(to_i8(q[0] * inv), to_i8(q[1] * inv), to_i8(q[2] * inv), to_i8(q[3] * inv));
-    }
-    if (lane == 0) s_sq[hh] = sq;
-  }
+  if (MODE == ATTN_PREP) return;
   __syncthreads();
 
-  // ---- scores: one thread per cache row
-  float* sc = dyn;                                   // [G][S]
-  const int nw = hd / 4;
+  // ---- scores: one thread per cache row, the row in chunks of CB bytes. sc is kept in the
+  // lane-major layout of the ordered sum (row t at osum_index(t)).
+  float* sc = dyn;
+  const int D = a.D, P = osum_stride(S, D);
+  const int nch = hd / CB;
+  const int8_t* kbase = a.kc + g * hd;
+  const float sq = s_sq;
+  float mloc = -__builtin_inff();
   for (int t = tid; t < T; t += kAttnThreads) {
-    int dots[kMaxG];
-    for (int hh = 0; hh < G; ++hh) dots[hh] = 0;
-    const bool fresh = MODE == ATTN_FUSED && t == pos;
-    const int8_t* krow = a.kc + (long long)t * kv_dim + g * hd;
-    for (int w = 0; w < nw; w += 4) {
-      int kw[4];
-      if (fresh) {
-        for (int b = 0; b < 4; ++b) kw[b] = w + b < nw ? s_kq[w + b] : 0;
-      } else if (w + 4 <= nw) {
-        const int4 k4 = *(const int4*)(krow + 4 * w);
-        kw[0] = k4.x; kw[1] = k4.y; kw[2] = k4.z; kw[3] = k4.w;
+    int dot = 0;
+    if (MODE == ATTN_FUSED && t == pos) {
+      for (int w = 0; w < hd / 4; ++w) dot = __builtin_amdgcn_sdot4(s_kq[w], s_qq[w], dot, false);
+    } else {
+      const int8_t* kr = kbase + (long long)t * kv_dim;
+      int kw[kMaxHd / 4];
+#pragma unroll
+      for (int c = 0; c < kMaxHd / CB; ++c)
+        if (c < nch) load_chunk<CB>(kr + c * CB, kw + c * CW);
+#pragma unroll
+      for (int w = 0; w < kMaxHd / 4; ++w)
+        if (w < hd / 4) dot = __builtin_amdgcn_sdot4(kw[w], s_qq[w], dot, false);
+    }
+    const float s = ((float)dot * sq) * a.a_k;
+    sc[osum_index(t, D, P)] = s;
+    mloc = nanmax(mloc, s);
+  }
+  const float m = block_max(mloc, red);
+  const int Tpad = ((T + D - 1) / D) * D;
+  for (int t = tid; t < Tpad; t += kAttnThreads) {
+    const int i = osum_index(t, D, P);
+    sc[i] = t < T ? sfu_exp(sc[i] - m) : 0.0f;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float s = 0.0f;
+    if (lane < D) s = ordered_sum_t<false>(sc, T, D, P, lane);
+    s = __shfl(s, 0);
+    if (lane == 0) s_r = sfu_recip(s);
+  }
+  __syncthreads();
+  int8_t* pq = (int8_t*)(dyn + D * P);
+  const float r = s_r;
+  for (int t = tid; t < T; t += kAttnThreads) pq[t] = (int8_t)to_i8((sc[osum_index(t, D, P)] * r) * 127.0f);
+  __syncthreads();
+
+  // ---- P.V: thread = (chunk slot c of CB columns, row slice ts); int32 partial sums, 4 rows in flight.
+  // Chunk slots are padded to a power of two (NCHP) so that the lanes of one chunk are an xor class.
+  const int NCH = hd / CB;                       // chunks per row
+  int NCHP = 1;
+  while (NCHP < NCH) NCHP <<= 1;
+  const int TS = kAttnThreads / NCHP;
+  const int c = tid & (NCHP - 1), ts = tid / NCHP;
+  int acc[CB];
+#pragma unroll
+  for (int b = 0; b < CB; ++b) acc[b] = 0;
+  if (c < NCH) {
+    const int8_t* vbase = a.vc + g * hd + c * CB;
+    int t = ts;
+    for (; t + 3 * TS < T; t += 4 * TS) {
+      int vw[4][CW];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int tt = t + u * TS;
+        if (MODE == ATTN_FUSED && tt == pos) {
+          for (int w = 0; w < CW; ++w) vw[u][w] = s_vq[c * CW + w];
+        } else {
+          load_chunk<CB>(vbase + (long long)tt * kv_dim, vw[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = pq[t + u * TS];
+#pragma unroll
+        for (int w = 0; w < CW; ++w)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) acc[4 * w + b] += p * sext8(vw[u][w], b);
+      }
+    }
+    for (; t < T; t += TS) {
+      int vw[CW];
+      if (MODE == ATTN_FUSED && t == pos) {
+        for (int w = 0; w < CW; ++w) vw[w] = s_vq[c * CW + w];
       } else {
-        for (int b = 0; b < 4; ++b) kw[b] = w + b < nw ? *(const int*)(krow + 4 * (w + b)) : 0;
+        load_chunk<CB>(vbase + (long long)t * kv_dim, vw);
       }
-      for (int hh = 0; hh < G; ++hh)
-        for (int b = 0; b < 4; ++b)
-          if (w + b < nw) dots[hh] = __builtin_amdgcn_sdot4(kw[b], s_qq[hh][w + b], dots[hh], false);
-    }
-    for (int hh = 0; hh < G; ++hh) sc[hh * S + t] = ((float)dots[hh] * s_sq[hh]) * a.a_k;
-  }
-  __syncthreads();
-  // max per head (order-free), then EXP
-  for (int hh = 0; hh < G; ++hh) {
-    float m = -__builtin_inff();
-    for (int t = tid; t < T; t += kAttnThreads) m = nanmax(m, sc[hh * S + t]);
-    m = block_max(m, red);
-    if (tid == 0) s_m[hh] = m;
-  }
-  __syncthreads();
-  for (int i = tid; i < G * T; i += kAttnThreads) {
-    const int hh = i / T, t = i % T;
-    sc[hh * S + t] = sfu_exp(sc[hh * S + t] - s_m[hh]);
-  }
-  __syncthreads();
-  // the ordered sum of e per head (D lanes of one wave each), RECIP
-  for (int hh = wave; hh < G; hh += kAttnThreads / 64) {
-    if (lane < a.D) {
-      const float s = ordered_sum<false>(sc + hh * S, T, a.D, lane);
-      if (lane == 0) s_r[hh] = sfu_recip(s);
+      const int p = pq[t];
+#pragma unroll
+      for (int w = 0; w < CW; ++w)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[4 * w + b] += p * sext8(vw[w], b);
     }
   }
-  __syncthreads();
-  // int8 probabilities
-  int8_t* pq = (int8_t*)(dyn + (G * S > 1024 * G ? G * S : 1024 * G));   // [G][S]
-  for (int i = tid; i < G * T; i += kAttnThreads) {
-    const int hh = i / T, t = i % T;
-    pq[hh * S + t] = (int8_t)to_i8((sc[hh * S + t] * s_r[hh]) * 127.0f);
-  }
-  __syncthreads();
-  // ---- P.V: thread = (column word cw, row slice ts); exact int32 partial sums, then a sum over slices
-  const int CW = nw, TS = kAttnThreads / CW;
-  const int cw = tid % CW, ts = tid / CW;
-  int acc[kMaxG][4];
-  for (int hh = 0; hh < G; ++hh)
-    for (int b = 0; b < 4; ++b) acc[hh][b] = 0;
-  if (ts < TS) {
-    for (int t = ts; t < T; t += TS) {
-      const int vw = (MODE == ATTN_FUSED && t == pos) ? s_vq[cw] : *(const int*)(a.vc + (long long)t * kv_dim + g * hd + 4 * cw);
-      const int v0 = (int)(int8_t)(vw & 0xFF), v1 = (int)(int8_t)((vw >> 8) & 0xFF);
-      const int v2 = (int)(int8_t)((vw >> 16) & 0xFF), v3 = vw >> 24;
-      for (int hh = 0; hh < G; ++hh) {
-        const int p = pq[hh * S + t];
-        acc[hh][0] += p * v0;
-        acc[hh][1] += p * v1;
-        acc[hh][2] += p * v2;
-        acc[hh][3] += p * v3;
-      }
-    }
-  }
-  __syncthreads();                                   // sc is dead: reuse it for the partial sums
-  int* part = (int*)dyn;                             // [TS][G][hd]
-  if (ts < TS)
-    for (int hh = 0; hh < G; ++hh)
-      for (int b = 0; b < 4; ++b) part[(ts * G + hh) * hd + 4 * cw + b] = acc[hh][b];
+  // lanes of a wave with the same chunk: xor-shuffle over the row-slice bits, then one partial per wave
+  for (int o = NCHP; o < 64; o <<= 1)
+#pragma unroll
+    for (int b = 0; b < CB; ++b) acc[b] += __shfl_xor(acc[b], o);
+  if (lane < NCH)
+    for (int b = 0; b < CB; ++b) part[wave][lane * CB + b] = acc[b];
   __syncthreads();
   float* out = a.att + row * a.att_stride;
-  for (int i = tid; i < G * hd; i += kAttnThreads) {
-    const int hh = i / hd, j = i % hd;
+  for (int j = tid; j < hd; j += kAttnThreads) {
     int s = 0;
-    for (int k = 0; k < TS; ++k) s += part[(k * G + hh) * hd + j];
-    out[(g * G + hh) * hd + j] = (float)s * a.a_v;
+    for (int w = 0; w < kAttnWaves; ++w) s += part[w][j];
+    out[h * hd + j] = (float)s * a.a_v;
   }
 }
 
-// dynamic LDS bytes of k_attn
-inline size_t attn_lds_bytes(int G, int S) {
-  const size_t f = (size_t)(G * S > 1024 * G ? G * S : 1024 * G);
-  return f * 4 + (size_t)G * S;
-}
+// dynamic LDS bytes of k_attn: the scores (lane-major, D * osum_stride(S, D) floats) and the int8
+// probabilities of S cache rows
+inline size_t attn_lds_bytes(int S, int D) { return (size_t)D * osum_stride(S, D) * 4 + (size_t)S; }
 
 }  // namespace t2r

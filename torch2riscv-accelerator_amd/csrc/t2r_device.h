@@ -169,10 +169,17 @@ T2R_DEV int dot16(int4 w, int4 x, int acc) {
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
+#ifndef T2R_NT_LOADS
+#define T2R_NT_LOADS 1
+#endif
 // 16-byte streaming load (non-temporal hint: weights are read once per token)
 T2R_DEV int4 load_nt16(const int8_t* p) {
+#if T2R_NT_LOADS
   const v4i_t v = __builtin_nontemporal_load((const v4i_t*)p);
   return make_int4(v.x, v.y, v.z, v.w);
+#else
+  return *(const int4*)p;
+#endif
 }
 
 T2R_DEV int pack_i8x4(int a, int b, int c, int d) {
@@ -213,13 +220,65 @@ template <bool SQ>
 T2R_DEV float ordered_sum(const float* vals, int n, int D, int l) {
   float acc = 0.0f;
   const int groups = n > 0 ? (n + D - 1) / D : 1;
-  for (int g = 0; g < groups; ++g) {
+  int g = 0;
+  // 8 groups at a time: the loads are independent, the adds stay one chain in group order
+  for (; g + 8 <= groups; g += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = (g + j) * D + l;
+      v[j] = i < n ? vals[i] : 0.0f;
+      if (SQ) v[j] = v[j] * v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc = (g + j == 0) ? v[j] : acc + v[j];
+  }
+  for (; g < groups; ++g) {
     const int i = g * D + l;
     float v = i < n ? vals[i] : 0.0f;
     if (SQ) v = v * v;
     acc = g == 0 ? v : acc + v;
   }
   // pairwise tree over the D lanes: lane l (a multiple of 2s) takes lane l + s
+  for (int s = 1; s < D; s <<= 1) {
+    float o = __shfl_down(acc, s, D);
+    if ((l & (2 * s - 1)) == 0) acc = acc + o;
+  }
+  return __shfl(acc, 0, D);
+}
+
+// The same ordered sum over a buffer in the "lane-major" layout: value i (lane i % D, group i / D)
+// is at osum_index(i) = (i % D) * P + i / D, with P = osum_stride(n, D) >= the group count, a
+// multiple of 4 (16-byte aligned runs). Lane l's chain is then contiguous: its values are read
+// 16 at a time with 128-bit loads, so the loads stay off the chain of adds. The writer stores +0
+// at the padding positions i in [n, groups * D).
+__host__ __device__ inline int osum_stride(int n, int D) {
+  const int G = n > 0 ? (n + D - 1) / D : 1;
+  return ((G + 3) & ~3) + 4;
+}
+__host__ __device__ inline int osum_index(int i, int D, int P) { return (i & (D - 1)) * P + i / D; }
+
+template <bool SQ>
+T2R_DEV float ordered_sum_t(const float* buf, int n, int D, int P, int l) {
+  const int G = n > 0 ? (n + D - 1) / D : 1;
+  const float* row = buf + l * P;
+  float acc = 0.0f;
+  int g = 0;
+  for (; g + 16 <= G; g += 16) {
+    const float4 a = *(const float4*)(row + g), b = *(const float4*)(row + g + 4);
+    const float4 c = *(const float4*)(row + g + 8), d = *(const float4*)(row + g + 12);
+    float v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (SQ) v[j] = v[j] * v[j];
+      acc = (g + j == 0) ? v[j] : acc + v[j];
+    }
+  }
+  for (; g < G; ++g) {
+    float v = row[g];
+    if (SQ) v = v * v;
+    acc = g == 0 ? v : acc + v;
+  }
   for (int s = 1; s < D; s <<= 1) {
     float o = __shfl_down(acc, s, D);
     if ((l & (2 * s - 1)) == 0) acc = acc + o;

@@ -25,6 +25,7 @@ namespace t2r {
 enum { PRO_XQ = 0, PRO_QUANT = 1, PRO_NORM_QUANT = 2 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 constexpr int kMaxK = 8192;
+constexpr int kOsumLds = kMaxK + 16 * 8;   // D * osum_stride(kMaxK, D) floats, D <= 16
 constexpr int kGemvThreads = 256;
 
 struct GemvArgs {
@@ -82,12 +83,17 @@ T2R_DEV float gemv_prologue(const GemvArgs& a, int row, int8_t* xq_lds, float* x
     return a.s_x[row];
   }
   const float* x = a.x + row * a.x_stride;
+  float r = 1.0f;
+  float* ot = xf_lds + kMaxK;                      // lane-major copy for the ordered sum
+  if (PRO == PRO_NORM_QUANT) {
+    const int P = osum_stride(K, a.D), pad = ((K + a.D - 1) / a.D) * a.D;
+    for (int i = tid; i < pad; i += kGemvThreads) ot[osum_index(i, a.D, P)] = i < K ? x[i] : 0.0f;
+  }
   for (int i = tid; i < K; i += kGemvThreads) xf_lds[i] = x[i];
   __syncthreads();
-  float r = 1.0f;
   if (PRO == PRO_NORM_QUANT) {
     if (tid < a.D) {
-      float ss = ordered_sum<true>(xf_lds, K, a.D, tid);
+      const float ss = ordered_sum_t<true>(ot, K, a.D, osum_stride(K, a.D), tid);
       if (tid == 0) red[32] = sfu_rsqrt(ss * a.inv_n + a.eps);
     }
     __syncthreads();
@@ -110,17 +116,137 @@ T2R_DEV float gemv_prologue(const GemvArgs& a, int row, int8_t* xq_lds, float* x
   return s_x;
 }
 
+// One wave's tile: RU rows x NCB 1024-byte chunks of weights (16 bytes per lane per chunk), and the
+// rows' scales and residuals, so the epilogue needs no load of its own.
+template <int EPI, int NCB, int RU>
+struct WTile {
+  int4 w[RU][NCB];
+  int4 w3[EPI == EPI_SWIGLU ? RU : 1][NCB];
+  float sw[RU], sw3[EPI == EPI_SWIGLU ? RU : 1], res[EPI == EPI_RESID ? RU : 1];
+};
+
+template <int EPI, int NCB, int RU>
+T2R_DEV void load_tile(WTile<EPI, NCB, RU>& t, const GemvArgs& a, const float* res, int row_in, int r0, int lane) {
+#pragma unroll
+  for (int u = 0; u < RU; ++u) {
+    const int row = r0 + u;
+    const bool rok = row < a.N;
+    const long long wr = rok ? weight_row(a, row_in, row) : 0;
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+      const int col = lane * 16 + c * 1024;
+      const bool ok = rok && col < a.K;
+      t.w[u][c] = ok ? load_nt16(a.w + wr * a.K + col) : make_int4(0, 0, 0, 0);
+      if (EPI == EPI_SWIGLU) t.w3[u][c] = ok ? load_nt16(a.w3 + wr * a.K + col) : make_int4(0, 0, 0, 0);
+    }
+    t.sw[u] = rok ? a.s_w[wr] : 0.0f;
+    if (EPI == EPI_SWIGLU) t.sw3[u] = rok ? a.s_w3[wr] : 0.0f;
+    if (EPI == EPI_RESID) t.res[u] = rok ? res[row] : 0.0f;
+  }
+}
+
+// The prologue's inputs, loaded into registers before the first weight tile is requested (the
+// wait for them then does not wait for the tile): K <= 1024 * NCB, so a thread holds at most
+// 4 * NCB of the K values (and 2 int4 of int8 activations).
+template <int PRO, int NCB>
+struct XStage {
+  static constexpr int NX = 4 * NCB;
+  float x[PRO == PRO_XQ ? 1 : NX];
+  float g[PRO == PRO_NORM_QUANT ? NX : 1];
+  int4 q[PRO == PRO_XQ ? 2 : 1];
+};
+
+template <int PRO, int NCB>
+T2R_DEV void stage_load(XStage<PRO, NCB>& st, const GemvArgs& a, int row) {
+  const int tid = threadIdx.x, K = a.K;
+  if (PRO == PRO_XQ) {
+    const int8_t* src = a.xq + row * a.xq_stride;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = (tid + j * kGemvThreads) * 16;
+      st.q[j] = i < K ? *(const int4*)(src + i) : make_int4(0, 0, 0, 0);
+    }
+  } else {
+    const float* x = a.x + row * a.x_stride;
+#pragma unroll
+    for (int j = 0; j < XStage<PRO, NCB>::NX; ++j) {
+      const int i = tid + j * kGemvThreads;
+      st.x[j] = i < K ? x[i] : 0.0f;
+      if (PRO == PRO_NORM_QUANT) st.g[j] = i < K ? a.g[i] : 0.0f;
+    }
+  }
+}
+
+// RMSNorm / quant_act from the staged registers (same numerics as gemv_prologue)
+template <int PRO, int NCB>
+T2R_DEV float stage_finish(const XStage<PRO, NCB>& st, const GemvArgs& a, int row, int8_t* xq_lds, float* xf_lds,
+                           float* red) {
+  const int tid = threadIdx.x, K = a.K;
+  constexpr int NX = XStage<PRO, NCB>::NX;
+  if (PRO == PRO_XQ) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = (tid + j * kGemvThreads) * 16;
+      if (i < K) *(int4*)(xq_lds + i) = st.q[j];
+    }
+    __syncthreads();
+    return a.s_x[row];
+  }
+  float r = 1.0f;
+  if (PRO == PRO_NORM_QUANT) {
+    const int P = osum_stride(K, a.D), pad = ((K + a.D - 1) / a.D) * a.D;
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+      const int i = tid + j * kGemvThreads;
+      if (i < pad) xf_lds[osum_index(i, a.D, P)] = i < K ? st.x[j] : 0.0f;
+    }
+    __syncthreads();
+    if (tid < a.D) {
+      const float ss = ordered_sum_t<true>(xf_lds, K, a.D, P, tid);
+      if (tid == 0) red[32] = sfu_rsqrt(ss * a.inv_n + a.eps);
+    }
+    __syncthreads();
+    r = red[32];
+  }
+  float v[NX];
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    v[j] = PRO == PRO_NORM_QUANT ? (st.x[j] * r) * st.g[j] : st.x[j];
+    if (tid + j * kGemvThreads < K) amax = nanmax(amax, fabsf(v[j]));
+  }
+  amax = block_max(amax, red);
+  const float s_x = amax * kInv127;
+  const float inv = sfu_recip(s_x);
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    const int i = tid + j * kGemvThreads;
+    if (i < K) xq_lds[i] = (int8_t)to_i8(v[j] * inv);
+  }
+  __syncthreads();
+  return s_x;
+}
+
 // NCB: 1024-byte column chunks per row covered by the register slice (K <= NCB * 1024);
-// RU: rows per wave iteration.
+// RU: rows per wave tile. A wave's first tile is requested right after the prologue's inputs and
+// before the prologue runs, and each next tile right after the current one's dot products, so HBM
+// stays busy while the prologue, the reductions and the epilogues run.
 template <int PRO, int EPI, int NCB, int RU>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
   __shared__ __align__(16) int8_t xq_lds[kMaxK];
-  __shared__ float xf_lds[PRO == PRO_XQ ? 1 : kMaxK];
+  __shared__ __align__(16) float xf_lds[PRO == PRO_NORM_QUANT ? kOsumLds : 1];
   __shared__ float red[64];
   const int row_in = blockIdx.y;                  // activation row (prefill runs rows on grid y)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int N = a.N, K = a.K;
-  const float s_x = gemv_prologue<PRO>(a, row_in, xq_lds, xf_lds, red);
+  const int nwaves = gridDim.x * (kGemvThreads / 64);
+  const float* res = a.res ? a.res + row_in * a.res_stride : nullptr;
+  int r0 = (blockIdx.x * (kGemvThreads / 64) + wave) * RU;
+  XStage<PRO, NCB> st;
+  stage_load(st, a, row_in);
+  WTile<EPI, NCB, RU> t;
+  if (r0 < N) load_tile(t, a, res, row_in, r0, lane);
+  const float s_x = stage_finish(st, a, row_in, xq_lds, xf_lds, red);
   if (a.xq_out != nullptr && blockIdx.x == 0) {
     for (int i = threadIdx.x; i < K; i += kGemvThreads) a.xq_out[row_in * a.xq_stride + i] = xq_lds[i];
     if (threadIdx.x == 0) a.sx_out[row_in] = s_x;
@@ -132,62 +258,72 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
     xr[c] = col < K ? *(const int4*)(xq_lds + col) : make_int4(0, 0, 0, 0);
   }
   float* y = a.y + row_in * a.y_stride;
-  const float* res = a.res ? a.res + row_in * a.res_stride : nullptr;
   unsigned long long best = 0;
-  const int nwaves = gridDim.x * (kGemvThreads / 64);
-  for (int r0 = (blockIdx.x * (kGemvThreads / 64) + wave) * RU; r0 < N; r0 += nwaves * RU) {
-    int4 wv[RU][NCB];
-    int4 wv3[EPI == EPI_SWIGLU ? RU : 1][NCB];
-    long long wrow[RU];
-#pragma unroll
-    for (int u = 0; u < RU; ++u) {
-      const int row = r0 + u;
-      wrow[u] = row < N ? weight_row(a, row_in, row) : 0;
-#pragma unroll
-      for (int c = 0; c < NCB; ++c) {
-        const int col = lane * 16 + c * 1024;
-        const bool ok = row < N && col < K;
-        wv[u][c] = ok ? load_nt16(a.w + wrow[u] * K + col) : make_int4(0, 0, 0, 0);
-        if (EPI == EPI_SWIGLU)
-          wv3[u][c] = ok ? load_nt16(a.w3 + wrow[u] * K + col)
-                         : make_int4(0, 0, 0, 0);
-      }
-    }
+  for (; r0 < N; r0 += nwaves * RU) {
     int acc[RU], acc3[RU];
+    float sw[RU], sw3[RU], rs[RU];
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       acc[u] = 0;
       acc3[u] = 0;
 #pragma unroll
       for (int c = 0; c < NCB; ++c) {
-        acc[u] = dot16(wv[u][c], xr[c], acc[u]);
-        if (EPI == EPI_SWIGLU) acc3[u] = dot16(wv3[u][c], xr[c], acc3[u]);
+        acc[u] = dot16(t.w[u][c], xr[c], acc[u]);
+        if (EPI == EPI_SWIGLU) acc3[u] = dot16(t.w3[u][c], xr[c], acc3[u]);
       }
+      sw[u] = t.sw[u];
+      sw3[u] = EPI == EPI_SWIGLU ? t.sw3[u] : 0.0f;
+      rs[u] = EPI == EPI_RESID ? t.res[u] : 0.0f;
+    }
+    if (r0 + nwaves * RU < N) load_tile(t, a, res, row_in, r0 + nwaves * RU, lane);
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
       acc[u] = wave_sum_i32(acc[u]);
       if (EPI == EPI_SWIGLU) acc3[u] = wave_sum_i32(acc3[u]);
     }
-    if (lane == 0) {
+    // every lane holds the RU sums (xor butterflies): lane u finishes row r0 + u
+    if (lane < RU) {
+      int ac = acc[0], ac3 = acc3[0];
+      float w1s = sw[0], w3s = sw3[0], rr = rs[0];
 #pragma unroll
-      for (int u = 0; u < RU; ++u) {
-        const int row = r0 + u;
-        if (row >= N) break;
-        float v = dequant(acc[u], a.s_w[wrow[u]], s_x);
-        if (EPI == EPI_SWIGLU) v = silu_mul(v, dequant(acc3[u], a.s_w3[wrow[u]], s_x));
-        if (EPI == EPI_RESID) v = res[row] + v;
+      for (int u = 1; u < RU; ++u)
+        if (lane == u) {
+          ac = acc[u]; ac3 = acc3[u]; w1s = sw[u]; w3s = sw3[u]; rr = rs[u];
+        }
+      const int row = r0 + lane;
+      if (row < N) {
+        float v = dequant(ac, w1s, s_x);
+        if (EPI == EPI_SWIGLU) v = silu_mul(v, dequant(ac3, w3s, s_x));
+        if (EPI == EPI_RESID) v = rr + v;
         y[row] = v;
         if (a.acc_out != nullptr) {
           const long long base = (long long)row_in * N * (EPI == EPI_SWIGLU ? 2 : 1);
-          a.acc_out[base + row] = acc[u];
-          if (EPI == EPI_SWIGLU) a.acc_out[base + N + row] = acc3[u];
+          a.acc_out[base + row] = ac;
+          if (EPI == EPI_SWIGLU) a.acc_out[base + N + row] = ac3;
         }
         if (a.argmax_key != nullptr) {
-          unsigned long long k = argmax_key(v, row);
+          const unsigned long long k = argmax_key(v, row);
           best = k > best ? k : best;
         }
       }
     }
   }
-  if (a.argmax_key != nullptr && lane == 0 && best != 0) atomicMax(a.argmax_key + row_in, best);
+  // greedy argmax: one atomic per block at most, skipped when the key already holds a larger one
+  if (a.argmax_key != nullptr) {
+    __shared__ unsigned long long bk[kGemvThreads / 64];
+    for (int o = 1; o < 64; o <<= 1) {
+      const unsigned long long other = __shfl_xor(best, o);
+      best = other > best ? other : best;
+    }
+    if (lane == 0) bk[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned long long b = bk[0];
+      for (int w = 1; w < kGemvThreads / 64; ++w) b = bk[w] > b ? bk[w] : b;
+      unsigned long long* key = a.argmax_key + row_in;
+      if (b != 0 && b > __atomic_load_n(key, __ATOMIC_RELAXED)) atomicMax(key, b);
+    }
+  }
 }
 
 }  // namespace t2r

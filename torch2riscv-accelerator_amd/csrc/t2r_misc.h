@@ -27,7 +27,7 @@ __global__ __launch_bounds__(256) void k_embed(const int8_t* emb_q, const float*
 // out_f: normalised rows (optional), xq / s_x: quantised rows (optional).
 __global__ __launch_bounds__(kGemvThreads) void k_rows_norm_quant(GemvArgs a, int norm, float* out_f, long long out_stride) {
   __shared__ __align__(16) int8_t xq_lds[kMaxK];
-  __shared__ float xf_lds[kMaxK];
+  __shared__ __align__(16) float xf_lds[kMaxK + kOsumLds];
   __shared__ float red[64];
   const int row = blockIdx.x;
   float s_x;
@@ -44,14 +44,20 @@ __global__ __launch_bounds__(kGemvThreads) void k_rows_norm_quant(GemvArgs a, in
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* g, int n, float inv_n, float eps, int D,
                                                  float* out) {
   __shared__ float xs[kMaxK];
+  __shared__ __align__(16) float ot[kOsumLds];
   __shared__ float rr;
   const int row = blockIdx.x;
   x += (long long)row * n;
   out += (long long)row * n;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) xs[i] = x[i];
+  const int P = osum_stride(n, D), pad = ((n + D - 1) / D) * D;
+  for (int i = threadIdx.x; i < pad; i += blockDim.x) {
+    const float v = i < n ? x[i] : 0.0f;
+    if (i < n) xs[i] = v;
+    ot[osum_index(i, D, P)] = v;
+  }
   __syncthreads();
   if (threadIdx.x < D) {
-    const float ss = ordered_sum<true>(xs, n, D, threadIdx.x);
+    const float ss = ordered_sum_t<true>(ot, n, D, P, threadIdx.x);
     if (threadIdx.x == 0) rr = sfu_rsqrt(ss * inv_n + eps);
   }
   __syncthreads();
@@ -135,7 +141,7 @@ struct RouteArgs {
 };
 __global__ __launch_bounds__(kGemvThreads) void k_moe_route(RouteArgs ra) {
   __shared__ __align__(16) int8_t xq_lds[kMaxK];
-  __shared__ float xf_lds[kMaxK];
+  __shared__ __align__(16) float xf_lds[kMaxK + kOsumLds];
   __shared__ float red[64];
   __shared__ float sc[64];
   __shared__ float ev[16];

@@ -152,3 +152,51 @@ class ResidentModel:
         for s in starts:
             out = self.prefill(tokens[s:s + M], start=s)
         return out
+
+    # ------------------------------------------------------------ timing
+    def profile(self, kinds=("qkv", "attn", "wo", "ffn_up", "ffn_down", "cls", "route", "other"), max_launches=65536):
+        """Record HIP events around every launch of these kernel classes from now on (t2r_model_profile);
+        kinds=() stops recording and frees the events."""
+        mask = 0
+        for k in kinds:
+            mask |= 1 << abi.PROF_KINDS.index(k)
+        abi.check("t2r_model_profile", self.lib.t2r_model_profile(self.handle, mask, max_launches if mask else 0))
+        self._prof_max = max_launches if mask else 0
+
+    def profile_read(self):
+        """{kind: [ms of each recorded launch]} since the last read (waits for the recorded events)."""
+        n = getattr(self, "_prof_max", 0)
+        kinds = np.zeros(max(n, 1), np.int32)
+        ms = np.zeros(max(n, 1), np.float32)
+        got = self.lib.t2r_model_profile_read(self.handle, kinds.ctypes.data, ms.ctypes.data, n)
+        if got < 0:
+            abi.check("t2r_model_profile_read", got)
+        out = {}
+        for k, t in zip(kinds[:got], ms[:got]):
+            out.setdefault(abi.PROF_KINDS[k], []).append(float(t))
+        return out
+
+    # ------------------------------------------------------------ HIP graphs
+    def capture_decode(self, steps):
+        """A HIP graph of `steps` greedy decode steps on the device-resident (tok, pos): each replay
+        runs them with the argmax and pos += 1 on the device and no host work. Replaying it again
+        continues from wherever (tok, pos) stand. Kernel timing (profile()) is switched off for the
+        capture: events recorded during stream capture cannot be timed afterwards."""
+        torch = self.torch
+        if getattr(self, "_prof_max", 0):
+            self.profile(kinds=())
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        tok, pos = self.tok.clone(), self.pos.clone()
+        with torch.cuda.stream(side):
+            self.step(logits=False, advance=True)          # one eager step on the capture stream first
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        with torch.cuda.graph(g, stream=side):
+            for _ in range(steps):
+                self.step(logits=False, advance=True)
+        self.tok.copy_(tok)
+        self.pos.copy_(pos)
+        torch.cuda.synchronize(self.device)
+        return g

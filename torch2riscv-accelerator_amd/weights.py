@@ -39,11 +39,19 @@ def to_i8(x):
 
 
 def quantize_rows(w):
-    """Symmetric int8 per row: (q int8, s float32) with s = max|row| / 127 (llm/ref_model.py:142-148)."""
+    """Symmetric int8 per row: (q int8, s float32) with s = max|row| / 127 and q = to_i8(w / s)
+    (llm/ref_model.py:142-148). w / s is finite except 0 / 0 on an all-zero row (NaN -> 0), so the
+    in-place rint + clip below is to_i8 exactly."""
     w = np.asarray(w, F)
     s = (np.abs(w).max(axis=-1) / F(127)).astype(F)
     with np.errstate(divide="ignore", invalid="ignore"):
-        q = to_i8(w / s[..., None])
+        q = np.divide(w, s[..., None])
+    np.rint(q, out=q)
+    np.clip(q, -127, 127, out=q)
+    q = q.astype(np.int8)
+    zero = s == 0
+    if zero.any():
+        q[zero] = 0
     return q, s
 
 
@@ -114,11 +122,12 @@ class QuantModel:
         cfg.validate()
         self.cfg = c = cfg
         L = c.layers
-        self.emb_q, self.emb_s = quantize_rows(fp32_tensor(c, "tok"))
-        if c.tied:
-            self.cls_q, self.cls_s = self.emb_q, self.emb_s
-        else:
-            self.cls_q, self.cls_s = quantize_rows(fp32_tensor(c, "wcls"))
+        # tensors are independent (one generator each): generate them in parallel threads (NumPy
+        # releases the GIL in its random fills and ufuncs)
+        from concurrent.futures import ThreadPoolExecutor
+        pool = ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
+        emb = pool.submit(lambda: quantize_rows(fp32_tensor(c, "tok")))
+        cls = None if c.tied else pool.submit(lambda: quantize_rows(fp32_tensor(c, "wcls")))
         self.rms_final = fp32_tensor(c, "rms_final")
         self.rms_att = np.stack([fp32_tensor(c, "rms_att", l) for l in range(L)])
         self.rms_ffn = np.stack([fp32_tensor(c, "rms_ffn", l) for l in range(L)])
@@ -127,7 +136,7 @@ class QuantModel:
         self.k_norm = np.stack([fp32_tensor(c, "k_norm", l) for l in range(L)]) if c.qk_norm else np.ones((L, hd), F)
 
         def stack(fn):
-            qs = [fn(l) for l in range(L)]
+            qs = list(pool.map(fn, range(L)))
             return np.stack([a for a, _ in qs]), np.stack([b for _, b in qs])
         self.wqkv, self.s_wqkv = stack(lambda l: quantize_rows(np.concatenate(
             [fp32_tensor(c, "wq", l), fp32_tensor(c, "wk", l), fp32_tensor(c, "wv", l)])))
@@ -141,6 +150,12 @@ class QuantModel:
             self.w1, self.s_w1 = stack(lambda l: quantize_rows(fp32_tensor(c, "w1", l)))
             self.w3, self.s_w3 = stack(lambda l: quantize_rows(fp32_tensor(c, "w3", l)))
             self.w2, self.s_w2 = stack(lambda l: quantize_rows(fp32_tensor(c, "w2", l)))
+        self.emb_q, self.emb_s = emb.result()
+        if c.tied:
+            self.cls_q, self.cls_s = self.emb_q, self.emb_s
+        else:
+            self.cls_q, self.cls_s = cls.result()
+        pool.shutdown()
         self.cos, self.sin = rope_tables(c)
         if kv_scales is None:
             kv_scales = stored_kv_scales(c)
