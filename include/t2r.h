@@ -80,12 +80,13 @@ int t2r_quant_act(const float* x, int rows, int n, int8_t* xq, float* s_x, void*
 /* The W8A8 linear layer of one activation row (DeviceModel.linear llm/ref_model.py:198-202;
  * SaFuncSim.gemv llm/sa_funcsim.py:138-162; CL.linear llm/compile_layer.py:93-182):
  * acc[n] = sum_k xq[k] w[n, k] (int32), y[n] = F(F(f32(acc) * s_w[n]) * s_x[0]) (+ residual[n]
- * first rounded sum, llm/compile_model.py:330-331). y and acc_out may be NULL (not both);
- * residual may be NULL or alias y. K % 16 == 0, K <= 8192. */
+ * first rounded sum, llm/compile_model.py:330-331). y is required; acc_out (the int32 sums, a parity
+ * hook) and residual may be NULL; residual may alias y. K % 16 == 0, K <= 8192. */
 int t2r_gemv_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const float* s_x, int N, int K, float* y,
                   int32_t* acc_out, const float* residual, void* stream);
 /* The same over M activation rows xq[M, K] with scales s_x[M] (prefill rows,
- * compiler/plugins/sa/transforms/SahlExpandKernels.cpp:205 expandLinearRows; int8 MFMA). */
+ * compiler/plugins/sa/transforms/SahlExpandKernels.cpp:205 expandLinearRows) on int8 MFMA;
+ * y, acc_out and residual are [M, N]. */
 int t2r_gemm_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const float* s_x, int M, int N, int K,
                   float* y, int32_t* acc_out, const float* residual, void* stream);
 /* RoPE of rows v[rows, n] in place at positions pos[rows] (DeviceModel.rope llm/ref_model.py:209-214;

@@ -220,6 +220,27 @@ int validate(const t2r_model_desc* d) {
   return T2R_OK;
 }
 
+// RMSNorm (g != nullptr) and quant_act of `rows` rows x[rows, K] into the workspace's int8 rows
+int rows_quant(Model* m, const float* x, long long x_stride, const float* g, int K, int rows, hipStream_t st) {
+  GemvArgs a = gemv_args();
+  a.x = x; a.x_stride = x_stride; a.g = g; a.K = K; a.D = m->d.D; a.eps = m->d.eps; a.inv_n = (float)(1.0 / K);
+  a.xq_out = m->xq; a.xq_stride = K; a.sx_out = m->sx;
+  hipLaunchKernelGGL(k_rows_norm_quant, dim3(rows), dim3(kGemvThreads), 0, st, a, g != nullptr ? 1 : 0, (float*)nullptr,
+                     0LL);
+  return launched();
+}
+
+// a prefill linear layer on the workspace's int8 rows (int8 MFMA)
+template <int EPI>
+int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, const float* s_w3, int N, int K, int rows,
+                float* y, long long y_stride, hipStream_t st) {
+  GemmArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.xq = m->xq; a.s_x = m->sx; a.w = w; a.s_w = s_w; a.w3 = w3; a.s_w3 = s_w3;
+  a.M = rows; a.N = N; a.K = K; a.y = y; a.y_stride = y_stride; a.res = EPI == EPI_RESID ? y : nullptr;
+  return gemm_launch<EPI>(a, st) ? T2R_EHIP : T2R_OK;
+}
+
 // one decoder layer on `rows` rows of the workspace at device positions pos[rows]
 int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStream_t st) {
   const t2r_model_desc& d = m->d;
@@ -234,7 +255,13 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
   a.N = m->qkv_dim; a.K = d.dim; a.y = m->qkv; a.y_stride = m->qkv_dim;
   {
     ProfScope p(m, T2R_PROF_QKV, st);
-    if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
+    if (decode) {
+      if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
+    } else {
+      if ((rc = rows_quant(m, m->x, d.dim, d.rms_att + L_dim, d.dim, rows, st))) return rc;
+      if ((rc = rows_linear<EPI_STORE>(m, a.w, a.s_w, nullptr, nullptr, m->qkv_dim, d.dim, rows, m->qkv, m->qkv_dim, st)))
+        return rc;
+    }
   }
   // attention (QK-norm, RoPE, KV append fused for decode)
   AttnArgs at;
@@ -268,7 +295,12 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
   a.N = d.dim; a.K = m->q_dim; a.y = m->x; a.y_stride = d.dim; a.res = m->x; a.res_stride = d.dim;
   {
     ProfScope p(m, T2R_PROF_WO, st);
-    if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+    if (decode) {
+      if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+    } else {
+      if ((rc = rows_quant(m, m->att, m->q_dim, nullptr, m->q_dim, rows, st))) return rc;
+      if ((rc = rows_linear<EPI_RESID>(m, a.w, a.s_w, nullptr, nullptr, d.dim, m->q_dim, rows, m->x, d.dim, st))) return rc;
+    }
   }
   if (d.n_experts == 0) {
     // SwiGLU: RMSNorm + quant_act + W1 / W3 + gate
@@ -279,7 +311,13 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
     a.N = d.hidden; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows;
     {
       ProfScope p(m, T2R_PROF_FFN_UP, st);
-      if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_SWIGLU>(a, rows, st))) return rc;
+      if (decode) {
+        if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_SWIGLU>(a, rows, st))) return rc;
+      } else {
+        if ((rc = rows_quant(m, m->x, d.dim, d.rms_ffn + L_dim, d.dim, rows, st))) return rc;
+        if ((rc = rows_linear<EPI_SWIGLU>(m, a.w, a.s_w, a.w3, a.s_w3, d.hidden, d.dim, rows, m->u, m->ffn_rows, st)))
+          return rc;
+      }
     }
     // W2: quant_act(u) + linear + residual
     a = gemv_args();
@@ -288,7 +326,13 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
     a.N = d.dim; a.K = d.hidden; a.y = m->x; a.y_stride = d.dim; a.res = m->x; a.res_stride = d.dim;
     {
       ProfScope p(m, T2R_PROF_FFN_DOWN, st);
-      if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+      if (decode) {
+        if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+      } else {
+        if ((rc = rows_quant(m, m->u, m->ffn_rows, nullptr, d.hidden, rows, st))) return rc;
+        if ((rc = rows_linear<EPI_RESID>(m, a.w, a.s_w, nullptr, nullptr, d.dim, d.hidden, rows, m->x, d.dim, st)))
+          return rc;
+      }
     }
   } else {
     const int E = d.n_experts, k = d.top_k, Fe = d.hidden;
@@ -442,25 +486,33 @@ int t2r_quant_act(const float* x, int rows, int n, int8_t* xq, float* s_x, void*
 
 int t2r_gemv_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const float* s_x, int N, int K, float* y,
                   int32_t* acc_out, const float* residual, void* stream) {
-  return t2r_gemm_w8a8(w, s_w, xq, s_x, 1, N, K, y, acc_out, residual, stream);
+  if (!w || !s_w || !xq || !s_x || !y) return T2R_EINVAL;
+  if (N <= 0 || K <= 0 || K % 16 || K > kMaxK) return T2R_ESHAPE;
+  T2R_INIT();
+  GemvArgs a = gemv_args();
+  a.w = w; a.s_w = s_w; a.xq = xq; a.xq_stride = K; a.s_x = s_x; a.N = N; a.K = K;
+  a.acc_out = acc_out; a.y = y; a.y_stride = N;
+  if (residual) {
+    a.res = residual; a.res_stride = N;
+    return gemv_launch<PRO_XQ, EPI_RESID>(a, 1, S(stream)) ? T2R_EHIP : T2R_OK;
+  }
+  return gemv_launch<PRO_XQ, EPI_STORE>(a, 1, S(stream)) ? T2R_EHIP : T2R_OK;
 }
 
 int t2r_gemm_w8a8(const int8_t* w, const float* s_w, const int8_t* xq, const float* s_x, int M, int N, int K,
                   float* y, int32_t* acc_out, const float* residual, void* stream) {
-  if (!w || !s_w || !xq || !s_x || (!y && !acc_out) || (residual && !y)) return T2R_EINVAL;
+  if (!w || !s_w || !xq || !s_x || !y) return T2R_EINVAL;
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 || K > kMaxK) return T2R_ESHAPE;
   T2R_INIT();
-  GemvArgs a = gemv_args();
-  a.w = w; a.s_w = s_w; a.xq = xq; a.xq_stride = K; a.s_x = s_x; a.N = N; a.K = K;
+  GemmArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.xq = xq; a.s_x = s_x; a.w = w; a.s_w = s_w; a.M = M; a.N = N; a.K = K; a.y = y; a.y_stride = N;
   a.acc_out = acc_out;
-  float* scratch_y = y;
-  if (!y) return T2R_EINVAL;   // y is required by the kernels' epilogue (acc_out is an extra)
-  a.y = scratch_y; a.y_stride = N;
   if (residual) {
-    a.res = residual; a.res_stride = N;
-    return gemm_dispatch<EPI_RESID>(a, M, S(stream));
+    a.res = residual;
+    return gemm_launch<EPI_RESID>(a, S(stream)) ? T2R_EHIP : T2R_OK;
   }
-  return gemm_dispatch<EPI_STORE>(a, M, S(stream));
+  return gemm_launch<EPI_STORE>(a, S(stream)) ? T2R_EHIP : T2R_OK;
 }
 
 int t2r_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* pos, int rows, int n, int half, int S_,

@@ -1,12 +1,24 @@
-// W8A8 GEMM over prefill rows: C[M, N] = xq[M, K] . W[N, K]^T (int32), dequantised per row and
-// column like the GEMV (expandLinearRows, compiler/plugins/sa/transforms/SahlExpandKernels.cpp:205).
+// W8A8 GEMM over prefill rows on CDNA4 int8 MFMA: acc[M, N] = xq[M, K] . W[N, K]^T in exact int32
+// (v_mfma_i32_32x32x32_i8), then per element y = F(F(f32(acc) * s_w[n]) * s_x[m]) with the same
+// epilogues as the decode GEMV (store, residual add, SwiGLU gate) (expandLinearRows,
+// compiler/plugins/sa/transforms/SahlExpandKernels.cpp:205; the rows are independent, so one pass
+// over all prompt rows gives the logits and KV of row-by-row decoding bit for bit).
+//
+// Tiling: a wave computes a 64 x 64 block of C as 2 x 2 MFMA tiles of 32 x 32; a workgroup is
+// WM x WN waves (BM = 64 WM rows, BN = 64 WN columns). K advances by 64: the next K-slab of A and B
+// is loaded from global memory into registers while the MFMAs consume the current slab from LDS
+// (two LDS buffers, rows padded to 80 bytes). Every lane feeds an MFMA 16 consecutive k-values of
+// its A row and of its B column, the same k for both operands, so the product is the exact sum
+// whatever order the instruction pairs them in. SwiGLU: the B tile's columns alternate 32 rows
+// of W1 and the same 32 rows of W3, so a lane holds h1 and h3 of the same (m, n).
 #pragma once
 #include "t2r_gemv.h"
 
 namespace t2r {
 
-inline int cdiv_i(long long a, long long b) { return (int)((a + b - 1) / b); }
+__host__ __device__ inline int cdiv_i(long long a, long long b) { return (int)((a + b - 1) / b); }
 
+// ------------------------------------------------------------------ GEMV launcher (decode, op level)
 // The GEMV over `rows` activation rows (grid y): register-slice width NCB by K, rows per wave RU
 // by N (enough waves to fill the 256 CUs, up to 8 per CU).
 template <int PRO, int EPI, int NCB>
@@ -34,10 +46,178 @@ int gemv_launch(const GemvArgs& a, int rows, hipStream_t st) {
   return gemv_launch_ncb<PRO, EPI, 8>(a, rows, st);
 }
 
-// Rows through the GEMV kernel, one activation row per grid row.
+// ------------------------------------------------------------------ MFMA GEMM
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 64;                 // K per slab
+constexpr int kLdsRow = kBK + 16;       // padded LDS row (bytes)
+
+struct GemmArgs {
+  const int8_t* xq;          // [M, K] activations
+  const float* s_x;          // [M]
+  const int8_t* w;           // [N, K] (SwiGLU: W1)
+  const float* s_w;          // [N]
+  const int8_t* w3;          // SwiGLU: W3 [N, K]
+  const float* s_w3;
+  int M, N, K;               // N: output columns (SwiGLU: F)
+  float* y;                  // [M, N] (stride y_stride)
+  const float* res;          // EPI_RESID residual [M, N] (stride y_stride; may alias y)
+  long long y_stride;
+  int32_t* acc_out;          // optional [M, N] (SwiGLU: [M, 2N], W1 then W3 columns)
+};
+
+// source row of tile column c (0 .. BN) for the block's column origin n0 (SwiGLU interleave)
 template <int EPI>
-int gemm_dispatch(const GemvArgs& a, int M, hipStream_t st) {
-  return gemv_launch<PRO_XQ, EPI>(a, M, st);
+T2R_DEV const int8_t* b_row(const GemmArgs& a, int n0, int c, int& n, bool& ok) {
+  if (EPI == EPI_SWIGLU) {
+    const int half = c >> 5 & 1;                 // 32-column groups alternate W1 / W3
+    n = (n0 >> 1) + ((c >> 6) << 5) + (c & 31);  // the block covers BN / 2 output columns
+    ok = n < a.N;
+    return (half ? a.w3 : a.w) + (long long)(ok ? n : 0) * a.K;
+  }
+  n = n0 + c;
+  ok = n < a.N;
+  return a.w + (long long)(ok ? n : 0) * a.K;
+}
+
+template <int EPI, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm(GemmArgs a) {
+  constexpr int BM = 64 * WM, BN = 64 * WN, NT = 64 * WM * WN;
+  constexpr int CH_A = BM * kBK / 16, CH_B = BN * kBK / 16;      // 16-byte chunks per slab
+  constexpr int PA = (CH_A + NT - 1) / NT, PB = (CH_B + NT - 1) / NT;
+  __shared__ __align__(16) int8_t As[2][BM * kLdsRow];
+  __shared__ __align__(16) int8_t Bs[2][BN * kLdsRow];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  // m tiles fastest: the workgroups that share a weight slab run together (L2 / MALL reuse)
+  const int mt = blockIdx.x % cdiv_i(a.M, BM), nt = blockIdx.x / cdiv_i(a.M, BM);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int K = a.K;
+
+  int4 ra[PA], rb[PB];
+  auto load_slab = [&](int k0) {
+#pragma unroll
+    for (int p = 0; p < PA; ++p) {
+      const int c = tid + p * NT, r = c / (kBK / 16), kc = (c % (kBK / 16)) * 16;
+      const int m = m0 + r, k = k0 + kc;
+      ra[p] = (c < CH_A && m < a.M && k < K) ? *(const int4*)(a.xq + (long long)m * K + k) : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int p = 0; p < PB; ++p) {
+      const int c = tid + p * NT, r = c / (kBK / 16), kc = (c % (kBK / 16)) * 16;
+      int n;
+      bool ok;
+      const int8_t* src = b_row<EPI>(a, n0, r, n, ok);
+      const int k = k0 + kc;
+      rb[p] = (c < CH_B && ok && k < K) ? load_nt16(src + k) : make_int4(0, 0, 0, 0);
+    }
+  };
+  auto store_slab = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < PA; ++p) {
+      const int c = tid + p * NT;
+      if (c < CH_A) *(int4*)(&As[buf][(c / (kBK / 16)) * kLdsRow + (c % (kBK / 16)) * 16]) = ra[p];
+    }
+#pragma unroll
+    for (int p = 0; p < PB; ++p) {
+      const int c = tid + p * NT;
+      if (c < CH_B) *(int4*)(&Bs[buf][(c / (kBK / 16)) * kLdsRow + (c % (kBK / 16)) * 16]) = rb[p];
+    }
+  };
+
+  v16i_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int nk = cdiv_i(K, kBK);
+  load_slab(0);
+  store_slab(0);
+  __syncthreads();
+  const int lr = lane & 31, lk = (lane >> 5) * 16;
+  for (int s = 0; s < nk; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nk) load_slab((s + 1) * kBK);
+#pragma unroll
+    for (int kk = 0; kk < kBK; kk += 32) {
+      v4i_t fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) fa[i] = *(const v4i_t*)(&As[buf][(wm * 64 + i * 32 + lr) * kLdsRow + kk + lk]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[j] = *(const v4i_t*)(&Bs[buf][(wn * 64 + j * 32 + lr) * kLdsRow + kk + lk]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    if (s + 1 < nk) {
+      store_slab(buf ^ 1);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds C[m][n] for n = lane % 32 of each 32 x 32 tile, m = 8 (r / 4) + 4 (lane / 32) + r % 4
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (m >= a.M) continue;
+      const float sx = a.s_x[m];
+      if (EPI == EPI_SWIGLU) {
+        // tile columns [wn * 64, wn * 64 + 32) are W1 rows, the next 32 the same W3 rows
+        const int n = (n0 >> 1) + wn * 32 + lr;
+        if (n >= a.N) continue;
+        const int ac1 = acc[i][0][r], ac3 = acc[i][1][r];
+        const float h1 = dequant(ac1, a.s_w[n], sx), h3 = dequant(ac3, a.s_w3[n], sx);
+        a.y[(long long)m * a.y_stride + n] = silu_mul(h1, h3);
+        if (a.acc_out) {
+          a.acc_out[(long long)m * 2 * a.N + n] = ac1;
+          a.acc_out[(long long)m * 2 * a.N + a.N + n] = ac3;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + wn * 64 + j * 32 + lr;
+          if (n >= a.N) continue;
+          float v = dequant(acc[i][j][r], a.s_w[n], sx);
+          if (EPI == EPI_RESID) v = a.res[(long long)m * a.y_stride + n] + v;
+          a.y[(long long)m * a.y_stride + n] = v;
+          if (a.acc_out) a.acc_out[(long long)m * a.N + n] = acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
+// Picks the workgroup shape: the largest tile that still gives >= 256 workgroups (one per CU).
+template <int EPI>
+int gemm_launch(const GemmArgs& a, hipStream_t st) {
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 16) return -2;
+  const int ncols = EPI == EPI_SWIGLU ? 2 * a.N : a.N;   // B rows the tiles cover
+  auto blocks = [&](int bm, int bn) { return (long long)cdiv_i(a.M, bm) * cdiv_i(ncols, bn); };
+  int wm = 1, wn = 1;
+  if (blocks(128, 128) >= 256) { wm = 2; wn = 2; }
+  else if (blocks(64, 128) >= 256) { wm = 1; wn = 2; }
+  const long long nb = blocks(64 * wm, 64 * wn);
+  if (nb > 0x7FFFFFFF) return -2;
+  dim3 grid((unsigned)nb), block(64 * wm * wn);
+  if (wm == 2) hipLaunchKernelGGL((k_gemm<EPI, 2, 2>), grid, block, 0, st, a);
+  else if (wn == 2) hipLaunchKernelGGL((k_gemm<EPI, 1, 2>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((k_gemm<EPI, 1, 1>), grid, block, 0, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// The op-level GEMM entry: MFMA over the rows.
+template <int EPI>
+int gemm_dispatch(const GemvArgs& g, int M, hipStream_t st) {
+  GemmArgs a;
+  a.xq = g.xq; a.s_x = g.s_x; a.w = g.w; a.s_w = g.s_w; a.w3 = g.w3; a.s_w3 = g.s_w3;
+  a.M = M; a.N = g.N; a.K = g.K; a.y = g.y; a.res = g.res; a.y_stride = g.y_stride; a.acc_out = g.acc_out;
+  return gemm_launch<EPI>(a, st);
 }
 
 }  // namespace t2r
