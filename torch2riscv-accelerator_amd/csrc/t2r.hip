@@ -86,14 +86,14 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   dim3 grid(a.H, rows), block(kAttnThreads);
   const bool c16 = a.hd % 16 == 0;
   if (mode == ATTN_FUSED) {
-    if (c16) hipLaunchKernelGGL((k_attn<ATTN_FUSED, 16>), grid, block, lds, st, a);
-    else hipLaunchKernelGGL((k_attn<ATTN_FUSED, 8>), grid, block, lds, st, a);
+    if (c16) launch((k_attn<ATTN_FUSED, 16>), grid, block, lds, st, a);
+    else launch((k_attn<ATTN_FUSED, 8>), grid, block, lds, st, a);
   } else if (mode == ATTN_PREP) {
-    if (c16) hipLaunchKernelGGL((k_attn<ATTN_PREP, 16>), grid, block, lds, st, a);
-    else hipLaunchKernelGGL((k_attn<ATTN_PREP, 8>), grid, block, lds, st, a);
+    if (c16) launch((k_attn<ATTN_PREP, 16>), grid, block, lds, st, a);
+    else launch((k_attn<ATTN_PREP, 8>), grid, block, lds, st, a);
   } else {
-    if (c16) hipLaunchKernelGGL((k_attn<ATTN_ONLY, 16>), grid, block, lds, st, a);
-    else hipLaunchKernelGGL((k_attn<ATTN_ONLY, 8>), grid, block, lds, st, a);
+    if (c16) launch((k_attn<ATTN_ONLY, 16>), grid, block, lds, st, a);
+    else launch((k_attn<ATTN_ONLY, 8>), grid, block, lds, st, a);
   }
   return launched();
 }
@@ -123,19 +123,23 @@ struct Model {
   int ev_used = 0;
 };
 
-// events around the launches of one kernel class
+// the launches of one kernel class between a start and a stop event (kernel start / kernel end)
 struct ProfScope {
   Model* m;
-  hipStream_t st;
   bool on;
-  ProfScope(Model* m_, int kind, hipStream_t s) : m(m_), st(s), on(false) {
+  ProfScope(Model* m_, int kind, hipStream_t) : m(m_), on(false) {
     if ((m->prof_mask >> kind) & 1 && m->ev_used + 2 <= (int)m->ev.size()) {
-      on = hipEventRecord(m->ev[m->ev_used], st) == hipSuccess;
-      if (on) m->ev_kind[m->ev_used / 2] = kind;
+      on = true;
+      m->ev_kind[m->ev_used / 2] = kind;
+      g_launch_events.start = m->ev[m->ev_used];
+      g_launch_events.stop = m->ev[m->ev_used + 1];
     }
   }
   ~ProfScope() {
-    if (on && hipEventRecord(m->ev[m->ev_used + 1], st) == hipSuccess) m->ev_used += 2;
+    if (on) {
+      m->ev_used += 2;
+      g_launch_events = LaunchEvents();
+    }
   }
 };
 
@@ -225,7 +229,7 @@ int rows_quant(Model* m, const float* x, long long x_stride, const float* g, int
   GemvArgs a = gemv_args();
   a.x = x; a.x_stride = x_stride; a.g = g; a.K = K; a.D = m->d.D; a.eps = m->d.eps; a.inv_n = (float)(1.0 / K);
   a.xq_out = m->xq; a.xq_stride = K; a.sx_out = m->sx;
-  hipLaunchKernelGGL(k_rows_norm_quant, dim3(rows), dim3(kGemvThreads), 0, st, a, g != nullptr ? 1 : 0, (float*)nullptr,
+  launch(k_rows_norm_quant, dim3(rows), dim3(kGemvThreads), 0, st, a, g != nullptr ? 1 : 0, (float*)nullptr,
                      0LL);
   return launched();
 }
@@ -345,7 +349,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
     ra.k = k; ra.ids = m->ids; ra.wts = m->wts;
     {
       ProfScope p(m, T2R_PROF_ROUTE, st);
-      hipLaunchKernelGGL(k_moe_route, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+      launch(k_moe_route, dim3(rows), dim3(kGemvThreads), 0, st, ra);
       if ((rc = launched())) return rc;
     }
     // expert gate / up of the k selected experts (rows j * Fe + n of the selected tables)
@@ -366,7 +370,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
     if (blocks > 512) blocks = 512;
     {
       ProfScope p(m, T2R_PROF_FFN_DOWN, st);
-      hipLaunchKernelGGL(k_moe_down, dim3(blocks, rows), dim3(256), 0, st, md);
+      launch(k_moe_down, dim3(blocks, rows), dim3(256), 0, st, md);
       if ((rc = launched())) return rc;
     }
   }
@@ -387,7 +391,7 @@ int run_final(Model* m, int row, float* logits, int32_t* next_token, int32_t* po
   }
   if (rc) return rc;
   if (next_token || advance) {
-    hipLaunchKernelGGL(k_finish, dim3(1), dim3(64), 0, st, m->keys, next_token, pos, advance);
+    launch(k_finish, dim3(1), dim3(64), 0, st, m->keys, next_token, pos, advance);
     return launched();
   }
   return T2R_OK;
@@ -429,7 +433,7 @@ int t2r_sfu(int fn, const uint32_t* x, uint32_t* y, int64_t n, void* stream) {
   if (n == 0) return T2R_OK;
   long long blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(k_sfu, dim3((unsigned)blocks), dim3(256), 0, S(stream), fn, x, y, (long long)n);
+  launch(k_sfu, dim3((unsigned)blocks), dim3(256), 0, S(stream), fn, x, y, (long long)n);
   return launched();
 }
 
@@ -439,7 +443,7 @@ int t2r_fp32_op(int op, const uint32_t* a, const uint32_t* b, uint32_t* y, int64
   if (n == 0) return T2R_OK;
   long long blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(k_fp32op, dim3((unsigned)blocks), dim3(256), 0, S(stream), op, a, b, y, (long long)n);
+  launch(k_fp32op, dim3((unsigned)blocks), dim3(256), 0, S(stream), op, a, b, y, (long long)n);
   return launched();
 }
 
@@ -451,7 +455,7 @@ int t2r_requant(const int32_t* r, int64_t n, int scale, int shift, int zp, int l
   if (n == 0) return T2R_OK;
   long long blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(k_requant, dim3((unsigned)blocks), dim3(256), 0, S(stream), r, (long long)n, scale, shift, zp,
+  launch(k_requant, dim3((unsigned)blocks), dim3(256), 0, S(stream), r, (long long)n, scale, shift, zp,
                      lo, hi, out);
   return launched();
 }
@@ -461,7 +465,7 @@ int t2r_embed(const int8_t* emb_q, const float* emb_s, const int32_t* tokens, in
   if (!emb_q || !emb_s || !tokens || !x) return T2R_EINVAL;
   if (rows <= 0 || dim <= 0 || vocab <= 0) return T2R_ESHAPE;
   T2R_INIT();
-  hipLaunchKernelGGL(k_embed, dim3(rows), dim3(256), 0, S(stream), emb_q, emb_s, tokens, dim, vocab, x,
+  launch(k_embed, dim3(rows), dim3(256), 0, S(stream), emb_q, emb_s, tokens, dim, vocab, x,
                      (long long)dim, (unsigned long long*)nullptr, 0, status);
   return launched();
 }
@@ -470,7 +474,7 @@ int t2r_rmsnorm(const float* x, const float* g, int rows, int n, float eps, int 
   if (!x || !g || !out) return T2R_EINVAL;
   if (rows <= 0 || n <= 0 || n > kMaxK || (D != 8 && D != 16)) return T2R_ESHAPE;
   T2R_INIT();
-  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, S(stream), x, g, n, (float)(1.0 / n), eps, D, out);
+  launch(k_rmsnorm, dim3(rows), dim3(256), 0, S(stream), x, g, n, (float)(1.0 / n), eps, D, out);
   return launched();
 }
 
@@ -480,7 +484,7 @@ int t2r_quant_act(const float* x, int rows, int n, int8_t* xq, float* s_x, void*
   T2R_INIT();
   GemvArgs a = gemv_args();
   a.x = x; a.x_stride = n; a.K = n; a.xq_out = xq; a.xq_stride = n; a.sx_out = s_x;
-  hipLaunchKernelGGL(k_rows_norm_quant, dim3(rows), dim3(kGemvThreads), 0, S(stream), a, 0, (float*)nullptr, 0LL);
+  launch(k_rows_norm_quant, dim3(rows), dim3(kGemvThreads), 0, S(stream), a, 0, (float*)nullptr, 0LL);
   return launched();
 }
 
@@ -520,7 +524,7 @@ int t2r_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* po
   if (!v || !cos_t || !sin_t || !pos) return T2R_EINVAL;
   if (rows <= 0 || n <= 0 || half <= 0 || n % (2 * half) || S_ <= 0) return T2R_ESHAPE;
   T2R_INIT();
-  hipLaunchKernelGGL(k_rope, dim3(rows), dim3(256), 0, S(stream), v, cos_t, sin_t, pos, n, half, S_);
+  launch(k_rope, dim3(rows), dim3(256), 0, S(stream), v, cos_t, sin_t, pos, n, half, S_);
   return launched();
 }
 
@@ -529,7 +533,7 @@ int t2r_kv_append(const float* k, const float* v, float inv_sk, float inv_sv, in
   if (!k || !v || !kc || !vc || !pos) return T2R_EINVAL;
   if (rows <= 0 || kv_dim <= 0 || S_ <= 0) return T2R_ESHAPE;
   T2R_INIT();
-  hipLaunchKernelGGL(k_kv_append, dim3(rows), dim3(256), 0, S(stream), k, v, inv_sk, inv_sv, kc, vc, pos, kv_dim, S_);
+  launch(k_kv_append, dim3(rows), dim3(256), 0, S(stream), k, v, inv_sk, inv_sv, kc, vc, pos, kv_dim, S_);
   return launched();
 }
 
@@ -564,7 +568,7 @@ int t2r_moe_route(const float* scores, int rows, int E, int k, int D, int32_t* i
   if (!scores || !ids || !weights) return T2R_EINVAL;
   if (rows <= 0 || E <= 0 || E > 64 || k < 1 || k > 8 || k > E || (D != 8 && D != 16)) return T2R_ESHAPE;
   T2R_INIT();
-  hipLaunchKernelGGL(k_route_scores, dim3(rows), dim3(64), 0, S(stream), scores, E, k, D, ids, weights);
+  launch(k_route_scores, dim3(rows), dim3(64), 0, S(stream), scores, E, k, D, ids, weights);
   return launched();
 }
 
@@ -572,7 +576,7 @@ int t2r_argmax(const float* x, int rows, int n, int32_t* idx, void* stream) {
   if (!x || !idx) return T2R_EINVAL;
   if (rows <= 0 || n <= 0) return T2R_ESHAPE;
   T2R_INIT();
-  hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(256), 0, S(stream), x, n, idx);
+  launch(k_argmax, dim3(rows), dim3(256), 0, S(stream), x, n, idx);
   return launched();
 }
 
@@ -653,7 +657,7 @@ int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logi
   int rc;
   {
     ProfScope p(m, T2R_PROF_OTHER, st);
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, d.emb_q, d.emb_s, token, d.dim, d.vocab, m->x,
+    launch(k_embed, dim3(1), dim3(256), 0, st, d.emb_q, d.emb_s, token, d.dim, d.vocab, m->x,
                        (long long)d.dim, m->keys, 1, m->status);
     rc = launched();
   }
@@ -671,7 +675,7 @@ int t2r_prefill(void* model, const int32_t* tokens, const int32_t* positions, in
   T2R_INIT();
   hipStream_t st = S(stream);
   const t2r_model_desc& d = m->d;
-  hipLaunchKernelGGL(k_embed, dim3(M), dim3(256), 0, st, d.emb_q, d.emb_s, tokens, d.dim, d.vocab, m->x,
+  launch(k_embed, dim3(M), dim3(256), 0, st, d.emb_q, d.emb_s, tokens, d.dim, d.vocab, m->x,
                      (long long)d.dim, m->keys, 1, m->status);
   int rc = launched();
   if (rc) return rc;

@@ -12,12 +12,32 @@
 //    is a signed zero. fadd_ftz / fmul_ftz / ldexp_ftz give that rule on top of the
 //    IEEE instructions (see each for why the fix-up is exact).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #define T2R_DEV __device__ __forceinline__
 
 namespace t2r {
+
+// Kernel timing: while a profiling scope of the model is open, launches go through
+// hipExtLaunchKernelGGL with events recorded at the kernel's own start (the scope's first launch)
+// and end (every launch; the last one stands), so the measured time excludes dispatch latency.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+inline thread_local LaunchEvents g_launch_events;
+
+template <typename K, typename... A>
+void launch(K kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t st, A... args) {
+  LaunchEvents& e = g_launch_events;
+  if (e.stop != nullptr) {
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)shmem, st, e.start, e.stop, 0, args...);
+    e.start = nullptr;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shmem, st, args...);
+  }
+}
 
 constexpr uint32_t kQNaN = 0x7FC00000u;
 constexpr uint32_t kPInf = 0x7F800000u;

@@ -30,9 +30,9 @@ int gemv_launch_ncb(const GemvArgs& a, int rows, hipStream_t st) {
   int blocks = cdiv_i(waves, kGemvThreads / 64);
   if (blocks > 2048) blocks = 2048;
   dim3 grid(blocks, rows), block(kGemvThreads);
-  if (ru == 1) hipLaunchKernelGGL((k_gemv<PRO, EPI, NCB, 1>), grid, block, 0, st, a);
-  else if (ru == 2) hipLaunchKernelGGL((k_gemv<PRO, EPI, NCB, (RUMAX >= 2 ? 2 : 1)>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((k_gemv<PRO, EPI, NCB, RUMAX>), grid, block, 0, st, a);
+  if (ru == 1) launch((k_gemv<PRO, EPI, NCB, 1>), grid, block, 0, st, a);
+  else if (ru == 2) launch((k_gemv<PRO, EPI, NCB, (RUMAX >= 2 ? 2 : 1)>), grid, block, 0, st, a);
+  else launch((k_gemv<PRO, EPI, NCB, RUMAX>), grid, block, 0, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
@@ -205,9 +205,9 @@ int gemm_launch(const GemmArgs& a, hipStream_t st) {
   const long long nb = blocks(64 * wm, 64 * wn);
   if (nb > 0x7FFFFFFF) return -2;
   dim3 grid((unsigned)nb), block(64 * wm * wn);
-  if (wm == 2) hipLaunchKernelGGL((k_gemm<EPI, 2, 2>), grid, block, 0, st, a);
-  else if (wn == 2) hipLaunchKernelGGL((k_gemm<EPI, 1, 2>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((k_gemm<EPI, 1, 1>), grid, block, 0, st, a);
+  if (wm == 2) launch((k_gemm<EPI, 2, 2>), grid, block, 0, st, a);
+  else if (wn == 2) launch((k_gemm<EPI, 1, 2>), grid, block, 0, st, a);
+  else launch((k_gemm<EPI, 1, 1>), grid, block, 0, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
