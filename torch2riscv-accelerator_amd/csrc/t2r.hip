@@ -26,6 +26,7 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_init_mu;
 bool g_inited[kMaxDevices];
+const float* g_sfu_addr[kMaxDevices];
 
 // The SFU tables (llm/sfu.py:42-56): segment start T and slope S of each function, computed in
 // double and rounded once to float.
@@ -57,6 +58,9 @@ int ensure_init() {
   float t[kSfuWords];
   sfu_host_tables(t);
   if (hipMemcpyToSymbol(HIP_SYMBOL(c_sfu), t, sizeof(t), 0, hipMemcpyHostToDevice) != hipSuccess) return T2R_EHIP;
+  void* addr = nullptr;
+  if (hipGetSymbolAddress(&addr, HIP_SYMBOL(c_sfu)) != hipSuccess || addr == nullptr) return T2R_EHIP;
+  g_sfu_addr[dev] = (const float*)addr;
   g_inited[dev] = true;
   return T2R_OK;
 }
@@ -71,10 +75,20 @@ inline int launched() { return hipGetLastError() == hipSuccess ? T2R_OK : T2R_EH
 inline hipStream_t S(void* s) { return (hipStream_t)s; }
 inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
 
+// The device address of this device's SFU tables: kernels that stage them into LDS read them
+// through this plain pointer (a load from the __constant__ symbol itself may be moved by the
+// compiler to its first use, behind the weight loads).
+const float* sfu_table_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  return g_sfu_addr[dev];
+}
+
 GemvArgs gemv_args() {
   GemvArgs a;
   std::memset(&a, 0, sizeof(a));
   a.D = 16;
+  a.tab = sfu_table_ptr();
   return a;
 }
 

@@ -44,9 +44,23 @@ constexpr uint32_t kPInf = 0x7F800000u;
 constexpr float kInv127 = (float)(1.0 / 127.0);      // F(1/127): double quotient rounded once
 
 // SFU tables in constant memory: [exp T | exp S | recip T | recip S | rsqrt T(128) | rsqrt S(128)].
+// Kernels whose SFU calls sit on a latency chain copy them into LDS at start (sfu_stage) and pass
+// the LDS copy: a lookup is then an LDS read instead of a dependent global load.
 constexpr int kSfuExpT = 0, kSfuExpS = 64, kSfuRecT = 128, kSfuRecS = 192, kSfuRsqT = 256, kSfuRsqS = 384;
 constexpr int kSfuWords = 512;
 extern __constant__ float c_sfu[kSfuWords];
+
+// The first kSfuWords / 4 threads of a block each fetch 4 table words into a register (issue this
+// with the block's first loads) and later store them (sfu_store, before a barrier that precedes the
+// first lookup).
+T2R_DEV float4 sfu_fetch() {
+  const int t = threadIdx.x;
+  return t < kSfuWords / 4 ? ((const float4*)c_sfu)[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+T2R_DEV void sfu_store(float* lds, float4 v) {
+  const int t = threadIdx.x;
+  if (t < kSfuWords / 4) ((float4*)lds)[t] = v;
+}
 
 T2R_DEV uint32_t fb(float x) { return __float_as_uint(x); }
 T2R_DEV float fv(uint32_t b) { return __uint_as_float(b); }
@@ -69,43 +83,38 @@ T2R_DEV float fadd_ftz(float a, float b) { return ftz(a + b); }
 // spacing. Only a result of exactly 2^-126 is ambiguous: recompute it scaled by 2^128
 // (both factors are then below 2 in magnitude, so nothing overflows) and compare.
 T2R_DEV float fmul_ftz(float a, float b) {
-  float r = a * b;
-  uint32_t m = fb(r) & 0x7FFFFFFFu;
-  if (m < 0x00800000u) return fv(fb(r) & 0x80000000u);
-  if (m == 0x00800000u) {
-    float r2 = (a * 0x1p64f) * (b * 0x1p64f);
-    if (fabsf(r2) < 4.0f) return fv(fb(r) & 0x80000000u);
-  }
-  return r;
+  const float r = a * b;
+  const uint32_t rb = fb(r), m = rb & 0x7FFFFFFFu;
+  const float r2 = (a * 0x1p64f) * (b * 0x1p64f);     // only looked at when |r| == 2^-126
+  const bool zero = m < 0x00800000u || (m == 0x00800000u && fabsf(r2) < 4.0f);
+  return zero ? fv(rb & 0x80000000u) : r;
 }
 
 // a * 2^n as an exponent-field add (llm/fp32.py:147-151): below the normal range a signed
 // zero, above it a signed inf; zero and inf pass through, NaN gives the canonical NaN.
+// (Straight-line selects, lowest precedence first: the SFU sequences run on latency chains.)
 T2R_DEV float ldexp_ftz(float a, int n) {
-  uint32_t b = fb(a), e = (b >> 23) & 0xFFu;
-  if (e == 0) return fv(b & 0x80000000u);
-  if (e == 255) return (b & 0x7FFFFFu) ? fv(kQNaN) : a;
-  int e2 = (int)e + n;
-  if (e2 < 1) return fv(b & 0x80000000u);
-  if (e2 > 254) return fv((b & 0x80000000u) | kPInf);
-  return fv((b & 0x807FFFFFu) | ((uint32_t)e2 << 23));
+  const uint32_t b = fb(a), e = (b >> 23) & 0xFFu, sg = b & 0x80000000u;
+  const int e2 = (int)e + n;
+  uint32_t r = (b & 0x807FFFFFu) | ((uint32_t)e2 << 23);
+  r = e2 < 1 ? sg : r;
+  r = e2 > 254 ? (sg | kPInf) : r;
+  r = e == 0 ? sg : r;
+  r = e == 255 ? ((b & 0x7FFFFFu) ? kQNaN : b) : r;
+  return fv(r);
 }
 
 // floor, saturated to int32, NaN -> 0 (llm/fp32.py:169-189, mode "floor")
 T2R_DEV int floor_sat(float t) {
-  if (t != t) return 0;
-  float f = floorf(t);
-  if (f >= 2147483648.0f) return 2147483647;
-  if (f < -2147483648.0f) return (int)0x80000000;
-  return (int)f;
+  const float f = floorf(t);
+  int r = (int)fminf(fmaxf(f, -2147483648.0f), 2147483520.0f);   // in range: defined conversion
+  r = f >= 2147483648.0f ? 2147483647 : r;
+  return t != t ? 0 : r;
 }
 
 // EXP (llm/sfu.py:7-11, 69-82)
-T2R_DEV float sfu_exp(float xin) {
+T2R_DEV float sfu_exp(float xin, const float* tab = c_sfu) {
   const float x = ftz(xin);
-  if (x != x) return fv(kQNaN);
-  if (x >= 89.0f) return fv(kPInf);
-  if (x <= -104.0f) return 0.0f;
   const float t = fmul_ftz(x, (float)1.4426950408889634);
   const int n = floor_sat(t);
   const float f = fadd_ftz(t, -(float)n);
@@ -113,40 +122,44 @@ T2R_DEV float sfu_exp(float xin) {
   int i = floor_sat(u);
   i = i < 0 ? 0 : (i > 63 ? 63 : i);
   const float r = fadd_ftz(u, -(float)i);
-  const float y = fadd_ftz(c_sfu[kSfuExpT + i], fmul_ftz(r, c_sfu[kSfuExpS + i]));
-  return ldexp_ftz(y, n < -300 ? -300 : (n > 300 ? 300 : n));
+  const float y = fadd_ftz(tab[kSfuExpT + i], fmul_ftz(r, tab[kSfuExpS + i]));
+  float out = ldexp_ftz(y, n < -300 ? -300 : (n > 300 ? 300 : n));
+  out = x <= -104.0f ? 0.0f : out;
+  out = x >= 89.0f ? fv(kPInf) : out;
+  return x != x ? fv(kQNaN) : out;
 }
 
 // (frac & 0x1FFFF) / 2^17, exact
 T2R_DEV float frac17(uint32_t frac) { return ldexp_ftz((float)(int)(frac & 0x1FFFFu), -17); }
 
 // RECIP (llm/sfu.py:12-15, 85-96)
-T2R_DEV float sfu_recip(float xin) {
+T2R_DEV float sfu_recip(float xin, const float* tab = c_sfu) {
   const uint32_t b = fb(ftz(xin));
   const uint32_t s = b & 0x80000000u, e = (b >> 23) & 0xFFu, frac = b & 0x7FFFFFu;
-  if (e == 0) return fv(s | kPInf);
-  if (e == 255) return frac ? fv(kQNaN) : fv(s);
   const int i = (int)(frac >> 17);
   const float m = fv(frac | 0x3F800000u);
-  const float y0 = fadd_ftz(c_sfu[kSfuRecT + i], fmul_ftz(frac17(frac), c_sfu[kSfuRecS + i]));
+  const float y0 = fadd_ftz(tab[kSfuRecT + i], fmul_ftz(frac17(frac), tab[kSfuRecS + i]));
   const float y1 = fmul_ftz(y0, fadd_ftz(2.0f, -fmul_ftz(m, y0)));
-  return fv(fb(ldexp_ftz(y1, 127 - (int)e)) | s);
+  uint32_t r = fb(ldexp_ftz(y1, 127 - (int)e)) | s;
+  r = e == 255 ? (frac ? kQNaN : s) : r;
+  r = e == 0 ? (s | kPInf) : r;
+  return fv(r);
 }
 
 // RSQRT (llm/sfu.py:16-20, 99-114)
-T2R_DEV float sfu_rsqrt(float xin) {
+T2R_DEV float sfu_rsqrt(float xin, const float* tab = c_sfu) {
   const uint32_t b = fb(ftz(xin));
   const uint32_t s = b >> 31, e = (b >> 23) & 0xFFu, frac = b & 0x7FFFFFu;
-  if (e == 255 && frac) return fv(kQNaN);
-  if (e == 0) return fv(kPInf);
-  if (s) return fv(kQNaN);
-  if (e == 255) return 0.0f;
   const int E = (int)e - 127, odd = E & 1;
   const int j = odd * 64 + (int)(frac >> 17);
   const float m2 = fv(frac | ((uint32_t)(127 + odd) << 23));
-  const float y0 = fadd_ftz(c_sfu[kSfuRsqT + j], fmul_ftz(frac17(frac), c_sfu[kSfuRsqS + j]));
+  const float y0 = fadd_ftz(tab[kSfuRsqT + j], fmul_ftz(frac17(frac), tab[kSfuRsqS + j]));
   const float d = fadd_ftz(1.5f, -fmul_ftz(fmul_ftz(m2, fmul_ftz(y0, y0)), 0.5f));
-  return ldexp_ftz(fmul_ftz(y0, d), -((E - odd) / 2));
+  float r = ldexp_ftz(fmul_ftz(y0, d), -((E - odd) / 2));
+  r = e == 255 ? 0.0f : r;
+  r = s ? fv(kQNaN) : r;
+  r = e == 0 ? fv(kPInf) : r;
+  return (e == 255 && frac) ? fv(kQNaN) : r;
 }
 
 // fp32 -> int8: round half to even, saturate to +-127, NaN -> 0 (llm/ref_model.py:136-139)
@@ -172,8 +185,8 @@ T2R_DEV float dequant(int acc, float s_w, float s_x) {
 }
 
 // SiLU gate: F(F(h1 * recip(F(1 + exp(F(h1 * -1))))) * h3) (llm/ref_model.py:249-250)
-T2R_DEV float silu_mul(float h1, float h3) {
-  float sig = sfu_recip(1.0f + sfu_exp(h1 * -1.0f));
+T2R_DEV float silu_mul(float h1, float h3, const float* tab = c_sfu) {
+  float sig = sfu_recip(1.0f + sfu_exp(h1 * -1.0f, tab), tab);
   float a = h1 * sig;
   return a * h3;
 }
@@ -208,15 +221,48 @@ T2R_DEV int pack_i8x4(int a, int b, int c, int d) {
 
 // ------------------------------------------------------------------ block-level helpers
 // Wave-wide reductions over 64 lanes. Integer sums and maxima are order-free, so any tree works.
+// DPP moves within 16-lane rows (no LDS round trip): xor 1 and xor 2 (quad permutes), then the
+// half-row and row mirrors pair groups that already agree, so after the four steps every lane
+// holds its row's result; the four rows are combined from lanes 0, 16, 32, 48.
+template <int CTRL>
+T2R_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+T2R_DEV float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+// every lane returns the sum over the wave (all 64 lanes active)
 T2R_DEV int wave_sum_i32(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v += dpp_i<kDppXor1>(v);
+  v += dpp_i<kDppXor2>(v);
+  v += dpp_i<kDppHalfMirror>(v);
+  v += dpp_i<kDppMirror>(v);
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 T2R_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = nanmax(v, __shfl_xor(v, o));
-  return v;
+  v = nanmax(v, dpp_f<kDppXor1>(v));
+  v = nanmax(v, dpp_f<kDppXor2>(v));
+  v = nanmax(v, dpp_f<kDppHalfMirror>(v));
+  v = nanmax(v, dpp_f<kDppMirror>(v));
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return nanmax(nanmax(a, b), nanmax(c, d));
+}
+
+// The pairwise tree of the ordered sum over lanes [0, D) of a row (D <= 16 a power of two):
+// lane l, l % 2s == 0, adds lane l + s; returns lane 0's total to every lane that calls it.
+T2R_DEV float lane_tree_sum(float acc, int D, int l) {
+  float o = dpp_f<0x101>(acc);                                  // row_shl:1
+  if (D > 1 && (l & 1) == 0) acc = acc + o;
+  o = dpp_f<0x102>(acc);
+  if (D > 2 && (l & 3) == 0) acc = acc + o;
+  o = dpp_f<0x104>(acc);
+  if (D > 4 && (l & 7) == 0) acc = acc + o;
+  o = dpp_f<0x108>(acc);
+  if (D > 8 && (l & 15) == 0) acc = acc + o;
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
 }
 
 // max over the block (NaN-propagating); every thread gets the result. `red` holds >= 16 floats.
@@ -233,77 +279,87 @@ T2R_DEV float block_max(float v, float* red) {
 
 // The device's ordered sum of vals[0..n) (llm/ref_model.py:179-186): +0 padding to a multiple
 // of D, lane l adds vals[l], vals[D + l], vals[2D + l], ... in order, then lanes pair up
-// (0+1, 2+3, ...) until one value is left. Run by the D lanes [lane0, lane0 + D) of one wave,
-// vals readable by them (LDS); returns the sum on every one of those lanes. `sq`: sum the
-// squares F(v * v) instead (RMSNorm).
+// (0+1, 2+3, ...) until one value is left. Run by lanes [0, D) of one wave, vals readable by them
+// (LDS); returns the sum on every one of those lanes. `sq`: sum the squares F(v * v) instead
+// (RMSNorm). A lane's chain starts from its first value (no +0 in front).
 template <bool SQ>
 T2R_DEV float ordered_sum(const float* vals, int n, int D, int l) {
-  float acc = 0.0f;
   const int groups = n > 0 ? (n + D - 1) / D : 1;
-  int g = 0;
+  auto val = [&](int g) {
+    const int i = g * D + l;
+    float v = i < n ? vals[i] : 0.0f;
+    return SQ ? v * v : v;
+  };
+  float acc = val(0);
+  int g = 1;
   // 8 groups at a time: the loads are independent, the adds stay one chain in group order
   for (; g + 8 <= groups; g += 8) {
     float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = (g + j) * D + l;
-      v[j] = i < n ? vals[i] : 0.0f;
-      if (SQ) v[j] = v[j] * v[j];
-    }
+    for (int j = 0; j < 8; ++j) v[j] = val(g + j);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc = (g + j == 0) ? v[j] : acc + v[j];
+    for (int j = 0; j < 8; ++j) acc = acc + v[j];
   }
-  for (; g < groups; ++g) {
-    const int i = g * D + l;
-    float v = i < n ? vals[i] : 0.0f;
-    if (SQ) v = v * v;
-    acc = g == 0 ? v : acc + v;
-  }
-  // pairwise tree over the D lanes: lane l (a multiple of 2s) takes lane l + s
-  for (int s = 1; s < D; s <<= 1) {
-    float o = __shfl_down(acc, s, D);
-    if ((l & (2 * s - 1)) == 0) acc = acc + o;
-  }
-  return __shfl(acc, 0, D);
+  for (; g < groups; ++g) acc = acc + val(g);
+  return lane_tree_sum(acc, D, l);
 }
 
-// The same ordered sum over a buffer in the "lane-major" layout: value i (lane i % D, group i / D)
-// is at osum_index(i) = (i % D) * P + i / D, with P = osum_stride(n, D) >= the group count, a
-// multiple of 4 (16-byte aligned runs). Lane l's chain is then contiguous: its values are read
-// 16 at a time with 128-bit loads, so the loads stay off the chain of adds. The writer stores +0
-// at the padding positions i in [n, groups * D).
+// The same sum over a lane-major copy: value i is at osum_index(i) = (i % D) * P + i / D, with
+// P = osum_stride(n, D) >= the group count, a multiple of 4 (16-byte aligned runs). Lane l's
+// chain is then contiguous: its values are read 16 at a time with 128-bit loads, the next 16
+// requested before the current 16 are added, so the loads stay off the chain of adds. The writer
+// stores +0 at the padding positions i in [n, groups * D).
 __host__ __device__ inline int osum_stride(int n, int D) {
   const int G = n > 0 ? (n + D - 1) / D : 1;
   return ((G + 3) & ~3) + 4;
 }
-__host__ __device__ inline int osum_index(int i, int D, int P) { return (i & (D - 1)) * P + i / D; }
+__host__ __device__ inline int osum_index(int i, int D, int P) {
+  return (i & (D - 1)) * P + (i >> __builtin_ctz((unsigned)D));   // D a power of two
+}
 
 template <bool SQ>
 T2R_DEV float ordered_sum_t(const float* buf, int n, int D, int P, int l) {
   const int G = n > 0 ? (n + D - 1) / D : 1;
   const float* row = buf + l * P;
-  float acc = 0.0f;
-  int g = 0;
-  for (; g + 16 <= G; g += 16) {
-    const float4 a = *(const float4*)(row + g), b = *(const float4*)(row + g + 4);
-    const float4 c = *(const float4*)(row + g + 8), d = *(const float4*)(row + g + 12);
-    float v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+  float acc;
+  int g;
+  if (G >= 16) {
+    float4 c0 = *(const float4*)(row), c1 = *(const float4*)(row + 4);
+    float4 c2 = *(const float4*)(row + 8), c3 = *(const float4*)(row + 12);
+    for (g = 0; g + 16 <= G; g += 16) {
+      const bool more = g + 32 <= G;
+      float4 n0 = c0, n1 = c1, n2 = c2, n3 = c3;
+      if (more) {
+        n0 = *(const float4*)(row + g + 16);
+        n1 = *(const float4*)(row + g + 20);
+        n2 = *(const float4*)(row + g + 24);
+        n3 = *(const float4*)(row + g + 28);
+      }
+      float v[16] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w, c2.x, c2.y, c2.z, c2.w, c3.x, c3.y, c3.z, c3.w};
+      if (SQ) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (SQ) v[j] = v[j] * v[j];
-      acc = (g + j == 0) ? v[j] : acc + v[j];
+        for (int j = 0; j < 16; ++j) v[j] = v[j] * v[j];
+      }
+      if (g == 0) {
+        acc = v[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) acc = acc + v[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc = acc + v[j];
+      }
+      c0 = n0; c1 = n1; c2 = n2; c3 = n3;
     }
+  } else {
+    acc = SQ ? row[0] * row[0] : row[0];
+    g = 1;
   }
   for (; g < G; ++g) {
     float v = row[g];
     if (SQ) v = v * v;
-    acc = g == 0 ? v : acc + v;
+    acc = acc + v;
   }
-  for (int s = 1; s < D; s <<= 1) {
-    float o = __shfl_down(acc, s, D);
-    if ((l & (2 * s - 1)) == 0) acc = acc + o;
-  }
-  return __shfl(acc, 0, D);
+  return lane_tree_sum(acc, D, l);
 }
 
 }  // namespace t2r

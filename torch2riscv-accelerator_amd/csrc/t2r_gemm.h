@@ -19,31 +19,78 @@ namespace t2r {
 __host__ __device__ inline int cdiv_i(long long a, long long b) { return (int)((a + b - 1) / b); }
 
 // ------------------------------------------------------------------ GEMV launcher (decode, op level)
-// The GEMV over `rows` activation rows (grid y): register-slice width NCB by K, rows per wave RU
-// by N (enough waves to fill the 256 CUs, up to 8 per CU).
+// The GEMV over `rows` activation rows (grid y) with register-slice width NCB (by K), RU rows per
+// wave and NT threads per block. Every block repeats the prologue over the whole input, so fewer,
+// larger blocks (one 512-thread block per CU when the waves of one tile each cover N) repeat it
+// less; RU grows while there are at least 2048 waves' worth of rows.
+template <int NCB>
+constexpr int gemv_rumax() { return NCB <= 2 ? 4 : (NCB == 4 ? 2 : 1); }
+
+struct GemvShape {
+  int ru, nt, blocks;
+};
+
+template <int NCB>
+inline GemvShape gemv_shape(int N) {
+  GemvShape g;
+  g.ru = 1;
+  while (g.ru < gemv_rumax<NCB>() && (long long)N / (2 * g.ru) >= 2048) g.ru *= 2;
+  const int waves = cdiv_i(N, g.ru);
+  g.nt = cdiv_i(waves, 8) >= 128 ? 512 : 256;
+  g.blocks = cdiv_i(waves, g.nt / 64);
+  const int cap = 2048 * 256 / g.nt;
+  if (g.blocks > cap) g.blocks = cap;
+  return g;
+}
+
+template <int PRO, int EPI, int NCB, int NT, bool IDX>
+void gemv_launch_nt(const GemvArgs& a, int rows, int ru, int blocks, hipStream_t st) {
+  constexpr int RUMAX = gemv_rumax<NCB>();
+  dim3 grid(blocks, rows), block(NT);
+  if (ru == 1) launch((k_gemv<PRO, EPI, NCB, 1, NT, IDX>), grid, block, 0, st, a);
+  else if (ru == 2) launch((k_gemv<PRO, EPI, NCB, (RUMAX >= 2 ? 2 : 1), NT, IDX>), grid, block, 0, st, a);
+  else launch((k_gemv<PRO, EPI, NCB, RUMAX, NT, IDX>), grid, block, 0, st, a);
+}
+
+// MoE id indirection (a.ids) exists for the expert gate / up GEMV only (int8 input, SwiGLU).
 template <int PRO, int EPI, int NCB>
-int gemv_launch_ncb(const GemvArgs& a, int rows, hipStream_t st) {
-  constexpr int RUMAX = NCB <= 2 ? 4 : (NCB == 4 ? 2 : 1);
-  int ru = 1;
-  while (ru < RUMAX && (long long)a.N / (2 * ru) >= 2048) ru *= 2;
-  const int waves = cdiv_i(a.N, ru);
-  int blocks = cdiv_i(waves, kGemvThreads / 64);
-  if (blocks > 2048) blocks = 2048;
-  dim3 grid(blocks, rows), block(kGemvThreads);
-  if (ru == 1) launch((k_gemv<PRO, EPI, NCB, 1>), grid, block, 0, st, a);
-  else if (ru == 2) launch((k_gemv<PRO, EPI, NCB, (RUMAX >= 2 ? 2 : 1)>), grid, block, 0, st, a);
-  else launch((k_gemv<PRO, EPI, NCB, RUMAX>), grid, block, 0, st, a);
+int gemv_launch_shape(const GemvArgs& a, int rows, GemvShape g, hipStream_t st) {
+  if (g.ru < 1 || g.ru > gemv_rumax<NCB>() || (g.ru & (g.ru - 1)) || g.blocks < 1) return -2;
+  if (g.nt != 256 && g.nt != 512) return -2;
+  if (a.ids != nullptr) {
+    if constexpr (PRO == PRO_XQ && EPI == EPI_SWIGLU) {
+      if (a.rows_per_id <= 0 || a.N % a.rows_per_id) return -2;
+      if (g.nt == 512) gemv_launch_nt<PRO, EPI, NCB, 512, true>(a, rows, g.ru, g.blocks, st);
+      else gemv_launch_nt<PRO, EPI, NCB, 256, true>(a, rows, g.ru, g.blocks, st);
+    } else {
+      return -2;
+    }
+  } else if (g.nt == 512) {
+    gemv_launch_nt<PRO, EPI, NCB, 512, false>(a, rows, g.ru, g.blocks, st);
+  } else {
+    gemv_launch_nt<PRO, EPI, NCB, 256, false>(a, rows, g.ru, g.blocks, st);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// Operand checks: the staged loads read the activations (and the SFU tables) 16 bytes at a time.
+template <int PRO, int EPI>
+inline bool gemv_operands_ok(const GemvArgs& a) {
+  if ((PRO != PRO_XQ || EPI == EPI_SWIGLU) && (a.tab == nullptr || ((uintptr_t)a.tab & 15))) return false;
+  if (PRO == PRO_XQ) return ((uintptr_t)a.xq & 15) == 0 && a.xq_stride % 16 == 0;
+  if (((uintptr_t)a.x & 15) || a.x_stride % 4) return false;
+  return PRO != PRO_NORM_QUANT || ((uintptr_t)a.g & 15) == 0;
 }
 
 template <int PRO, int EPI>
 int gemv_launch(const GemvArgs& a, int rows, hipStream_t st) {
   if (a.K <= 0 || a.K % 16 || a.K > kMaxK || a.N <= 0 || rows <= 0) return -2;
+  if (!gemv_operands_ok<PRO, EPI>(a)) return -2;
   const int nc = cdiv_i(a.K, 1024);
-  if (nc <= 1) return gemv_launch_ncb<PRO, EPI, 1>(a, rows, st);
-  if (nc <= 2) return gemv_launch_ncb<PRO, EPI, 2>(a, rows, st);
-  if (nc <= 4) return gemv_launch_ncb<PRO, EPI, 4>(a, rows, st);
-  return gemv_launch_ncb<PRO, EPI, 8>(a, rows, st);
+  if (nc <= 1) return gemv_launch_shape<PRO, EPI, 1>(a, rows, gemv_shape<1>(a.N), st);
+  if (nc <= 2) return gemv_launch_shape<PRO, EPI, 2>(a, rows, gemv_shape<2>(a.N), st);
+  if (nc <= 4) return gemv_launch_shape<PRO, EPI, 4>(a, rows, gemv_shape<4>(a.N), st);
+  return gemv_launch_shape<PRO, EPI, 8>(a, rows, gemv_shape<8>(a.N), st);
 }
 
 // ------------------------------------------------------------------ MFMA GEMM

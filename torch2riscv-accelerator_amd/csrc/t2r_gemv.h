@@ -50,6 +50,7 @@ struct GemvArgs {
   const int32_t* ids;        // optional row indirection (MoE experts): output row r reads weight row
   int rows_per_id;           //   ids[row * ids_stride + r / rows_per_id] * rows_per_id + r % rows_per_id
   int ids_stride;
+  const float* tab;          // the SFU tables (kSfuWords floats, 16-byte aligned) in device memory
 };
 
 T2R_DEV long long weight_row(const GemvArgs& a, int row_in, int row) {
@@ -125,130 +126,165 @@ struct WTile {
   float sw[RU], sw3[EPI == EPI_SWIGLU ? RU : 1], res[EPI == EPI_RESID ? RU : 1];
 };
 
-template <int EPI, int NCB, int RU>
+// Branch-free: every lane issues every load. A row past N reads row N - 1 (its result is never
+// stored) and a column past K reads the row's last 16 bytes (the activations there are +0, so the
+// products vanish). Loads under branches would cost more than the wasted bytes: the compiler
+// could no longer count them, and would wait for all of them before the prologue's first use of
+// its own (earlier) loads. IDX: weight rows through the MoE id table, looked up first.
+template <int EPI, int NCB, int RU, bool IDX>
 T2R_DEV void load_tile(WTile<EPI, NCB, RU>& t, const GemvArgs& a, const float* res, int row_in, int r0, int lane) {
+  long long wr[RU];
+  int rc[RU];
 #pragma unroll
   for (int u = 0; u < RU; ++u) {
-    const int row = r0 + u;
-    const bool rok = row < a.N;
-    const long long wr = rok ? weight_row(a, row_in, row) : 0;
+    rc[u] = min(r0 + u, a.N - 1);
+    wr[u] = IDX ? weight_row(a, row_in, rc[u]) : rc[u];
+  }
+#pragma unroll
+  for (int u = 0; u < RU; ++u) {
 #pragma unroll
     for (int c = 0; c < NCB; ++c) {
-      const int col = lane * 16 + c * 1024;
-      const bool ok = rok && col < a.K;
-      t.w[u][c] = ok ? load_nt16(a.w + wr * a.K + col) : make_int4(0, 0, 0, 0);
-      if (EPI == EPI_SWIGLU) t.w3[u][c] = ok ? load_nt16(a.w3 + wr * a.K + col) : make_int4(0, 0, 0, 0);
+      const int col = min(lane * 16 + c * 1024, a.K - 16);
+      t.w[u][c] = load_nt16(a.w + wr[u] * a.K + col);
+      if (EPI == EPI_SWIGLU) t.w3[u][c] = load_nt16(a.w3 + wr[u] * a.K + col);
     }
-    t.sw[u] = rok ? a.s_w[wr] : 0.0f;
-    if (EPI == EPI_SWIGLU) t.sw3[u] = rok ? a.s_w3[wr] : 0.0f;
-    if (EPI == EPI_RESID) t.res[u] = rok ? res[row] : 0.0f;
+    t.sw[u] = a.s_w[wr[u]];
+    if (EPI == EPI_SWIGLU) t.sw3[u] = a.s_w3[wr[u]];
+    if (EPI == EPI_RESID) t.res[u] = res[rc[u]];
   }
 }
 
 // The prologue's inputs, loaded into registers before the first weight tile is requested (the
-// wait for them then does not wait for the tile): K <= 1024 * NCB, so a thread holds at most
-// 4 * NCB of the K values (and 2 int4 of int8 activations).
-template <int PRO, int NCB>
+// wait for them then does not wait for the tile): K <= 1024 * NCB. NORM/QUANT inputs are read as
+// float4 (thread t holds elements 4 (t + NT j) .. + 3), int8 inputs as int4; the SFU tables travel
+// with them when the kernel looks anything up.
+template <int PRO, int EPI, int NCB, int NT>
 struct XStage {
-  static constexpr int NX = 4 * NCB;
-  float x[PRO == PRO_XQ ? 1 : NX];
-  float g[PRO == PRO_NORM_QUANT ? NX : 1];
-  int4 q[PRO == PRO_XQ ? 2 : 1];
+  static constexpr int NX = (256 * NCB) / NT > 0 ? (256 * NCB) / NT : 1;   // float4 per thread
+  static constexpr int NQ = (64 * NCB) / NT > 0 ? (64 * NCB) / NT : 1;     // int4 per thread
+  static constexpr bool SFU = PRO != PRO_XQ || EPI == EPI_SWIGLU;
+  float4 x[PRO == PRO_XQ ? 1 : NX];
+  float4 g[PRO == PRO_NORM_QUANT ? NX : 1];
+  int4 q[PRO == PRO_XQ ? NQ : 1];
+  float4 tab;
 };
 
-template <int PRO, int NCB>
-T2R_DEV void stage_load(XStage<PRO, NCB>& st, const GemvArgs& a, int row) {
+template <int PRO, int EPI, int NCB, int NT>
+T2R_DEV void stage_load(XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& a, int row) {
+  typedef XStage<PRO, EPI, NCB, NT> S;
   const int tid = threadIdx.x, K = a.K;
+  // unconditional loads at clamped addresses (see load_tile); elements past K are never used
+  if (S::SFU) st.tab = ((const float4*)a.tab)[tid & (kSfuWords / 4 - 1)];
   if (PRO == PRO_XQ) {
     const int8_t* src = a.xq + row * a.xq_stride;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = (tid + j * kGemvThreads) * 16;
-      st.q[j] = i < K ? *(const int4*)(src + i) : make_int4(0, 0, 0, 0);
-    }
+    for (int j = 0; j < S::NQ; ++j) st.q[j] = *(const int4*)(src + min((tid + j * NT) * 16, K - 16));
   } else {
     const float* x = a.x + row * a.x_stride;
 #pragma unroll
-    for (int j = 0; j < XStage<PRO, NCB>::NX; ++j) {
-      const int i = tid + j * kGemvThreads;
-      st.x[j] = i < K ? x[i] : 0.0f;
-      if (PRO == PRO_NORM_QUANT) st.g[j] = i < K ? a.g[i] : 0.0f;
+    for (int j = 0; j < S::NX; ++j) {
+      const int i = min((tid + j * NT) * 4, K - 4);
+      st.x[j] = *(const float4*)(x + i);
+      if (PRO == PRO_NORM_QUANT) st.g[j] = *(const float4*)(a.g + i);
     }
   }
 }
 
-// RMSNorm / quant_act from the staged registers (same numerics as gemv_prologue)
-template <int PRO, int NCB>
-T2R_DEV float stage_finish(const XStage<PRO, NCB>& st, const GemvArgs& a, int row, int8_t* xq_lds, float* xf_lds,
-                           float* red) {
+// RMSNorm / quant_act from the staged registers (same numerics as gemv_prologue); leaves the int8
+// activations in xq_lds and the SFU tables in tab_lds, returns s_x
+template <int PRO, int EPI, int NCB, int NT>
+T2R_DEV float stage_finish(const XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& a, int row, int8_t* xq_lds,
+                           float* xf_lds, float* tab_lds, float* red) {
+  typedef XStage<PRO, EPI, NCB, NT> S;
   const int tid = threadIdx.x, K = a.K;
-  constexpr int NX = XStage<PRO, NCB>::NX;
+  if (S::SFU) sfu_store(tab_lds, st.tab);
   if (PRO == PRO_XQ) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = (tid + j * kGemvThreads) * 16;
+    for (int j = 0; j < S::NQ; ++j) {
+      const int i = (tid + j * NT) * 16;
       if (i < K) *(int4*)(xq_lds + i) = st.q[j];
     }
     __syncthreads();
     return a.s_x[row];
   }
+  constexpr int NV = 4 * S::NX;
+  float xv[NV];
+#pragma unroll
+  for (int j = 0; j < S::NX; ++j) {
+    xv[4 * j] = st.x[j].x; xv[4 * j + 1] = st.x[j].y; xv[4 * j + 2] = st.x[j].z; xv[4 * j + 3] = st.x[j].w;
+  }
   float r = 1.0f;
   if (PRO == PRO_NORM_QUANT) {
-    const int P = osum_stride(K, a.D), pad = ((K + a.D - 1) / a.D) * a.D;
+    // the squares F(x * x), lane-major for the ordered sum (K % D == 0: no padding)
+    const int P = osum_stride(K, a.D);
 #pragma unroll
-    for (int j = 0; j < NX; ++j) {
-      const int i = tid + j * kGemvThreads;
-      if (i < pad) xf_lds[osum_index(i, a.D, P)] = i < K ? st.x[j] : 0.0f;
-    }
+    for (int j = 0; j < S::NX; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = (tid + j * NT) * 4 + e;
+        if (i < K) xf_lds[osum_index(i, a.D, P)] = xv[4 * j + e] * xv[4 * j + e];
+      }
     __syncthreads();
     if (tid < a.D) {
-      const float ss = ordered_sum_t<true>(xf_lds, K, a.D, P, tid);
-      if (tid == 0) red[32] = sfu_rsqrt(ss * a.inv_n + a.eps);
+      const float ss = ordered_sum_t<false>(xf_lds, K, a.D, P, tid);
+      if (tid == 0) red[32] = sfu_rsqrt(ss * a.inv_n + a.eps, tab_lds);
     }
     __syncthreads();
     r = red[32];
+#pragma unroll
+    for (int j = 0; j < S::NX; ++j) {
+      xv[4 * j] = (xv[4 * j] * r) * st.g[j].x;
+      xv[4 * j + 1] = (xv[4 * j + 1] * r) * st.g[j].y;
+      xv[4 * j + 2] = (xv[4 * j + 2] * r) * st.g[j].z;
+      xv[4 * j + 3] = (xv[4 * j + 3] * r) * st.g[j].w;
+    }
   }
-  float v[NX];
   float amax = 0.0f;
 #pragma unroll
-  for (int j = 0; j < NX; ++j) {
-    v[j] = PRO == PRO_NORM_QUANT ? (st.x[j] * r) * st.g[j] : st.x[j];
-    if (tid + j * kGemvThreads < K) amax = nanmax(amax, fabsf(v[j]));
-  }
+  for (int j = 0; j < S::NX; ++j)
+    if ((tid + j * NT) * 4 < K)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) amax = nanmax(amax, fabsf(xv[4 * j + e]));
   amax = block_max(amax, red);
   const float s_x = amax * kInv127;
-  const float inv = sfu_recip(s_x);
+  const float inv = sfu_recip(s_x, tab_lds);
 #pragma unroll
-  for (int j = 0; j < NX; ++j) {
-    const int i = tid + j * kGemvThreads;
-    if (i < K) xq_lds[i] = (int8_t)to_i8(v[j] * inv);
+  for (int j = 0; j < S::NX; ++j) {
+    const int i = (tid + j * NT) * 4;
+    if (i < K)
+      *(int*)(xq_lds + i) = pack_i8x4(to_i8(xv[4 * j] * inv), to_i8(xv[4 * j + 1] * inv), to_i8(xv[4 * j + 2] * inv),
+                                      to_i8(xv[4 * j + 3] * inv));
   }
   __syncthreads();
   return s_x;
 }
 
 // NCB: 1024-byte column chunks per row covered by the register slice (K <= NCB * 1024);
-// RU: rows per wave tile. A wave's first tile is requested right after the prologue's inputs and
-// before the prologue runs, and each next tile right after the current one's dot products, so HBM
-// stays busy while the prologue, the reductions and the epilogues run.
-template <int PRO, int EPI, int NCB, int RU>
-__global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
+// RU: rows per wave tile; NT: threads per block. A wave's first tile is requested right after the
+// prologue's inputs and before the prologue runs, and each next tile right after the current one's
+// dot products, so HBM stays busy while the prologue, the reductions and the epilogues run.
+template <int PRO, int EPI, int NCB, int RU, int NT, bool IDX>
+__global__ __launch_bounds__(NT) void k_gemv(GemvArgs a) {
   __shared__ __align__(16) int8_t xq_lds[kMaxK];
   __shared__ __align__(16) float xf_lds[PRO == PRO_NORM_QUANT ? kOsumLds : 1];
+  __shared__ __align__(16) float tab_lds[XStage<PRO, EPI, NCB, NT>::SFU ? kSfuWords : 1];
   __shared__ float red[64];
-  const int row_in = blockIdx.y;                  // activation row (prefill runs rows on grid y)
+  const int row_in = blockIdx.y;                  // activation row (MoE prefill runs rows on grid y)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int N = a.N, K = a.K;
-  const int nwaves = gridDim.x * (kGemvThreads / 64);
+  const int nwaves = gridDim.x * (NT / 64);
   const float* res = a.res ? a.res + row_in * a.res_stride : nullptr;
-  int r0 = (blockIdx.x * (kGemvThreads / 64) + wave) * RU;
-  XStage<PRO, NCB> st;
+  int r0 = (blockIdx.x * (NT / 64) + wave) * RU;
+  XStage<PRO, EPI, NCB, NT> st;
   stage_load(st, a, row_in);
+  // keep the issue order: the prologue's loads strictly before the tile's (waits count in order)
+  __builtin_amdgcn_sched_barrier(0);
   WTile<EPI, NCB, RU> t;
-  if (r0 < N) load_tile(t, a, res, row_in, r0, lane);
-  const float s_x = stage_finish(st, a, row_in, xq_lds, xf_lds, red);
+  load_tile<EPI, NCB, RU, IDX>(t, a, res, row_in, r0, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const float s_x = stage_finish(st, a, row_in, xq_lds, xf_lds, tab_lds, red);
   if (a.xq_out != nullptr && blockIdx.x == 0) {
-    for (int i = threadIdx.x; i < K; i += kGemvThreads) a.xq_out[row_in * a.xq_stride + i] = xq_lds[i];
+    for (int i = threadIdx.x; i < K; i += NT) a.xq_out[row_in * a.xq_stride + i] = xq_lds[i];
     if (threadIdx.x == 0) a.sx_out[row_in] = s_x;
   }
   int4 xr[NCB];
@@ -275,7 +311,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
       sw3[u] = EPI == EPI_SWIGLU ? t.sw3[u] : 0.0f;
       rs[u] = EPI == EPI_RESID ? t.res[u] : 0.0f;
     }
-    if (r0 + nwaves * RU < N) load_tile(t, a, res, row_in, r0 + nwaves * RU, lane);
+    if (r0 + nwaves * RU < N) load_tile<EPI, NCB, RU, IDX>(t, a, res, row_in, r0 + nwaves * RU, lane);
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       acc[u] = wave_sum_i32(acc[u]);
@@ -293,7 +329,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
       const int row = r0 + lane;
       if (row < N) {
         float v = dequant(ac, w1s, s_x);
-        if (EPI == EPI_SWIGLU) v = silu_mul(v, dequant(ac3, w3s, s_x));
+        if (EPI == EPI_SWIGLU) v = silu_mul(v, dequant(ac3, w3s, s_x), tab_lds);
         if (EPI == EPI_RESID) v = rr + v;
         y[row] = v;
         if (a.acc_out != nullptr) {
@@ -310,7 +346,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
   }
   // greedy argmax: one atomic per block at most, skipped when the key already holds a larger one
   if (a.argmax_key != nullptr) {
-    __shared__ unsigned long long bk[kGemvThreads / 64];
+    __shared__ unsigned long long bk[NT / 64];
     for (int o = 1; o < 64; o <<= 1) {
       const unsigned long long other = __shfl_xor(best, o);
       best = other > best ? other : best;
@@ -319,7 +355,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
     __syncthreads();
     if (threadIdx.x == 0) {
       unsigned long long b = bk[0];
-      for (int w = 1; w < kGemvThreads / 64; ++w) b = bk[w] > b ? bk[w] : b;
+      for (int w = 1; w < NT / 64; ++w) b = bk[w] > b ? bk[w] : b;
       unsigned long long* key = a.argmax_key + row_in;
       if (b != 0 && b > __atomic_load_n(key, __ATOMIC_RELAXED)) atomicMax(key, b);
     }
