@@ -68,6 +68,15 @@ def test_sfu_sweep_vs_oracle(env, name):
     assert bad.size == 0, [(hex(x[i]), hex(got[i]), hex(want[i])) for i in bad[:6]]
 
 
+@pytest.mark.parametrize("name", ["exp", "recip", "rsqrt"])
+def test_sfu_exhaustive_vs_literal_sequence(env, name):
+    """All 2^32 inputs: the datapath SFU (plain IEEE steps where the FTZ rule cannot change a result)
+    equals the per-operation FTZ sequence of llm/sfu.py, which the sweep above pins to the oracle."""
+    torch, N, ops, T, H = env
+    bad, first = ops.sfu_check(name)
+    assert bad == 0, (name, bad, None if first is None else hex(first))
+
+
 def test_fp32_primitives(env):
     torch, N, ops, T, H = env
     g = np.load(os.path.join(GOLD, "sfu_golden.npz"))

@@ -15,7 +15,7 @@ T2R_ABI_VERSION = 1
 T2R_OK, T2R_EINVAL, T2R_ESHAPE, T2R_ERANGE, T2R_EHIP, T2R_ENOMEM, T2R_ESTATE = 0, -1, -2, -3, -4, -5, -6
 T2R_ADVANCE_POS = 1
 
-c_int, c_int64, c_float, c_void_p = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+c_int, c_int64, c_uint64, c_float, c_void_p = ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_void_p
 P = c_void_p    # every tensor argument is a raw device pointer
 
 
@@ -49,6 +49,7 @@ _SIGS = {
     "t2r_init": (c_int, []),
     "t2r_sfu_tables": (c_int, [P]),
     "t2r_sfu": (c_int, [c_int, P, P, c_int64, P]),
+    "t2r_sfu_check": (c_int, [c_int, c_uint64, c_uint64, P, P]),
     "t2r_fp32_op": (c_int, [c_int, P, P, P, c_int64, P]),
     "t2r_requant": (c_int, [P, c_int64, c_int, c_int, c_int, c_int, c_int, P, P]),
     "t2r_embed": (c_int, [P, P, P, c_int, c_int, c_int, P, P, P]),

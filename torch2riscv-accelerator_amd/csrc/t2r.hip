@@ -99,7 +99,16 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   const size_t lds = mode == ATTN_PREP ? 0 : attn_lds_bytes(a.S, a.D);
   dim3 grid(a.H, rows), block(kAttnThreads);
   const bool c16 = a.hd % 16 == 0;
-  if (mode == ATTN_FUSED) {
+  if (mode == ATTN_FUSED && a.tab != nullptr && a.hd % 16 == 0 &&
+      (a.hd == 16 || a.hd == 32 || a.hd == 48 || a.hd == 64 || a.hd == 128)) {
+    switch (a.hd / 16) {
+      case 1: launch((k_attn_dec<1>), grid, block, lds, st, a); break;
+      case 2: launch((k_attn_dec<2>), grid, block, lds, st, a); break;
+      case 3: launch((k_attn_dec<3>), grid, block, lds, st, a); break;
+      case 4: launch((k_attn_dec<4>), grid, block, lds, st, a); break;
+      default: launch((k_attn_dec<8>), grid, block, lds, st, a); break;
+    }
+  } else if (mode == ATTN_FUSED) {
     if (c16) launch((k_attn<ATTN_FUSED, 16>), grid, block, lds, st, a);
     else launch((k_attn<ATTN_FUSED, 8>), grid, block, lds, st, a);
   } else if (mode == ATTN_PREP) {
@@ -296,6 +305,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
   at.eps = d.eps; at.inv_hd = (float)(1.0 / d.head_dim);
   at.H = d.heads; at.Hk = d.kv_heads; at.hd = d.head_dim; at.D = d.D; at.S = d.seq_len;
   at.att = m->att; at.att_stride = m->q_dim;
+  at.tab = sfu_table_ptr();
   {
     ProfScope p(m, T2R_PROF_ATTN, st);
     if (decode) {
@@ -448,6 +458,15 @@ int t2r_sfu(int fn, const uint32_t* x, uint32_t* y, int64_t n, void* stream) {
   long long blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   launch(k_sfu, dim3((unsigned)blocks), dim3(256), 0, S(stream), fn, x, y, (long long)n);
+  return launched();
+}
+
+int t2r_sfu_check(int fn, uint64_t first, uint64_t count, uint32_t* out, void* stream) {
+  if (fn < 0 || fn > 2 || !out || first > 0xFFFFFFFFull || count > 0x100000000ull - first) return T2R_EINVAL;
+  T2R_INIT();
+  launch(k_sfu_check_init, dim3(1), dim3(64), 0, S(stream), out);
+  if (count > 0) launch(k_sfu_check, dim3(8192), dim3(256), 0, S(stream), fn, (unsigned long long)first,
+                        (unsigned long long)count, out);
   return launched();
 }
 

@@ -42,6 +42,7 @@ struct AttnArgs {
   int H, Hk, hd, D, S;
   float* att;                // [rows, q_dim] (stride att_stride)
   long long att_stride;
+  const float* tab;          // the SFU tables in device memory (k_attn_dec)
 };
 
 // RMSNorm (optional) and RoPE of one head vector v[0..hd) in LDS, by one wave.
@@ -268,6 +269,299 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     int s = 0;
     for (int w = 0; w < kAttnWaves; ++w) s += part[w][j];
     out[h * hd + j] = (float)s * a.a_v;
+  }
+}
+
+// ------------------------------------------------------------------ decode attention
+// Same numerics as k_attn<ATTN_FUSED>, organised around memory latency and instruction count.
+// Every thread owns one 16-byte chunk (slot c of the NCHP slots per row) of R rows
+// t = ts + TS i, for both K and V. The position is the only load the others wait for; right after
+// it the workgroup issues the row's k / v or q, the RoPE inputs, the SFU tables and its K and V
+// chunks. K and V go through buffer loads whose range ends at row pos: rows past it read as zero
+// without a memory access, so the loads stay unconditional (exact in-order wait counts) and cost
+// nothing when the sequence is short. Per row, the slot lanes' partial dot products meet by DPP.
+// Each lane exps one row in NCHP; the exps go to the lane-major copy for the D-lane ordered sum,
+// and are read back from it. P.V packs four rows' int8 probabilities into one word and the V
+// chunks, transposed 4 x 4 bytes with v_perm, into words of four rows: one v_dot4 per column per
+// four rows.
+T2R_DEV __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+T2R_DEV v4i_t buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// 4 x 4 byte transpose: in r0..r3 (four rows, four columns each), out k = column k of the four rows
+T2R_DEV void transpose4x4(int r0, int r1, int r2, int r3, int* out) {
+  const int a = __builtin_amdgcn_perm(r1, r0, 0x05010400);   // r0.b0 r1.b0 r0.b1 r1.b1
+  const int b = __builtin_amdgcn_perm(r1, r0, 0x07030602);   // r0.b2 r1.b2 r0.b3 r1.b3
+  const int c = __builtin_amdgcn_perm(r3, r2, 0x05010400);
+  const int d = __builtin_amdgcn_perm(r3, r2, 0x07030602);
+  out[0] = __builtin_amdgcn_perm(c, a, 0x05040100);          // a.b0 a.b1 c.b0 c.b1
+  out[1] = __builtin_amdgcn_perm(c, a, 0x07060302);          // a.b2 a.b3 c.b2 c.b3
+  out[2] = __builtin_amdgcn_perm(d, b, 0x05040100);
+  out[3] = __builtin_amdgcn_perm(d, b, 0x07060302);
+}
+
+// sum over the NCHP lanes of a slot group (consecutive lanes)
+template <int NCHP>
+T2R_DEV int slot_group_sum(int v) {
+  if (NCHP >= 2) v += dpp_i<kDppXor1>(v);
+  if (NCHP >= 4) v += dpp_i<kDppXor2>(v);
+  if (NCHP >= 8) v += dpp_i<kDppHalfMirror>(v);
+  return v;
+}
+
+template <int NCH>   // 16-byte chunks per head row: hd = 16 NCH
+__global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
+  constexpr int HD = 16 * NCH;
+  constexpr int NCHP = NCH <= 1 ? 1 : (NCH <= 2 ? 2 : (NCH <= 4 ? 4 : 8));
+  constexpr int TS = kAttnThreads / NCHP;                   // row slices
+  // rows per thread per pass (R % 4 == 0): 8 keeps the unconditional loads cheap (each costs the
+  // CU's load pipeline ~16 clocks whether or not its rows exist); longer contexts take more passes
+  constexpr int R = 8;
+  constexpr int NV = HD > 64 ? 2 : 1;                       // head-vector floats per lane
+  extern __shared__ __align__(16) float dyn[];              // sc (lane-major)
+  __shared__ __align__(16) float tab[kSfuWords];
+  __shared__ __align__(16) float s_k[HD], s_q[HD], s_v[HD];
+  __shared__ __align__(16) int s_qq[HD / 4], s_kq[HD / 4], s_vq[HD / 4];
+  __shared__ int part[kAttnWaves * 4][HD];
+  __shared__ float red[16];
+  __shared__ float s_sq, s_r;
+
+  const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int G = a.H / a.Hk, g = h / G, S = a.S;
+  const long long q_dim = (long long)a.H * HD;
+  const int kv_dim = a.Hk * HD;
+  const int pos = a.pos[row];
+  if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
+  const int T = pos + 1;
+  const float* qkv = a.qkv + row * a.qkv_stride;
+  const int c = tid & (NCHP - 1), ts = tid / NCHP;
+  const bool cok = c < NCH;
+  // cache rows [0, pos): byte range of this KV head's columns up to row pos
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.kc + (long long)g * HD, (uint32_t)pos * kv_dim);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc + (long long)g * HD, (uint32_t)pos * kv_dim);
+  auto chunk_off = [&](int t) -> uint32_t { return cok ? (uint32_t)t * kv_dim + 16 * c : 0xFFFFFFF0u; };
+
+  // ---- issue: SFU tables, head vectors, K and V chunks (in this order; waits count in order)
+  v4f_t tb[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) tb[k] = ((const v4f_t*)a.tab)[(lane + 64 * k) & (kSfuWords / 4 - 1)];
+  const float* va = wave == 0 ? qkv + q_dim + (long long)g * HD : qkv + (long long)h * HD;
+  const float* vb = wave == 0 ? qkv + q_dim + kv_dim + (long long)g * HD : va;
+  const float* gn = wave == 0 ? a.kn : a.qn;
+  const bool norm = gn != nullptr;
+  if (!norm) gn = va;                            // any readable address: the values are unused
+  float xa[NV], xb[NV], xg[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int j = min(lane + 64 * k, HD - 1);
+    xa[k] = va[j];
+    xb[k] = vb[j];
+    xg[k] = gn[j];
+  }
+  const int ip = min(lane, HD / 2 - 1);
+  const float cs = a.cos_t[(long long)pos * (HD / 2) + ip], sn = a.sin_t[(long long)pos * (HD / 2) + ip];
+  __builtin_amdgcn_sched_barrier(0);
+  // unconditional: a branch around a load would make the compiler's wait counts path-dependent
+  // (it then waits for every later load too); rows past pos read as zero
+  v4i_t kw[R], vw[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) kw[i] = buffer_load16(krs, chunk_off(ts + TS * i));
+#pragma unroll
+  for (int i = 0; i < R; ++i) vw[i] = buffer_load16(vrs, chunk_off(ts + TS * i));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- tables to LDS; wave 0: k (norm, RoPE), k / v to int8 (+ cache row); wave 1: q to int8
+#pragma unroll
+  for (int k = 0; k < 2; ++k) ((v4f_t*)tab)[lane + 64 * k] = tb[k];
+  if (wave <= 1) {
+    float* vec = wave == 0 ? s_k : s_q;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (lane + 64 * k < HD) {
+        vec[lane + 64 * k] = xa[k];
+        if (wave == 0) s_v[lane + 64 * k] = xb[k];
+      }
+    __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0): this wave's LDS stores (tables, vector) done
+    __builtin_amdgcn_wave_barrier();
+    if (norm) {
+      float ss = 0.0f;
+      if (lane < a.D) ss = ordered_sum<true>(vec, HD, a.D, lane);
+      const float r = sfu_rsqrt(__shfl(ss, 0) * a.inv_hd + a.eps, tab);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) xa[k] = (xa[k] * r) * xg[k];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        if (lane + 64 * k < HD) vec[lane + 64 * k] = xa[k];
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+    }
+    // RoPE on the pairs (2i, 2i + 1): lane i < HD / 2 rotates pair i
+    float o0 = 0.0f, o1 = 0.0f;
+    if (lane < HD / 2) {
+      const float v0 = vec[2 * lane], v1 = vec[2 * lane + 1];
+      o0 = (v0 * cs) + ((-v1) * sn);
+      o1 = (v1 * cs) + (v0 * sn);
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < HD / 2) {
+      vec[2 * lane] = o0;
+      vec[2 * lane + 1] = o1;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    if (wave == 0) {
+      for (int j = lane; j < HD / 4; j += 64) {
+        const int kq = pack_i8x4(to_i8(vec[4 * j] * a.inv_sk), to_i8(vec[4 * j + 1] * a.inv_sk),
+                                 to_i8(vec[4 * j + 2] * a.inv_sk), to_i8(vec[4 * j + 3] * a.inv_sk));
+        const int vq = pack_i8x4(to_i8(s_v[4 * j] * a.inv_sv), to_i8(s_v[4 * j + 1] * a.inv_sv),
+                                 to_i8(s_v[4 * j + 2] * a.inv_sv), to_i8(s_v[4 * j + 3] * a.inv_sv));
+        s_kq[j] = kq;
+        s_vq[j] = vq;
+        if (h % G == 0) {
+          *(int*)(a.kc + (long long)pos * kv_dim + (long long)g * HD + 4 * j) = kq;
+          *(int*)(a.vc + (long long)pos * kv_dim + (long long)g * HD + 4 * j) = vq;
+        }
+      }
+    } else {
+      uint32_t am = 0;
+      for (int j = lane; j < HD; j += 64) am = max(am, abs_bits(vec[j]));
+      const float sq = fv(wave_max_u32(am)) * kInv127;
+      const float inv = sfu_recip(sq, tab);
+      for (int j = lane; j < HD / 4; j += 64)
+        s_qq[j] = pack_i8x4(to_i8(vec[4 * j] * inv), to_i8(vec[4 * j + 1] * inv), to_i8(vec[4 * j + 2] * inv),
+                            to_i8(vec[4 * j + 3] * inv));
+      if (lane == 0) s_sq = sq;
+    }
+  }
+  __syncthreads();
+
+  // ---- scores: slot c's partial dot products of the thread's rows, summed over the slot group
+  float* sc = dyn;
+  const int D = a.D, P = osum_stride(S, D);
+  const float sq = s_sq;
+  const int cc = cok ? c : 0;
+  int qw[4], kpos[4], vpos[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    qw[w] = cok ? s_qq[4 * cc + w] : 0;
+    kpos[w] = s_kq[4 * cc + w];
+    vpos[w] = s_vq[4 * cc + w];
+  }
+  const int npass = (T + TS * R - 1) / (TS * R);
+  constexpr int RM = R / NCHP;                   // rows a lane keeps per pass: i = j NCHP + c
+  float mloc = -__builtin_inff();
+  for (int pass = 0; pass < npass; ++pass) {
+    const int base = pass * TS * R;
+    if (pass > 0) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) kw[i] = buffer_load16(krs, chunk_off(base + ts + TS * i));
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (base + TS * i >= T) break;             // uniform: no row of this step is in range
+      const int t = base + ts + TS * i;
+      const bool here = t == pos;
+      int dot = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) dot = __builtin_amdgcn_sdot4(here ? kpos[w] : kw[i][w], qw[w], dot, false);
+      dot = slot_group_sum<NCHP>(dot);
+      const float s = ((float)dot * sq) * a.a_k;
+      if (t < T) {
+        if (c == (i & (NCHP - 1))) sc[osum_index(t, D, P)] = s;   // one lane per row keeps it
+        mloc = nanmax(mloc, s);
+      }
+    }
+  }
+  mloc = wave_max(mloc);
+  if (lane == 0) red[wave] = mloc;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < kAttnWaves; ++w) m = nanmax(m, red[w]);
+
+  // ---- e = EXP(s - m) by the row's keeping lane (+0 padding to a multiple of D), ordered sum, RECIP
+  const int Tpad = ((T + D - 1) / D) * D;
+  for (int pass = 0; pass < npass + 1; ++pass) {
+    const int base = pass * TS * R;
+#pragma unroll
+    for (int j = 0; j < RM; ++j) {
+      if (base + TS * j * NCHP >= Tpad) break;   // uniform: the step's first row is past the padding
+      const int t = base + ts + TS * (j * NCHP + c);
+      if (t < Tpad) {
+        const int k = osum_index(t, D, P);
+        sc[k] = t < T ? sfu_exp(sc[k] - m, tab) : 0.0f;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float ssum = 0.0f;
+    if (lane < D) ssum = ordered_sum_t<false>(sc, T, D, P, lane);
+    if (lane == 0) s_r = sfu_recip(ssum, tab);
+  }
+  __syncthreads();
+  const float rr = s_r;
+
+  // ---- P.V over the thread's rows, four at a time: int8 p of the four rows against V transposed
+  int acc[16];
+#pragma unroll
+  for (int b = 0; b < 16; ++b) acc[b] = 0;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int base = pass * TS * R;
+    if (pass > 0) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) vw[i] = buffer_load16(vrs, chunk_off(base + ts + TS * i));
+    }
+#pragma unroll
+    for (int i4 = 0; i4 < R; i4 += 4) {
+      if (base + TS * i4 >= T) break;
+      int pk[4], rw[4][4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = base + ts + TS * (i4 + u);
+        const bool here = t == pos;
+        const float ev = sc[osum_index(min(t, T - 1), D, P)];
+        pk[u] = t < T ? to_i8((ev * rr) * 127.0f) : 0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) rw[u][w] = here ? vpos[w] : vw[i4 + u][w];
+      }
+      const int pp = pack_i8x4(pk[0], pk[1], pk[2], pk[3]);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        int col[4];
+        transpose4x4(rw[0][w], rw[1][w], rw[2][w], rw[3][w], col);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[4 * w + k] = __builtin_amdgcn_sdot4(col[k], pp, acc[4 * w + k], false);
+      }
+    }
+  }
+  // ---- partial sums: lanes of a 16-lane row with the same slot rotate-and-add over the row-slice
+  // bits, then one partial per row of lanes and wave meets in LDS
+#pragma unroll
+  for (int b = 0; b < 16; ++b) {
+    int v = acc[b];
+    if (NCHP <= 1) v += dpp_i<0x121>(v);                      // row_ror:1
+    if (NCHP <= 2) v += dpp_i<0x122>(v);                      // row_ror:2
+    if (NCHP <= 4) v += dpp_i<0x124>(v);                      // row_ror:4
+    if (NCHP <= 8) v += dpp_i<0x128>(v);                      // row_ror:8
+    acc[b] = v;
+  }
+  if ((lane & 15) < NCHP && cok) {
+#pragma unroll
+    for (int b = 0; b < 16; ++b) part[wave * 4 + (lane >> 4)][16 * c + b] = acc[b];
+  }
+  __syncthreads();
+  float* out = a.att + row * a.att_stride;
+  for (int j = tid; j < HD; j += kAttnThreads) {
+    int ssum = 0;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
+    out[(long long)h * HD + j] = (float)ssum * a.a_v;
   }
 }
 

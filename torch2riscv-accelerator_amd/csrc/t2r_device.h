@@ -20,6 +20,11 @@
 
 namespace t2r {
 
+// Native vector types for values that are loaded and stored whole (HIP's int4 / float4 are
+// structs; arrays of them copied as aggregates can end up in scratch memory).
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
 // Kernel timing: while a profiling scope of the model is open, launches go through
 // hipExtLaunchKernelGGL with events recorded at the kernel's own start (the scope's first launch)
 // and end (every launch; the last one stands), so the measured time excludes dispatch latency.
@@ -50,20 +55,24 @@ constexpr int kSfuExpT = 0, kSfuExpS = 64, kSfuRecT = 128, kSfuRecS = 192, kSfuR
 constexpr int kSfuWords = 512;
 extern __constant__ float c_sfu[kSfuWords];
 
-// The first kSfuWords / 4 threads of a block each fetch 4 table words into a register (issue this
-// with the block's first loads) and later store them (sfu_store, before a barrier that precedes the
-// first lookup).
-T2R_DEV float4 sfu_fetch() {
+// The first kSfuWords / 4 threads of a block store 4 table words each (fetched into a register with
+// the block's first loads), before a barrier that precedes the first lookup.
+T2R_DEV void sfu_store(float* lds, v4f_t v) {
   const int t = threadIdx.x;
-  return t < kSfuWords / 4 ? ((const float4*)c_sfu)[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-}
-T2R_DEV void sfu_store(float* lds, float4 v) {
-  const int t = threadIdx.x;
-  if (t < kSfuWords / 4) ((float4*)lds)[t] = v;
+  if (t < kSfuWords / 4) ((v4f_t*)lds)[t] = v;
 }
 
 T2R_DEV uint32_t fb(float x) { return __float_as_uint(x); }
 T2R_DEV float fv(uint32_t b) { return __uint_as_float(b); }
+
+// A copy of x in a vector register that the compiler cannot prove wave-uniform: the SFU sequences
+// below are straight-line selects, and on a value known to be uniform the compiler would turn them
+// back into scalar branches, each a VALU -> SALU round trip.
+T2R_DEV float vreg(float x) {
+  float r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
 
 // subnormal -> zero of the same sign
 T2R_DEV float ftz(float x) {
@@ -112,35 +121,54 @@ T2R_DEV int floor_sat(float t) {
   return t != t ? 0 : r;
 }
 
+// The three SFU functions below follow the reference's operation sequence. They use plain IEEE
+// operations where the FTZ rule cannot change a result, and the FTZ helpers where it can. The
+// rule only differs from IEEE on a result below 2^-126 (or, for a product, exactly 2^-126).
+// After the input is flushed, every intermediate of these sequences is zero or at least 2^-126
+// in magnitude:
+//  - the table terms are in [2^-9, 2);
+//  - a fraction times a slope is at least 2^-17 * 2^-9 for RECIP / RSQRT;
+//  - EXP's slope term can be smaller, but it is then added to T >= 1 and vanishes either way.
+// So only the final scaling by a power of two (ldexp_norm) can leave the normal range, and that
+// step keeps the rule. Special inputs are selected at the end, never branched on.
+
+// y * 2^n for a normal y, with the FTZ rule on the result
+T2R_DEV float ldexp_norm(float y, int n) {
+  const uint32_t b = fb(y), sg = b & 0x80000000u;
+  const int e2 = (int)((b >> 23) & 0xFFu) + n;
+  uint32_t r = (b & 0x807FFFFFu) | ((uint32_t)e2 << 23);
+  r = e2 < 1 ? sg : r;
+  return fv(e2 > 254 ? (sg | kPInf) : r);
+}
+
+// (frac & 0x1FFFF) / 2^17, exact
+T2R_DEV float frac17(uint32_t frac) { return (float)(int)(frac & 0x1FFFFu) * 0x1p-17f; }
+
 // EXP (llm/sfu.py:7-11, 69-82)
 T2R_DEV float sfu_exp(float xin, const float* tab = c_sfu) {
-  const float x = ftz(xin);
-  const float t = fmul_ftz(x, (float)1.4426950408889634);
+  const float x = ftz(vreg(xin));
+  const float t = x * (float)1.4426950408889634;
   const int n = floor_sat(t);
-  const float f = fadd_ftz(t, -(float)n);
-  const float u = fmul_ftz(f, 64.0f);
-  int i = floor_sat(u);
-  i = i < 0 ? 0 : (i > 63 ? 63 : i);
-  const float r = fadd_ftz(u, -(float)i);
-  const float y = fadd_ftz(tab[kSfuExpT + i], fmul_ftz(r, tab[kSfuExpS + i]));
-  float out = ldexp_ftz(y, n < -300 ? -300 : (n > 300 ? 300 : n));
+  const float f = t - (float)n;
+  const float u = f * 64.0f;
+  const int i = min(max(floor_sat(u), 0), 63);
+  const float r = u - (float)i;
+  const float y = tab[kSfuExpT + i] + r * tab[kSfuExpS + i];
+  float out = ldexp_norm(y, min(max(n, -300), 300));
   out = x <= -104.0f ? 0.0f : out;
   out = x >= 89.0f ? fv(kPInf) : out;
   return x != x ? fv(kQNaN) : out;
 }
 
-// (frac & 0x1FFFF) / 2^17, exact
-T2R_DEV float frac17(uint32_t frac) { return ldexp_ftz((float)(int)(frac & 0x1FFFFu), -17); }
-
 // RECIP (llm/sfu.py:12-15, 85-96)
 T2R_DEV float sfu_recip(float xin, const float* tab = c_sfu) {
-  const uint32_t b = fb(ftz(xin));
+  const uint32_t b = fb(ftz(vreg(xin)));
   const uint32_t s = b & 0x80000000u, e = (b >> 23) & 0xFFu, frac = b & 0x7FFFFFu;
   const int i = (int)(frac >> 17);
   const float m = fv(frac | 0x3F800000u);
-  const float y0 = fadd_ftz(tab[kSfuRecT + i], fmul_ftz(frac17(frac), tab[kSfuRecS + i]));
-  const float y1 = fmul_ftz(y0, fadd_ftz(2.0f, -fmul_ftz(m, y0)));
-  uint32_t r = fb(ldexp_ftz(y1, 127 - (int)e)) | s;
+  const float y0 = tab[kSfuRecT + i] + frac17(frac) * tab[kSfuRecS + i];
+  const float y1 = y0 * (2.0f - m * y0);
+  uint32_t r = fb(ldexp_norm(y1, 127 - (int)e)) | s;
   r = e == 255 ? (frac ? kQNaN : s) : r;
   r = e == 0 ? (s | kPInf) : r;
   return fv(r);
@@ -148,19 +176,65 @@ T2R_DEV float sfu_recip(float xin, const float* tab = c_sfu) {
 
 // RSQRT (llm/sfu.py:16-20, 99-114)
 T2R_DEV float sfu_rsqrt(float xin, const float* tab = c_sfu) {
-  const uint32_t b = fb(ftz(xin));
+  const uint32_t b = fb(ftz(vreg(xin)));
   const uint32_t s = b >> 31, e = (b >> 23) & 0xFFu, frac = b & 0x7FFFFFu;
   const int E = (int)e - 127, odd = E & 1;
   const int j = odd * 64 + (int)(frac >> 17);
   const float m2 = fv(frac | ((uint32_t)(127 + odd) << 23));
-  const float y0 = fadd_ftz(tab[kSfuRsqT + j], fmul_ftz(frac17(frac), tab[kSfuRsqS + j]));
-  const float d = fadd_ftz(1.5f, -fmul_ftz(fmul_ftz(m2, fmul_ftz(y0, y0)), 0.5f));
-  float r = ldexp_ftz(fmul_ftz(y0, d), -((E - odd) / 2));
+  const float y0 = tab[kSfuRsqT + j] + frac17(frac) * tab[kSfuRsqS + j];
+  const float d = 1.5f - (m2 * (y0 * y0)) * 0.5f;
+  float r = ldexp_norm(y0 * d, -((E - odd) / 2));
   r = e == 255 ? 0.0f : r;
   r = s ? fv(kQNaN) : r;
   r = e == 0 ? fv(kPInf) : r;
   return (e == 255 && frac) ? fv(kQNaN) : r;
 }
+
+// The same three functions as the reference's literal sequence, the FTZ rule applied after every
+// operation. Not used on the datapath: t2r_sfu_check compares the functions above with these on
+// every one of the 2^32 inputs.
+namespace seq {
+T2R_DEV float frac17(uint32_t frac) { return ldexp_ftz((float)(int)(frac & 0x1FFFFu), -17); }
+T2R_DEV float sfu_exp(float xin, const float* tab) {
+  const float x = ftz(xin);
+  const float t = fmul_ftz(x, (float)1.4426950408889634);
+  const int n = floor_sat(t);
+  const float f = fadd_ftz(t, -(float)n);
+  const float u = fmul_ftz(f, 64.0f);
+  const int i = min(max(floor_sat(u), 0), 63);
+  const float r = fadd_ftz(u, -(float)i);
+  const float y = fadd_ftz(tab[kSfuExpT + i], fmul_ftz(r, tab[kSfuExpS + i]));
+  float out = ldexp_ftz(y, min(max(n, -300), 300));
+  out = x <= -104.0f ? 0.0f : out;
+  out = x >= 89.0f ? fv(kPInf) : out;
+  return x != x ? fv(kQNaN) : out;
+}
+T2R_DEV float sfu_recip(float xin, const float* tab) {
+  const uint32_t b = fb(ftz(xin));
+  const uint32_t s = b & 0x80000000u, e = (b >> 23) & 0xFFu, frac = b & 0x7FFFFFu;
+  if (e == 0) return fv(s | kPInf);
+  if (e == 255) return frac ? fv(kQNaN) : fv(s);
+  const int i = (int)(frac >> 17);
+  const float m = fv(frac | 0x3F800000u);
+  const float y0 = fadd_ftz(tab[kSfuRecT + i], fmul_ftz(frac17(frac), tab[kSfuRecS + i]));
+  const float y1 = fmul_ftz(y0, fadd_ftz(2.0f, -fmul_ftz(m, y0)));
+  return fv(fb(ldexp_ftz(y1, 127 - (int)e)) | s);
+}
+T2R_DEV float sfu_rsqrt(float xin, const float* tab) {
+  const uint32_t b = fb(ftz(xin));
+  const uint32_t s = b >> 31, e = (b >> 23) & 0xFFu, frac = b & 0x7FFFFFu;
+  if (e == 255 && frac) return fv(kQNaN);
+  if (e == 0) return fv(kPInf);
+  if (s) return fv(kQNaN);
+  if (e == 255) return 0.0f;
+  const int E = (int)e - 127, odd = E & 1;
+  const int j = odd * 64 + (int)(frac >> 17);
+  const float m2 = fv(frac | ((uint32_t)(127 + odd) << 23));
+  const float y0 = fadd_ftz(tab[kSfuRsqT + j], fmul_ftz(frac17(frac), tab[kSfuRsqS + j]));
+  const float d = fadd_ftz(1.5f, -fmul_ftz(fmul_ftz(m2, fmul_ftz(y0, y0)), 0.5f));
+  return ldexp_ftz(fmul_ftz(y0, d), -((E - odd) / 2));
+}
+}  // namespace seq
 
 // fp32 -> int8: round half to even, saturate to +-127, NaN -> 0 (llm/ref_model.py:136-139)
 T2R_DEV int to_i8(float y) {
@@ -170,12 +244,18 @@ T2R_DEV int to_i8(float y) {
   return (int)r;
 }
 
-// max that propagates NaN (NumPy's np.max)
+// max that propagates NaN (NumPy's np.max); selects only (early returns become exec-mask branches)
 T2R_DEV float nanmax(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  return a > b ? a : b;
+  float r = a > b ? a : b;
+  r = b != b ? b : r;
+  return a != a ? a : r;
 }
+
+// Bits of |x| for an order-free maximum of magnitudes: for values >= 0 the unsigned order of the
+// bits is the numeric order, and every NaN (any payload, sign cleared) is above +inf, so the
+// integer maximum propagates NaN as np.max does.
+T2R_DEV uint32_t abs_bits(float x) { return fb(x) & 0x7FFFFFFFu; }
+
 
 // int32 accumulator -> fp32 (RNE), times the row scale, times the activation scale:
 // y = F(F(f32(acc) * s_w) * s_x) (llm/ref_model.py:198-202)
@@ -200,7 +280,7 @@ T2R_DEV int dot16(int4 w, int4 x, int acc) {
   return acc;
 }
 
-typedef int v4i_t __attribute__((ext_vector_type(4)));
+
 
 #ifndef T2R_NT_LOADS
 #define T2R_NT_LOADS 1
@@ -263,6 +343,29 @@ T2R_DEV float lane_tree_sum(float acc, int D, int l) {
   o = dpp_f<0x108>(acc);
   if (D > 8 && (l & 15) == 0) acc = acc + o;
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+}
+
+// maximum of abs_bits values over the wave / the block (order-free, so any tree works); every
+// thread gets the result. `red` holds >= 16 words.
+T2R_DEV uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)dpp_i<kDppXor1>((int)v));
+  v = max(v, (uint32_t)dpp_i<kDppXor2>((int)v));
+  v = max(v, (uint32_t)dpp_i<kDppHalfMirror>((int)v));
+  v = max(v, (uint32_t)dpp_i<kDppMirror>((int)v));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+T2R_DEV float block_absmax(uint32_t v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  uint32_t* r = (uint32_t*)red;
+  v = wave_max_u32(v);
+  __syncthreads();
+  if (lane == 0) r[wave] = v;
+  __syncthreads();
+  uint32_t m = r[0];
+  for (int i = 1; i < nw; ++i) m = max(m, r[i]);
+  return fv(m);
 }
 
 // max over the block (NaN-propagating); every thread gets the result. `red` holds >= 16 floats.

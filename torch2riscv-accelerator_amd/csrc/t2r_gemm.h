@@ -21,8 +21,10 @@ __host__ __device__ inline int cdiv_i(long long a, long long b) { return (int)((
 // ------------------------------------------------------------------ GEMV launcher (decode, op level)
 // The GEMV over `rows` activation rows (grid y) with register-slice width NCB (by K), RU rows per
 // wave and NT threads per block. Every block repeats the prologue over the whole input, so fewer,
-// larger blocks (one 512-thread block per CU when the waves of one tile each cover N) repeat it
-// less; RU grows while there are at least 2048 waves' worth of rows.
+// larger tiles repeat it less: RU is the largest that still leaves >= 768 waves (3 per CU), and a
+// long input (NCB >= 4) takes 512-thread blocks. (Measured on the Llama-3.2-1B decode shapes:
+// W1/W3 8192 x 2048 best at RU 4 / 256 threads, Wqkv 3072 x 2048 at RU 4, Wo 2048 x 2048 at RU 2,
+// W2 2048 x 8192 at 512 threads.)
 template <int NCB>
 constexpr int gemv_rumax() { return NCB <= 2 ? 4 : (NCB == 4 ? 2 : 1); }
 
@@ -34,9 +36,9 @@ template <int NCB>
 inline GemvShape gemv_shape(int N) {
   GemvShape g;
   g.ru = 1;
-  while (g.ru < gemv_rumax<NCB>() && (long long)N / (2 * g.ru) >= 2048) g.ru *= 2;
+  while (g.ru < gemv_rumax<NCB>() && (long long)N / (2 * g.ru) >= 768) g.ru *= 2;
   const int waves = cdiv_i(N, g.ru);
-  g.nt = cdiv_i(waves, 8) >= 128 ? 512 : 256;
+  g.nt = NCB >= 4 ? 512 : 256;
   g.blocks = cdiv_i(waves, g.nt / 64);
   const int cap = 2048 * 256 / g.nt;
   if (g.blocks > cap) g.blocks = cap;

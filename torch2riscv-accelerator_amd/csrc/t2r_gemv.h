@@ -100,16 +100,16 @@ T2R_DEV float gemv_prologue(const GemvArgs& a, int row, int8_t* xq_lds, float* x
     __syncthreads();
     r = red[32];
   }
-  float amax = 0.0f;
+  uint32_t am = 0;
   for (int i = tid; i < K; i += kGemvThreads) {
     float v = xf_lds[i];
     if (PRO == PRO_NORM_QUANT) {
       v = (v * r) * a.g[i];
       xf_lds[i] = v;
     }
-    amax = nanmax(amax, fabsf(v));
+    am = max(am, abs_bits(v));
   }
-  amax = block_max(amax, red);
+  const float amax = block_absmax(am, red);
   const float s_x = amax * kInv127;
   const float inv = sfu_recip(s_x);
   for (int i = tid; i < K; i += kGemvThreads) xq_lds[i] = (int8_t)to_i8(xf_lds[i] * inv);
@@ -165,8 +165,8 @@ struct XStage {
   static constexpr bool SFU = PRO != PRO_XQ || EPI == EPI_SWIGLU;
   float4 x[PRO == PRO_XQ ? 1 : NX];
   float4 g[PRO == PRO_NORM_QUANT ? NX : 1];
-  int4 q[PRO == PRO_XQ ? NQ : 1];
-  float4 tab;
+  v4i_t q[PRO == PRO_XQ ? NQ : 1];
+  v4f_t tab;
 };
 
 template <int PRO, int EPI, int NCB, int NT>
@@ -174,11 +174,11 @@ T2R_DEV void stage_load(XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& a, int ro
   typedef XStage<PRO, EPI, NCB, NT> S;
   const int tid = threadIdx.x, K = a.K;
   // unconditional loads at clamped addresses (see load_tile); elements past K are never used
-  if (S::SFU) st.tab = ((const float4*)a.tab)[tid & (kSfuWords / 4 - 1)];
+  if (S::SFU) st.tab = ((const v4f_t*)a.tab)[tid & (kSfuWords / 4 - 1)];
   if (PRO == PRO_XQ) {
     const int8_t* src = a.xq + row * a.xq_stride;
 #pragma unroll
-    for (int j = 0; j < S::NQ; ++j) st.q[j] = *(const int4*)(src + min((tid + j * NT) * 16, K - 16));
+    for (int j = 0; j < S::NQ; ++j) st.q[j] = *(const v4i_t*)(src + min((tid + j * NT) * 16, K - 16));
   } else {
     const float* x = a.x + row * a.x_stride;
 #pragma unroll
@@ -202,7 +202,7 @@ T2R_DEV float stage_finish(const XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& 
 #pragma unroll
     for (int j = 0; j < S::NQ; ++j) {
       const int i = (tid + j * NT) * 16;
-      if (i < K) *(int4*)(xq_lds + i) = st.q[j];
+      if (i < K) *(v4i_t*)(xq_lds + i) = st.q[j];
     }
     __syncthreads();
     return a.s_x[row];
@@ -239,13 +239,13 @@ T2R_DEV float stage_finish(const XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& 
       xv[4 * j + 3] = (xv[4 * j + 3] * r) * st.g[j].w;
     }
   }
-  float amax = 0.0f;
+  uint32_t am = 0;
 #pragma unroll
   for (int j = 0; j < S::NX; ++j)
     if ((tid + j * NT) * 4 < K)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) amax = nanmax(amax, fabsf(xv[4 * j + e]));
-  amax = block_max(amax, red);
+      for (int e = 0; e < 4; ++e) am = max(am, abs_bits(xv[4 * j + e]));
+  const float amax = block_absmax(am, red);
   const float s_x = amax * kInv127;
   const float inv = sfu_recip(s_x, tab_lds);
 #pragma unroll

@@ -203,10 +203,9 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeDownArgs m) {
   const float* u = m.u + (long long)row * k * F;
   // quant_act of each expert's u (one wave per expert)
   for (int j = wave; j < k; j += 4) {
-    float amax = 0.0f;
-    for (int i = lane; i < F; i += 64) amax = nanmax(amax, fabsf(u[j * F + i]));
-    amax = wave_max(amax);
-    const float s = amax * kInv127, inv = sfu_recip(s);
+    uint32_t am = 0;
+    for (int i = lane; i < F; i += 64) am = max(am, abs_bits(u[j * F + i]));
+    const float s = fv(wave_max_u32(am)) * kInv127, inv = sfu_recip(s);
     for (int i = lane; i < F; i += 64) hq[j * 1024 + i] = (int8_t)to_i8(u[j * F + i] * inv);
     if (lane == 0) {
       s_h[j] = s;
@@ -268,6 +267,40 @@ __global__ void k_finish(const unsigned long long* key, int32_t* next_token, int
 }
 
 // ---- test hooks: the SFU and the flush-to-zero primitives on bit patterns
+// Every input in [first, first + count) through the datapath SFU and through the literal
+// sequence (namespace seq): out[0] counts the inputs whose bits differ, out[1] keeps the smallest
+// such input (initialised by k_sfu_check_init).
+__global__ void k_sfu_check_init(uint32_t* out) {
+  if (threadIdx.x == 0) {
+    out[0] = 0;
+    out[1] = 0xFFFFFFFFu;
+  }
+}
+__global__ void k_sfu_check(int fn, unsigned long long first, unsigned long long count, uint32_t* out) {
+  uint32_t bad = 0, lowest = 0xFFFFFFFFu;
+  for (unsigned long long k = blockIdx.x * (unsigned long long)blockDim.x + threadIdx.x; k < count;
+       k += (unsigned long long)gridDim.x * blockDim.x) {
+    const uint32_t xb = (uint32_t)(first + k);
+    const float v = fv(xb);
+    uint32_t a, b;
+    if (fn == 0) {
+      a = fb(sfu_exp(v)); b = fb(seq::sfu_exp(v, c_sfu));
+    } else if (fn == 1) {
+      a = fb(sfu_recip(v)); b = fb(seq::sfu_recip(v, c_sfu));
+    } else {
+      a = fb(sfu_rsqrt(v)); b = fb(seq::sfu_rsqrt(v, c_sfu));
+    }
+    if (a != b) {
+      ++bad;
+      lowest = min(lowest, xb);
+    }
+  }
+  if (bad) {
+    atomicAdd(out, bad);
+    atomicMin(out + 1, lowest);
+  }
+}
+
 __global__ void k_sfu(int fn, const uint32_t* x, uint32_t* y, long long n) {
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
     const float v = fv(x[i]);

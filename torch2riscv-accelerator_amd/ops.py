@@ -32,6 +32,16 @@ def sfu(fn, x_bits):
     return y
 
 
+def sfu_check(fn, first=0, count=1 << 32):
+    """Inputs [first, first + count) through the datapath SFU and the literal FTZ sequence; returns
+    (number of differing results, smallest differing input or None)."""
+    code = {"exp": 0, "recip": 1, "rsqrt": 2}[fn]
+    out = torch.empty(2, dtype=torch.int32, device="cuda")
+    abi.call("t2r_sfu_check", code, first, count, abi.ptr(out), _s())
+    n, lo = (int(v) & 0xFFFFFFFF for v in out.cpu().tolist())
+    return n, (None if n == 0 else lo)
+
+
 def fp32_op(op, a_bits, b_bits):
     """The fp32 primitives on bit patterns: 'add', 'sub', 'mul', 'ldexp', 'floor', 'to_i8', 'from_int',
     'ieee_mul', 'ieee_add' (see include/t2r.h t2r_fp32_op)."""
