@@ -60,6 +60,11 @@ int ensure_init() {
   if (hipMemcpyToSymbol(HIP_SYMBOL(c_sfu), t, sizeof(t), 0, hipMemcpyHostToDevice) != hipSuccess) return T2R_EHIP;
   void* addr = nullptr;
   if (hipGetSymbolAddress(&addr, HIP_SYMBOL(c_sfu)) != hipSuccess || addr == nullptr) return T2R_EHIP;
+  // the prefill attention keeps up to kPreMaxLds of score rows in LDS (160 KB per CU on gfx950)
+  const void* pre[] = {(const void*)k_attn_pre<32>, (const void*)k_attn_pre<64>, (const void*)k_attn_pre<128>};
+  for (const void* f : pre)
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPreMaxLds) != hipSuccess)
+      return T2R_EHIP;
   g_sfu_addr[dev] = (const float*)addr;
   g_inited[dev] = true;
   return T2R_OK;
@@ -92,6 +97,12 @@ GemvArgs gemv_args() {
   return a;
 }
 
+// the multi-row prefill attention: head dims 16..128 (multiples of 16), cache rows whose
+// score rows fit the LDS the kernels are set up for (kPreMaxLds)
+bool pre_ok(const AttnArgs& a) {
+  return a.hd % 16 == 0 && a.hd <= 128 && attn_pre_lds_bytes(a.S, (a.hd + 31) & ~31) <= kPreMaxLds;
+}
+
 int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   if (a.H <= 0 || a.Hk <= 0 || a.H % a.Hk || a.hd <= 0 || a.hd > kMaxHd || a.hd % 8 || a.S <= 0 || a.S > kMaxS ||
       (a.D != 8 && a.D != 16))
@@ -101,12 +112,13 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   const bool c16 = a.hd % 16 == 0;
   if (mode == ATTN_FUSED && a.tab != nullptr && a.hd % 16 == 0 &&
       (a.hd == 16 || a.hd == 32 || a.hd == 48 || a.hd == 64 || a.hd == 128)) {
+    const size_t dl = attn_dec_lds_bytes(a.S, a.D);
     switch (a.hd / 16) {
-      case 1: launch((k_attn_dec<1>), grid, block, lds, st, a); break;
-      case 2: launch((k_attn_dec<2>), grid, block, lds, st, a); break;
-      case 3: launch((k_attn_dec<3>), grid, block, lds, st, a); break;
-      case 4: launch((k_attn_dec<4>), grid, block, lds, st, a); break;
-      default: launch((k_attn_dec<8>), grid, block, lds, st, a); break;
+      case 1: launch((k_attn_dec<1>), grid, block, dl, st, a); break;
+      case 2: launch((k_attn_dec<2>), grid, block, dl, st, a); break;
+      case 3: launch((k_attn_dec<3>), grid, block, dl, st, a); break;
+      case 4: launch((k_attn_dec<4>), grid, block, dl, st, a); break;
+      default: launch((k_attn_dec<8>), grid, block, dl, st, a); break;
     }
   } else if (mode == ATTN_FUSED) {
     if (c16) launch((k_attn<ATTN_FUSED, 16>), grid, block, lds, st, a);
@@ -114,6 +126,13 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   } else if (mode == ATTN_PREP) {
     if (c16) launch((k_attn<ATTN_PREP, 16>), grid, block, lds, st, a);
     else launch((k_attn<ATTN_PREP, 8>), grid, block, lds, st, a);
+  } else if (a.tab != nullptr && pre_ok(a)) {
+    const int hdp = (a.hd + 31) & ~31;
+    dim3 pg(a.H, cdiv(rows, kPreRows));
+    const size_t pl = attn_pre_lds_bytes(a.S, hdp);
+    if (hdp == 32) launch((k_attn_pre<32>), pg, dim3(kPreThreads), pl, st, a, rows);
+    else if (hdp == 64) launch((k_attn_pre<64>), pg, dim3(kPreThreads), pl, st, a, rows);
+    else launch((k_attn_pre<128>), pg, dim3(kPreThreads), pl, st, a, rows);
   } else {
     if (c16) launch((k_attn<ATTN_ONLY, 16>), grid, block, lds, st, a);
     else launch((k_attn<ATTN_ONLY, 8>), grid, block, lds, st, a);

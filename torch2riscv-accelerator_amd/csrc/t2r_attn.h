@@ -362,8 +362,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     xb[k] = vb[j];
     xg[k] = gn[j];
   }
-  const int ip = min(lane, HD / 2 - 1);
-  const float cs = a.cos_t[(long long)pos * (HD / 2) + ip], sn = a.sin_t[(long long)pos * (HD / 2) + ip];
+  float cs[NV], sn[NV];                          // RoPE of element j = lane + 64 k: pair j / 2
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const long long ip = (long long)pos * (HD / 2) + min((lane + 64 * k) >> 1, HD / 2 - 1);
+    cs[k] = a.cos_t[ip];
+    sn[k] = a.sin_t[ip];
+  }
   __builtin_amdgcn_sched_barrier(0);
   // unconditional: a branch around a load would make the compiler's wait counts path-dependent
   // (it then waits for every later load too); rows past pos read as zero
@@ -374,67 +379,60 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   for (int i = 0; i < R; ++i) vw[i] = buffer_load16(vrs, chunk_off(ts + TS * i));
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- tables to LDS; wave 0: k (norm, RoPE), k / v to int8 (+ cache row); wave 1: q to int8
+  // ---- tables to LDS; wave 0: k (norm, RoPE), k / v to int8 (+ cache row); wave 1: q to int8.
+  // Lane j holds element j (and j + 64); the RoPE partner of element j is element j ^ 1 (DPP).
 #pragma unroll
   for (int k = 0; k < 2; ++k) ((v4f_t*)tab)[lane + 64 * k] = tb[k];
   if (wave <= 1) {
-    float* vec = wave == 0 ? s_k : s_q;
-#pragma unroll
-    for (int k = 0; k < NV; ++k)
-      if (lane + 64 * k < HD) {
-        vec[lane + 64 * k] = xa[k];
-        if (wave == 0) s_v[lane + 64 * k] = xb[k];
-      }
-    __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0): this wave's LDS stores (tables, vector) done
+    __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0): this wave's table stores are done
     __builtin_amdgcn_wave_barrier();
     if (norm) {
-      float ss = 0.0f;
-      if (lane < a.D) ss = ordered_sum<true>(vec, HD, a.D, lane);
-      const float r = sfu_rsqrt(__shfl(ss, 0) * a.inv_hd + a.eps, tab);
-#pragma unroll
-      for (int k = 0; k < NV; ++k) xa[k] = (xa[k] * r) * xg[k];
-      __builtin_amdgcn_wave_barrier();
+      float* vec = wave == 0 ? s_k : s_q;
 #pragma unroll
       for (int k = 0; k < NV; ++k)
         if (lane + 64 * k < HD) vec[lane + 64 * k] = xa[k];
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_wave_barrier();
+      float ss = 0.0f;
+      if (lane < a.D) ss = ordered_sum<true>(vec, HD, a.D, lane);
+      const float r = sfu_rsqrt(__shfl(ss, 0) * a.inv_hd + a.eps, tab);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) xa[k] = (xa[k] * r) * xg[k];
     }
-    // RoPE on the pairs (2i, 2i + 1): lane i < HD / 2 rotates pair i
-    float o0 = 0.0f, o1 = 0.0f;
-    if (lane < HD / 2) {
-      const float v0 = vec[2 * lane], v1 = vec[2 * lane + 1];
-      o0 = (v0 * cs) + ((-v1) * sn);
-      o1 = (v1 * cs) + (v0 * sn);
+    float xr[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const float partner = dpp_f<kDppXor1>(xa[k]);
+      xr[k] = (lane & 1) ? (xa[k] * cs[k]) + (partner * sn[k]) : (xa[k] * cs[k]) + ((-partner) * sn[k]);
     }
-    __builtin_amdgcn_wave_barrier();
-    if (lane < HD / 2) {
-      vec[2 * lane] = o0;
-      vec[2 * lane + 1] = o1;
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
+    int8_t* kq8 = (int8_t*)s_kq;
+    int8_t* vq8 = (int8_t*)s_vq;
+    int8_t* qq8 = (int8_t*)s_qq;
     if (wave == 0) {
-      for (int j = lane; j < HD / 4; j += 64) {
-        const int kq = pack_i8x4(to_i8(vec[4 * j] * a.inv_sk), to_i8(vec[4 * j + 1] * a.inv_sk),
-                                 to_i8(vec[4 * j + 2] * a.inv_sk), to_i8(vec[4 * j + 3] * a.inv_sk));
-        const int vq = pack_i8x4(to_i8(s_v[4 * j] * a.inv_sv), to_i8(s_v[4 * j + 1] * a.inv_sv),
-                                 to_i8(s_v[4 * j + 2] * a.inv_sv), to_i8(s_v[4 * j + 3] * a.inv_sv));
-        s_kq[j] = kq;
-        s_vq[j] = vq;
-        if (h % G == 0) {
-          *(int*)(a.kc + (long long)pos * kv_dim + (long long)g * HD + 4 * j) = kq;
-          *(int*)(a.vc + (long long)pos * kv_dim + (long long)g * HD + 4 * j) = vq;
+      const long long crow = (long long)pos * kv_dim + (long long)g * HD;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int j = lane + 64 * k;
+        const int8_t kb = (int8_t)to_i8(xr[k] * a.inv_sk), vb8 = (int8_t)to_i8(xb[k] * a.inv_sv);
+        if (j < HD) {
+          kq8[j] = kb;
+          vq8[j] = vb8;
+          if (h % G == 0) {
+            a.kc[crow + j] = kb;
+            a.vc[crow + j] = vb8;
+          }
         }
       }
     } else {
       uint32_t am = 0;
-      for (int j = lane; j < HD; j += 64) am = max(am, abs_bits(vec[j]));
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        if (lane + 64 * k < HD) am = max(am, abs_bits(xr[k]));       // lanes past HD hold no element
       const float sq = fv(wave_max_u32(am)) * kInv127;
       const float inv = sfu_recip(sq, tab);
-      for (int j = lane; j < HD / 4; j += 64)
-        s_qq[j] = pack_i8x4(to_i8(vec[4 * j] * inv), to_i8(vec[4 * j + 1] * inv), to_i8(vec[4 * j + 2] * inv),
-                            to_i8(vec[4 * j + 3] * inv));
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        if (lane + 64 * k < HD) qq8[lane + 64 * k] = (int8_t)to_i8(xr[k] * inv);
       if (lane == 0) s_sq = sq;
     }
   }
@@ -454,6 +452,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   }
   const int npass = (T + TS * R - 1) / (TS * R);
   constexpr int RM = R / NCHP;                   // rows a lane keeps per pass: i = j NCHP + c
+  const int dummy = D * P + lane;                // per-lane LDS slot for stores that keep nothing
   float mloc = -__builtin_inff();
   for (int pass = 0; pass < npass; ++pass) {
     const int base = pass * TS * R;
@@ -461,20 +460,35 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < R; ++i) kw[i] = buffer_load16(krs, chunk_off(base + ts + TS * i));
     }
+    int dots[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      if (base + TS * i >= T) break;             // uniform: no row of this step is in range
-      const int t = base + ts + TS * i;
-      const bool here = t == pos;
+      const bool here = base + ts + TS * i == pos;
       int dot = 0;
 #pragma unroll
       for (int w = 0; w < 4; ++w) dot = __builtin_amdgcn_sdot4(here ? kpos[w] : kw[i][w], qw[w], dot, false);
-      dot = slot_group_sum<NCHP>(dot);
-      const float s = ((float)dot * sq) * a.a_k;
-      if (t < T) {
-        if (c == (i & (NCHP - 1))) sc[osum_index(t, D, P)] = s;   // one lane per row keeps it
-        mloc = nanmax(mloc, s);
-      }
+      dots[i] = dot;
+    }
+    // the slot group's partial sums, the DPP steps of all rows interleaved
+    if (NCHP >= 2) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) dots[i] += dpp_i<kDppXor1>(dots[i]);
+    }
+    if (NCHP >= 4) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) dots[i] += dpp_i<kDppXor2>(dots[i]);
+    }
+    if (NCHP >= 8) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) dots[i] += dpp_i<kDppHalfMirror>(dots[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int t = base + ts + TS * i;
+      const float sv = ((float)dots[i] * sq) * a.a_k;
+      const bool ok = t < T;
+      sc[ok && c == (i & (NCHP - 1)) ? osum_index(t, D, P) : dummy] = sv;   // one lane per row keeps it
+      mloc = nanmax(mloc, ok ? sv : -__builtin_inff());
     }
   }
   mloc = wave_max(mloc);
@@ -486,16 +500,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 
   // ---- e = EXP(s - m) by the row's keeping lane (+0 padding to a multiple of D), ordered sum, RECIP
   const int Tpad = ((T + D - 1) / D) * D;
-  for (int pass = 0; pass < npass + 1; ++pass) {
+  const int epass = (Tpad + TS * R - 1) / (TS * R);
+  for (int pass = 0; pass < epass; ++pass) {
     const int base = pass * TS * R;
 #pragma unroll
     for (int j = 0; j < RM; ++j) {
-      if (base + TS * j * NCHP >= Tpad) break;   // uniform: the step's first row is past the padding
       const int t = base + ts + TS * (j * NCHP + c);
-      if (t < Tpad) {
-        const int k = osum_index(t, D, P);
-        sc[k] = t < T ? sfu_exp(sc[k] - m, tab) : 0.0f;
-      }
+      const int k = t < Tpad ? osum_index(t, D, P) : dummy;
+      const float ev = sfu_exp(sc[k] - m, tab);
+      sc[k] = t < T ? ev : 0.0f;
     }
   }
   __syncthreads();
@@ -565,8 +578,225 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ prefill attention
+// ATTN_ONLY for many rows at once (rows whose q is rotated and whose KV rows are in the cache), one
+// workgroup per (query head, 16 consecutive rows). Scores and P.V run on the int8 matrix cores
+// (v_mfma_i32_32x32x32_i8, query rows 16..31 of each tile zero): every lane feeds 16 consecutive
+// k-bytes of its A row and of its B row, the same k for both, so each int32 is the exact dot
+// product. The softmax is per row and follows the decode numerics exactly:
+//  - thread (row i, lane l < D) scans the row's scores t = l, l + D, ... in order;
+//  - it forms EXP(s - max) and keeps that chain of adds, which is the lane chain of the D-lane
+//    ordered sum;
+//  - DPP then pairs the D lanes, and RECIP gives r.
+// P.V packs to_i8(e r 127) of 16 t per lane against V transposed in LDS (wave-private tiles).
+constexpr int kPreRows = 16;
+constexpr int kPreThreads = 256;
+constexpr int kPreTiles = 8;                  // 32-row cache tiles a wave loads at once
+constexpr size_t kPreMaxLds = 136 * 1024;     // dynamic LDS the kernels are set up for (of 160 KB per CU)
+
+T2R_DEV int pre_est(int S) { return (S + 16 + 31) & ~31; }   // row stride of the score / exp rows
+
+template <int HDP>   // head dim padded to a multiple of 32 (MFMA k-steps)
+__global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
+  constexpr int KS = HDP / 32;                 // k-steps of the score MFMA; column tiles of P.V
+  constexpr int NV = HDP > 64 ? 2 : 1;
+  extern __shared__ __align__(16) float E[];   // [16][est] scores, then exps; then partial P.V sums
+  __shared__ __align__(16) float tab[kSfuWords];
+  __shared__ __align__(16) int8_t Q8[kPreRows][HDP];
+  __shared__ __align__(16) int8_t VT[4][HDP][32];
+  __shared__ float s_sq[kPreRows], s_r[kPreRows];
+  __shared__ int s_T[kPreRows];
+  const int h = blockIdx.x, r0 = blockIdx.y * kPreRows, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int HD = a.hd, G = a.H / a.Hk, g = h / G, S = a.S, D = a.D;
+  const int kv_dim = a.Hk * HD, est = pre_est(S);
+  if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = ((const v4f_t*)a.tab)[tid];
+  __syncthreads();
+
+  // ---- q of the block's rows to int8 (one wave per 4 rows); rows without a valid position: T = 0
+  for (int i = wave; i < kPreRows; i += 4) {
+    const int r = min(r0 + i, M - 1);
+    const int pos = a.pos[r];
+    const bool ok = r0 + i < M && pos >= 0 && pos < S;
+    const float* q = a.qkv + (long long)r * a.qkv_stride + (long long)h * HD;
+    float x[NV];
+    uint32_t am = 0;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int j = lane + 64 * k;
+      x[k] = q[min(j, HD - 1)];
+      if (j < HD) am = max(am, abs_bits(x[k]));
+    }
+    const float sq = fv(wave_max_u32(am)) * kInv127;
+    const float inv = sfu_recip(sq, tab);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int j = lane + 64 * k;
+      if (j < HDP) Q8[i][j] = (int8_t)(ok && j < HD ? to_i8(x[k] * inv) : 0);
+    }
+    if (lane == 0) {
+      s_sq[i] = sq;
+      s_T[i] = ok ? pos + 1 : 0;
+    }
+  }
+  __syncthreads();
+  int Tmax = 0;
+#pragma unroll
+  for (int i = 0; i < kPreRows; ++i) Tmax = max(Tmax, s_T[i]);
+  const int ntile = (Tmax + 31) / 32;
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.kc, (uint32_t)S * kv_dim);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc, (uint32_t)S * kv_dim);
+  const int lr = lane & 31, lk = (lane >> 5) * 16;
+
+  // ---- scores of the wave's tiles (t = 32 tile + n), kPreTiles tiles' K rows in flight at a time
+  v4i_t qa[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    qa[ks] = lr < kPreRows ? *(const v4i_t*)&Q8[lr][32 * ks + lk] : v4i_t{0, 0, 0, 0};
+  for (int c0 = wave; c0 < ntile; c0 += 4 * kPreTiles) {
+    v4i_t kb[kPreTiles][KS];
+#pragma unroll
+    for (int u = 0; u < kPreTiles; ++u) {
+      const uint32_t off = (uint32_t)(32 * (c0 + 4 * u) + lr) * kv_dim + g * HD + lk;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kb[u][ks] = buffer_load16(krs, off + 32 * ks);
+    }
+#pragma unroll
+    for (int u = 0; u < kPreTiles; ++u) {
+      const int ti = c0 + 4 * u;
+      if (ti >= ntile) break;
+      v16i_t acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[ks], kb[u][ks], acc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {                   // output rows m < 16
+        const int m = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        E[m * est + 32 * ti + lr] = ((float)acc[r] * s_sq[m]) * a.a_k;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- per row: max, e = EXP(s - max) (+0 padding), the D-lane ordered sum, RECIP
+  {
+    const int i = tid >> 4, l = tid & 15;
+    const int T = s_T[i];
+    float* row = E + i * est;
+    float mx = -__builtin_inff();
+    if (l < D)
+      for (int t = l; t < T; t += D) mx = nanmax(mx, row[t]);
+    mx = nanmax(mx, dpp_f<kDppXor1>(mx));
+    mx = nanmax(mx, dpp_f<kDppXor2>(mx));
+    mx = nanmax(mx, dpp_f<kDppHalfMirror>(mx));
+    mx = nanmax(mx, dpp_f<kDppMirror>(mx));
+    float acc = 0.0f;
+    const int groups = T > 0 ? (T + D - 1) / D : 0;
+    if (l < D) {
+      for (int gi = 0; gi < groups; ++gi) {
+        const int t = l + gi * D;
+        const float e = t < T ? sfu_exp(row[t] - mx, tab) : 0.0f;
+        row[t] = e;
+        acc = gi == 0 ? e : acc + e;
+      }
+    }
+    // pairwise tree over the D lanes of the row group (lane l, l % 2s == 0, takes lane l + s)
+    float o = dpp_f<0x101>(acc);
+    if (D > 1 && (l & 1) == 0) acc = acc + o;
+    o = dpp_f<0x102>(acc);
+    if (D > 2 && (l & 3) == 0) acc = acc + o;
+    o = dpp_f<0x104>(acc);
+    if (D > 4 && (l & 7) == 0) acc = acc + o;
+    o = dpp_f<0x108>(acc);
+    if (D > 8 && (l & 15) == 0) acc = acc + o;
+    if (l == 0) s_r[i] = sfu_recip(acc, tab);
+  }
+  __syncthreads();
+
+  // ---- P.V: per tile, int8 p of 16 t per lane (A) against V transposed (B), exact int32
+  v16i_t pv[KS];
+#pragma unroll
+  for (int jt = 0; jt < KS; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pv[jt][r] = 0;
+  const int pm = lr;                                  // A row of this lane
+  const float rm = pm < kPreRows ? s_r[pm] : 0.0f;
+  const int Tm = pm < kPreRows ? s_T[pm] : 0;
+  int8_t* vt = &VT[wave][0][0];
+  for (int c0 = wave; c0 < ntile; c0 += 4 * kPreTiles) {
+    v4i_t vb[kPreTiles][HDP / 32];                    // V rows: lane takes row (lane & 31), half of the columns
+#pragma unroll
+    for (int u = 0; u < kPreTiles; ++u) {
+      const uint32_t off = (uint32_t)(32 * (c0 + 4 * u) + lr) * kv_dim + g * HD + (lane >> 5) * (HDP / 2);
+#pragma unroll
+      for (int q = 0; q < HDP / 32; ++q) vb[u][q] = buffer_load16(vrs, off + 16 * q);
+    }
+#pragma unroll
+    for (int u = 0; u < kPreTiles; ++u) {
+      const int ti = c0 + 4 * u;
+      if (ti >= ntile) break;
+      // V tile transposed: VT[j][tt] for the 32 rows tt of the tile
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = 0; q < HDP / 32; ++q) {
+        const int jb = (lane >> 5) * (HDP / 2) + 16 * q;
+        const int w4[4] = {vb[u][q].x, vb[u][q].y, vb[u][q].z, vb[u][q].w};
+#pragma unroll
+        for (int b = 0; b < 16; ++b) vt[(jb + b) * 32 + lr] = (int8_t)(w4[b >> 2] >> (8 * (b & 3)));
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      // A: p of row pm, t = 32 ti + lk + 0..15
+      int pw[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        int bytes[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int t = 32 * ti + lk + 4 * w + b;
+          const float e = E[min(pm, kPreRows - 1) * est + t];
+          bytes[b] = t < Tm ? to_i8((e * rm) * 127.0f) : 0;
+        }
+        pw[w] = pack_i8x4(bytes[0], bytes[1], bytes[2], bytes[3]);
+      }
+      const v4i_t pa = {pw[0], pw[1], pw[2], pw[3]};
+#pragma unroll
+      for (int jt = 0; jt < KS; ++jt) {
+        const v4i_t fb = *(const v4i_t*)&vt[(32 * jt + lr) * 32 + lk];
+        pv[jt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, fb, pv[jt], 0, 0, 0);
+      }
+    }
+  }
+  __syncthreads();                                    // E is free: partial sums of the four waves
+  int* part = (int*)E;                                // [4][16][HDP]
+#pragma unroll
+  for (int jt = 0; jt < KS; ++jt)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int m = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      part[(wave * kPreRows + m) * HDP + 32 * jt + lr] = pv[jt][r];
+    }
+  __syncthreads();
+  for (int k = tid; k < kPreRows * HD; k += kPreThreads) {
+    const int m = k / HD, j = k % HD;
+    if (s_T[m] == 0) continue;
+    const int sum = part[(0 * kPreRows + m) * HDP + j] + part[(1 * kPreRows + m) * HDP + j] +
+                    part[(2 * kPreRows + m) * HDP + j] + part[(3 * kPreRows + m) * HDP + j];
+    a.att[(long long)(r0 + m) * a.att_stride + (long long)h * HD + j] = (float)sum * a.a_v;
+  }
+}
+
+// dynamic LDS bytes of k_attn_pre: 16 rows of scores / exps (also the partial sums afterwards)
+inline size_t attn_pre_lds_bytes(int S, int HDP) {
+  const size_t e = (size_t)kPreRows * ((S + 16 + 31) & ~31) * 4, p = (size_t)4 * kPreRows * HDP * 4;
+  return e > p ? e : p;
+}
+
 // dynamic LDS bytes of k_attn: the scores (lane-major, D * osum_stride(S, D) floats) and the int8
 // probabilities of S cache rows
 inline size_t attn_lds_bytes(int S, int D) { return (size_t)D * osum_stride(S, D) * 4 + (size_t)S; }
+// dynamic LDS bytes of k_attn_dec: the scores (lane-major) and one spare slot per lane
+inline size_t attn_dec_lds_bytes(int S, int D) { return ((size_t)D * osum_stride(S, D) + 64) * 4; }
 
 }  // namespace t2r

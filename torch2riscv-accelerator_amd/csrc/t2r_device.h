@@ -24,6 +24,7 @@ namespace t2r {
 // structs; arrays of them copied as aggregates can end up in scratch memory).
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
+typedef int v16i_t __attribute__((ext_vector_type(16)));   // int8 MFMA 32 x 32 accumulators
 
 // Kernel timing: while a profiling scope of the model is open, launches go through
 // hipExtLaunchKernelGGL with events recorded at the kernel's own start (the scope's first launch)

@@ -96,7 +96,6 @@ int gemv_launch(const GemvArgs& a, int rows, hipStream_t st) {
 }
 
 // ------------------------------------------------------------------ MFMA GEMM
-typedef int v16i_t __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 64;                 // K per slab
 constexpr int kLdsRow = kBK + 16;       // padded LDS row (bytes)
