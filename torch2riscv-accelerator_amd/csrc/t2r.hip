@@ -145,6 +145,8 @@ struct Model {
   t2r_model_desc d;
   std::vector<float> kvc;           // [L, 4]
   int q_dim, kv_dim, qkv_dim, ffn_rows, max_in;
+  int32_t* part;                    // split-K partial sums of the prefill linears
+  int part_rows;
   float* x;
   float* qkv;
   float* att;
@@ -222,6 +224,10 @@ long long carve(Model* m, char* base, int M) {
   m->mxq = c.take<int8_t>((long long)M * d.dim);
   m->msx = c.take<float>(M);
   m->status = c.take<int32_t>(1);
+  // split-K partial sums of the prefill linears: 4 splits of up to 512 rows of the widest
+  // STORE / RESID output
+  m->part_rows = M < 512 ? M : 512;
+  m->part = c.take<int32_t>(4LL * m->part_rows * (m->qkv_dim > d.dim ? m->qkv_dim : d.dim));
   return c.off;
 }
 
@@ -284,7 +290,8 @@ int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, c
   std::memset(&a, 0, sizeof(a));
   a.xq = m->xq; a.s_x = m->sx; a.w = w; a.s_w = s_w; a.w3 = w3; a.s_w3 = s_w3;
   a.M = rows; a.N = N; a.K = K; a.y = y; a.y_stride = y_stride; a.res = EPI == EPI_RESID ? y : nullptr;
-  return gemm_launch<EPI>(a, st) ? T2R_EHIP : T2R_OK;
+  a.part = m->part;
+  return gemm_launch<EPI>(a, st, m->part_rows) ? T2R_EHIP : T2R_OK;
 }
 
 // one decoder layer on `rows` rows of the workspace at device positions pos[rows]

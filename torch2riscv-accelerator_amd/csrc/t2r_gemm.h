@@ -112,6 +112,7 @@ struct GemmArgs {
   const float* res;          // EPI_RESID residual [M, N] (stride y_stride; may alias y)
   long long y_stride;
   int32_t* acc_out;          // optional [M, N] (SwiGLU: [M, 2N], W1 then W3 columns)
+  int32_t* part;             // split-K partial sums [splits, M, N] (nullptr: no split)
 };
 
 // source row of tile column c (0 .. BN) for the block's column origin n0 (SwiGLU interleave)
@@ -242,10 +243,190 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(GemmArgs a) {
 }
 
 // Picks the workgroup shape: the largest tile that still gives >= 256 workgroups (one per CU).
+// ---- pipelined GEMM (K % 64 == 0): 128 x 128 tiles, four waves (2 x 2, 64 x 64 each), kGD slabs of
+// loads in flight in a register ring ahead of the two LDS stages the MFMAs read (kGD = 2 keeps the
+// kernel at two workgroups per CU; deeper rings cost more registers than they hide). The loads are
+// unconditional (clamped rows), so the compiler's in-order wait counts are exact and only the slab
+// about to be stored is waited for. Split-K over grid z (STORE / RESID): each z takes a slab range
+// and writes int32 partials; k_gemm_fin adds them (exact) and applies the epilogue.
+constexpr int kGT = 128;
+constexpr int kGD = 2;
+
+template <int EPI, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemm_p(GemmArgs a) {
+  __shared__ __align__(16) int8_t As[2][kGT * kLdsRow];
+  __shared__ __align__(16) int8_t Bs[2][kGT * kLdsRow];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int mtiles = cdiv_i(a.M, kGT);
+  const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;   // m tiles fastest: weight slabs shared in L2
+  const int m0 = mt * kGT, n0 = nt * kGT;
+  const int K = a.K, nslab = K / kBK;
+  const int per = cdiv_i(nslab, (int)gridDim.z);
+  const int s0 = (int)blockIdx.z * per, nk = max(0, min(nslab, s0 + per) - s0);
+  // this thread's two A and two B 16-byte chunks of every slab: tile row c / 4, bytes (c % 4) 16
+  const int8_t* pa[2];
+  const int8_t* pb[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int c = tid + p * 256, r = c >> 2, kc = (c & 3) * 16;
+    pa[p] = a.xq + (long long)min(m0 + r, a.M - 1) * K + kc;
+    int n;
+    bool ok;
+    pb[p] = b_row<EPI>(a, n0, r, n, ok) + kc;
+  }
+  auto load = [&](int s, v4i_t (&ra)[2], v4i_t (&rb)[2]) {
+    const long long k0 = (long long)min(s0 + s, nslab - 1) * kBK;   // past the range: re-read the last slab
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      ra[p] = *(const v4i_t*)(pa[p] + k0);
+      rb[p] = __builtin_nontemporal_load((const v4i_t*)(pb[p] + k0));
+    }
+  };
+  auto store = [&](int buf, const v4i_t (&ra)[2], const v4i_t (&rb)[2]) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int c = tid + p * 256, off = (c >> 2) * kLdsRow + (c & 3) * 16;
+      *(v4i_t*)&As[buf][off] = ra[p];
+      *(v4i_t*)&Bs[buf][off] = rb[p];
+    }
+  };
+  v16i_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  const int lr = lane & 31, lk = (lane >> 5) * 16;
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < kBK; kk += 32) {
+      v4i_t fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) fa[i] = *(const v4i_t*)(&As[buf][(wm * 64 + i * 32 + lr) * kLdsRow + kk + lk]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[j] = *(const v4i_t*)(&Bs[buf][(wn * 64 + j * 32 + lr) * kLdsRow + kk + lk]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  v4i_t ra[kGD][2], rb[kGD][2];
+#pragma unroll
+  for (int d = 0; d < kGD; ++d) {
+    load(d, ra[d], rb[d]);
+    __builtin_amdgcn_sched_barrier(0);           // slab order = issue order (waits count in order)
+  }
+  store(0, ra[0], rb[0]);
+  __syncthreads();
+  // slab j lives in ring slot j % kGD; step u of the unrolled group handles slab s + u
+#define T2R_GEMM_STEP(u)                                                   \
+  {                                                                        \
+    const int j = s + (u);                                                 \
+    if (j >= nk) break;                                                    \
+    compute(j & 1);                                                        \
+    if (j + 1 < nk) store((j + 1) & 1, ra[((u) + 1) % kGD], rb[((u) + 1) % kGD]); \
+    __builtin_amdgcn_sched_barrier(0);                                     \
+    load(j + kGD, ra[u], rb[u]);                                           \
+    __builtin_amdgcn_sched_barrier(0);                                     \
+    __syncthreads();                                                       \
+  }
+  for (int s = 0; s < nk; s += kGD) {
+    T2R_GEMM_STEP(0)
+    T2R_GEMM_STEP(1)
+  }
+#undef T2R_GEMM_STEP
+
+  // lane holds C[m][n] for n = lane % 32 of each 32 x 32 tile, m = 8 (r / 4) + 4 (lane / 32) + r % 4
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (m >= a.M) continue;
+      if (SPLIT) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + wn * 64 + j * 32 + lr;
+          if (n < a.N) a.part[((long long)blockIdx.z * a.M + m) * a.N + n] = acc[i][j][r];
+        }
+        continue;
+      }
+      const float sx = a.s_x[m];
+      if (EPI == EPI_SWIGLU) {
+        const int n = (n0 >> 1) + wn * 32 + lr;
+        if (n >= a.N) continue;
+        const int ac1 = acc[i][0][r], ac3 = acc[i][1][r];
+        const float h1 = dequant(ac1, a.s_w[n], sx), h3 = dequant(ac3, a.s_w3[n], sx);
+        a.y[(long long)m * a.y_stride + n] = silu_mul(h1, h3);
+        if (a.acc_out) {
+          a.acc_out[(long long)m * 2 * a.N + n] = ac1;
+          a.acc_out[(long long)m * 2 * a.N + a.N + n] = ac3;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + wn * 64 + j * 32 + lr;
+          if (n >= a.N) continue;
+          float v = dequant(acc[i][j][r], a.s_w[n], sx);
+          if (EPI == EPI_RESID) v = a.res[(long long)m * a.y_stride + n] + v;
+          a.y[(long long)m * a.y_stride + n] = v;
+          if (a.acc_out) a.acc_out[(long long)m * a.N + n] = acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
+// split-K finish: acc = sum of the nz partials (exact), then the STORE / RESID epilogue
 template <int EPI>
-int gemm_launch(const GemmArgs& a, hipStream_t st) {
+__global__ __launch_bounds__(256) void k_gemm_fin(GemmArgs a, int nz) {
+  const long long total = (long long)a.M * a.N;
+  for (long long e = blockIdx.x * 256LL + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
+    const int m = (int)(e / a.N), n = (int)(e % a.N);
+    int acc = 0;
+    for (int z = 0; z < nz; ++z) acc += a.part[(long long)z * total + e];
+    float v = dequant(acc, a.s_w[n], a.s_x[m]);
+    if (EPI == EPI_RESID) v = a.res[(long long)m * a.y_stride + n] + v;
+    a.y[(long long)m * a.y_stride + n] = v;
+    if (a.acc_out) a.acc_out[e] = acc;
+  }
+}
+
+// split count for the pipelined GEMM: enough workgroups for the 256 CUs, >= 8 slabs each, and the
+// partials within the `part_rows` rows x 4 splits the caller's buffer holds (0: no buffer)
+inline int gemm_splits(int M, int ncols, int K, int part_rows, int epi) {
+  if (epi == EPI_SWIGLU || part_rows <= 0) return 1;
+  const long long tiles = (long long)cdiv_i(M, kGT) * cdiv_i(ncols, kGT);
+  int z = 1;
+  while (z < 4 && tiles * z * 2 <= 256 && K / kBK >= 16 * z && (long long)M * z * 2 <= 4LL * part_rows) z *= 2;
+  return z;
+}
+
+template <int EPI>
+int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 16) return -2;
   const int ncols = EPI == EPI_SWIGLU ? 2 * a.N : a.N;   // B rows the tiles cover
+  // the pipelined split-K kernel for STORE / RESID; the SwiGLU GEMM (wide N) keeps the kernel below
+  if (EPI != EPI_SWIGLU && a.K % kBK == 0) {
+    const int z = gemm_splits(a.M, ncols, a.K, a.part != nullptr ? part_rows : 0, EPI);
+    const long long nb = (long long)cdiv_i(a.M, kGT) * cdiv_i(ncols, kGT);
+    if (nb > 0x7FFFFFFF) return -2;
+    dim3 grid((unsigned)nb, 1, z);
+    if constexpr (EPI != EPI_SWIGLU) {
+      if (z == 1) {
+        launch((k_gemm_p<EPI, false>), grid, dim3(256), 0, st, a);
+      } else {
+        launch((k_gemm_p<EPI, true>), grid, dim3(256), 0, st, a);
+        const long long total = (long long)a.M * a.N;
+        launch((k_gemm_fin<EPI>), dim3((unsigned)min(4096LL, (total + 255) / 256)), dim3(256), 0, st, a, z);
+      }
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+  }
   auto blocks = [&](int bm, int bn) { return (long long)cdiv_i(a.M, bm) * cdiv_i(ncols, bn); };
   int wm = 1, wn = 1;
   if (blocks(128, 128) >= 256) { wm = 2; wn = 2; }
