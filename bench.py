@@ -44,6 +44,21 @@ def gemv_bytes(cfg):
     }
 
 
+def measured_traffic(kind, cfg_name):
+    """HBM bytes per launch of the dominant kernel, as measured by the rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE passes summarised in profiles/ (scaled by a known-size copy); None when not recorded
+    for this configuration. The counters need the profiler, so the bench reads the recorded figure."""
+    path = os.path.join(ROOT, "profiles", "gemv_swiglu_c4_decode_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            _, k, c, v = line.split()
+            if k == kind and c == cfg_name:
+                return int(v)
+    return None
+
+
 def cpu_baseline(qm, prompt, seconds):
     """The oracle (NumPy restatement, bit-exact with the reference) decoding on this host's cores."""
     import numpy as np
@@ -83,6 +98,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager decode steps instead of a HIP graph")
+    ap.add_argument("--copy-calib-mb", type=int, default=0,
+                    help="first copy this many MiB device to device (the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the datapath runs on a single "
@@ -96,6 +114,14 @@ def main():
     from t2r_amd import weights as W
     from t2r_amd.model import ResidentModel
     cfg = C.get(args.config)
+    if args.copy_calib_mb > 0:
+        n = args.copy_calib_mb << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {n} bytes read, {n} bytes written")
+        del src, dst
     t0 = time.time()
     qm = W.QuantModel(cfg)
     log(f"{cfg.name}: weights generated and quantised in {time.time() - t0:.1f} s")
@@ -210,7 +236,7 @@ def main():
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
                      "bytes_per_launch": nbytes["ffn_up"], "avg_us": dom.get("avg_us"),
-                     "launches": dom.get("launches"), "traffic": None},
+                     "launches": dom.get("launches"), "traffic": measured_traffic("ffn_up", cfg.name)},
     }
 
     # ---- CPU baseline (+ a bit-exactness spot check of the same positions on the GPU)
