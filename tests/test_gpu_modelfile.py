@@ -1,0 +1,81 @@
+"""LlamaDevice on model files: a .w8a8 (version 1 and 2) with a tokenizer.bin next to it runs the
+same numbers as the in-memory model, and generate() takes text and yields text pieces
+(llm/runtime.py:75-146)."""
+import struct
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LETTERS = [chr(c).encode() for c in range(ord("a"), ord("z") + 1)]
+
+
+def tokenizer_bin(path, vocab):
+    """A tokenizer.bin of exactly `vocab` pieces: <unk>, <s>, </s>, " ", a..z, " a".." z", then
+    two-letter pieces (scores favour the " x" merges)."""
+    pieces = [b"<unk>", b"\n<s>\n", b"\n</s>\n", b" "] + LETTERS + [b" " + c for c in LETTERS]
+    scores = [0.0] * 4 + [-5.0] * 26 + [-1.0] * 26
+    extra = [a + b for a in LETTERS for b in LETTERS]
+    pieces += extra[:vocab - len(pieces)]
+    scores += [-3.0] * (vocab - len(scores))
+    assert len(pieces) == vocab
+    with open(path, "wb") as f:
+        f.write(struct.pack("<i", 8))
+        for p, s in zip(pieces, scores):
+            f.write(struct.pack("<fi", s, len(p)))
+            f.write(p)
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny-qwen"])
+def test_llamadevice_from_w8a8(tmp_path, name):
+    import t2r_amd.config as C
+    from t2r_amd import modelfile as MF
+    from t2r_amd import weights as W
+    from t2r_amd.runtime import LlamaDevice
+    cfg = C.get(name)
+    qm = W.QuantModel(cfg)
+    path = str(tmp_path / f"{name}.w8a8")
+    MF.write_w8a8(qm, path)
+    tokenizer_bin(str(tmp_path / "tokenizer.bin"), cfg.vocab)
+    print(f"{name}: files written", flush=True)
+    a = LlamaDevice(qm)
+    b = LlamaDevice(path)                                  # tokenizer.bin found next to the model
+    assert b.tok is not None and b.cfg.vocab == cfg.vocab
+    toks = b.tok.encode("ab c")
+    assert toks[0] == 1 and len(toks) >= 3
+    for t in toks[:6]:
+        la, lb = a.forward(t), b.forward(t)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    got = list(b.generate("ab c", steps=min(12, cfg.seq_len)))
+    want = list(a.generate(toks, steps=min(12, cfg.seq_len)))
+    assert [t for t, _ in got] == [t for t, _ in want]
+    assert all(isinstance(s, str) for _, s in got)
+    with pytest.raises(ValueError):
+        next(a.generate("text without a tokenizer"))
+    a.close()
+    b.close()
+
+
+def test_llamadevice_from_llama2c_checkpoint(tmp_path):
+    """A llama2.c fp32 checkpoint is quantised on load (the KV scales calibrated over an fp32 run):
+    its greedy tokens equal those of the same arrays through QuantModel.from_arrays."""
+    import t2r_amd.config as C
+    from t2r_amd import modelfile as MF
+    from t2r_amd import weights as W
+    from t2r_amd.runtime import LlamaDevice
+    cfg = C.get("tiny")
+    w = {"tok": W.fp32_tensor(cfg, "tok"), "rms_final": W.fp32_tensor(cfg, "rms_final")}
+    for n in ("rms_att", "rms_ffn", "wq", "wk", "wv", "wo", "w1", "w2", "w3"):
+        w[n] = np.stack([W.fp32_tensor(cfg, n, l) for l in range(cfg.layers)])
+    path = str(tmp_path / "tiny.bin")
+    MF.write_llama2c(path, cfg, w)
+    dev = LlamaDevice(path)
+    c2, w2 = MF.read_llama2c(path)
+    qm = MF.quant_model_from_fp32(c2, w2)
+    ref = LlamaDevice(qm)
+    assert dev.tok is None
+    prompt = [1, 5, 9, 17]
+    assert [t for t, _ in dev.generate(prompt, steps=10)] == [t for t, _ in ref.generate(prompt, steps=10)]
+    dev.close()
+    ref.close()

@@ -1,0 +1,443 @@
+"""Model files and tokenizers of the reference's runtime, read (and written) on the host.
+
+- `.w8a8` device files (llm/export_w8a8.py:15-30 layout, :97-128 writer, :131-167 reader): a
+  64-byte header, a table of 32-byte entries, then every tensor 64-byte aligned; per-layer
+  tensors at layer_base + l * layer_stride. Linear weights are stored as D-wide B tiles
+  (out / D, in, D): tile t holds output rows [t D, (t + 1) D) transposed. Version 1 is the
+  reference's llama2.c-shaped model. Version 2 (this package's extension, which a version-1 reader
+  refuses) adds what version 1 cannot express: q_dim != dim, QK-norm, MoE, theta / eps, the RoPE
+  method and an untied classifier, in a `cfg` entry and extra named tensors; its linear weights
+  are row-major (out, in) int8 (the B tiles serve the reference's matrix engine, not this device).
+- llama2.c legacy fp32 checkpoints (llm/checkpoint.py:30-59): 7 int32 (dim, hidden, layers, heads,
+  kv_heads, vocab, seq_len; vocab < 0: separate classifier), then the fp32 tensors in run.c's order.
+- `tokenizer.bin`, llama2.c's SentencePiece-style BPE (llm/tokenizer.py:10-67).
+- HuggingFace `tokenizer.json` through the `tokenizers` library, which the reference's own port
+  (compiler/frontend/hf_tokenizer.py:1-20) states it is identical to.
+"""
+import dataclasses
+import os
+import re
+import struct
+
+import numpy as np
+
+from . import config as C
+from . import weights as W
+
+F = np.float32
+MAGIC = b"W8A8LLM\0"
+HEADER = struct.Struct("<8s12I")      # magic, version, D, dim, hidden, layers, heads, kv_heads, vocab,
+#                                       seq_len, n_entries, layer_base, layer_stride (padded to 64 bytes)
+ENTRY = struct.Struct("<16s4I")       # name, offset, bytes, per_layer, reserved
+ALIGN = 64
+V1_LAYER = ("rms_att", "rms_ffn", "wqkv", "s_wqkv", "wo", "s_wo", "w13", "s_w13", "w2", "s_w2", "kvp")
+INT8 = {"emb_q", "wcls", "wqkv", "wo", "w13", "w2", "router", "wg", "wu", "wd"}
+BOS, EOS = 1, 2
+
+
+def _up(n):
+    return (n + ALIGN - 1) // ALIGN * ALIGN
+
+
+# ------------------------------------------------------------------ B tiles
+def to_tiles(q, d):
+    """int8 rows (out, in) -> D-wide B tiles (out / d, in, d): tiles[t, k, j] = q[t d + j, k]."""
+    out, k = q.shape
+    if out % d or k % d:
+        raise ValueError(f"linear {out} x {k} is not a multiple of D = {d}")
+    return np.ascontiguousarray(np.swapaxes(q.reshape(out // d, d, k), 1, 2))
+
+
+def from_tiles(tiles):
+    """B tiles (n, in, d) -> rows (n d, in)."""
+    n, k, d = tiles.shape
+    return np.ascontiguousarray(np.swapaxes(tiles, 1, 2).reshape(n * d, k))
+
+
+# ------------------------------------------------------------------ .w8a8
+def _rope_wide(t, width):
+    """Per-head table (seq, hd / 2) -> (seq, width): column c holds pair c // 2 of its head (each value
+    twice, for both elements of its rotation pair)."""
+    hp = t.shape[1]
+    return np.ascontiguousarray(t[:, (np.arange(width) // 2) % hp]).astype(F)
+
+
+def _rope_head(wide, hd):
+    """(seq, width) -> the per-head table (seq, hd / 2); every head's columns must agree."""
+    hp = hd // 2
+    first = wide[:, 0:hd:2]
+    for h in range(1, wide.shape[1] // hd):
+        if not np.array_equal(wide[:, h * hd:(h + 1) * hd:2].view(np.uint32), first.view(np.uint32)):
+            raise ValueError("RoPE table differs between heads")
+    if not np.array_equal(wide[:, 1:hd:2].view(np.uint32), first.view(np.uint32)):
+        raise ValueError("RoPE table pair elements differ")
+    return np.ascontiguousarray(first[:, :hp]).astype(F)
+
+
+def _kvp(qm):
+    """(L, 8) float32: s_k, s_v, 1/s_k, 1/s_v, s_k / sqrt(head_dim), s_v / 127, 0, 0 per layer."""
+    out = np.zeros((qm.cfg.layers, 8), F)
+    out[:, 0:2] = qm.kv_scales
+    out[:, 2:6] = qm.kvc
+    return out
+
+
+_CFG_WORDS = 16
+
+
+def _cfg_block(c):
+    w = np.zeros(_CFG_WORDS, np.uint32)
+    w[0:6] = [c.head_dim, int(c.qk_norm), int(c.tied), c.n_experts, c.top_k, 1 if c.rope_method == "f64" else 0]
+    w[6:8] = np.array([c.eps], np.float64).view(np.uint32)       # float64: the config's values exactly
+    w[8:10] = np.array([c.theta], np.float64).view(np.uint32)
+    return w
+
+
+def is_v1(cfg):
+    """Whether the reference's version-1 layout can hold the model (llama2.c shape: q_dim == dim,
+    head_dim = dim / heads, no QK-norm, no MoE)."""
+    c = cfg
+    return (c.q_dim == c.dim and c.head_dim * c.heads == c.dim and not c.qk_norm and not c.moe
+            and c.eps == 1e-5 and c.rope_method == "f32" and c.theta == 10000.0)
+
+
+def write_w8a8(qm, path, d=None):
+    """Write a QuantModel as a .w8a8 file (version 1 when the model fits it, else 2); returns bytes."""
+    c = qm.cfg
+    d = d or c.D
+    v1 = is_v1(c)
+    width = c.dim if v1 else c.head_dim
+    lin = (lambda q: to_tiles(q, d)) if v1 else (lambda q: q)
+    glob = [("emb_q", qm.emb_q), ("emb_s", qm.emb_s), ("rms_final", qm.rms_final),
+            ("wcls", lin(qm.cls_q)), ("s_wcls", qm.cls_s),
+            ("rope_cos", _rope_wide(qm.cos, width)), ("rope_sin", _rope_wide(qm.sin, width))]
+    if not v1:
+        glob.append(("cfg", _cfg_block(c)))
+    kvp = _kvp(qm)
+
+    def layer(l):
+        t = [("rms_att", qm.rms_att[l]), ("rms_ffn", qm.rms_ffn[l]), ("wqkv", lin(qm.wqkv[l])),
+             ("s_wqkv", qm.s_wqkv[l]), ("wo", lin(qm.wo[l])), ("s_wo", qm.s_wo[l])]
+        if c.moe:
+            t += [("router", qm.router[l]), ("s_router", qm.s_router[l]), ("wg", qm.wg[l]), ("s_wg", qm.s_wg[l]),
+                  ("wu", qm.wu[l]), ("s_wu", qm.s_wu[l]), ("wd", qm.wd[l]), ("s_wd", qm.s_wd[l])]
+        else:
+            t += [("w13", lin(np.concatenate([qm.w1[l], qm.w3[l]]))),
+                  ("s_w13", np.concatenate([qm.s_w1[l], qm.s_w3[l]])),
+                  ("w2", lin(qm.w2[l])), ("s_w2", qm.s_w2[l])]
+        t.append(("kvp", kvp[l]))
+        if c.qk_norm:
+            t += [("q_norm", qm.q_norm[l]), ("k_norm", qm.k_norm[l])]
+        return [(n, np.ascontiguousarray(a)) for n, a in t]
+
+    first = layer(0)
+    n_entries = len(glob) + len(first)
+    offs, pos = [], _up(64 + ENTRY.size * n_entries)
+    for n, a in glob:
+        offs.append((n, pos, a.nbytes, 0))
+        pos = _up(pos + a.nbytes)
+    layer_base, rel = pos, 0
+    for n, a in first:
+        offs.append((n, rel, a.nbytes, 1))
+        rel = _up(rel + a.nbytes)
+    stride = rel
+    total = layer_base + stride * c.layers
+    with open(path, "wb") as f:
+        f.truncate(total)
+        f.seek(0)
+        f.write(HEADER.pack(MAGIC, 1 if v1 else 2, d, c.dim, c.hidden, c.layers, c.heads, c.kv_heads, c.vocab,
+                            c.seq_len, n_entries, layer_base, stride))
+        f.seek(64)
+        for n, o, nb, per in offs:
+            f.write(ENTRY.pack(n.encode().ljust(16, b"\0"), o, nb, per, 0))
+        for (n, a), (_, o, _, _) in zip(glob, offs):
+            f.seek(o)
+            f.write(a.tobytes())
+        for l in range(c.layers):
+            for (n, a), (_, o, nb, _) in zip(layer(l) if l else first, offs[len(glob):]):
+                if a.nbytes != nb:
+                    raise ValueError(f"layer {l}: {n} has {a.nbytes} bytes, layer 0 {nb}")
+                f.seek(layer_base + l * stride + o)
+                f.write(a.tobytes())
+    return total
+
+
+class W8A8File:
+    """A .w8a8 file, memory-mapped: header fields, the entry table and each tensor as a view."""
+
+    def __init__(self, path):
+        self.path = path
+        self.raw = np.memmap(path, dtype=np.uint8, mode="r")
+        if self.raw.size < 64:
+            raise ValueError(f"{path}: not a w8a8 file")
+        h = HEADER.unpack(self.raw[:HEADER.size].tobytes())
+        if h[0] != MAGIC or h[1] not in (1, 2):
+            raise ValueError(f"{path}: not a w8a8 v1 / v2 file")
+        (self.version, self.d, self.dim, self.hidden, self.layers, self.heads, self.kv_heads, self.vocab,
+         self.seq_len, n, self.layer_base, self.layer_stride) = h[1:]
+        self.entries = {}
+        for i in range(n):
+            name, off, nb, per, _ = ENTRY.unpack(self.raw[64 + i * ENTRY.size:64 + (i + 1) * ENTRY.size].tobytes())
+            self.entries[name.rstrip(b"\0").decode()] = (off, nb, bool(per))
+        end = self.layer_base + self.layer_stride * self.layers
+        if end > self.raw.size:
+            raise ValueError(f"{path}: {self.raw.size} bytes, the layers need {end}")
+
+    def offset(self, name, layer=None):
+        off, _, per = self.entries[name]
+        if per:
+            if layer is None:
+                raise ValueError(f"{name} is per layer")
+            return self.layer_base + layer * self.layer_stride + off
+        return off
+
+    def get(self, name, layer=None):
+        """The tensor's bytes as a flat view of its element type (int8 weights, uint32 cfg, float32)."""
+        off, nb = self.offset(name, layer), self.entries[name][1]
+        dt = np.int8 if name in INT8 else (np.uint32 if name == "cfg" else F)
+        return self.raw[off:off + nb].view(dt)
+
+    def config(self, name=None):
+        """The ModelConfig the file describes."""
+        name = name or os.path.splitext(os.path.basename(self.path))[0]
+        base = dict(name=name, dim=self.dim, hidden=self.hidden, layers=self.layers, heads=self.heads,
+                    kv_heads=self.kv_heads, vocab=self.vocab, seq_len=self.seq_len, D=self.d)
+        if self.version == 1:
+            return C.ModelConfig(head_dim=self.dim // self.heads, theta=10000.0, eps=1e-5, rope_method="f32",
+                                 tied=False, **base)
+        w = self.get("cfg")
+        return C.ModelConfig(head_dim=int(w[0]), qk_norm=bool(w[1]), tied=bool(w[2]), n_experts=int(w[3]),
+                             top_k=int(w[4]), rope_method="f64" if w[5] else "f32",
+                             eps=float(np.array(w[6:8]).view(np.float64)[0]),
+                             theta=float(np.array(w[8:10]).view(np.float64)[0]), **base)
+
+    def quant_model(self, name=None):
+        """The QuantModel (row-major int8 weights) of the file. A version-1 classifier equal to the
+        embedding rows becomes a tied one (one copy on the device)."""
+        c = self.config(name)
+        L, d, hd = c.layers, self.d, c.head_dim
+
+        def rows(x, n_out, k):                     # a linear's int8 rows from its stored form
+            return from_tiles(x.reshape(n_out // d, k, d)) if self.version == 1 else np.asarray(x).reshape(n_out, k)
+        a = {"emb_q": self.get("emb_q").reshape(c.vocab, c.dim), "emb_s": self.get("emb_s"),
+             "rms_final": self.get("rms_final")}
+        cls_q = rows(self.get("wcls"), c.vocab, c.dim)
+        cls_s = np.array(self.get("s_wcls"))
+        if self.version == 1 and np.array_equal(cls_q, a["emb_q"]) and np.array_equal(
+                cls_s.view(np.uint32), a["emb_s"].view(np.uint32)):
+            c = dataclasses.replace(c, tied=True)
+        a["cls_q"], a["cls_s"] = (a["emb_q"], a["emb_s"]) if c.tied else (cls_q, cls_s)
+        a["cos"] = _rope_head(self.get("rope_cos").reshape(c.seq_len, -1), hd)
+        a["sin"] = _rope_head(self.get("rope_sin").reshape(c.seq_len, -1), hd)
+
+        def per(n, f=lambda x: x):
+            return np.stack([f(self.get(n, l)) for l in range(L)])
+        a["rms_att"], a["rms_ffn"] = per("rms_att"), per("rms_ffn")
+        a["wqkv"] = per("wqkv", lambda x: rows(x, c.q_dim + 2 * c.kv_dim, c.dim))
+        a["s_wqkv"] = per("s_wqkv")
+        a["wo"] = per("wo", lambda x: rows(x, c.dim, c.q_dim))
+        a["s_wo"] = per("s_wo")
+        if c.moe:
+            E, Fh = c.n_experts, c.hidden
+            a["router"], a["s_router"] = per("router", lambda x: x.reshape(E, c.dim)), per("s_router")
+            a["wg"], a["s_wg"] = per("wg", lambda x: x.reshape(E, Fh, c.dim)), per("s_wg", lambda x: x.reshape(E, Fh))
+            a["wu"], a["s_wu"] = per("wu", lambda x: x.reshape(E, Fh, c.dim)), per("s_wu", lambda x: x.reshape(E, Fh))
+            a["wd"], a["s_wd"] = per("wd", lambda x: x.reshape(E, c.dim, Fh)), per("s_wd", lambda x: x.reshape(E, c.dim))
+        else:
+            w13 = per("w13", lambda x: rows(x, 2 * c.hidden, c.dim))
+            s13 = per("s_w13")
+            a["w1"], a["w3"] = w13[:, :c.hidden], w13[:, c.hidden:]
+            a["s_w1"], a["s_w3"] = s13[:, :c.hidden], s13[:, c.hidden:]
+            a["w2"] = per("w2", lambda x: rows(x, c.dim, c.hidden))
+            a["s_w2"] = per("s_w2")
+        kvp = per("kvp")
+        a["kv_scales"], a["kvc"] = kvp[:, 0:2], kvp[:, 2:6]
+        if c.qk_norm:
+            a["q_norm"], a["k_norm"] = per("q_norm"), per("k_norm")
+        return W.QuantModel.from_arrays(c, a)
+
+
+def read_w8a8(path, name=None):
+    """QuantModel of a .w8a8 file."""
+    return W8A8File(path).quant_model(name)
+
+
+# ------------------------------------------------------------------ llama2.c checkpoints
+def read_llama2c(path):
+    """(ModelConfig, {name: float32 array}) of a llama2.c legacy checkpoint, memory-mapped.
+    Names: tok, rms_att, wq, wk, wv, wo, rms_ffn, w1, w2, w3, rms_final, wcls (the embedding
+    when shared); linear weights (out, in) per layer."""
+    raw = np.memmap(path, dtype=F, mode="r")
+    if raw.size < 7:
+        raise ValueError(f"{path}: not a llama2.c checkpoint")
+    dim, hidden, layers, heads, kv_heads, vocab, seq = struct.unpack("<7i", raw[:7].tobytes())
+    shared = vocab > 0
+    vocab = abs(vocab)
+    if min(dim, hidden, layers, heads, kv_heads, vocab, seq) <= 0 or dim % heads:
+        raise ValueError(f"{path}: header {dim, hidden, layers, heads, kv_heads, vocab, seq} is not a llama2.c one")
+    hs = dim // heads
+    kv = kv_heads * hs
+    order = [("tok", (vocab, dim)), ("rms_att", (layers, dim)), ("wq", (layers, dim, dim)), ("wk", (layers, kv, dim)),
+             ("wv", (layers, kv, dim)), ("wo", (layers, dim, dim)), ("rms_ffn", (layers, dim)),
+             ("w1", (layers, hidden, dim)), ("w2", (layers, dim, hidden)), ("w3", (layers, hidden, dim)),
+             ("rms_final", (dim,)), ("rope", (seq * hs,))]       # run.c's (unused) precomputed RoPE floats
+    if not shared:
+        order.append(("wcls", (vocab, dim)))
+    w, pos = {}, 7
+    for name, shape in order:
+        n = int(np.prod(shape))
+        w[name] = raw[pos:pos + n].reshape(shape)
+        pos += n
+    if pos != raw.size:
+        raise ValueError(f"{path}: {raw.size} floats, a llama2.c checkpoint of this header has {pos}")
+    del w["rope"]
+    if shared:
+        w["wcls"] = w["tok"]
+    cfg = C.ModelConfig(name=os.path.splitext(os.path.basename(path))[0], dim=dim, hidden=hidden, layers=layers,
+                        heads=heads, kv_heads=kv_heads, head_dim=hs, vocab=vocab, seq_len=seq, theta=10000.0,
+                        eps=1e-5, rope_method="f32", tied=shared)
+    return cfg, w
+
+
+def quant_model_from_fp32(cfg, w, kv_scales=None, calib_tokens=None):
+    """Quantise fp32 llama2.c-named weights (read_llama2c) as the reference's exporter does
+    (llm/export_w8a8.py:75-95: per-row int8 of every linear, q | k | v rows stacked). kv_scales
+    (layers, 2) as the reference's --kv file; None: calibrated by an fp32 run of calib_tokens."""
+    L = cfg.layers
+
+    def stack(fn):
+        qs = [fn(l) for l in range(L)]
+        return np.stack([q for q, _ in qs]), np.stack([s for _, s in qs])
+    a = {}
+    a["emb_q"], a["emb_s"] = W.quantize_rows(w["tok"])
+    if cfg.tied:
+        a["cls_q"], a["cls_s"] = a["emb_q"], a["emb_s"]
+    else:
+        a["cls_q"], a["cls_s"] = W.quantize_rows(w["wcls"])
+    a["rms_final"] = np.array(w["rms_final"], F)
+    a["rms_att"], a["rms_ffn"] = np.array(w["rms_att"], F), np.array(w["rms_ffn"], F)
+    a["wqkv"], a["s_wqkv"] = stack(lambda l: W.quantize_rows(np.concatenate([w["wq"][l], w["wk"][l], w["wv"][l]])))
+    for n in ("wo", "w1", "w3", "w2"):
+        a[n], a["s_" + n] = stack(lambda l, n=n: W.quantize_rows(w[n][l]))
+    if kv_scales is None:
+        names = {"tok": "tok"}
+
+        def weight(c, name, layer=-1):
+            v = w[names.get(name, name)]
+            return np.asarray(v if layer < 0 or name == "tok" else v[layer], F)
+        toks = list(calib_tokens) if calib_tokens is not None else [BOS] + list(range(3, 3 + min(31, cfg.vocab - 3)))
+        kv_scales = W.calibrate_kv(cfg, toks, weight=weight)
+    a["kv_scales"] = np.asarray(kv_scales, F).reshape(L, 2)
+    return W.QuantModel.from_arrays(cfg, a)
+
+
+def write_llama2c(path, cfg, w):
+    """Write fp32 weights as a llama2.c legacy checkpoint (the layout read_llama2c reads)."""
+    hs = cfg.dim // cfg.heads
+    with open(path, "wb") as f:
+        f.write(struct.pack("<7i", cfg.dim, cfg.hidden, cfg.layers, cfg.heads, cfg.kv_heads,
+                            cfg.vocab if cfg.tied else -cfg.vocab, cfg.seq_len))
+        for n in ("tok", "rms_att", "wq", "wk", "wv", "wo", "rms_ffn", "w1", "w2", "w3", "rms_final"):
+            f.write(np.ascontiguousarray(w[n], F).tobytes())
+        f.write(np.zeros(cfg.seq_len * hs, F).tobytes())
+        if not cfg.tied:
+            f.write(np.ascontiguousarray(w["wcls"], F).tobytes())
+
+
+# ------------------------------------------------------------------ tokenizers
+class Llama2cTokenizer:
+    """tokenizer.bin of llama2.c: int32 max_token_length, then per id a float32 score, an int32
+    length and the piece's bytes. encode() follows run.c (llm/tokenizer.py:24-52): BOS, a " " dummy
+    prefix for non-empty text, one piece per UTF-8 code point (else its bytes, id = byte + 3), then
+    repeatedly the adjacent pair whose merged piece has the highest score (the leftmost such pair
+    on ties) is merged. decode() prints as run.c: the space after BOS dropped, <0xNN> pieces as
+    their byte, other single bytes only when printable or whitespace."""
+
+    def __init__(self, path, vocab_size):
+        with open(path, "rb") as f:
+            data = f.read()
+        (self.max_token_length,) = struct.unpack_from("<i", data, 0)
+        pos = 4
+        self.pieces, self.scores = [], []
+        for _ in range(vocab_size):
+            score, n = struct.unpack_from("<fi", data, pos)
+            pos += 8
+            self.pieces.append(data[pos:pos + n])
+            self.scores.append(score)
+            pos += n
+        self.ids = {}
+        for i, p in enumerate(self.pieces):
+            if p not in self.ids:                # the first id of a repeated piece wins
+                self.ids[p] = i
+        self._hex = re.compile(rb"<0x([0-9A-Fa-f]{2})>")
+
+    def encode(self, text, bos=True, eos=False):
+        data = text.encode("utf-8")
+        out = [BOS] if bos else []
+        if data:
+            out.append(self.ids[b" "])
+        i = 0
+        while i < len(data):
+            j = i + 1
+            while j < len(data) and j - i < 4 and (data[j] & 0xC0) == 0x80:
+                j += 1
+            cp = data[i:j]
+            tid = self.ids.get(cp)
+            out.extend([tid] if tid is not None else [b + 3 for b in cp])
+            i = j
+        while len(out) > 1:                       # over the whole list, BOS included, as run.c
+            best = None                            # (score, position, id)
+            for k in range(len(out) - 1):
+                tid = self.ids.get(self.pieces[out[k]] + self.pieces[out[k + 1]])
+                if tid is not None and (best is None or self.scores[tid] > best[0]):
+                    best = (self.scores[tid], k, tid)
+            if best is None:
+                break
+            _, k, tid = best
+            out[k:k + 2] = [tid]
+        if eos:
+            out.append(EOS)
+        return out
+
+    def piece(self, prev, token):
+        p = self.pieces[token]
+        if prev == BOS and p.startswith(b" "):
+            p = p[1:]
+        m = self._hex.fullmatch(p)
+        if m:
+            p = bytes([int(m.group(1), 16)])
+        if len(p) == 1 and not (32 <= p[0] < 127 or p in (b" ", b"\t", b"\n", b"\r", b"\x0b", b"\x0c")):
+            return b""
+        return p
+
+    def decode(self, tokens):
+        """Text of a token sequence that starts with BOS (run.c's printing of tokens[1:])."""
+        return b"".join(self.piece(a, b) for a, b in zip(tokens, tokens[1:])).decode("utf-8", "replace")
+
+
+class HFTokenizer:
+    """A HuggingFace tokenizer.json (a file, or a directory holding one) through the `tokenizers`
+    library: encode() without the file's post-processor (BOS only when asked), decode() keeping
+    special tokens, as the reference's port does (compiler/frontend/hf_tokenizer.py:149-205)."""
+
+    def __init__(self, path, bos_id=None):
+        from tokenizers import Tokenizer
+        if os.path.isdir(path):
+            path = os.path.join(path, "tokenizer.json")
+        self.tk = Tokenizer.from_file(path)
+        self.bos_id = bos_id
+
+    def encode(self, text, bos=True, eos=False):
+        ids = self.tk.encode(text, add_special_tokens=False).ids
+        return ([self.bos_id] if bos and self.bos_id is not None else []) + ids
+
+    def decode(self, tokens):
+        return self.tk.decode(list(tokens), skip_special_tokens=False)
+
+
+def open_tokenizer(path, vocab_size, bos_id=None):
+    """tokenizer.bin (llama2.c, BOS = 1) or tokenizer.json / a directory with one (HuggingFace; BOS
+    prepended only when bos_id is given, as the reference's callers do)."""
+    if os.path.isdir(path) or path.endswith(".json"):
+        return HFTokenizer(path, bos_id=bos_id)
+    return Llama2cTokenizer(path, vocab_size)

@@ -1,8 +1,8 @@
 """The llm/runtime.py API on the MI355X datapath: LlamaDevice and run.c's Sampler.
 
-    dev = LlamaDevice("c1-stories15m")                     # a config (synthetic weights) or a QuantModel
-    for tok, text in dev.generate([1, 400, 22], steps=64):
-        ...
+    dev = LlamaDevice("stories15M_d16.w8a8", "tokenizer.bin")
+    for tok, text in dev.generate("Once upon a time", steps=64, temperature=0.8, topp=0.9):
+        print(text, end="", flush=True)
     dev.close()
 
 Same methods, arguments, yields and exceptions as the reference's LlamaDevice
@@ -10,15 +10,22 @@ Same methods, arguments, yields and exceptions as the reference's LlamaDevice
 the logits and advances pos (ValueError when the sequence is full, RuntimeError when a step
 fails), generate() feeds the prompt through the decode path and then samples. The FPGA-only
 constructor arguments (bitfile, firmware, use_irq) are accepted and ignored; `device` names the
-GPU ("cuda:0") instead of an injectable PYNQ Device. Additions: prefill() runs prompt rows
-through the int8 MFMA GEMM path (bit-identical to feeding them one by one), and
+GPU ("cuda:0") instead of an injectable PYNQ Device.
+
+Models: the reference's .w8a8 files (version 1; version 2, this package's extension, for
+q_dim != dim, QK-norm and MoE), llama2.c fp32 checkpoints (quantised on load), a config name
+(synthetic weights) or a QuantModel. Tokenizers: llama2.c tokenizer.bin (the default, next to
+the model file) and HuggingFace tokenizer.json (t2r_amd.modelfile). Additions: prefill() runs
+prompt rows through the int8 MFMA GEMM path (bit-identical to feeding them one by one), and
 greedy_on_device() runs a whole greedy loop without host round trips.
 """
+import os
 import time
 
 import numpy as np
 
 from . import config as C
+from . import modelfile as MF
 from . import weights as W
 from .model import ResidentModel
 
@@ -73,19 +80,28 @@ def _resolve_model(model):
     if isinstance(model, C.ModelConfig):
         return W.QuantModel(model)
     if isinstance(model, str):
+        if os.path.isfile(model):
+            if model.endswith(".bin"):                     # llama2.c fp32 checkpoint: quantised here
+                cfg, w = MF.read_llama2c(model)
+                return MF.quant_model_from_fp32(cfg, w)
+            return MF.read_w8a8(model)                      # the device file (llm/runtime.py:80)
         return W.QuantModel(C.get(model))
-    raise TypeError(f"model: a ModelConfig, a config name or a QuantModel, not {type(model).__name__}")
+    raise TypeError(f"model: a .w8a8 / llama2.c .bin path, a ModelConfig, a config name or a QuantModel, "
+                    f"not {type(model).__name__}")
 
 
 class LlamaDevice:
     def __init__(self, model_path, tokenizer_path=None, bitfile=None, firmware=None, use_irq=True, device=None,
-                 max_rows=None):
+                 max_rows=None, bos_id=None):
         self.qm = _resolve_model(model_path)
         c = self.cfg = self.qm.cfg
         self.d = c.D
         self.tok = None
+        if tokenizer_path is None and isinstance(model_path, str) and os.path.isfile(model_path):
+            guess = os.path.join(os.path.dirname(os.path.abspath(model_path)), "tokenizer.bin")
+            tokenizer_path = guess if os.path.exists(guess) else None     # (the reference's default)
         if tokenizer_path is not None:
-            raise NotImplementedError("tokenizer files are not supported yet; pass token ids")
+            self.tok = MF.open_tokenizer(tokenizer_path, c.vocab, bos_id=bos_id)
         self.m = ResidentModel(self.qm, device=device or "cuda:0", max_rows=max_rows)
         self.pos = 0
         self.stats = []                          # per token: (pos, device ns, wall seconds)
@@ -130,9 +146,14 @@ class LlamaDevice:
 
     def generate(self, prompt, steps=256, temperature=0.0, topp=0.9, seed=1, stop_at_bos=True, forced=None):
         """Yield (token, text piece) per generated token, run.c style: the prompt tokens are fed first,
-        then sampled tokens until `steps` positions (or BOS). prompt: token ids (a tokenizer is not
-        loaded; the text piece is None). forced: teacher forcing, yields (argmax, logits) per position."""
+        then sampled tokens until `steps` positions (or BOS). prompt: text (encoded by the loaded
+        tokenizer, BOS first) or token ids; the text piece is None without a tokenizer. forced:
+        teacher forcing, yields (argmax, logits) per position."""
         self.reset()
+        if forced is None and isinstance(prompt, str):
+            if self.tok is None:
+                raise ValueError("a text prompt needs a tokenizer (tokenizer_path); pass token ids instead")
+            prompt = self.tok.encode(prompt)
         toks = list(forced) if forced is not None else list(prompt)
         sample = Sampler(temperature, topp, seed)
         token = toks[0]
@@ -147,8 +168,14 @@ class LlamaDevice:
             nxt = toks[pos + 1] if pos + 1 < len(toks) else sample(logits)
             if nxt == BOS and stop_at_bos:
                 return
-            yield nxt, None
+            yield nxt, self._piece(token, nxt)
             token = nxt
+
+    def _piece(self, token, nxt):
+        """The text nxt adds after token (llm/runtime.py:146: decode of the pair minus decode of token)."""
+        if self.tok is None:
+            return None
+        return self.tok.decode([token, nxt])[len(self.tok.decode([token])):]
 
     def greedy_on_device(self, prompt, steps, use_prefill=True):
         """Prompt (prefilled, or fed as decode steps), then greedy decode until `steps` positions, with

@@ -72,7 +72,7 @@ def fp32_tensor(cfg, name, layer=-1):
     """One fp32 tensor of the synthetic model (PyTorch orientation: linear weights are (out, in))."""
     d, q, kv, f = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden
     E = cfg.n_experts
-    shapes = {"tok": ((cfg.vocab, d), d), "wq": ((q, d), d), "wk": ((kv, d), d), "wv": ((kv, d), d),
+    shapes = {"tok": ((cfg.vocab, d), d), "wcls": ((cfg.vocab, d), d), "wq": ((q, d), d), "wk": ((kv, d), d), "wv": ((kv, d), d),
               "wo": ((d, q), q), "w1": ((f, d), d), "w3": ((f, d), d), "w2": ((d, f), f),
               "router": ((E, d), d), "wg": ((E, f, d), d), "wu": ((E, f, d), d), "wd": ((E, d, f), f)}
     if name in ("rms_att", "rms_ffn", "rms_final"):
@@ -162,6 +162,45 @@ class QuantModel:
         self.kv_scales = np.asarray(kv_scales, F).reshape(L, 2)
         self.kvc = kv_constants(c, self.kv_scales)
 
+    # the arrays a model consists of (dense; MoE replaces w1 / w3 / w2 with router / wg / wu / wd)
+    DENSE = ("w1", "s_w1", "w3", "s_w3", "w2", "s_w2")
+    MOE = ("router", "s_router", "wg", "s_wg", "wu", "s_wu", "wd", "s_wd")
+    COMMON = ("emb_q", "emb_s", "rms_final", "rms_att", "rms_ffn", "q_norm", "k_norm", "wqkv", "s_wqkv", "wo",
+              "s_wo", "cls_q", "cls_s", "cos", "sin", "kv_scales", "kvc")
+
+    @classmethod
+    def from_arrays(cls, cfg, arrays):
+        """A model from given arrays (a model file's), no synthetic generation: every name of COMMON
+        and of DENSE or MOE, with the shapes the class docstring states; q_norm / k_norm may be None
+        (gains of 1), kvc may be None (computed from kv_scales), cos / sin may be None (computed)."""
+        cfg.validate()
+        self = cls.__new__(cls)
+        self.cfg = c = cfg
+        L, hd = c.layers, c.head_dim
+        for k in cls.COMMON + (cls.MOE if c.moe else cls.DENSE):
+            v = arrays.get(k)
+            if v is None and k in ("q_norm", "k_norm"):
+                v = np.ones((L, hd), F)
+            if v is None and k in ("cos", "sin", "kvc"):
+                continue
+            if v is None:
+                raise ValueError(f"{cfg.name}: array {k} missing")
+            setattr(self, k, np.ascontiguousarray(v))
+        if getattr(self, "cos", None) is None or getattr(self, "sin", None) is None:
+            self.cos, self.sin = rope_tables(c)
+        self.kv_scales = np.asarray(self.kv_scales, F).reshape(L, 2)
+        if getattr(self, "kvc", None) is None:
+            self.kvc = kv_constants(c, self.kv_scales)
+        expect = {"emb_q": (c.vocab, c.dim), "wqkv": (L, c.q_dim + 2 * c.kv_dim, c.dim), "wo": (L, c.dim, c.q_dim),
+                  "cls_q": (c.vocab, c.dim), "cos": (c.seq_len, hd // 2), "sin": (c.seq_len, hd // 2),
+                  "kvc": (L, 4), "rms_att": (L, c.dim), "rms_ffn": (L, c.dim), "rms_final": (c.dim,)}
+        if not c.moe:
+            expect.update({"w1": (L, c.hidden, c.dim), "w3": (L, c.hidden, c.dim), "w2": (L, c.dim, c.hidden)})
+        for k, shp in expect.items():
+            if getattr(self, k).shape != shp:
+                raise ValueError(f"{cfg.name}: {k} has shape {getattr(self, k).shape}, expected {shp}")
+        return self
+
     def digest(self):
         """sha256 over every array (a fingerprint of the model data)."""
         h = hashlib.sha256()
@@ -174,12 +213,13 @@ class QuantModel:
 
 
 # ------------------------------------------------------------------ KV calibration
-def _fp32_forward_rows(cfg, tokens, amax_out):
+def _fp32_forward_rows(cfg, tokens, amax_out, weight=None):
     """Causal fp32 forward of `tokens` at positions 0.. (all rows at once, torch on the CPU),
     recording max|k| and max|v| per layer (after RoPE for k). llama2.c run.c semantics
     (llm/ref_model.py:45-91) generalised as compiler/frontend/qhf.py:206-243."""
     import torch
     c = cfg
+    fp32_tensor = weight if weight is not None else globals()["fp32_tensor"]
     M = len(tokens)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
     H, Hk, hd = c.heads, c.kv_heads, c.head_dim
@@ -196,7 +236,7 @@ def _fp32_forward_rows(cfg, tokens, amax_out):
         return torch.stack((-p[..., 1], p[..., 0]), dim=-1).reshape(v.shape)
 
     with torch.no_grad():
-        x = t(fp32_tensor(c, "tok"))[torch.tensor(tokens)]
+        x = t(fp32_tensor(c, "tok", -1))[torch.tensor(tokens)]
         mask = torch.tril(torch.ones(M, M, dtype=torch.bool))
         for l in range(c.layers):
             xb = rms(x, t(fp32_tensor(c, "rms_att", l)))
@@ -234,13 +274,14 @@ def _fp32_forward_rows(cfg, tokens, amax_out):
                 x = x + h @ t(fp32_tensor(c, "w2", l)).T
 
 
-def calibrate_kv(cfg, tokens=None, chunk=None):
+def calibrate_kv(cfg, tokens=None, chunk=None, weight=None):
     """Static per-layer KV scales: max(absmax, 1e-8) / 127 over an fp32 run of the prompt
-    (llm/test_l4.py:51-55, compiler/frontend/qhf.py:246-251)."""
+    (llm/test_l4.py:51-55, compiler/frontend/qhf.py:246-251). weight(cfg, name, layer): the fp32
+    tensors (default: the synthetic ones of fp32_tensor)."""
     tokens = cfg.prompt() if tokens is None else list(tokens)
     tokens = tokens[:cfg.seq_len]
     amax = np.zeros((cfg.layers, 2), np.float64)
-    _fp32_forward_rows(cfg, tokens, amax)
+    _fp32_forward_rows(cfg, tokens, amax, weight)
     return (np.maximum(amax, 1e-8) / 127.0).astype(F)
 
 
