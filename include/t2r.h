@@ -175,6 +175,16 @@ int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logi
 int t2r_prefill(void* model, const int32_t* tokens, const int32_t* positions, int M, float* last_logits,
                 int32_t* next_token, void* stream);
 
+/* Batched decode: one token of each of B sequences (BatchLlamaDevice.step llm/runtime.py:193-208;
+ * compile_batch.BatchCompiler llm/compile_batch.py:1-25): row b is sequence b at positions[b] with
+ * tokens[b], its KV cache at k_caches / v_caches + b * cache_stride bytes (each laid out as the
+ * model's k_cache / v_cache: [layers, seq_len, kv_dim] int8; cache_stride >= that size when B > 1).
+ * The linear layers run once over the B rows (int8 MFMA), attention per row; logits [B, vocab]
+ * fp32, next_tokens [B] the first maximum per row (may be NULL). Row b is bit-identical to a decode
+ * step of sequence b alone. B <= max_rows. The model's own caches are not touched. */
+int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* positions, int B, int8_t* k_caches,
+                     int8_t* v_caches, int64_t cache_stride, float* logits, int32_t* next_tokens, void* stream);
+
 /* Kernel timing of a resident model with HIP events on the launch stream (the GPU counterpart of
  * the reference's event counters and per-list cycle counts: rtl/sysarray/sa_perf.v,
  * driver/pynq_matmul.py:969-981, 1029-1066). t2r_model_profile creates 2 * max_launches events

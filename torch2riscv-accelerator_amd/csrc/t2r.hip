@@ -126,7 +126,7 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   } else if (mode == ATTN_PREP) {
     if (c16) launch((k_attn<ATTN_PREP, 16>), grid, block, lds, st, a);
     else launch((k_attn<ATTN_PREP, 8>), grid, block, lds, st, a);
-  } else if (a.tab != nullptr && pre_ok(a)) {
+  } else if (a.tab != nullptr && a.kv_row_stride == 0 && pre_ok(a)) {
     const int hdp = (a.hd + 31) & ~31;
     dim3 pg(a.H, cdiv(rows, kPreRows));
     const size_t pl = attn_pre_lds_bytes(a.S, hdp);
@@ -160,6 +160,10 @@ struct Model {
   int8_t* mxq;
   float* msx;
   int32_t* status;
+  // batched decode (t2r_decode_batch): the caches of the step's sequences, kv_rs bytes apart
+  int8_t* kcb = nullptr;
+  int8_t* vcb = nullptr;
+  long long kv_rs = 0;
   // kernel timing (t2r_model_profile)
   int prof_mask = 0;
   std::vector<hipEvent_t> ev;
@@ -296,8 +300,14 @@ int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, c
 }
 
 // one decoder layer on `rows` rows of the workspace at device positions pos[rows]
-int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStream_t st) {
+// RUN_DECODE: one row per decode GEMV (rows on grid y), fused attention; RUN_PREFILL: rows of one
+// sequence through the MFMA GEMMs and the prefill attention; RUN_BATCH: one sequence per row (its
+// own position and cache, m->kcb / m->vcb), the MFMA GEMMs and the fused per-row attention.
+enum { RUN_DECODE = 0, RUN_PREFILL = 1, RUN_BATCH = 2 };
+
+int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream_t st) {
   const t2r_model_desc& d = m->d;
+  const bool decode = mode == RUN_DECODE, batch = mode == RUN_BATCH;
   const long long L_dim = (long long)l * d.dim;
   const float inv_d = (float)(1.0 / d.dim);
   int rc;
@@ -321,8 +331,9 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
   AttnArgs at;
   std::memset(&at, 0, sizeof(at));
   at.qkv = m->qkv; at.qkv_stride = m->qkv_dim;
-  at.kc = d.k_cache + (long long)l * d.seq_len * m->kv_dim;
-  at.vc = d.v_cache + (long long)l * d.seq_len * m->kv_dim;
+  at.kc = (batch ? m->kcb : d.k_cache) + (long long)l * d.seq_len * m->kv_dim;
+  at.vc = (batch ? m->vcb : d.v_cache) + (long long)l * d.seq_len * m->kv_dim;
+  at.kv_row_stride = batch ? m->kv_rs : 0;
   at.pos = pos;
   at.qn = d.qk_norm ? d.q_norm + (long long)l * d.head_dim : nullptr;
   at.kn = d.qk_norm ? d.k_norm + (long long)l * d.head_dim : nullptr;
@@ -335,7 +346,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, bool decode, hipStr
   at.tab = sfu_table_ptr();
   {
     ProfScope p(m, T2R_PROF_ATTN, st);
-    if (decode) {
+    if (decode || batch) {
       if ((rc = attn_launch(ATTN_FUSED, at, rows, st))) return rc;
     } else {
       if ((rc = attn_launch(ATTN_PREP, at, rows, st))) return rc;
@@ -723,7 +734,7 @@ int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logi
   }
   if (rc) return rc;
   for (int l = 0; l < d.layers; ++l)
-    if ((rc = run_layer(m, l, 1, pos, true, st))) return rc;
+    if ((rc = run_layer(m, l, 1, pos, RUN_DECODE, st))) return rc;
   return run_final(m, 0, logits, next_token, pos, flags & T2R_ADVANCE_POS, st);
 }
 
@@ -740,8 +751,43 @@ int t2r_prefill(void* model, const int32_t* tokens, const int32_t* positions, in
   int rc = launched();
   if (rc) return rc;
   for (int l = 0; l < d.layers; ++l)
-    if ((rc = run_layer(m, l, M, positions, false, st))) return rc;
+    if ((rc = run_layer(m, l, M, positions, RUN_PREFILL, st))) return rc;
   return run_final(m, M - 1, last_logits, next_token, nullptr, 0, st);
+}
+
+int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* positions, int B, int8_t* k_caches,
+                     int8_t* v_caches, int64_t cache_stride, float* logits, int32_t* next_tokens, void* stream) {
+  Model* m = (Model*)model;
+  if (!m || !tokens || !positions || !k_caches || !v_caches || !logits) return T2R_EINVAL;
+  if (B < 1 || B > m->d.max_rows) return T2R_ERANGE;
+  const t2r_model_desc& d = m->d;
+  const long long cache_bytes = (long long)d.layers * d.seq_len * m->kv_dim;
+  if (B > 1 && cache_stride < cache_bytes) return T2R_ESHAPE;
+  T2R_INIT();
+  hipStream_t st = S(stream);
+  launch(k_embed, dim3(B), dim3(256), 0, st, d.emb_q, d.emb_s, tokens, d.dim, d.vocab, m->x, (long long)d.dim,
+         m->keys, 1, m->status);
+  int rc = launched();
+  if (rc) return rc;
+  m->kcb = k_caches;
+  m->vcb = v_caches;
+  m->kv_rs = B > 1 ? cache_stride : 0;
+  for (int l = 0; l < d.layers && rc == 0; ++l) rc = run_layer(m, l, B, positions, RUN_BATCH, st);
+  m->kcb = m->vcb = nullptr;
+  m->kv_rs = 0;
+  if (rc) return rc;
+  // every row's final RMSNorm + quant_act, the classifier over the rows, a first-maximum per row
+  if ((rc = rows_quant(m, m->x, d.dim, d.rms_final, d.dim, B, st))) return rc;
+  {
+    ProfScope p(m, T2R_PROF_CLS, st);
+    if ((rc = rows_linear<EPI_STORE>(m, d.cls_q, d.cls_s, nullptr, nullptr, d.vocab, d.dim, B, logits, d.vocab, st)))
+      return rc;
+  }
+  if (next_tokens) {
+    launch(k_argmax, dim3(B), dim3(256), 0, st, (const float*)logits, d.vocab, next_tokens);
+    return launched();
+  }
+  return T2R_OK;
 }
 
 }  // extern "C"

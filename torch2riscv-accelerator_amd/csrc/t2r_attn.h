@@ -43,6 +43,8 @@ struct AttnArgs {
   float* att;                // [rows, q_dim] (stride att_stride)
   long long att_stride;
   const float* tab;          // the SFU tables in device memory (k_attn_dec)
+  long long kv_row_stride;   // bytes between the caches of consecutive rows (batched decode: one
+                             // sequence per row); 0: every row uses the one cache (prefill rows)
 };
 
 // RMSNorm (optional) and RoPE of one head vector v[0..hd) in LDS, by one wave.
@@ -114,6 +116,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
   const int lane = tid & 63, wave = tid >> 6;
   const int hd = a.hd, G = a.H / a.Hk, S = a.S, g = h / G;
   const int q_dim = a.H * hd, kv_dim = a.Hk * hd;
+  a.kc += row * a.kv_row_stride;                 // this row's sequence cache
+  a.vc += row * a.kv_row_stride;
   const int pos = a.pos[row];
   if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
   const int T = pos + 1;
@@ -332,6 +336,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int G = a.H / a.Hk, g = h / G, S = a.S;
+  a.kc += row * a.kv_row_stride;                 // this row's sequence cache
+  a.vc += row * a.kv_row_stride;
   const long long q_dim = (long long)a.H * HD;
   const int kv_dim = a.Hk * HD;
   const int pos = a.pos[row];

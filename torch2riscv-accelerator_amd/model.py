@@ -142,6 +142,36 @@ class ResidentModel:
             i += M
         return self.logits
 
+    def batch_caches(self, B):
+        """Zeroed KV caches for B sequences of decode_batch: two int8 tensors (B, layers, seq_len, kv_dim)."""
+        c = self.cfg
+        kc = self.torch.zeros((B, c.layers, c.seq_len, c.kv_dim), dtype=self.torch.int8, device=self.device)
+        return kc, self.torch.zeros_like(kc)
+
+    def decode_batch(self, tokens, positions, kc, vc, logits=None, next_tokens=None):
+        """One decode token of each of B sequences (t2r_decode_batch): row b is tokens[b] at
+        positions[b] with the caches kc[b] / vc[b] (batch_caches). Returns the logits [B, vocab]
+        (a device tensor: `logits` when given); next_tokens, when given, receives each row's argmax."""
+        torch = self.torch
+        B = len(tokens)
+        if not 1 <= B <= self.max_rows:
+            raise ValueError(f"{B} sequences: between 1 and max_rows = {self.max_rows}")
+        if len(positions) != B or kc.shape[0] < B or vc.shape != kc.shape:
+            raise ValueError("one position and one cache per sequence")
+        c = self.cfg
+        if kc.shape[1:] != (c.layers, c.seq_len, c.kv_dim) or kc.dtype != torch.int8 or not kc.is_contiguous():
+            raise ValueError("caches: contiguous int8 (B, layers, seq_len, kv_dim), as batch_caches makes them")
+        pos = [int(p) for p in positions]
+        if min(pos) < 0 or max(pos) >= c.seq_len:
+            raise ValueError(f"positions outside [0, {c.seq_len})")
+        self.rows_tok[:B].copy_(torch.tensor([int(t) for t in tokens], dtype=torch.int32))
+        self.rows_pos[:B].copy_(torch.tensor(pos, dtype=torch.int32))
+        out = logits if logits is not None else torch.empty((B, c.vocab), dtype=torch.float32, device=self.device)
+        abi.check("t2r_decode_batch", self.lib.t2r_decode_batch(
+            self.handle, abi.ptr(self.rows_tok), abi.ptr(self.rows_pos), B, abi.ptr(kc), abi.ptr(vc),
+            kc[0].numel(), abi.ptr(out), abi.ptr(next_tokens), abi.stream_ptr()))
+        return out
+
     def prefill_chunks(self, tokens, M=16):
         """The reference's chunk schedule (compiler/frontend/export.py:69-72): chunks of M rows at
         0, M, 2M, ... and a last one at P - M (it recomputes rows the one before wrote, with the same

@@ -211,3 +211,96 @@ class LlamaDevice:
 
     def close(self):
         self.m.close()
+
+
+class BatchLlamaDevice:
+    """Batched decode (llm/runtime.py:155-245): `slots` sequences per step, each with its own KV
+    cache and position; step() runs one token of every slot through t2r_decode_batch (the linear
+    layers once over all rows on the int8 matrix cores, attention per row). A slot without a
+    sequence runs a dummy token (BOS) at pos 0; its KV row 0 is rewritten when a sequence starts in
+    it. Every row is bit-identical to the same token of that sequence run alone. slots defaults to
+    the model's D, the reference's batch width."""
+    DUMMY = BOS
+
+    def __init__(self, model_path, tokenizer_path=None, bitfile=None, firmware=None, use_irq=True, device=None,
+                 slots=None, bos_id=None):
+        self.qm = _resolve_model(model_path)
+        c = self.cfg = self.qm.cfg
+        self.d = int(slots or c.D)
+        self.tok = None
+        if tokenizer_path is None and isinstance(model_path, str) and os.path.isfile(model_path):
+            guess = os.path.join(os.path.dirname(os.path.abspath(model_path)), "tokenizer.bin")
+            tokenizer_path = guess if os.path.exists(guess) else None
+        if tokenizer_path is not None:
+            self.tok = MF.open_tokenizer(tokenizer_path, c.vocab, bos_id=bos_id)
+        self.m = ResidentModel(self.qm, device=device or "cuda:0", max_rows=self.d)
+        self.kc, self.vc = self.m.batch_caches(self.d)
+        self.stats = []                          # per step: (device ns or None, wall seconds)
+
+    def clear_slot(self, b):
+        """Empty slot b's KV cache."""
+        self.kc[b].zero_()
+        self.vc[b].zero_()
+
+    def step(self, poses, tokens, perf=False):
+        """One token for each of the slots; returns the (slots, vocab) logits (float32 copy)."""
+        if len(poses) != self.d or len(tokens) != self.d:
+            raise ValueError(f"one position and one token per slot ({self.d})")
+        torch = self.m.torch
+        t0 = time.perf_counter()
+        if perf:
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record()
+        try:
+            lg = self.m.decode_batch(tokens, poses, self.kc, self.vc)
+            if perf:
+                ev1.record()
+            out = lg.cpu().numpy().copy()
+        except RuntimeError as e:
+            raise RuntimeError(f"step failed: {e}") from e
+        self.stats.append((int(ev0.elapsed_time(ev1) * 1e6) if perf else None, time.perf_counter() - t0))
+        return out
+
+    def generate(self, prompts, steps, stagger=0, temperature=0.0, topp=0.9, seed=1, on_logits=None):
+        """Generate for len(prompts) <= slots sequences at once; sequence b starts at step b * stagger
+        and runs `steps` positions (prompt tokens fed first, then sampled; BOS does not stop it).
+        prompts: texts (with a tokenizer) or token lists. on_logits(b, pos, logits) sees every
+        position. Returns the token lists."""
+        d = self.d
+        n = len(prompts)
+        if n > d:
+            raise ValueError(f"at most {d} sequences")
+        toks = []
+        for p in prompts:
+            if isinstance(p, str):
+                if self.tok is None:
+                    raise ValueError("text prompts need a tokenizer (tokenizer_path)")
+                p = self.tok.encode(p)
+            toks.append(list(p))
+        steps = min(steps, self.cfg.seq_len)
+        samplers = [Sampler(temperature, topp, seed + b) for b in range(n)]
+        out = [[t[0]] for t in toks]
+        start = [b * stagger for b in range(n)]
+        for b in range(d):
+            self.clear_slot(b)
+        total = max(start) + steps if n else 0
+        for s in range(total):
+            poses, cur, live = [0] * d, [self.DUMMY] * d, [False] * d
+            for b in range(n):
+                p = s - start[b]
+                if 0 <= p < steps:
+                    poses[b], cur[b], live[b] = p, out[b][p], True
+            logits = self.step(poses, cur)
+            for b in range(n):
+                if not live[b]:
+                    continue
+                p = poses[b]
+                if on_logits:
+                    on_logits(b, p, logits[b])
+                if p + 1 < steps:
+                    out[b].append(toks[b][p + 1] if p + 1 < len(toks[b]) else samplers[b](logits[b]))
+        return out
+
+    def close(self):
+        self.m.close()
+
