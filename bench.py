@@ -98,6 +98,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager decode steps instead of a HIP graph")
+    ap.add_argument("--batch", default="4,8,16",
+                    help="batched-decode sizes to time (t2r_decode_batch; '' to skip)")
+    ap.add_argument("--batch-steps", type=int, default=32)
     ap.add_argument("--copy-calib-mb", type=int, default=0,
                     help="first copy this many MiB device to device (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -192,6 +195,40 @@ def main():
     tok_s = steps / dt
     log(f"decode {mode}: {steps} steps, {dt / steps * 1e3:.3f} ms/token ({tok_s:.1f} tok/s)")
 
+    # (3) batched decode: B sequences per step, each continuing the prompt from its own copy of the
+    # prompt's KV rows; greedy tokens and positions stay on the device
+    batch = {}
+    from t2r_amd import abi
+    for B in [int(b) for b in args.batch.split(",") if b.strip()]:
+        K = min(args.batch_steps, cfg.seq_len - P - 2)
+        if B > rm.max_rows or K < 1:
+            continue
+        kc, vc = rm.batch_caches(B)
+        kc[:] = rm.kc
+        vc[:] = rm.vc
+        lg = torch.empty((B, cfg.vocab), dtype=torch.float32, device=rm.device)
+        toks, poss = rm.rows_tok[:B], rm.rows_pos[:B]
+
+        def bstep():
+            abi.check("t2r_decode_batch", rm.lib.t2r_decode_batch(
+                rm.handle, abi.ptr(toks), abi.ptr(poss), B, abi.ptr(kc), abi.ptr(vc), kc[0].numel(), abi.ptr(lg),
+                abi.ptr(toks), abi.stream_ptr()))
+            poss.add_(1)
+        toks.copy_((after_prompt.to(torch.int64) + torch.arange(B, device=rm.device)) % cfg.vocab)
+        poss.fill_(P)
+        bstep()
+        bstep()
+        poss.fill_(P)
+        sync()
+        t = time.perf_counter()
+        for _ in range(K):
+            bstep()
+        sync()
+        bdt = time.perf_counter() - t
+        batch[str(B)] = {"tok_s": round(B * K / bdt, 1), "ms_per_step": round(bdt / K * 1e3, 4), "steps": K}
+        log(f"batched decode B={B}: {bdt / K * 1e3:.3f} ms/step ({B * K / bdt:.0f} tok/s aggregate)")
+        del kc, vc, lg
+
     nbytes = gemv_bytes(cfg)
     classes = {}
     gemv_b = gemv_t = 0.0
@@ -231,6 +268,7 @@ def main():
         "gemv_all_GBps": round(gemv_b / gemv_t / 1e9, 1) if gemv_t else None,
         "gemv_all_frac": round(gemv_b / gemv_t / 1e9 / HBM_PEAK_GBS, 4) if gemv_t else None,
         "decode_mode": mode,
+        "batch_decode": batch,
         "eager_tok_s": round(steps / eager_dt, 2),
         "roofline": {"kernel": "k_gemv<PRO_NORM_QUANT, EPI_SWIGLU> (fused SwiGLU decode GEMV)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
