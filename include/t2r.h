@@ -175,6 +175,14 @@ int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logi
 int t2r_prefill(void* model, const int32_t* tokens, const int32_t* positions, int M, float* last_logits,
                 int32_t* next_token, void* stream);
 
+/* t2r_prefill at the positions start .. start + M - 1 (the reference's chunk schedule,
+ * compiler/frontend/export.py:69-72, compiler/runtime/tools/sa_llm_run.c:255-330). Every row then
+ * attends to at most start + M positions, which sizes the attention's score rows (and lets more
+ * of its workgroups share a CU than the cache length would); results are those of t2r_prefill.
+ * 0 <= start, start + M <= seq_len, M <= max_rows. */
+int t2r_prefill_at(void* model, const int32_t* tokens, int start, int M, float* last_logits, int32_t* next_token,
+                   void* stream);
+
 /* Batched decode: one token of each of B sequences (BatchLlamaDevice.step llm/runtime.py:193-208;
  * compile_batch.BatchCompiler llm/compile_batch.py:1-25): row b is sequence b at positions[b] with
  * tokens[b], its KV cache at k_caches / v_caches + b * cache_stride bytes (each laid out as the

@@ -137,3 +137,31 @@ def test_llamadevice_api():
     forced = list(dev.generate(None, steps=6, forced=[1, 2, 3, 4]))
     assert len(forced) == 4 and forced[0][1].shape == (C.TINY.vocab,)
     dev.close()
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen", "c1-stories15m"])
+def test_prefill_at_equals_prefill_with_positions(name):
+    """t2r_prefill_at (positions start.., score rows sized by start + M) and t2r_prefill (positions
+    passed in, score rows sized by the cache length) write the same KV rows and logits."""
+    import torch
+    import t2r_amd.config as C
+    from t2r_amd import abi
+    cfg = C.get(name)
+    qm, rm = resident(cfg, max_rows=32)
+    toks = (cfg.prompt() * 4)[:min(24, cfg.seq_len - 4)]
+    M, start = len(toks) - 4, 4
+    rm.reset()
+    rm.prefill(toks[:start])
+    rm.prefill(toks[start:], start=start)
+    a_lg, a_k, a_v = rm.logits.cpu().numpy().copy(), rm.kc.cpu().numpy().copy(), rm.vc.cpu().numpy().copy()
+    rm.reset()
+    rm.prefill(toks[:start])
+    rm.rows_tok[:M].copy_(torch.tensor(toks[start:], dtype=torch.int32))
+    rm.rows_pos[:M].copy_(torch.arange(start, start + M, dtype=torch.int32))
+    abi.check("t2r_prefill", rm.lib.t2r_prefill(rm.handle, abi.ptr(rm.rows_tok), abi.ptr(rm.rows_pos), M,
+                                                abi.ptr(rm.logits), None, abi.stream_ptr()))
+    assert np.array_equal(rm.logits.cpu().numpy().view(np.uint32), a_lg.view(np.uint32))
+    assert np.array_equal(rm.kc.cpu().numpy(), a_k) and np.array_equal(rm.vc.cpu().numpy(), a_v)
+    with pytest.raises(ValueError):
+        rm.prefill([1] * 4, start=cfg.seq_len - 2)
+    rm.close()

@@ -97,10 +97,13 @@ GemvArgs gemv_args() {
   return a;
 }
 
+// positions a prefill row may attend to: the caller's bound (t2r_prefill_at), else the cache length
+int pre_cap(const AttnArgs& a) { return a.t_cap > 0 && a.t_cap < a.S ? a.t_cap : a.S; }
+
 // the multi-row prefill attention: head dims 16..128 (multiples of 16), cache rows whose
 // score rows fit the LDS the kernels are set up for (kPreMaxLds)
 bool pre_ok(const AttnArgs& a) {
-  return a.hd % 16 == 0 && a.hd <= 128 && attn_pre_lds_bytes(a.S, (a.hd + 31) & ~31) <= kPreMaxLds;
+  return a.hd % 16 == 0 && a.hd <= 128 && attn_pre_lds_bytes(pre_cap(a), (a.hd + 31) & ~31) <= kPreMaxLds;
 }
 
 int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
@@ -129,7 +132,7 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   } else if (a.tab != nullptr && a.kv_row_stride == 0 && pre_ok(a)) {
     const int hdp = (a.hd + 31) & ~31;
     dim3 pg(a.H, cdiv(rows, kPreRows));
-    const size_t pl = attn_pre_lds_bytes(a.S, hdp);
+    const size_t pl = attn_pre_lds_bytes(pre_cap(a), hdp);
     if (hdp == 32) launch((k_attn_pre<32>), pg, dim3(kPreThreads), pl, st, a, rows);
     else if (hdp == 64) launch((k_attn_pre<64>), pg, dim3(kPreThreads), pl, st, a, rows);
     else launch((k_attn_pre<128>), pg, dim3(kPreThreads), pl, st, a, rows);
@@ -164,6 +167,9 @@ struct Model {
   int8_t* kcb = nullptr;
   int8_t* vcb = nullptr;
   long long kv_rs = 0;
+  // t2r_prefill_at: positions start .. start + M - 1 (device), and their bound for the attention
+  int32_t* pos_rows = nullptr;
+  int t_cap = 0;
   // kernel timing (t2r_model_profile)
   int prof_mask = 0;
   std::vector<hipEvent_t> ev;
@@ -228,6 +234,7 @@ long long carve(Model* m, char* base, int M) {
   m->mxq = c.take<int8_t>((long long)M * d.dim);
   m->msx = c.take<float>(M);
   m->status = c.take<int32_t>(1);
+  m->pos_rows = c.take<int32_t>(M);
   // split-K partial sums of the prefill linears: 4 splits of up to 512 rows of the widest
   // STORE / RESID output
   m->part_rows = M < 512 ? M : 512;
@@ -334,6 +341,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
   at.kc = (batch ? m->kcb : d.k_cache) + (long long)l * d.seq_len * m->kv_dim;
   at.vc = (batch ? m->vcb : d.v_cache) + (long long)l * d.seq_len * m->kv_dim;
   at.kv_row_stride = batch ? m->kv_rs : 0;
+  at.t_cap = mode == RUN_PREFILL ? m->t_cap : 0;
   at.pos = pos;
   at.qn = d.qk_norm ? d.q_norm + (long long)l * d.head_dim : nullptr;
   at.kn = d.qk_norm ? d.k_norm + (long long)l * d.head_dim : nullptr;
@@ -753,6 +761,22 @@ int t2r_prefill(void* model, const int32_t* tokens, const int32_t* positions, in
   for (int l = 0; l < d.layers; ++l)
     if ((rc = run_layer(m, l, M, positions, RUN_PREFILL, st))) return rc;
   return run_final(m, M - 1, last_logits, next_token, nullptr, 0, st);
+}
+
+int t2r_prefill_at(void* model, const int32_t* tokens, int start, int M, float* last_logits, int32_t* next_token,
+                   void* stream) {
+  Model* m = (Model*)model;
+  if (!m || !tokens) return T2R_EINVAL;
+  if (M < 1 || M > m->d.max_rows || start < 0 || start + M > m->d.seq_len) return T2R_ERANGE;
+  T2R_INIT();
+  hipStream_t st = S(stream);
+  launch(k_iota, dim3(cdiv(M, 256)), dim3(256), 0, st, m->pos_rows, start, M);
+  int rc = launched();
+  if (rc) return rc;
+  m->t_cap = start + M;
+  rc = t2r_prefill(model, tokens, m->pos_rows, M, last_logits, next_token, stream);
+  m->t_cap = 0;
+  return rc;
 }
 
 int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* positions, int B, int8_t* k_caches,

@@ -45,6 +45,8 @@ struct AttnArgs {
   const float* tab;          // the SFU tables in device memory (k_attn_dec)
   long long kv_row_stride;   // bytes between the caches of consecutive rows (batched decode: one
                              // sequence per row); 0: every row uses the one cache (prefill rows)
+  int t_cap;                 // prefill attention: every row attends to <= t_cap positions (sizes the
+                             // score rows in LDS); 0: S
 };
 
 // RMSNorm (optional) and RoPE of one head vector v[0..hd) in LDS, by one wave.
@@ -615,7 +617,8 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   const int h = blockIdx.x, r0 = blockIdx.y * kPreRows, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int HD = a.hd, G = a.H / a.Hk, g = h / G, S = a.S, D = a.D;
-  const int kv_dim = a.Hk * HD, est = pre_est(S);
+  const int cap = a.t_cap > 0 && a.t_cap < S ? a.t_cap : S;   // positions a row may attend to
+  const int kv_dim = a.Hk * HD, est = pre_est(cap);
   if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = ((const v4f_t*)a.tab)[tid];
   __syncthreads();
 
@@ -642,7 +645,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
     }
     if (lane == 0) {
       s_sq[i] = sq;
-      s_T[i] = ok ? pos + 1 : 0;
+      s_T[i] = ok ? min(pos + 1, cap) : 0;       // (cap bounds every position by construction)
     }
   }
   __syncthreads();

@@ -259,6 +259,12 @@ __global__ __launch_bounds__(256) void k_argmax(const float* x, int n, int32_t* 
 }
 
 // End of a decode step: the greedy token from the argmax key; optionally pos += 1.
+// positions start .. start + n - 1 (t2r_prefill_at)
+__global__ __launch_bounds__(256) void k_iota(int32_t* out, int start, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = start + i;
+}
+
 __global__ void k_finish(const unsigned long long* key, int32_t* next_token, int32_t* pos, int advance) {
   if (threadIdx.x == 0) {
     if (next_token) *next_token = (int32_t)(0xFFFFFFFFu - (uint32_t)(*key & 0xFFFFFFFFu));

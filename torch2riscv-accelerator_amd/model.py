@@ -133,10 +133,9 @@ class ResidentModel:
             chunk = toks[i:i + self.max_rows]
             M = len(chunk)
             self.rows_tok[:M].copy_(torch.tensor(chunk, dtype=torch.int32))
-            self.rows_pos[:M].copy_(torch.arange(start + i, start + i + M, dtype=torch.int32))
             last = i + M >= len(toks)
-            abi.check("t2r_prefill", self.lib.t2r_prefill(
-                self.handle, abi.ptr(self.rows_tok), abi.ptr(self.rows_pos), M,
+            abi.check("t2r_prefill_at", self.lib.t2r_prefill_at(
+                self.handle, abi.ptr(self.rows_tok), start + i, M,
                 abi.ptr(self.logits) if (last and logits) else None, abi.ptr(self.next) if last else None,
                 abi.stream_ptr()))
             i += M
