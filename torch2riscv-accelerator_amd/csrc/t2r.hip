@@ -127,8 +127,7 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
     if (c16) launch((k_attn<ATTN_FUSED, 16>), grid, block, lds, st, a);
     else launch((k_attn<ATTN_FUSED, 8>), grid, block, lds, st, a);
   } else if (mode == ATTN_PREP) {
-    if (c16) launch((k_attn<ATTN_PREP, 16>), grid, block, lds, st, a);
-    else launch((k_attn<ATTN_PREP, 8>), grid, block, lds, st, a);
+    launch(k_attn_prep, dim3(cdiv(a.H + a.Hk, kPrepWaves), rows), dim3(64 * kPrepWaves), 0, st, a);
   } else if (a.tab != nullptr && a.kv_row_stride == 0 && pre_ok(a)) {
     const int hdp = (a.hd + 31) & ~31;
     dim3 pg(a.H, cdiv(rows, kPreRows));

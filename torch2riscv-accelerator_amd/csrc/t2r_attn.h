@@ -14,8 +14,8 @@
 // one of the group writes it to the cache, and each uses it from LDS, so no workgroup reads a
 // row another one writes.
 // Modes: ATTN_FUSED (decode: the stages, then attention), ATTN_PREP (prefill: the stages for every
-// row, q rotated in place), ATTN_ONLY (prefill: attention of rows whose q is rotated and whose KV
-// rows are all in the cache).
+// row, q rotated in place: k_attn_prep), ATTN_ONLY (prefill: attention of rows whose q is rotated
+// and whose KV rows are all in the cache).
 #pragma once
 #include "t2r_device.h"
 
@@ -153,22 +153,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     for (int j = lane; j < hd; j += 64) s_q[j] = qkv[h * hd + j];
     __builtin_amdgcn_wave_barrier();
     if (MODE != ATTN_ONLY) head_norm_rope(s_q, a.qn, a, pos, lane);
-    if (MODE == ATTN_PREP) {
-      for (int j = lane; j < hd; j += 64) qkv[h * hd + j] = s_q[j];
-    } else {
-      // quant_act of the head
-      float m = 0.0f;
-      for (int j = lane; j < hd; j += 64) m = nanmax(m, fabsf(s_q[j]));
-      m = wave_max(m);
-      const float sq = m * kInv127;
-      const float inv = sfu_recip(sq);
-      for (int j = lane; j < hd / 4; j += 64)
-        s_qq[j] = pack_i8x4(to_i8(s_q[4 * j] * inv), to_i8(s_q[4 * j + 1] * inv), to_i8(s_q[4 * j + 2] * inv),
-                            to_i8(s_q[4 * j + 3] * inv));
-      if (lane == 0) s_sq = sq;
-    }
+    // quant_act of the head
+    float m = 0.0f;
+    for (int j = lane; j < hd; j += 64) m = nanmax(m, fabsf(s_q[j]));
+    m = wave_max(m);
+    const float sq = m * kInv127;
+    const float inv = sfu_recip(sq);
+    for (int j = lane; j < hd / 4; j += 64)
+      s_qq[j] = pack_i8x4(to_i8(s_q[4 * j] * inv), to_i8(s_q[4 * j + 1] * inv), to_i8(s_q[4 * j + 2] * inv),
+                          to_i8(s_q[4 * j + 3] * inv));
+    if (lane == 0) s_sq = sq;
   }
-  if (MODE == ATTN_PREP) return;
   __syncthreads();
 
   // ---- scores: one thread per cache row, the row in chunks of CB bytes. sc is kept in the
@@ -583,6 +578,51 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 #pragma unroll
     for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
     out[(long long)h * HD + j] = (float)ssum * a.a_v;
+  }
+}
+
+// ---- prefill prep (ATTN_PREP): one wave per head vector of a row (the H query heads, then the Hk
+// KV heads): QK-norm and RoPE by head_norm_rope, the decode kernels' numerics; q back into qkv
+// (fp32), k and v to int8 into the cache row at the row's position. Each KV head's row is formed
+// once, by its own wave.
+constexpr int kPrepWaves = 4;
+
+__global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
+  __shared__ float sv[kPrepWaves][2][kMaxHd];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = blockIdx.y, vi = blockIdx.x * kPrepWaves + wave;
+  const int hd = a.hd;
+  if (vi >= a.H + a.Hk) return;                  // (wave-uniform; the kernel has no block barrier)
+  const int pos = a.pos[row];
+  if (pos < 0 || pos >= a.S) return;             // a position outside the cache: nothing is written
+  const int q_dim = a.H * hd, kv_dim = a.Hk * hd;
+  float* qkv = a.qkv + row * a.qkv_stride;
+  float* v0 = sv[wave][0];
+  if (vi < a.H) {
+    for (int j = lane; j < hd; j += 64) v0[j] = qkv[vi * hd + j];
+    __builtin_amdgcn_wave_barrier();
+    head_norm_rope(v0, a.qn, a, pos, lane);
+    for (int j = lane; j < hd; j += 64) qkv[vi * hd + j] = v0[j];
+    return;
+  }
+  const int g = vi - a.H;
+  float* v1 = sv[wave][1];
+  for (int j = lane; j < hd; j += 64) {
+    v0[j] = qkv[q_dim + g * hd + j];
+    v1[j] = qkv[q_dim + kv_dim + g * hd + j];
+  }
+  __builtin_amdgcn_wave_barrier();
+  head_norm_rope(v0, a.kn, a, pos, lane);
+  int8_t* kc = a.kc + row * a.kv_row_stride + (long long)pos * kv_dim + g * hd;
+  int8_t* vc = a.vc + row * a.kv_row_stride + (long long)pos * kv_dim + g * hd;
+  for (int j = lane; j < hd / 4; j += 64) {
+    int k4[4], v4[4];
+    for (int b = 0; b < 4; ++b) {
+      k4[b] = to_i8(v0[4 * j + b] * a.inv_sk);
+      v4[b] = to_i8(v1[4 * j + b] * a.inv_sv);
+    }
+    *(int*)(kc + 4 * j) = pack_i8x4(k4[0], k4[1], k4[2], k4[3]);
+    *(int*)(vc + 4 * j) = pack_i8x4(v4[0], v4[1], v4[2], v4[3]);
   }
 }
 
