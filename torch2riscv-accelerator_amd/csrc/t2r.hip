@@ -287,8 +287,25 @@ int rows_quant(Model* m, const float* x, long long x_stride, const float* g, int
   GemvArgs a = gemv_args();
   a.x = x; a.x_stride = x_stride; a.g = g; a.K = K; a.D = m->d.D; a.eps = m->d.eps; a.inv_n = (float)(1.0 / K);
   a.xq_out = m->xq; a.xq_stride = K; a.sx_out = m->sx;
-  launch(k_rows_norm_quant, dim3(rows), dim3(kGemvThreads), 0, st, a, g != nullptr ? 1 : 0, (float*)nullptr,
-                     0LL);
+  const bool staged = K % 16 == 0 && K <= kMaxK && a.tab != nullptr && ((uintptr_t)x & 15) == 0 && x_stride % 4 == 0 &&
+                      (g == nullptr || ((uintptr_t)g & 15) == 0);
+  if (!staged) {
+    launch(k_rows_norm_quant, dim3(rows), dim3(kGemvThreads), 0, st, a, g != nullptr ? 1 : 0, (float*)nullptr, 0LL);
+    return launched();
+  }
+  const int nc = cdiv(K, 1024);
+  const dim3 grid(rows), block(kGemvThreads);
+  if (g != nullptr) {
+    if (nc <= 1) launch((k_rows_quant<PRO_NORM_QUANT, 1>), grid, block, 0, st, a);
+    else if (nc <= 2) launch((k_rows_quant<PRO_NORM_QUANT, 2>), grid, block, 0, st, a);
+    else if (nc <= 4) launch((k_rows_quant<PRO_NORM_QUANT, 4>), grid, block, 0, st, a);
+    else launch((k_rows_quant<PRO_NORM_QUANT, 8>), grid, block, 0, st, a);
+  } else {
+    if (nc <= 1) launch((k_rows_quant<PRO_QUANT, 1>), grid, block, 0, st, a);
+    else if (nc <= 2) launch((k_rows_quant<PRO_QUANT, 2>), grid, block, 0, st, a);
+    else if (nc <= 4) launch((k_rows_quant<PRO_QUANT, 4>), grid, block, 0, st, a);
+    else launch((k_rows_quant<PRO_QUANT, 8>), grid, block, 0, st, a);
+  }
   return launched();
 }
 

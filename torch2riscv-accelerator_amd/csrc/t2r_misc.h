@@ -40,6 +40,24 @@ __global__ __launch_bounds__(kGemvThreads) void k_rows_norm_quant(GemvArgs a, in
   if (threadIdx.x == 0 && a.sx_out) a.sx_out[row] = s_x;
 }
 
+// Prefill rows: RMSNorm (PRO_NORM_QUANT) or quant_act alone (PRO_QUANT) of row blockIdx.x into the
+// int8 rows the MFMA GEMM reads (K <= 1024 NCB): the decode GEMV's staged prologue (inputs in
+// registers, lane-major squares for the one ordered chain, block max), same numerics.
+template <int PRO, int NCB>
+__global__ __launch_bounds__(kGemvThreads) void k_rows_quant(GemvArgs a) {
+  __shared__ __align__(16) int8_t xq_lds[1024 * NCB];
+  __shared__ __align__(16) float xf_lds[PRO == PRO_NORM_QUANT ? 1024 * NCB + 128 : 1];
+  __shared__ __align__(16) float tab_lds[kSfuWords];
+  __shared__ float red[64];
+  const int row = blockIdx.x;
+  XStage<PRO, EPI_STORE, NCB, kGemvThreads> st;
+  stage_load(st, a, row);
+  const float s_x = stage_finish(st, a, row, xq_lds, xf_lds, tab_lds, red);
+  int8_t* out = a.xq_out + row * a.xq_stride;
+  for (int i = threadIdx.x * 16; i < a.K; i += kGemvThreads * 16) *(v4i_t*)(out + i) = *(const v4i_t*)(xq_lds + i);
+  if (threadIdx.x == 0) a.sx_out[row] = s_x;
+}
+
 // RMSNorm alone (no quantisation): out = F(F(x * r) * g), r = RSQRT(F(F(ss * F(1/n)) + F(eps)))
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* g, int n, float inv_n, float eps, int D,
                                                  float* out) {
