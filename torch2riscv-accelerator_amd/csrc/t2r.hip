@@ -318,6 +318,7 @@ int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, c
   a.xq = m->xq; a.s_x = m->sx; a.w = w; a.s_w = s_w; a.w3 = w3; a.s_w3 = s_w3;
   a.M = rows; a.N = N; a.K = K; a.y = y; a.y_stride = y_stride; a.res = EPI == EPI_RESID ? y : nullptr;
   a.part = m->part;
+  a.part_cap = 4LL * m->part_rows * (m->qkv_dim > m->d.dim ? m->qkv_dim : m->d.dim);
   a.tab = sfu_table_ptr();
   return gemm_launch<EPI>(a, st, m->part_rows) ? T2R_EHIP : T2R_OK;
 }

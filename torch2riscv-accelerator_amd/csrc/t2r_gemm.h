@@ -113,6 +113,7 @@ struct GemmArgs {
   long long y_stride;
   int32_t* acc_out;          // optional [M, N] (SwiGLU: [M, 2N], W1 then W3 columns)
   int32_t* part;             // split-K partial sums [splits, M, N] (nullptr: no split)
+  long long part_cap;        // int32 elements `part` holds (0: as many as the GEMM split needs)
   const float* tab;          // SFU tables (device copy of c_sfu; required for EPI_SWIGLU)
 };
 
@@ -477,13 +478,162 @@ int gemm_d_launch(const GemmArgs& a, hipStream_t st, int part_rows, int ncols) {
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-// The M-row GEMM: the direct-to-LDS kernel when K % 64 == 0 (split-K into the caller's
+// ---- batched decode linears (M <= 32 activation rows): y[m][n] on int8 MFMA with every weight
+// byte read once, in whole 128-byte lines. A workgroup takes a tile of 32 weight rows (SwiGLU: 16
+// rows of W1 and the same 16 of W3) and kBgWin-byte k-windows of it, one window per wave at a time:
+// the wave copies its 32 x 256-byte window into its own 8 KB of LDS with global_load_lds (four rows
+// of 256 contiguous bytes per instruction), loads the matching activation bytes into registers in
+// the MFMA layout (L2-resident rows), then runs 8 k-steps of v_mfma_i32_32x32x32_i8 (A: activation
+// row lane % 32, B: weight row lane % 32, the same 16 k-bytes in both: exact int32 sums). No
+// workgroup barrier until the waves' tiles are added in LDS. With nz > 1 the windows are split over
+// nz workgroups per tile, which write int32 partials [nz, M, N] for k_gemm_fin. Activation rows past
+// M read row M - 1 and are never stored.
+constexpr int kBgMaxRows = 32;
+constexpr int kBgWin = 256;                       // k-bytes of a wave window
+constexpr int kBgWaveLds = 32 * kBgWin;           // one wave's window of 32 weight rows
+
+
+template <int EPI, int KW, bool SPLIT>
+__global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
+  extern __shared__ __align__(16) int8_t lds[];    // KW x kBgWaveLds
+  __shared__ __align__(16) float tab_lds[EPI == EPI_SWIGLU ? kSfuWords : 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, kh = lane >> 5;
+  constexpr int NT = EPI == EPI_SWIGLU ? 16 : 32;            // output columns per tile
+  const int tile = blockIdx.x / nz, z = blockIdx.x % nz;
+  const int n0 = tile * NT, K = a.K;
+  const int nwin = cdiv_i(K, kBgWin), wpz = cdiv_i(nwin, nz);
+  const int w_end = min(nwin, (z + 1) * wpz);
+  int8_t* wl = lds + wave * kBgWaveLds;
+  if (EPI == EPI_SWIGLU && tid < kSfuWords / 4) ((v4f_t*)tab_lds)[tid] = ((const v4f_t*)a.tab)[tid];
+  // chunk q of window row r sits at 256 r + 16 (q ^ (r & 15)): the 16 rows a 16-lane LDS pass reads
+  // (rows {0-3, 8-11, 20-23, 28-31} or the other 16 of a half-wave, one chunk) hit 16 bank groups
+  const int8_t* rowp[8];
+  int qo[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane >> 4);
+    qo[i] = 16 * ((lane & 15) ^ (r & 15));
+    if (EPI == EPI_SWIGLU) rowp[i] = (r < 16 ? a.w : a.w3) + (long long)min(n0 + (r & 15), a.N - 1) * K;
+    else rowp[i] = a.w + (long long)min(n0 + r, a.N - 1) * K;
+  }
+  const int8_t* xrow = a.xq + (long long)min(lr, a.M - 1) * K + 16 * kh;
+  // the epilogue's scales and residuals, loaded now (their latency hides under the weight stream):
+  // output i of this thread is o = tid + i 64 KW, (m, j) = (o / NT, o % NT)
+  constexpr int OPT = (32 * NT + 64 * KW - 1) / (64 * KW);
+  float e_sx[OPT], e_sw[OPT], e_sw3[OPT], e_res[OPT];
+  if constexpr (!SPLIT) {
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) {
+      const int o = tid + i * 64 * KW, m = min(o / NT, a.M - 1), n = min(n0 + o % NT, a.N - 1);
+      e_sx[i] = a.s_x[m];
+      e_sw[i] = a.s_w[n];
+      if (EPI == EPI_SWIGLU) e_sw3[i] = a.s_w3[n];
+      if (EPI == EPI_RESID) e_res[i] = a.res[(long long)m * a.y_stride + n];
+    }
+  }
+  v16i_t acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0;
+  for (int w = z * wpz + wave; w < w_end; w += KW) {
+    const int k0 = w * kBgWin, nst = min(kBgWin, K - k0) >> 5;   // k-steps of this window (uniform)
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i)                                 // (chunks past K: clamped, unused)
+      __builtin_amdgcn_global_load_lds((const void*)(rowp[i] + min(k0 + qo[i], K - 16)), (void*)(wl + 1024 * i), 16, 0, 0);
+    v4i_t xv[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) xv[st] = *(const v4i_t*)(xrow + min(k0 + 32 * st, K - 32));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      if (st < nst) {
+        const v4i_t wv = *(const v4i_t*)(wl + 256 * lr + 16 * ((2 * st + kh) ^ (lr & 15)));
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[st], wv, acc, 0, 0, 0);
+      }
+    }
+  }
+  // the wave's 32 x 32 tile into its own LDS (its DMA has landed and its reads are done)
+  asm volatile("" ::: "memory");
+  int* red = (int*)wl;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[((r >> 2) * 8 + kh * 4 + (r & 3)) * 33 + lr] = acc[r];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < OPT; ++i) {
+    const int o = tid + i * 64 * KW, m = o / NT, j = o % NT, n = n0 + j;
+    if (m >= a.M || n >= a.N) continue;
+    int s1 = 0, s3 = 0;
+#pragma unroll
+    for (int v = 0; v < KW; ++v) {
+      const int* rv = (const int*)(lds + v * kBgWaveLds);
+      s1 += rv[m * 33 + j];
+      if (EPI == EPI_SWIGLU) s3 += rv[m * 33 + 16 + j];
+    }
+    if constexpr (SPLIT) {
+      a.part[((long long)z * a.M + m) * a.N + n] = s1;
+    } else if constexpr (EPI == EPI_SWIGLU) {
+      a.y[(long long)m * a.y_stride + n] = silu_mul(dequant(s1, e_sw[i], e_sx[i]), dequant(s3, e_sw3[i], e_sx[i]), tab_lds);
+      if (a.acc_out) {
+        a.acc_out[(long long)m * 2 * a.N + n] = s1;
+        a.acc_out[(long long)m * 2 * a.N + a.N + n] = s3;
+      }
+    } else {
+      float v = dequant(s1, e_sw[i], e_sx[i]);
+      if (EPI == EPI_RESID) v = e_res[i] + v;
+      a.y[(long long)m * a.y_stride + n] = v;
+      if (a.acc_out) a.acc_out[(long long)m * a.N + n] = s1;
+    }
+  }
+}
+
+// the batched-decode linear when it applies (1 <= M <= 32, K % 32 == 0, 16-byte aligned rows), else -1.
+// Waves per workgroup: one per window up to 8; the windows split over up to 4 workgroups per tile when
+// the caller's partial buffer (a.part, a.part_cap int32) holds the partials (STORE / RESID only).
+template <int EPI>
+int bgemv_launch(const GemmArgs& a, hipStream_t st) {
+  if (a.M < 1 || a.M > kBgMaxRows || a.K % 32 || ((uintptr_t)a.w & 15) || ((uintptr_t)a.xq & 15)) return -1;
+  if (EPI == EPI_SWIGLU && (!a.tab || !a.w3 || ((uintptr_t)a.tab & 15) || ((uintptr_t)a.w3 & 15))) return -1;
+  const int nwin = cdiv_i(a.K, kBgWin);
+  const int kw = nwin >= 8 ? 8 : nwin >= 4 ? 4 : nwin >= 2 ? 2 : 1;
+  int nz = 1;
+  if (EPI != EPI_SWIGLU && a.part)
+    while (nz < 4 && nwin > kw * nz && (long long)(2 * nz) * a.M * a.N <= a.part_cap) nz *= 2;
+  const long long blocks = (long long)cdiv_i(a.N, EPI == EPI_SWIGLU ? 16 : 32) * nz;
+  if (blocks > 0x7FFFFFFF) return -2;
+  const dim3 grid((unsigned)blocks), block(64 * kw);
+  const size_t lb = (size_t)kw * kBgWaveLds;
+  auto go = [&](auto kern) { launch(kern, grid, block, lb, st, a, nz); };
+  if (nz > 1) {
+    if constexpr (EPI != EPI_SWIGLU) {
+      if (kw == 8) go(k_bgemv<EPI, 8, true>);
+      else if (kw == 4) go(k_bgemv<EPI, 4, true>);
+      else if (kw == 2) go(k_bgemv<EPI, 2, true>);
+      else go(k_bgemv<EPI, 1, true>);
+      const long long total = (long long)a.M * a.N;
+      launch((k_gemm_fin<EPI>), dim3((unsigned)min(4096LL, (total + 255) / 256)), dim3(256), 0, st, a, nz);
+    }
+  } else {
+    if (kw == 8) go(k_bgemv<EPI, 8, false>);
+    else if (kw == 4) go(k_bgemv<EPI, 4, false>);
+    else if (kw == 2) go(k_bgemv<EPI, 2, false>);
+    else go(k_bgemv<EPI, 1, false>);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// The M-row GEMM: the batched-decode kernel for M <= 32, else the direct-to-LDS kernel when K % 64 == 0 (split-K into the caller's
 // `part_rows`-row partial buffer for narrow layers), else the register-staged k_gemm with the
 // largest tile that still gives >= 256 workgroups (one per CU).
 template <int EPI>
 int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 16) return -2;
   if (EPI == EPI_SWIGLU && (a.tab == nullptr || ((uintptr_t)a.tab & 15))) return -1;
+  if (a.M <= kBgMaxRows) {                                 // few rows: stream the weights once
+    const int r = bgemv_launch<EPI>(a, st);
+    if (r != -1) return r;
+  }
   const int ncols = EPI == EPI_SWIGLU ? 2 * a.N : a.N;   // B rows the tiles cover
   // the direct-to-LDS kernel (split-K for the narrow STORE / RESID layers)
   if (a.K % 64 == 0) return a.K % 128 == 0 ? gemm_d_launch<EPI, 128, 2>(a, st, part_rows, ncols)
