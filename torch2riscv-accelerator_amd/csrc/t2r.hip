@@ -149,6 +149,11 @@ struct Model {
   int q_dim, kv_dim, qkv_dim, ffn_rows, max_in;
   int32_t* part;                    // split-K partial sums of the prefill linears
   int part_rows;
+  // a residual linear (Wo, W2) whose split-K partials in `part` are not yet added into x: the
+  // next row norm/quant of x finishes them in the same pass (k_rows_fin_quant), any other reader
+  // of x first runs the plain finish (fin_flush)
+  int pend_z = 0, pend_rows = 0;
+  const float* pend_sw = nullptr;
   float* x;
   float* qkv;
   float* att;
@@ -282,8 +287,53 @@ int validate(const t2r_model_desc* d) {
   return T2R_OK;
 }
 
-// RMSNorm (g != nullptr) and quant_act of `rows` rows x[rows, K] into the workspace's int8 rows
+// the pending residual linear's finish on its own: x += dequant(sum of the partials)
+int fin_flush(Model* m, hipStream_t st) {
+  if (m->pend_z <= 1) return T2R_OK;
+  GemmArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.s_x = m->sx; a.s_w = m->pend_sw; a.M = m->pend_rows; a.N = m->d.dim; a.K = m->d.dim;
+  a.y = m->x; a.y_stride = m->d.dim; a.res = m->x; a.part = m->part;
+  const int nz = m->pend_z;
+  m->pend_z = 0;
+  const long long total = (long long)a.M * a.N;
+  launch((k_gemm_fin<EPI_RESID>), dim3((unsigned)(total < 4096LL * 256 ? (total + 255) / 256 : 4096)), dim3(256), 0, st, a,
+         nz);
+  return launched();
+}
+
+int rows_quant_staged(Model* m, const float* x, long long x_stride, const float* g, int K, int rows, hipStream_t st);
+
+// RMSNorm (g != nullptr) and quant_act of `rows` rows x[rows, K] into the workspace's int8 rows. On
+// the residual rows with a pending residual-linear finish, the finish runs in the same pass.
 int rows_quant(Model* m, const float* x, long long x_stride, const float* g, int K, int rows, hipStream_t st) {
+  if (m->pend_z > 1 && x == m->x) {
+    const bool fused = g != nullptr && rows == m->pend_rows && K == m->d.dim && x_stride == K && K % 16 == 0 &&
+                       K <= 8 * 1024 && ((uintptr_t)g & 15) == 0;
+    if (!fused) {
+      int rc = fin_flush(m, st);
+      if (rc) return rc;
+    } else {
+      GemvArgs a = gemv_args();
+      a.x = x; a.x_stride = x_stride; a.g = g; a.K = K; a.D = m->d.D; a.eps = m->d.eps; a.inv_n = (float)(1.0 / K);
+      a.xq_out = m->xq; a.xq_stride = K; a.sx_out = m->sx;
+      FinArgs f;
+      f.part = m->part; f.zstride = (long long)rows * K; f.nz = m->pend_z; f.s_w = m->pend_sw; f.s_x = m->sx;
+      f.x = m->x;
+      m->pend_z = 0;
+      const int nc = cdiv(K, 1024);
+      const dim3 grid(rows), block(kGemvThreads);
+      if (nc <= 1) launch(k_rows_fin_quant<1>, grid, block, 0, st, a, f);
+      else if (nc <= 2) launch(k_rows_fin_quant<2>, grid, block, 0, st, a, f);
+      else if (nc <= 4) launch(k_rows_fin_quant<4>, grid, block, 0, st, a, f);
+      else launch(k_rows_fin_quant<8>, grid, block, 0, st, a, f);
+      return launched();
+    }
+  }
+  return rows_quant_staged(m, x, x_stride, g, K, rows, st);
+}
+
+int rows_quant_staged(Model* m, const float* x, long long x_stride, const float* g, int K, int rows, hipStream_t st) {
   GemvArgs a = gemv_args();
   a.x = x; a.x_stride = x_stride; a.g = g; a.K = K; a.D = m->d.D; a.eps = m->d.eps; a.inv_n = (float)(1.0 / K);
   a.xq_out = m->xq; a.xq_stride = K; a.sx_out = m->sx;
@@ -310,9 +360,11 @@ int rows_quant(Model* m, const float* x, long long x_stride, const float* g, int
 }
 
 // a prefill linear layer on the workspace's int8 rows (int8 MFMA)
+// defer_z (STORE): the caller finishes a split itself (its split count back in *defer_z, partials in
+// m->part). A residual linear into x leaves a split's finish pending for the next norm/quant of x.
 template <int EPI>
 int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, const float* s_w3, int N, int K, int rows,
-                float* y, long long y_stride, hipStream_t st) {
+                float* y, long long y_stride, hipStream_t st, int* defer_z = nullptr) {
   GemmArgs a;
   std::memset(&a, 0, sizeof(a));
   a.xq = m->xq; a.s_x = m->sx; a.w = w; a.s_w = s_w; a.w3 = w3; a.s_w3 = s_w3;
@@ -320,7 +372,18 @@ int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, c
   a.part = m->part;
   a.part_cap = 4LL * m->part_rows * (m->qkv_dim > m->d.dim ? m->qkv_dim : m->d.dim);
   a.tab = sfu_table_ptr();
-  return gemm_launch<EPI>(a, st, m->part_rows) ? T2R_EHIP : T2R_OK;
+  if (m->pend_z > 1) return T2R_ESTATE;          // the partials buffer still holds an unfinished linear
+  const bool resid_x = EPI == EPI_RESID && y == m->x && y_stride == m->d.dim && N == m->d.dim;
+  int z = 1;
+  if (gemm_launch<EPI>(a, st, m->part_rows, resid_x || defer_z ? &z : nullptr)) return T2R_EHIP;
+  if (defer_z) {
+    *defer_z = z;
+  } else if (z > 1) {
+    m->pend_z = z;
+    m->pend_rows = rows;
+    m->pend_sw = s_w;
+  }
+  return T2R_OK;
 }
 
 // one decoder layer on `rows` rows of the workspace at device positions pos[rows]
@@ -341,13 +404,15 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
   a.s_w = d.s_wqkv + (long long)l * m->qkv_dim;
   a.x = m->x; a.x_stride = d.dim; a.g = d.rms_att + L_dim; a.inv_n = inv_d; a.eps = d.eps; a.D = d.D;
   a.N = m->qkv_dim; a.K = d.dim; a.y = m->qkv; a.y_stride = m->qkv_dim;
+  int qz = 1;                                       // prefill: Wqkv's split finished by the prep kernel
   {
     ProfScope p(m, T2R_PROF_QKV, st);
     if (decode) {
       if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
     } else {
       if ((rc = rows_quant(m, m->x, d.dim, d.rms_att + L_dim, d.dim, rows, st))) return rc;
-      if ((rc = rows_linear<EPI_STORE>(m, a.w, a.s_w, nullptr, nullptr, m->qkv_dim, d.dim, rows, m->qkv, m->qkv_dim, st)))
+      if ((rc = rows_linear<EPI_STORE>(m, a.w, a.s_w, nullptr, nullptr, m->qkv_dim, d.dim, rows, m->qkv, m->qkv_dim, st,
+                                       mode == RUN_PREFILL ? &qz : nullptr)))
         return rc;
     }
   }
@@ -369,6 +434,10 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
   at.H = d.heads; at.Hk = d.kv_heads; at.hd = d.head_dim; at.D = d.D; at.S = d.seq_len;
   at.att = m->att; at.att_stride = m->q_dim;
   at.tab = sfu_table_ptr();
+  if (qz > 1) {
+    at.part = m->part; at.part_nz = qz; at.part_zstride = (long long)rows * m->qkv_dim;
+    at.part_sw = a.s_w; at.part_sx = m->sx;
+  }
   {
     ProfScope p(m, T2R_PROF_ATTN, st);
     if (decode || batch) {
@@ -426,6 +495,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
       }
     }
   } else {
+    if ((rc = fin_flush(m, st))) return rc;         // the router reads x
     const int E = d.n_experts, k = d.top_k, Fe = d.hidden;
     RouteArgs ra;
     std::memset(&ra, 0, sizeof(ra));
@@ -467,11 +537,12 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
 // final RMSNorm + quant_act + classifier of workspace row `row`, with the greedy argmax
 int run_final(Model* m, int row, float* logits, int32_t* next_token, int32_t* pos, int advance, hipStream_t st) {
   const t2r_model_desc& d = m->d;
+  int rc = fin_flush(m, st);
+  if (rc) return rc;
   GemvArgs a = gemv_args();
   a.w = d.cls_q; a.s_w = d.cls_s;
   a.x = m->x + (long long)row * d.dim; a.g = d.rms_final; a.inv_n = (float)(1.0 / d.dim); a.eps = d.eps; a.D = d.D;
   a.N = d.vocab; a.K = d.dim; a.y = logits ? logits : m->logits; a.argmax_key = m->keys;
-  int rc;
   {
     ProfScope p(m, T2R_PROF_CLS, st);
     rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, 1, st);
@@ -748,6 +819,7 @@ int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logi
   Model* m = (Model*)model;
   if (!m || !token || !pos) return T2R_EINVAL;
   T2R_INIT();
+  m->pend_z = 0;
   hipStream_t st = S(stream);
   const t2r_model_desc& d = m->d;
   int rc;
@@ -769,6 +841,7 @@ int t2r_prefill(void* model, const int32_t* tokens, const int32_t* positions, in
   if (!m || !tokens || !positions) return T2R_EINVAL;
   if (M < 1 || M > m->d.max_rows) return T2R_ERANGE;
   T2R_INIT();
+  m->pend_z = 0;
   hipStream_t st = S(stream);
   const t2r_model_desc& d = m->d;
   launch(k_embed, dim3(M), dim3(256), 0, st, d.emb_q, d.emb_s, tokens, d.dim, d.vocab, m->x,
@@ -805,6 +878,7 @@ int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* position
   const long long cache_bytes = (long long)d.layers * d.seq_len * m->kv_dim;
   if (B > 1 && cache_stride < cache_bytes) return T2R_ESHAPE;
   T2R_INIT();
+  m->pend_z = 0;
   hipStream_t st = S(stream);
   launch(k_embed, dim3(B), dim3(256), 0, st, d.emb_q, d.emb_s, tokens, d.dim, d.vocab, m->x, (long long)d.dim,
          m->keys, 1, m->status);

@@ -47,6 +47,14 @@ struct AttnArgs {
                              // sequence per row); 0: every row uses the one cache (prefill rows)
   int t_cap;                 // prefill attention: every row attends to <= t_cap positions (sizes the
                              // score rows in LDS); 0: S
+  // k_attn_prep: the Wqkv linear's split-K partials [part_nz, rows, qkv_stride] when part_nz > 1
+  // (then column c of a row is F(F(f32(sum_z part) * part_sw[c]) * part_sx[row]), the store
+  // epilogue, instead of qkv[c])
+  const int32_t* part;
+  long long part_zstride;
+  int part_nz;
+  const float* part_sw;
+  const float* part_sx;
 };
 
 // RMSNorm (optional) and RoPE of one head vector v[0..hd) in LDS, by one wave.
@@ -584,7 +592,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 // ---- prefill prep (ATTN_PREP): one wave per head vector of a row (the H query heads, then the Hk
 // KV heads): QK-norm and RoPE by head_norm_rope, the decode kernels' numerics; q back into qkv
 // (fp32), k and v to int8 into the cache row at the row's position. Each KV head's row is formed
-// once, by its own wave.
+// once, by its own wave. With Wqkv's split-K partials pending, the wave finishes its columns first.
 constexpr int kPrepWaves = 4;
 
 __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
@@ -597,9 +605,17 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
   if (pos < 0 || pos >= a.S) return;             // a position outside the cache: nothing is written
   const int q_dim = a.H * hd, kv_dim = a.Hk * hd;
   float* qkv = a.qkv + row * a.qkv_stride;
+  const int32_t* pr = a.part + row * a.qkv_stride;
+  const float sx = a.part_nz > 1 ? a.part_sx[row] : 0.0f;
+  auto col = [&](int c) {                        // column c of the row's [q | k | v]
+    if (a.part_nz <= 1) return qkv[c];
+    int acc = 0;
+    for (int z = 0; z < a.part_nz; ++z) acc += pr[z * a.part_zstride + c];
+    return dequant(acc, a.part_sw[c], sx);
+  };
   float* v0 = sv[wave][0];
   if (vi < a.H) {
-    for (int j = lane; j < hd; j += 64) v0[j] = qkv[vi * hd + j];
+    for (int j = lane; j < hd; j += 64) v0[j] = col(vi * hd + j);
     __builtin_amdgcn_wave_barrier();
     head_norm_rope(v0, a.qn, a, pos, lane);
     for (int j = lane; j < hd; j += 64) qkv[vi * hd + j] = v0[j];
@@ -608,8 +624,8 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
   const int g = vi - a.H;
   float* v1 = sv[wave][1];
   for (int j = lane; j < hd; j += 64) {
-    v0[j] = qkv[q_dim + g * hd + j];
-    v1[j] = qkv[q_dim + kv_dim + g * hd + j];
+    v0[j] = col(q_dim + g * hd + j);
+    v1[j] = col(q_dim + kv_dim + g * hd + j);
   }
   __builtin_amdgcn_wave_barrier();
   head_norm_rope(v0, a.kn, a, pos, lane);
@@ -654,7 +670,9 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   __shared__ __align__(16) int8_t VT[4][HDP][32];
   __shared__ float s_sq[kPreRows], s_r[kPreRows];
   __shared__ int s_T[kPreRows];
-  const int h = blockIdx.x, r0 = blockIdx.y * kPreRows, tid = threadIdx.x;
+  // row blocks in reverse: a causal prompt's later rows attend to more positions, and the blocks
+  // dispatched first should be the longest (the short ones then fill in behind them)
+  const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kPreRows, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int HD = a.hd, G = a.H / a.Hk, g = h / G, S = a.S, D = a.D;
   const int cap = a.t_cap > 0 && a.t_cap < S ? a.t_cap : S;   // positions a row may attend to

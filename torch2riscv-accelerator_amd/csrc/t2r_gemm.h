@@ -451,19 +451,24 @@ __global__ __launch_bounds__(256) void k_gemm_fin(GemmArgs a, int nz) {
   }
 }
 
-// split count for the pipelined GEMM: enough workgroups for the 256 CUs, >= 8 slabs each, and the
-// partials within the `part_rows` rows x 4 splits the caller's buffer holds (0: no buffer)
-inline int gemm_splits(int M, int ncols, int K, int part_rows, int epi) {
-  if (epi == EPI_SWIGLU || part_rows <= 0) return 1;
+// split count for the pipelined GEMM. Only a caller that finishes the partials in a pass it runs
+// anyway (`defer`) gets a split: a separate finishing pass costs more than the split saves (C4 prefill
+// Wqkv 512 x 3072 x 2048: 13.7 us whole, 15.8 + 6.3 us split in two). Up to one workgroup per CU,
+// >= 8 slabs each, the partials within the `part_rows` rows x 4 splits of the caller's buffer.
+inline int gemm_splits(int M, int ncols, int K, int part_rows, int epi, bool defer) {
+  if (epi == EPI_SWIGLU || part_rows <= 0 || !defer) return 1;
   const long long tiles = (long long)cdiv_i(M, kGT) * cdiv_i(ncols, kGT);
   int z = 1;
-  while (z < 4 && tiles * z * 2 <= 256 && K / kBK >= 16 * z && (long long)M * z * 2 <= 4LL * part_rows) z *= 2;
+  while (z < 4 && tiles * z <= 256 && K / kBK >= 16 * z && (long long)M * z * 2 <= 4LL * part_rows) z *= 2;
   return z;
 }
 
+// defer_z (STORE / RESID): when the launch splits K, the int32 partials [z, M, N] are left in a.part
+// for the caller's own finishing pass and *defer_z = z; otherwise *defer_z = 1 (output written)
 template <int EPI, int BKD, int NST>
-int gemm_d_launch(const GemmArgs& a, hipStream_t st, int part_rows, int ncols) {
-  const int z = gemm_splits(a.M, ncols, a.K, a.part != nullptr ? part_rows : 0, EPI);
+int gemm_d_launch(const GemmArgs& a, hipStream_t st, int part_rows, int ncols, int* defer_z) {
+  const int z = gemm_splits(a.M, ncols, a.K, a.part != nullptr ? part_rows : 0, EPI, defer_z != nullptr);
+  if (defer_z) *defer_z = z;
   const long long nb = (long long)cdiv_i(a.M, kGT) * cdiv_i(ncols, kGT);
   if (nb * z > 0x7FFFFFFF) return -2;
   const dim3 grid((unsigned)(nb * z));
@@ -473,7 +478,7 @@ int gemm_d_launch(const GemmArgs& a, hipStream_t st, int part_rows, int ncols) {
   } else if constexpr (EPI != EPI_SWIGLU) {
     launch((k_gemm_d<EPI, true, BKD, NST>), grid, dim3(256), lb, st, a, (int)nb, z);
     const long long total = (long long)a.M * a.N;
-    launch((k_gemm_fin<EPI>), dim3((unsigned)min(4096LL, (total + 255) / 256)), dim3(256), 0, st, a, z);
+    if (!defer_z) launch((k_gemm_fin<EPI>), dim3((unsigned)min(4096LL, (total + 255) / 256)), dim3(256), 0, st, a, z);
   }
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
@@ -590,18 +595,19 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
 
 // the batched-decode linear when it applies (1 <= M <= 32, K % 32 == 0, 16-byte aligned rows), else -1.
 // Waves per workgroup: one per window up to 8; the windows split over up to 4 workgroups per tile when
-// the caller's partial buffer (a.part, a.part_cap int32) holds the partials (STORE / RESID only).
+// the caller finishes the partials (defer_z) and its buffer (a.part, a.part_cap int32) holds them.
 template <int EPI>
-int bgemv_launch(const GemmArgs& a, hipStream_t st) {
+int bgemv_launch(const GemmArgs& a, hipStream_t st, int* defer_z) {
   if (a.M < 1 || a.M > kBgMaxRows || a.K % 32 || ((uintptr_t)a.w & 15) || ((uintptr_t)a.xq & 15)) return -1;
   if (EPI == EPI_SWIGLU && (!a.tab || !a.w3 || ((uintptr_t)a.tab & 15) || ((uintptr_t)a.w3 & 15))) return -1;
   const int nwin = cdiv_i(a.K, kBgWin);
   const int kw = nwin >= 8 ? 8 : nwin >= 4 ? 4 : nwin >= 2 ? 2 : 1;
-  int nz = 1;
-  if (EPI != EPI_SWIGLU && a.part)
+  int nz = 1;                                     // (split only into a finish the caller runs anyway)
+  if (EPI != EPI_SWIGLU && a.part && defer_z)
     while (nz < 4 && nwin > kw * nz && (long long)(2 * nz) * a.M * a.N <= a.part_cap) nz *= 2;
   const long long blocks = (long long)cdiv_i(a.N, EPI == EPI_SWIGLU ? 16 : 32) * nz;
   if (blocks > 0x7FFFFFFF) return -2;
+  if (defer_z) *defer_z = nz;
   const dim3 grid((unsigned)blocks), block(64 * kw);
   const size_t lb = (size_t)kw * kBgWaveLds;
   auto go = [&](auto kern) { launch(kern, grid, block, lb, st, a, nz); };
@@ -612,7 +618,7 @@ int bgemv_launch(const GemmArgs& a, hipStream_t st) {
       else if (kw == 2) go(k_bgemv<EPI, 2, true>);
       else go(k_bgemv<EPI, 1, true>);
       const long long total = (long long)a.M * a.N;
-      launch((k_gemm_fin<EPI>), dim3((unsigned)min(4096LL, (total + 255) / 256)), dim3(256), 0, st, a, nz);
+      if (!defer_z) launch((k_gemm_fin<EPI>), dim3((unsigned)min(4096LL, (total + 255) / 256)), dim3(256), 0, st, a, nz);
     }
   } else {
     if (kw == 8) go(k_bgemv<EPI, 8, false>);
@@ -627,17 +633,19 @@ int bgemv_launch(const GemmArgs& a, hipStream_t st) {
 // `part_rows`-row partial buffer for narrow layers), else the register-staged k_gemm with the
 // largest tile that still gives >= 256 workgroups (one per CU).
 template <int EPI>
-int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0) {
+int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0, int* defer_z = nullptr) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 16) return -2;
   if (EPI == EPI_SWIGLU && (a.tab == nullptr || ((uintptr_t)a.tab & 15))) return -1;
   if (a.M <= kBgMaxRows) {                                 // few rows: stream the weights once
-    const int r = bgemv_launch<EPI>(a, st);
+    const int r = bgemv_launch<EPI>(a, st, EPI == EPI_SWIGLU ? nullptr : defer_z);
     if (r != -1) return r;
   }
   const int ncols = EPI == EPI_SWIGLU ? 2 * a.N : a.N;   // B rows the tiles cover
   // the direct-to-LDS kernel (split-K for the narrow STORE / RESID layers)
-  if (a.K % 64 == 0) return a.K % 128 == 0 ? gemm_d_launch<EPI, 128, 2>(a, st, part_rows, ncols)
-                                            : gemm_d_launch<EPI, 64, 4>(a, st, part_rows, ncols);
+  if (EPI == EPI_SWIGLU) defer_z = nullptr;
+  if (defer_z) *defer_z = 1;
+  if (a.K % 64 == 0) return a.K % 128 == 0 ? gemm_d_launch<EPI, 128, 2>(a, st, part_rows, ncols, defer_z)
+                                            : gemm_d_launch<EPI, 64, 4>(a, st, part_rows, ncols, defer_z);
   auto blocks = [&](int bm, int bn) { return (long long)cdiv_i(a.M, bm) * cdiv_i(ncols, bn); };
   int wm = 1, wn = 1;
   if (blocks(128, 128) >= 256) { wm = 2; wn = 2; }

@@ -58,6 +58,64 @@ __global__ __launch_bounds__(kGemvThreads) void k_rows_quant(GemvArgs a) {
   if (threadIdx.x == 0) a.sx_out[row] = s_x;
 }
 
+// The split-K finish of a residual linear fused with the row RMSNorm / quant_act that reads its
+// output: x[row] = F(res + F(F(f32(sum_z part[z, row]) * s_w) * s_x_in[row])) (the residual epilogue,
+// llm/ref_model.py:198-202 and :229-230; the int32 sum is exact in any order) is stored back into the
+// residual rows, then normalised and quantised as k_rows_quant<PRO_NORM_QUANT> does. The partials are
+// [nz, rows, K] (K = the linear's output width). s_x_in may be a.sx_out: each row's scale is read
+// before its new one is written.
+struct FinArgs {
+  const int32_t* part;
+  long long zstride;                 // rows * K
+  int nz;
+  const float* s_w;                  // [K] the linear's row scales
+  const float* s_x;                  // [rows] its input scales
+  float* x;                          // the residual rows (a.x, writable)
+};
+
+template <int NCB>
+__global__ __launch_bounds__(kGemvThreads) void k_rows_fin_quant(GemvArgs a, FinArgs f) {
+  __shared__ __align__(16) int8_t xq_lds[1024 * NCB];
+  __shared__ __align__(16) float xf_lds[1024 * NCB + 128];
+  __shared__ __align__(16) float tab_lds[kSfuWords];
+  __shared__ float red[64];
+  typedef XStage<PRO_NORM_QUANT, EPI_STORE, NCB, kGemvThreads> S;
+  const int row = blockIdx.x, tid = threadIdx.x, K = a.K;
+  S st;
+  st.tab = ((const v4f_t*)a.tab)[tid & (kSfuWords / 4 - 1)];
+  const float sx = f.s_x[row];
+  float* xr = f.x + row * a.x_stride;
+  const int32_t* pr = f.part + (long long)row * K;
+  v4i_t acc[S::NX];
+  float4 sw[S::NX];
+#pragma unroll
+  for (int j = 0; j < S::NX; ++j) {                // loads first (clamped, unconditional), then arithmetic
+    const int i = min((tid + j * kGemvThreads) * 4, K - 4);
+    st.x[j] = *(const float4*)(xr + i);
+    st.g[j] = *(const float4*)(a.g + i);
+    sw[j] = *(const float4*)(f.s_w + i);
+    acc[j] = *(const v4i_t*)(pr + i);
+  }
+  for (int z = 1; z < f.nz; ++z)
+#pragma unroll
+    for (int j = 0; j < S::NX; ++j) acc[j] += *(const v4i_t*)(pr + z * f.zstride + min((tid + j * kGemvThreads) * 4, K - 4));
+#pragma unroll
+  for (int j = 0; j < S::NX; ++j) {
+    float4 v = st.x[j];
+    v.x = v.x + dequant(acc[j].x, sw[j].x, sx);
+    v.y = v.y + dequant(acc[j].y, sw[j].y, sx);
+    v.z = v.z + dequant(acc[j].z, sw[j].z, sx);
+    v.w = v.w + dequant(acc[j].w, sw[j].w, sx);
+    st.x[j] = v;
+    const int i = (tid + j * kGemvThreads) * 4;
+    if (i < K) *(float4*)(xr + i) = v;
+  }
+  const float s_x = stage_finish(st, a, row, xq_lds, xf_lds, tab_lds, red);
+  int8_t* out = a.xq_out + row * a.xq_stride;
+  for (int i = tid * 16; i < K; i += kGemvThreads * 16) *(v4i_t*)(out + i) = *(const v4i_t*)(xq_lds + i);
+  if (tid == 0) a.sx_out[row] = s_x;
+}
+
 // RMSNorm alone (no quantisation): out = F(F(x * r) * g), r = RSQRT(F(F(ss * F(1/n)) + F(eps)))
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* g, int n, float inv_n, float eps, int D,
                                                  float* out) {
