@@ -7,8 +7,11 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
+# The full-size shapes run the grouped-query attention kernel (one workgroup per row and KV head):
+# head dims 64 and 128, groups of 2, 3 and 4 query heads, QK-norm and MoE.
 @pytest.mark.parametrize("name,B", [("tiny", 4), ("tiny-gqa", 3), ("tiny-qwen", 4), ("tiny-moe", 4),
-                                    ("c1-stories15m", 8)])
+                                    ("c1-stories15m", 8), ("c2-smollm2-135m", 4), ("c3-qwen3-0.6b", 3),
+                                    ("c4-llama3.2-1b", 4), ("c5-granite-1b-a400m", 4)])
 def test_decode_batch_equals_single(name, B):
     import torch
     import t2r_amd.config as C
@@ -71,3 +74,37 @@ def test_batch_llamadevice_generate():
     assert all(s == (cfg.vocab,) for _, _, s in seen)
     bd.close()
     one.close()
+
+
+@pytest.mark.parametrize("name,lens", [("c4-llama3.2-1b", [40, 700, 1100]), ("c3-qwen3-0.6b", [33, 1500])])
+def test_decode_batch_long_context(name, lens):
+    """Sequences at positions past several 32-key tiles and past one 1024-key pass of the grouped
+    attention: each slot's cache holds a prefilled prompt of its own length; one batched step equals
+    each sequence's single decode at that position (logits and the new KV row)."""
+    import torch
+    import t2r_amd.config as C
+    from t2r_amd import weights as W
+    from t2r_amd.model import ResidentModel
+    cfg = C.get(name)
+    qm = W.QuantModel(cfg)
+    B = len(lens)
+    rm = ResidentModel(qm, max_rows=max(lens))
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, cfg.vocab, n).tolist() for n in lens]
+    nxt = [int(rng.integers(0, cfg.vocab)) for _ in lens]
+    kc, vc = rm.batch_caches(B)
+    for b, p in enumerate(prompts):
+        rm.reset()
+        rm.prefill(p, logits=False)
+        kc[b].copy_(rm.kc)
+        vc[b].copy_(rm.vc)
+    print(f"{name}: positions {lens}", flush=True)
+    got = rm.decode_batch(nxt, lens, kc, vc).cpu().numpy()
+    for b, p in enumerate(prompts):
+        rm.reset()
+        rm.prefill(p, logits=False)
+        want = rm.decode(nxt[b], lens[b]).cpu().numpy()
+        assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), f"sequence {b} at {lens[b]}"
+        assert torch.equal(kc[b, :, lens[b]], rm.kc[:, lens[b]])
+        assert torch.equal(vc[b, :, lens[b]], rm.vc[:, lens[b]])
+    rm.close()

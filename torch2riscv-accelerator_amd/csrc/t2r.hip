@@ -113,6 +113,16 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   const size_t lds = mode == ATTN_PREP ? 0 : attn_lds_bytes(a.S, a.D);
   dim3 grid(a.H, rows), block(kAttnThreads);
   const bool c16 = a.hd % 16 == 0;
+  // batched decode: one workgroup per (row, KV head) for its group of 2..4 query heads
+  const int G = a.H / a.Hk;
+  if (mode == ATTN_FUSED && rows > 1 && a.tab != nullptr && G >= 2 && G <= kGqaMaxG &&
+      (a.hd == 64 || a.hd == 128) && attn_gqa_lds_bytes(a.S, a.D, G) <= 65536) {
+    const dim3 gg(a.Hk, rows);
+    const size_t gl = attn_gqa_lds_bytes(a.S, a.D, G);
+    if (a.hd == 64) launch((k_attn_gqa<4>), gg, dim3(kGqaThreads), gl, st, a);
+    else launch((k_attn_gqa<8>), gg, dim3(kGqaThreads), gl, st, a);
+    return launched();
+  }
   if (mode == ATTN_FUSED && a.tab != nullptr && a.hd % 16 == 0 &&
       (a.hd == 16 || a.hd == 32 || a.hd == 48 || a.hd == 64 || a.hd == 128)) {
     const size_t dl = attn_dec_lds_bytes(a.S, a.D);

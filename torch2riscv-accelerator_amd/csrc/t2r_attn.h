@@ -866,4 +866,327 @@ inline size_t attn_lds_bytes(int S, int D) { return (size_t)D * osum_stride(S, D
 // dynamic LDS bytes of k_attn_dec: the scores (lane-major) and one spare slot per lane
 inline size_t attn_dec_lds_bytes(int S, int D) { return ((size_t)D * osum_stride(S, D) + 64) * 4; }
 
+// ------------------------------------------------------------------ grouped decode attention
+// Decode attention with one workgroup per (row, KV head g) for the G <= 4 query heads that share
+// the KV head, instead of one per query head: the numerics are k_attn_dec's step for step, the work
+// is split differently.
+//  - Vector jobs, one per wave: the KV head (k: QK-norm, RoPE, int8; v: int8; the cache row) and
+//    the G query heads (QK-norm, RoPE, quant_act). This workgroup is the row's only writer of its
+//    KV head's cache row.
+//  - Scores: the K rows are read once for the group, straight into the MFMA B layout (lane = key
+//    row, 16 k-bytes), and v_mfma_i32_32x32x32_i8 takes the G int8 q vectors as its A rows (rows
+//    past G zero): exact int32 dot products of all G heads, 32 keys per instruction pair.
+//  - Per key, the G heads' EXPs side by side (independent table-lookup chains); per head the
+//    D-lane ordered sum (one wave each) and RECIP; then the int8 probabilities of every (head, key)
+//    into LDS rows, so P.V reads one word per four consecutive keys and head.
+//  - P.V: a thread takes four consecutive V rows of one 16-byte chunk, transposes them once
+//    (4 x 4 bytes, v_perm) for all G heads' v_dot4s; partial sums meet by DPP within 16-lane rows,
+//    then in LDS, one slot per (wave, row of 16 lanes): no atomics.
+constexpr int kGqaThreads = 512, kGqaWaves = kGqaThreads / 64, kGqaMaxG = 4;   // G + 1 <= 8 vector jobs
+constexpr int kGqaRK = 4;                        // key tiles (32 rows) per wave per pass
+
+// dynamic LDS: per head the lane-major scores (D P floats + 64 spare), then per head S int8 p
+inline size_t attn_gqa_lds_bytes(int S, int D, int G) {
+  return (size_t)G * ((size_t)D * osum_stride(S, D) + 64) * 4 + (size_t)G * ((S + 15) & ~15);
+}
+
+template <int NCH>   // 16-byte chunks per head row: hd = 16 NCH (64 or 128)
+__global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
+  constexpr int HD = 16 * NCH, KS = HD / 32;                // MFMA k-steps per key tile
+  constexpr int NCHP = NCH;                                 // (4 or 8: a power of two)
+  constexpr int TS = kGqaThreads / NCHP;                    // V row slices (4 rows each)
+  constexpr int RQ = 2;                                     // 4-row groups per thread per pass
+  constexpr int NV = HD > 64 ? 2 : 1;                       // head-vector floats per lane
+  static_assert(HD == 64 || HD == 128, "k_attn_gqa: hd 64 or 128");
+  extern __shared__ __align__(16) float dyn[];
+  __shared__ __align__(16) float tab[kSfuWords];
+  __shared__ __align__(16) int8_t s_q8[kGqaMaxG][HD];
+  __shared__ __align__(16) int8_t s_k8[HD], s_v8[HD];
+  __shared__ __align__(16) float s_vec[kGqaWaves][HD];
+  __shared__ float s_sq[kGqaMaxG], s_r[kGqaMaxG];
+  __shared__ float red[kGqaWaves][kGqaMaxG];
+  __shared__ int part[kGqaWaves * 4][kGqaMaxG * HD];
+
+  const int g = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, lr = lane & 31, kh = lane >> 5;
+  const int G = a.H / a.Hk, S = a.S, D = a.D, P = osum_stride(S, D), SH = D * P + 64;
+  const int SP = (S + 15) & ~15;                 // int8 p row stride
+  int8_t* pq = (int8_t*)(dyn + G * SH);
+  a.kc += row * a.kv_row_stride;                 // this row's sequence cache
+  a.vc += row * a.kv_row_stride;
+  const long long q_dim = (long long)a.H * HD;
+  const int kv_dim = a.Hk * HD;
+  const int pos = a.pos[row];
+  if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
+  const int T = pos + 1;
+  const float* qkv = a.qkv + row * a.qkv_stride;
+  // cache rows [0, pos) of this KV head's columns: rows past pos - 1 read as zero
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.kc + (long long)g * HD, (uint32_t)pos * kv_dim);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc + (long long)g * HD, (uint32_t)pos * kv_dim);
+
+  // ---- issue: SFU tables, this wave's vector job inputs, the first pass of K tiles and V chunks
+  v4f_t tb[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) tb[k] = ((const v4f_t*)a.tab)[(lane + 64 * k) & (kSfuWords / 4 - 1)];
+  const int job = wave;                          // 0: the KV head, 1 .. G: query head job - 1 (G < waves)
+  const bool has_job = job <= G;
+  const int hq = g * G + (job - 1);              // global query head of job >= 1
+  const float* va = job == 0 ? qkv + q_dim + (long long)g * HD : qkv + (long long)(has_job ? hq : 0) * HD;
+  const float* vb = job == 0 ? qkv + q_dim + kv_dim + (long long)g * HD : va;
+  const float* gn = job == 0 ? a.kn : a.qn;
+  const bool norm = gn != nullptr;
+  if (!norm) gn = va;                            // any readable address: the values are unused
+  float xa[NV], xb[NV], xg[NV], cs[NV], sn[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int j = min(lane + 64 * k, HD - 1);
+    xa[k] = va[j];
+    xb[k] = vb[j];
+    xg[k] = gn[j];
+    const long long ip = (long long)pos * (HD / 2) + (j >> 1);
+    cs[k] = a.cos_t[ip];
+    sn[k] = a.sin_t[ip];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  v4i_t kw[kGqaRK][KS];
+  auto load_k = [&](int pass) {
+#pragma unroll
+    for (int i = 0; i < kGqaRK; ++i) {
+      const int t = 32 * (pass * kGqaWaves * kGqaRK + wave + kGqaWaves * i) + lr;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kw[i][s] = buffer_load16(krs, (uint32_t)t * kv_dim + 32 * s + 16 * kh);
+    }
+  };
+  const int c = tid & (NCHP - 1), ts = tid / NCHP;
+  v4i_t vw[RQ][4];                               // rows 4 (ts + TS j) + u
+  auto load_v = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < RQ; ++j)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) vw[j][u] = buffer_load16(vrs, (uint32_t)(base + 4 * (ts + TS * j) + u) * kv_dim + 16 * c);
+  };
+  load_k(0);
+  load_v(0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- tables to LDS (each wave writes all of them, so it needs only its own stores); the jobs
+#pragma unroll
+  for (int k = 0; k < 2; ++k) ((v4f_t*)tab)[lane + 64 * k] = tb[k];
+  __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0): this wave's table stores are done
+  __builtin_amdgcn_wave_barrier();
+  if (has_job) {
+    if (norm) {
+      float* vec = s_vec[wave];
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        if (lane + 64 * k < HD) vec[lane + 64 * k] = xa[k];
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      float ss = 0.0f;
+      if (lane < D) ss = ordered_sum<true>(vec, HD, D, lane);
+      const float r = sfu_rsqrt(__shfl(ss, 0) * a.inv_hd + a.eps, tab);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) xa[k] = (xa[k] * r) * xg[k];
+    }
+    float xr[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const float partner = dpp_f<kDppXor1>(xa[k]);
+      xr[k] = (lane & 1) ? (xa[k] * cs[k]) + (partner * sn[k]) : (xa[k] * cs[k]) + ((-partner) * sn[k]);
+    }
+    if (job == 0) {
+      const long long crow = (long long)pos * kv_dim + (long long)g * HD;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int j = lane + 64 * k;
+        const int8_t kb = (int8_t)to_i8(xr[k] * a.inv_sk), vb8 = (int8_t)to_i8(xb[k] * a.inv_sv);
+        if (j < HD) {
+          s_k8[j] = kb;
+          s_v8[j] = vb8;
+          a.kc[crow + j] = kb;
+          a.vc[crow + j] = vb8;
+        }
+      }
+    } else {
+      uint32_t am = 0;
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        if (lane + 64 * k < HD) am = max(am, abs_bits(xr[k]));       // lanes past HD hold no element
+      const float sq = fv(wave_max_u32(am)) * kInv127;
+      const float inv = sfu_recip(sq, tab);
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        if (lane + 64 * k < HD) s_q8[job - 1][lane + 64 * k] = (int8_t)to_i8(xr[k] * inv);
+      if (lane == 0) s_sq[job - 1] = sq;
+    }
+  }
+  __syncthreads();
+
+  // ---- scores of the G heads: C[head][key] = q8[head] . k8[key] on MFMA, 32 keys per tile.
+  // Lane (lr, kh) holds key lr of the tile and heads 4 kh + r (r < 4) in acc[r].
+  v4i_t qa[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const v4i_t z = {0, 0, 0, 0};
+    qa[s] = lr < G ? *(const v4i_t*)(&s_q8[lr < G ? lr : 0][32 * s + 16 * kh]) : z;
+  }
+  float sqh[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sqh[r] = s_sq[r < G ? r : 0];
+  const int ntile = (T + 31) >> 5;
+  const int npk = (ntile + kGqaWaves * kGqaRK - 1) / (kGqaWaves * kGqaRK);
+  float mloc[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  for (int pass = 0; pass < npk; ++pass) {
+    if (pass > 0) load_k(pass);
+#pragma unroll
+    for (int i = 0; i < kGqaRK; ++i) {
+      const int t0 = 32 * (pass * kGqaWaves * kGqaRK + wave + kGqaWaves * i);
+      if (t0 >= T) break;                        // (wave-uniform)
+      const int t = t0 + lr;
+      v16i_t acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const v4i_t kn = t == pos ? *(const v4i_t*)(&s_k8[32 * s + 16 * kh]) : kw[i][s];
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[s], kn, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * kh + r;
+        const bool ok = h < G && t < T;
+        const float sv = ((float)acc[r] * sqh[r]) * a.a_k;
+        dyn[ok ? h * SH + osum_index(t, D, P) : (r < G ? r : 0) * SH + D * P + lane] = sv;   // (spare slot)
+        mloc[r] = nanmax(mloc[r], ok ? sv : -__builtin_inff());
+      }
+    }
+  }
+  // per head: the maximum over the wave's 32 lanes of half kh = 0 (G <= 4), then over the waves
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = mloc[r];
+    v = nanmax(v, dpp_f<kDppXor1>(v));
+    v = nanmax(v, dpp_f<kDppXor2>(v));
+    v = nanmax(v, dpp_f<kDppHalfMirror>(v));
+    v = nanmax(v, dpp_f<kDppMirror>(v));
+    const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    if (lane == 0 && r < G) red[wave][r] = nanmax(m0, m1);
+  }
+  __syncthreads();
+
+  // ---- e = EXP(s - m) (+0 padding to a multiple of D), key t by thread t % 512, all heads at once
+  const int Tpad = ((T + D - 1) / D) * D;
+  float mh[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = r < G ? r : 0;
+    float m = red[0][h];
+#pragma unroll
+    for (int w = 1; w < kGqaWaves; ++w) m = nanmax(m, red[w][h]);
+    mh[r] = m;
+  }
+  for (int t = tid; t < Tpad; t += kGqaThreads) {
+    const int k = osum_index(t, D, P);
+    float sv[4], ev[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) sv[h] = dyn[(h < G ? h : 0) * SH + k];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) ev[h] = sfu_exp(sv[h] - mh[h], tab);
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      if (h < G) dyn[h * SH + k] = t < T ? ev[h] : 0.0f;
+  }
+  __syncthreads();
+  if (wave < G) {
+    float ssum = 0.0f;
+    if (lane < D) ssum = ordered_sum_t<false>(dyn + wave * SH, T, D, P, lane);
+    if (lane == 0) s_r[wave] = sfu_recip(ssum, tab);
+  }
+  __syncthreads();
+
+  // ---- the int8 probabilities p = to_i8(F(F(e r) 127)) of every (head, key) in [0, T4), zero past T
+  float rh[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) rh[r] = s_r[r < G ? r : 0];
+  const int T4 = (T + 3) & ~3;
+  for (int t = tid; t < T4; t += kGqaThreads) {
+    const int k = osum_index(min(t, T - 1), D, P);
+    float ev[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) ev[h] = dyn[(h < G ? h : 0) * SH + k];
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      if (h < G) pq[h * SP + t] = (int8_t)(t < T ? to_i8((ev[h] * rh[h]) * 127.0f) : 0);
+  }
+  __syncthreads();
+
+  // ---- P.V: thread (chunk c, row slice ts) takes rows 4 (ts + TS j) + u; the four rows' V chunks
+  // transposed once, then per head one word of four p against each column word
+  int vpos[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) vpos[w] = ((const int*)s_v8)[4 * c + w];
+  int acc[kGqaMaxG][16];
+#pragma unroll
+  for (int h = 0; h < kGqaMaxG; ++h)
+#pragma unroll
+    for (int b = 0; b < 16; ++b) acc[h][b] = 0;
+  const int npv = (T + 4 * TS * RQ - 1) / (4 * TS * RQ);
+  for (int pass = 0; pass < npv; ++pass) {
+    const int base = pass * 4 * TS * RQ;
+    if (pass > 0) load_v(base);
+#pragma unroll
+    for (int j = 0; j < RQ; ++j) {
+      const int t0 = base + 4 * (ts + TS * j);
+      if (t0 < T) {
+        int rw[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) rw[u][w] = t0 + u == pos ? vpos[w] : vw[j][u][w];
+        int col[4][4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) transpose4x4(rw[0][w], rw[1][w], rw[2][w], rw[3][w], col[w]);
+        int pp[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) pp[h] = *(const int*)(pq + (h < G ? h : 0) * SP + t0);
+#pragma unroll
+        for (int h = 0; h < kGqaMaxG; ++h)
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[h][4 * w + k] = __builtin_amdgcn_sdot4(col[w][k], pp[h], acc[h][4 * w + k], false);
+      }
+    }
+  }
+  // lanes of a 16-lane row with the same chunk rotate-and-add over the row-slice bits; then one
+  // partial row per (wave, row of 16 lanes) in LDS, summed by (head, column)
+#pragma unroll
+  for (int h = 0; h < kGqaMaxG; ++h)
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      int v = acc[h][b];
+      if (NCHP <= 2) v += dpp_i<0x122>(v);                    // row_ror:2
+      if (NCHP <= 4) v += dpp_i<0x124>(v);                    // row_ror:4
+      if (NCHP <= 8) v += dpp_i<0x128>(v);                    // row_ror:8
+      acc[h][b] = v;
+    }
+  if ((lane & 15) < NCHP) {
+#pragma unroll
+    for (int h = 0; h < kGqaMaxG; ++h)
+      if (h < G)
+#pragma unroll
+        for (int b = 0; b < 16; ++b) part[wave * 4 + (lane >> 4)][h * HD + 16 * c + b] = acc[h][b];
+  }
+  __syncthreads();
+  float* out = a.att + row * a.att_stride;
+  for (int idx = tid; idx < G * HD; idx += kGqaThreads) {
+    int ssum = 0;
+#pragma unroll
+    for (int w = 0; w < kGqaWaves * 4; ++w) ssum += part[w][idx];
+    const int h = idx / HD, j = idx - h * HD;
+    out[(long long)(g * G + h) * HD + j] = (float)ssum * a.a_v;
+  }
+}
+
 }  // namespace t2r
