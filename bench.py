@@ -44,6 +44,19 @@ def gemv_bytes(cfg):
     }
 
 
+MFMA_INT8_PEAK_TOPS = 5000.0            # MI355X dense int8 matrix peak (5.0 POP/s)
+
+
+def gemm_weights(cfg):
+    """Weights (N x K) of each prefill GEMM class per layer: ops per launch are 2 * rows * this. (An
+    MoE model's expert FFN runs as row GEMVs over the selected experts, not as a GEMM class.)"""
+    d, q, kv, F = cfg.dim, cfg.q_dim, cfg.kv_dim, cfg.hidden
+    w = {"qkv": (q + 2 * kv) * d, "wo": d * q}
+    if not cfg.n_experts:
+        w.update({"ffn_up": 2 * F * d, "ffn_down": d * F})
+    return w
+
+
 def measured_traffic(kind, cfg_name):
     """HBM bytes per launch of the dominant kernel, as measured by the rocprofv3 --pmc FETCH_SIZE and
     WRITE_SIZE passes summarised in profiles/ (scaled by a known-size copy); None when not recorded
@@ -144,6 +157,24 @@ def main():
         times.append(time.perf_counter() - t)
     prefill_s = float(np.median(times[1:])) if len(times) > 1 else times[0]
     log(f"prefill {P} rows: {prefill_s * 1e3:.2f} ms ({P / prefill_s:.0f} tok/s)")
+    # the prefill GEMMs' int8 MFMA rate: one more prefill with HIP events around each GEMM launch
+    # (the per-class scopes of a multi-row linear cover the GEMM alone)
+    rm.reset()
+    rm.profile(kinds=("qkv", "wo", "ffn_up", "ffn_down"), max_launches=4 * cfg.layers + 8)
+    rm.prefill(prompt)
+    pprof = rm.profile_read()
+    rm.profile(kinds=())
+    gemm_ops = {k: 2 * P * v for k, v in gemm_weights(cfg).items()}
+    g_ops = sum(gemm_ops[k] * len(v) for k, v in pprof.items() if k in gemm_ops)
+    g_ms = sum(sum(v) for k, v in pprof.items() if k in gemm_ops)
+    prefill_gemm = {k: {"launches": len(v), "avg_us": round(sum(v) / len(v) * 1e3, 3),
+                        "TOPS": round(gemm_ops[k] / (sum(v) / len(v) * 1e-3) * 1e-12, 1)}
+                    for k, v in pprof.items() if k in gemm_ops and v}
+    g_tops = g_ops / (g_ms * 1e-3) * 1e-12 if g_ms > 0 else None
+    if g_tops:
+        prefill_gemm["all"] = {"TOPS": round(g_tops, 1), "frac": round(g_tops / MFMA_INT8_PEAK_TOPS, 4),
+                               "peak_TOPS": MFMA_INT8_PEAK_TOPS, "total_us": round(g_ms * 1e3, 1)}
+        log(f"prefill GEMMs: {g_ms * 1e3:.0f} us, {g_tops:.0f} int8 TOPS ({g_tops / MFMA_INT8_PEAK_TOPS:.3f} of peak)")
     after_prompt = rm.next.clone()
 
     # ---- decode: greedy on the device, batch 1, positions P .. P + steps.
@@ -214,19 +245,51 @@ def main():
                 rm.handle, abi.ptr(toks), abi.ptr(poss), B, abi.ptr(kc), abi.ptr(vc), kc[0].numel(), abi.ptr(lg),
                 abi.ptr(toks), abi.stream_ptr()))
             poss.add_(1)
-        toks.copy_((after_prompt.to(torch.int64) + torch.arange(B, device=rm.device)) % cfg.vocab)
-        poss.fill_(P)
+        tok0 = (after_prompt.to(torch.int64) + torch.arange(B, device=rm.device)) % cfg.vocab
+
+        def rewind_b():
+            toks.copy_(tok0)
+            poss.fill_(P)
+        rewind_b()
         bstep()
         bstep()
-        poss.fill_(P)
+        rewind_b()
         sync()
         t = time.perf_counter()
         for _ in range(K):
             bstep()
         sync()
-        bdt = time.perf_counter() - t
-        batch[str(B)] = {"tok_s": round(B * K / bdt, 1), "ms_per_step": round(bdt / K * 1e3, 4), "steps": K}
-        log(f"batched decode B={B}: {bdt / K * 1e3:.3f} ms/step ({B * K / bdt:.0f} tok/s aggregate)")
+        edt = time.perf_counter() - t
+        # the same K steps replayed from one HIP graph (the step's launches without host work)
+        bdt, bmode = edt, "eager"
+        if not args.no_graph:
+            try:
+                side = torch.cuda.Stream(device=rm.device)
+                side.wait_stream(torch.cuda.current_stream(rm.device))
+                rewind_b()
+                with torch.cuda.stream(side):
+                    bstep()
+                torch.cuda.current_stream(rm.device).wait_stream(side)
+                sync()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=side):
+                    for _ in range(K):
+                        bstep()
+                rewind_b()
+                g.replay()
+                rewind_b()
+                sync()
+                t = time.perf_counter()
+                g.replay()
+                sync()
+                bdt, bmode = time.perf_counter() - t, "hip-graph"
+                del g
+            except Exception as e:                          # capture not available: eager timing only
+                log(f"batched HIP graph capture failed ({e}); eager timing")
+        batch[str(B)] = {"tok_s": round(B * K / bdt, 1), "ms_per_step": round(bdt / K * 1e3, 4), "steps": K,
+                         "mode": bmode, "eager_tok_s": round(B * K / edt, 1)}
+        log(f"batched decode B={B} ({bmode}): {bdt / K * 1e3:.3f} ms/step ({B * K / bdt:.0f} tok/s aggregate); "
+            f"eager {edt / K * 1e3:.3f} ms/step")
         del kc, vc, lg
 
     nbytes = gemv_bytes(cfg)
@@ -269,6 +332,7 @@ def main():
         "gemv_all_frac": round(gemv_b / gemv_t / 1e9 / HBM_PEAK_GBS, 4) if gemv_t else None,
         "decode_mode": mode,
         "batch_decode": batch,
+        "prefill_gemm": prefill_gemm,
         "eager_tok_s": round(steps / eager_dt, 2),
         "roofline": {"kernel": "k_gemv<PRO_NORM_QUANT, EPI_SWIGLU> (fused SwiGLU decode GEMV)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -415,16 +415,16 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
   a.x = m->x; a.x_stride = d.dim; a.g = d.rms_att + L_dim; a.inv_n = inv_d; a.eps = d.eps; a.D = d.D;
   a.N = m->qkv_dim; a.K = d.dim; a.y = m->qkv; a.y_stride = m->qkv_dim;
   int qz = 1;                                       // prefill: Wqkv's split finished by the prep kernel
-  {
+  // (the timed class of a multi-row linear is the GEMM alone: its row norm/quant runs before the scope)
+  if (decode) {
     ProfScope p(m, T2R_PROF_QKV, st);
-    if (decode) {
-      if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
-    } else {
-      if ((rc = rows_quant(m, m->x, d.dim, d.rms_att + L_dim, d.dim, rows, st))) return rc;
-      if ((rc = rows_linear<EPI_STORE>(m, a.w, a.s_w, nullptr, nullptr, m->qkv_dim, d.dim, rows, m->qkv, m->qkv_dim, st,
-                                       mode == RUN_PREFILL ? &qz : nullptr)))
-        return rc;
-    }
+    if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
+  } else {
+    if ((rc = rows_quant(m, m->x, d.dim, d.rms_att + L_dim, d.dim, rows, st))) return rc;
+    ProfScope p(m, T2R_PROF_QKV, st);
+    if ((rc = rows_linear<EPI_STORE>(m, a.w, a.s_w, nullptr, nullptr, m->qkv_dim, d.dim, rows, m->qkv, m->qkv_dim, st,
+                                     mode == RUN_PREFILL ? &qz : nullptr)))
+      return rc;
   }
   // attention (QK-norm, RoPE, KV append fused for decode)
   AttnArgs at;
@@ -463,14 +463,13 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
   a.s_w = d.s_wo + L_dim;
   a.x = m->att; a.x_stride = m->q_dim;
   a.N = d.dim; a.K = m->q_dim; a.y = m->x; a.y_stride = d.dim; a.res = m->x; a.res_stride = d.dim;
-  {
+  if (decode) {
     ProfScope p(m, T2R_PROF_WO, st);
-    if (decode) {
-      if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
-    } else {
-      if ((rc = rows_quant(m, m->att, m->q_dim, nullptr, m->q_dim, rows, st))) return rc;
-      if ((rc = rows_linear<EPI_RESID>(m, a.w, a.s_w, nullptr, nullptr, d.dim, m->q_dim, rows, m->x, d.dim, st))) return rc;
-    }
+    if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+  } else {
+    if ((rc = rows_quant(m, m->att, m->q_dim, nullptr, m->q_dim, rows, st))) return rc;
+    ProfScope p(m, T2R_PROF_WO, st);
+    if ((rc = rows_linear<EPI_RESID>(m, a.w, a.s_w, nullptr, nullptr, d.dim, m->q_dim, rows, m->x, d.dim, st))) return rc;
   }
   if (d.n_experts == 0) {
     // SwiGLU: RMSNorm + quant_act + W1 / W3 + gate
@@ -479,30 +478,28 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     a.w3 = d.w3 + (long long)l * d.hidden * d.dim; a.s_w3 = d.s_w3 + (long long)l * d.hidden;
     a.x = m->x; a.x_stride = d.dim; a.g = d.rms_ffn + L_dim; a.inv_n = inv_d; a.eps = d.eps; a.D = d.D;
     a.N = d.hidden; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows;
-    {
+    if (decode) {
       ProfScope p(m, T2R_PROF_FFN_UP, st);
-      if (decode) {
-        if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_SWIGLU>(a, rows, st))) return rc;
-      } else {
-        if ((rc = rows_quant(m, m->x, d.dim, d.rms_ffn + L_dim, d.dim, rows, st))) return rc;
-        if ((rc = rows_linear<EPI_SWIGLU>(m, a.w, a.s_w, a.w3, a.s_w3, d.hidden, d.dim, rows, m->u, m->ffn_rows, st)))
-          return rc;
-      }
+      if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_SWIGLU>(a, rows, st))) return rc;
+    } else {
+      if ((rc = rows_quant(m, m->x, d.dim, d.rms_ffn + L_dim, d.dim, rows, st))) return rc;
+      ProfScope p(m, T2R_PROF_FFN_UP, st);
+      if ((rc = rows_linear<EPI_SWIGLU>(m, a.w, a.s_w, a.w3, a.s_w3, d.hidden, d.dim, rows, m->u, m->ffn_rows, st)))
+        return rc;
     }
     // W2: quant_act(u) + linear + residual
     a = gemv_args();
     a.w = d.w2 + (long long)l * d.dim * d.hidden; a.s_w = d.s_w2 + L_dim;
     a.x = m->u; a.x_stride = m->ffn_rows;
     a.N = d.dim; a.K = d.hidden; a.y = m->x; a.y_stride = d.dim; a.res = m->x; a.res_stride = d.dim;
-    {
+    if (decode) {
       ProfScope p(m, T2R_PROF_FFN_DOWN, st);
-      if (decode) {
-        if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
-      } else {
-        if ((rc = rows_quant(m, m->u, m->ffn_rows, nullptr, d.hidden, rows, st))) return rc;
-        if ((rc = rows_linear<EPI_RESID>(m, a.w, a.s_w, nullptr, nullptr, d.dim, d.hidden, rows, m->x, d.dim, st)))
-          return rc;
-      }
+      if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
+    } else {
+      if ((rc = rows_quant(m, m->u, m->ffn_rows, nullptr, d.hidden, rows, st))) return rc;
+      ProfScope p(m, T2R_PROF_FFN_DOWN, st);
+      if ((rc = rows_linear<EPI_RESID>(m, a.w, a.s_w, nullptr, nullptr, d.dim, d.hidden, rows, m->x, d.dim, st)))
+        return rc;
     }
   } else {
     if ((rc = fin_flush(m, st))) return rc;         // the router reads x
