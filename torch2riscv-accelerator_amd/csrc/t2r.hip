@@ -65,6 +65,13 @@ int ensure_init() {
   for (const void* f : pre)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPreMaxLds) != hipSuccess)
       return T2R_EHIP;
+  // the GEMM's deep-ring configuration: 128 KB of LDS, one workgroup per CU
+  const void* deep[] = {(const void*)k_gemm_d<EPI_STORE, false, 128, 4>, (const void*)k_gemm_d<EPI_STORE, true, 128, 4>,
+                        (const void*)k_gemm_d<EPI_RESID, false, 128, 4>, (const void*)k_gemm_d<EPI_RESID, true, 128, 4>,
+                        (const void*)k_gemm_d<EPI_SWIGLU, false, 128, 4>};
+  for (const void* f : deep)
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmDDeepLds) != hipSuccess)
+      return T2R_EHIP;
   g_sfu_addr[dev] = (const float*)addr;
   g_inited[dev] = true;
   return T2R_OK;

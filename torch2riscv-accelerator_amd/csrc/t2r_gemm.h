@@ -274,6 +274,8 @@ constexpr size_t gemm_d_lds() { return (size_t)NST * 2 * kGT * BKD; }
 // buffered when K % 128 == 0, else 64-byte slabs four deep; both 64 KB of LDS, two workgroups per CU
 constexpr size_t kGemmDLds = gemm_d_lds<128, 2>();
 static_assert(gemm_d_lds<64, 4>() == kGemmDLds, "both GEMM configurations use the same LDS");
+// and the deep ring for grids of at most one workgroup per CU (needs the large-LDS launch attribute)
+constexpr size_t kGemmDDeepLds = gemm_d_lds<128, 4>();
 
 template <int EPI, bool SPLIT, int BKD, int NST>
 __global__ __launch_bounds__(256) void k_gemm_d(GemmArgs a, int ntile, int nz) {
@@ -452,24 +454,23 @@ __global__ __launch_bounds__(256) void k_gemm_fin(GemmArgs a, int nz) {
 }
 
 // split count for the pipelined GEMM. Only a caller that finishes the partials in a pass it runs
-// anyway (`defer`) gets a split: a separate finishing pass costs more than the split saves (C4 prefill
-// Wqkv 512 x 3072 x 2048: 13.7 us whole, 15.8 + 6.3 us split in two). Up to one workgroup per CU,
-// >= 8 slabs each, the partials within the `part_rows` rows x 4 splits of the caller's buffer.
+// anyway (`defer`) gets a split: a separate finishing pass costs more than the split saves. Up to
+// one workgroup per CU (the deep-ring configuration then runs), >= 8 slabs each, the partials within
+// the `part_rows` rows x 4 splits of the caller's buffer.
 inline int gemm_splits(int M, int ncols, int K, int part_rows, int epi, bool defer) {
   if (epi == EPI_SWIGLU || part_rows <= 0 || !defer) return 1;
   const long long tiles = (long long)cdiv_i(M, kGT) * cdiv_i(ncols, kGT);
   int z = 1;
-  while (z < 4 && tiles * z <= 256 && K / kBK >= 16 * z && (long long)M * z * 2 <= 4LL * part_rows) z *= 2;
+  while (z < 4 && tiles * z * 2 <= 256 && K / kBK >= 16 * z && (long long)M * z * 2 <= 4LL * part_rows) z *= 2;
   return z;
 }
 
 // defer_z (STORE / RESID): when the launch splits K, the int32 partials [z, M, N] are left in a.part
 // for the caller's own finishing pass and *defer_z = z; otherwise *defer_z = 1 (output written)
 template <int EPI, int BKD, int NST>
-int gemm_d_launch(const GemmArgs& a, hipStream_t st, int part_rows, int ncols, int* defer_z) {
-  const int z = gemm_splits(a.M, ncols, a.K, a.part != nullptr ? part_rows : 0, EPI, defer_z != nullptr);
+int gemm_d_launch(const GemmArgs& a, hipStream_t st, int z, int* defer_z) {
   if (defer_z) *defer_z = z;
-  const long long nb = (long long)cdiv_i(a.M, kGT) * cdiv_i(ncols, kGT);
+  const long long nb = (long long)cdiv_i(a.M, kGT) * cdiv_i(EPI == EPI_SWIGLU ? 2 * a.N : a.N, kGT);
   if (nb * z > 0x7FFFFFFF) return -2;
   const dim3 grid((unsigned)(nb * z));
   const size_t lb = gemm_d_lds<BKD, NST>();
@@ -644,8 +645,15 @@ int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0, int* defer
   // the direct-to-LDS kernel (split-K for the narrow STORE / RESID layers)
   if (EPI == EPI_SWIGLU) defer_z = nullptr;
   if (defer_z) *defer_z = 1;
-  if (a.K % 64 == 0) return a.K % 128 == 0 ? gemm_d_launch<EPI, 128, 2>(a, st, part_rows, ncols, defer_z)
-                                            : gemm_d_launch<EPI, 64, 4>(a, st, part_rows, ncols, defer_z);
+  if (a.K % 64 == 0) {
+    const int z = gemm_splits(a.M, ncols, a.K, a.part != nullptr ? part_rows : 0, EPI, defer_z != nullptr);
+    // a grid of at most one workgroup per CU takes the deep ring (4 x 32 KB: three 128-byte slabs in
+    // flight, measured faster on the narrow layers: Wqkv / Wo / W2 at 512 rows 18.6 / 16.3 / 54.8 us
+    // -> 14.0 / 12.8 / 42.0); larger grids two workgroups per CU with the double buffer
+    const long long nwg = (long long)cdiv_i(a.M, kGT) * cdiv_i(ncols, kGT) * z;
+    if (a.K % 128) return gemm_d_launch<EPI, 64, 4>(a, st, z, defer_z);
+    return nwg <= 256 ? gemm_d_launch<EPI, 128, 4>(a, st, z, defer_z) : gemm_d_launch<EPI, 128, 2>(a, st, z, defer_z);
+  }
   auto blocks = [&](int bm, int bn) { return (long long)cdiv_i(a.M, bm) * cdiv_i(ncols, bn); };
   int wm = 1, wn = 1;
   if (blocks(128, 128) >= 256) { wm = 2; wn = 2; }
