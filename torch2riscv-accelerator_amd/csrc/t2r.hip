@@ -379,9 +379,12 @@ int rows_quant_staged(Model* m, const float* x, long long x_stride, const float*
 // a prefill linear layer on the workspace's int8 rows (int8 MFMA)
 // defer_z (STORE): the caller finishes a split itself (its split count back in *defer_z, partials in
 // m->part). A residual linear into x leaves a split's finish pending for the next norm/quant of x.
+// argmax (STORE): per row the greedy key into argmax[row] (zeroed before) when the batched-decode
+// kernel runs the linear; *argmax_done says whether it did
 template <int EPI>
 int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, const float* s_w3, int N, int K, int rows,
-                float* y, long long y_stride, hipStream_t st, int* defer_z = nullptr) {
+                float* y, long long y_stride, hipStream_t st, int* defer_z = nullptr,
+                unsigned long long* argmax = nullptr, bool* argmax_done = nullptr) {
   GemmArgs a;
   std::memset(&a, 0, sizeof(a));
   a.xq = m->xq; a.s_x = m->sx; a.w = w; a.s_w = s_w; a.w3 = w3; a.s_w3 = s_w3;
@@ -390,6 +393,17 @@ int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, c
   a.part_cap = 4LL * m->part_rows * (m->qkv_dim > m->d.dim ? m->qkv_dim : m->d.dim);
   a.tab = sfu_table_ptr();
   if (m->pend_z > 1) return T2R_ESTATE;          // the partials buffer still holds an unfinished linear
+  if (argmax_done) *argmax_done = false;
+  if (argmax && EPI == EPI_STORE && rows <= kBgMaxRows) {
+    a.argmax_key = argmax;
+    const int r = bgemv_launch<EPI>(a, st, nullptr);
+    if (r == 0) {
+      if (argmax_done) *argmax_done = true;
+      return T2R_OK;
+    }
+    if (r != -1) return T2R_EHIP;
+    a.argmax_key = nullptr;                      // not taken: the GEMM below, the caller's argmax after it
+  }
   const bool resid_x = EPI == EPI_RESID && y == m->x && y_stride == m->d.dim && N == m->d.dim;
   int z = 1;
   if (gemm_launch<EPI>(a, st, m->part_rows, resid_x || defer_z ? &z : nullptr)) return T2R_EHIP;
@@ -895,7 +909,7 @@ int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* position
   m->pend_z = 0;
   hipStream_t st = S(stream);
   launch(k_embed, dim3(B), dim3(256), 0, st, d.emb_q, d.emb_s, tokens, d.dim, d.vocab, m->x, (long long)d.dim,
-         m->keys, 1, m->status);
+         m->keys, B, m->status);
   int rc = launched();
   if (rc) return rc;
   m->kcb = k_caches;
@@ -907,13 +921,16 @@ int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* position
   if (rc) return rc;
   // every row's final RMSNorm + quant_act, the classifier over the rows, a first-maximum per row
   if ((rc = rows_quant(m, m->x, d.dim, d.rms_final, d.dim, B, st))) return rc;
+  bool fused = false;                              // greedy keys in the classifier's epilogue
   {
     ProfScope p(m, T2R_PROF_CLS, st);
-    if ((rc = rows_linear<EPI_STORE>(m, d.cls_q, d.cls_s, nullptr, nullptr, d.vocab, d.dim, B, logits, d.vocab, st)))
+    if ((rc = rows_linear<EPI_STORE>(m, d.cls_q, d.cls_s, nullptr, nullptr, d.vocab, d.dim, B, logits, d.vocab, st,
+                                     nullptr, next_tokens ? m->keys : nullptr, &fused)))
       return rc;
   }
   if (next_tokens) {
-    launch(k_argmax, dim3(B), dim3(256), 0, st, (const float*)logits, d.vocab, next_tokens);
+    if (fused) launch(k_keys_tokens, dim3(cdiv(B, 64)), dim3(64), 0, st, (const unsigned long long*)m->keys, next_tokens, B);
+    else launch(k_argmax, dim3(B), dim3(256), 0, st, (const float*)logits, d.vocab, next_tokens);
     return launched();
   }
   return T2R_OK;

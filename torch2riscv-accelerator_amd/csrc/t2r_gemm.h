@@ -115,6 +115,8 @@ struct GemmArgs {
   int32_t* part;             // split-K partial sums [splits, M, N] (nullptr: no split)
   long long part_cap;        // int32 elements `part` holds (0: as many as the GEMM split needs)
   const float* tab;          // SFU tables (device copy of c_sfu; required for EPI_SWIGLU)
+  unsigned long long* argmax_key;  // optional (k_bgemv, EPI_STORE): per row m the atomic max of
+                                   // argmax_key(y, n), the greedy token of the row (keys zeroed before)
 };
 
 // source row of tile column c (0 .. BN) for the block's column origin n0 (SwiGLU interleave)
@@ -569,6 +571,22 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
 #pragma unroll
   for (int i = 0; i < OPT; ++i) {
     const int o = tid + i * 64 * KW, m = o / NT, j = o % NT, n = n0 + j;
+    if (EPI == EPI_STORE && !SPLIT && a.argmax_key) {
+      // the row's greedy key over this tile's 32 columns: the 32 threads of row m are one half-wave
+      unsigned long long key = 0;
+      if (m < a.M && n < a.N) {
+        int s = 0;
+#pragma unroll
+        for (int v = 0; v < KW; ++v) s += ((const int*)(lds + v * kBgWaveLds))[m * 33 + j];
+        key = argmax_key(dequant(s, e_sw[i], e_sx[i]), n);
+      }
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) {
+        const unsigned long long other = __shfl_xor(key, off);
+        key = other > key ? other : key;
+      }
+      if (j == 0 && m < a.M && key != 0) atomicMax(a.argmax_key + m, key);
+    }
     if (m >= a.M || n >= a.N) continue;
     int s1 = 0, s3 = 0;
 #pragma unroll

@@ -341,6 +341,12 @@ __global__ __launch_bounds__(256) void k_iota(int32_t* out, int start, int n) {
   if (i < n) out[i] = start + i;
 }
 
+// the greedy tokens of n rows from their argmax keys
+__global__ void k_keys_tokens(const unsigned long long* key, int32_t* next_tokens, int n) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r < n) next_tokens[r] = (int32_t)(0xFFFFFFFFu - (uint32_t)(key[r] & 0xFFFFFFFFu));
+}
+
 __global__ void k_finish(const unsigned long long* key, int32_t* next_token, int32_t* pos, int advance) {
   if (threadIdx.x == 0) {
     if (next_token) *next_token = (int32_t)(0xFFFFFFFFu - (uint32_t)(*key & 0xFFFFFFFFu));
