@@ -585,7 +585,9 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
         const unsigned long long other = __shfl_xor(key, off);
         key = other > key ? other : key;
       }
-      if (j == 0 && m < a.M && key != 0) atomicMax(a.argmax_key + m, key);
+      // all tiles hit the same M keys: skip the atomic when the key already holds a larger one
+      if (j == 0 && m < a.M && key != 0 && key > __atomic_load_n(a.argmax_key + m, __ATOMIC_RELAXED))
+        atomicMax(a.argmax_key + m, key);
     }
     if (m >= a.M || n >= a.N) continue;
     int s1 = 0, s3 = 0;
