@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define T2R_ABI_VERSION 1
+#define T2R_ABI_VERSION 2
 
 enum {
   T2R_OK = 0,
@@ -122,6 +122,26 @@ int t2r_swiglu_w8a8(const int8_t* w1, const float* s_w1, const int8_t* w3, const
  * compiler/tests/oracle.py:558-585): top-k ids in descending score order (equal scores: lower
  * id first), weights w = F(e * RECIP(red_sum(e))), e = EXP(F(v - v0)). E <= 64, k <= 8. */
 int t2r_moe_route(const float* scores, int rows, int E, int k, int D, int32_t* ids, float* weights, void* stream);
+/* The HF path's attention options at op level (compiler/frontend/hf_generic.py:153-187, 231-292):
+ * t2r_attn_decode with flags T2R_ATTN_QSUM (qsum normalisation), ch_sk [Hk * hd] (K per channel:
+ * q = F(q * ch_sk[c]) before its quant_act; NULL: per layer) and ch_av [Hk * hd] (V per channel: the
+ * output channel scaled by ch_av[c] instead of a_v; NULL: per layer). */
+#define T2R_ATTN_QSUM 1
+int t2r_attn_decode_opt(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H,
+                        int Hk, int hd, int S, float a_k, float a_v, int D, int flags, const float* ch_sk,
+                        const float* ch_av, float* att, void* stream);
+/* KV append with per-channel inverse scales inv_sk[kv_dim], inv_sv[kv_dim] (hf_generic.py:203-218):
+ * kc[pos[r]][c] = to_i8(F(k[r][c] * inv_sk[c])); either vector may be NULL for the scalar one. */
+int t2r_kv_append_ch(const float* k, const float* v, float inv_sk, float inv_sv, const float* inv_sk_ch,
+                     const float* inv_sv_ch, int8_t* kc, int8_t* vc, const int32_t* pos, int rows, int kv_dim, int S,
+                     void* stream);
+/* The gated FFN up-projection of one row with the gate activation act: 0 SiLU (t2r_swiglu_w8a8),
+ * 1 GELU-tanh (GeGLU: F(gelu(h1) * h3), gelu(x) = F(x * RECIP(F(EXP(z) + 1))),
+ * z = F(x * F(A + F(F(x * x) * B))), A = f32(-2 sqrt(2/pi)), B = f32(A * 0.044715):
+ * compiler/frontend/hf_generic.py:840-852), then hq, s_h = quant_act(u). */
+int t2r_gated_ffn_w8a8(int act, const int8_t* w1, const float* s_w1, const int8_t* w3, const float* s_w3,
+                       const int8_t* xq, const float* s_x, int F, int K, float* u_out, int8_t* hq, float* s_h,
+                       void* stream);
 /* First index of the largest value of each row (np.argmax; llm/ref_model.py:277). */
 int t2r_argmax(const float* x, int rows, int n, int32_t* idx, void* stream);
 
@@ -153,6 +173,16 @@ typedef struct t2r_model_desc {
   int8_t* k_cache; int8_t* v_cache;                 /* [L, seq_len, kv_dim] */
   void* workspace; int64_t workspace_bytes;         /* see t2r_model_workspace_bytes */
   int32_t max_rows;                                 /* prefill rows per call the workspace holds */
+  /* ABI 2: the numerics options of the reference's HF path (compiler/frontend/hf_generic.py), all
+   * zero / NULL = DeviceModel's form. A descriptor with abi_version 1 ends before these fields and
+   * is read with them off. */
+  int32_t attn_qsum;        /* 1: qsum normalisation (:265-292): pq = to_i8(F(e * 127)), att =
+                               F(F(f32(sum pq V) * F(RECIP(f32(sum pq)) * 127)) * a_v) */
+  int32_t ffn_act;          /* FFN gate: 0 SiLU (SwiGLU), 1 GELU-tanh from EXP / RECIP (GeGLU, :840-852) */
+  const float* kv_channel;  /* [L, 4, kv_dim] per cache channel: s_k, 1/s_k, 1/s_v, a_v (:153-187);
+                               NULL when no layer has per-channel scales */
+  const int32_t* kv_channel_flags;  /* HOST [L]: bit 0 K per channel (q = F(q * s_k) before its quant,
+                                       kv_consts' a_k then f32(1 / sqrt(hd))), bit 1 V per channel; NULL: none */
 } t2r_model_desc;
 
 /* Bytes of workspace a model needs for prefill calls of up to max_rows rows (>= 1). */

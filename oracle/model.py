@@ -13,11 +13,22 @@ to the structure the reference's HF path adds (compiler/frontend/qhf.py:321-409)
   device's top-k order (compiler/tests/oracle.py:558-585) and the route weights
   e = EXP(v - v0), w = e * RECIP(red_sum(e)).
 
-With q_dim = dim, no QK-norm, theta 1e4 (float32 tables), eps 1e-5 and a dense FFN it
-computes exactly DeviceModel(sfu=SfuExact); tests/golden holds runs of the reference
-that pin that. The generalised parts (QK-norm, q_dim != dim, MoE routing) have no
-reference implementation with these numerics: their parity is unpinned beyond the
-construction from pinned primitives (see the tests that cover them).
+The HF path's numerics options (compiler/frontend/hf_generic.py; cfg.attn_norm,
+cfg.kv_channel, cfg.act, cfg.logits_scaling, the last folded into the classifier's
+scales by the model data) change these steps, with the device's primitives:
+- qsum (hf_generic.py:265-292): eq = to_i8(F(e * 127)), att = sum eq V (int32),
+  rq = F(RECIP(f32(sum eq)) * 127) (the sum exact in float32), out = F(F(f32(att) * rq) * a_v);
+- K per channel (hf_generic.py:153-187, 252-254): q = F(q * s_k) per channel before its
+  quant_act, a_k = f32(1 / sqrt(hd)); the cache row to_i8(F(k * inv_sk[c]));
+- V per channel: to_i8(F(v * inv_sv[c])), and a_v[c] per output channel;
+- GELU-tanh gate (hf_generic.py:840-852): numerics.gelu_mul in place of silu_mul.
+
+With q_dim = dim, no QK-norm, theta 1e4 (float32 tables), eps 1e-5, a dense FFN and no
+options it computes exactly DeviceModel(sfu=SfuExact); tests/golden holds runs of the
+reference that pin that. The generalised parts (QK-norm, q_dim != dim, MoE routing, the
+HF options) have no runnable reference implementation with these numerics: they are
+pinned by properties and by float64 attention / GELU within stated tolerances (see the
+tests that cover them), not by reference vectors.
 
 Prefill (qhf.QModel.prefill, compiler/frontend/qhf.py:356-409): every row is a decode
 step at its own position; rows only share the linear layers, whose numerics are
@@ -104,30 +115,24 @@ class OracleModel:
         q = N.rope(q, cs, sn).reshape(M, c.q_dim)
         k = N.rope(k, cs, sn).reshape(M, c.kv_dim)
         inv_sk, inv_sv = qm.kvc[l, 0], qm.kvc[l, 1]
+        fl = int(qm.kv_flags[l]) if getattr(qm, "kv_flags", None) is not None else 0
+        if fl & 1:
+            inv_sk = qm.kvch[l, 1]
+        if fl & 2:
+            inv_sv = qm.kvch[l, 2]
         self.kc[l, pos] = N.to_i8((k * inv_sk).astype(F))
         self.vc[l, pos] = N.to_i8((v * inv_sv).astype(F))
         return q
 
     def attention(self, l, q, pos):
-        """One query row q [q_dim] at position pos against the cache rows 0..pos (llm/ref_model.py:230-243)."""
-        c, D = self.cfg, self.D
-        hd, G, T = c.head_dim, c.group, pos + 1
-        a_k, a_v = self.qm.kvc[l, 2], self.qm.kvc[l, 3]
-        K = self.kc[l, :T].reshape(T, c.kv_heads, hd).astype(np.int64)
-        V = self.vc[l, :T].reshape(T, c.kv_heads, hd).astype(np.int64)
-        qq, s_q = N.quant_act(q.reshape(c.heads, hd))                           # (H, hd), (H,)
-        kk = np.repeat(K, G, axis=1)                                             # (T, H, hd)
-        vv = np.repeat(V, G, axis=1)
-        dots = np.einsum("thd,hd->ht", kk, qq.astype(np.int64))                  # (H, T) exact
-        sc = (dots.astype(np.float64).astype(F) * s_q[:, None]).astype(F)
-        sc = (sc * a_k).astype(F)
-        m = np.max(sc, axis=-1, keepdims=True)
-        e = N.sfu_exp((sc - m).astype(F))
-        r = N.sfu_recip(N.red_sum(e, D))
-        p = (e * r[:, None]).astype(F)
-        pq = N.to_i8((p * F(127)).astype(F)).astype(np.int64)
-        att = np.einsum("ht,thd->hd", pq, vv)
-        return (att.astype(np.float64).astype(F) * a_v).astype(F).reshape(c.q_dim)
+        """One query row q [q_dim] at position pos against the cache rows 0..pos (llm/ref_model.py:230-243;
+        the HF options as numerics.attention states them)."""
+        c, qm = self.cfg, self.qm
+        T = pos + 1
+        fl = int(qm.kv_flags[l]) if getattr(qm, "kv_flags", None) is not None else 0
+        return N.attention(q, self.kc[l, :T], self.vc[l, :T], c.heads, c.kv_heads, qm.kvc[l, 2], qm.kvc[l, 3],
+                           self.D, qsum=c.attn_norm == "qsum", ch_sk=qm.kvch[l, 0] if fl & 1 else None,
+                           ch_av=qm.kvch[l, 3] if fl & 2 else None)
 
     def moe(self, l, xq, s_x):
         """Top-k MoE FFN of one row (compiler/frontend/hf_generic.py:641-657 with device numerics)."""
@@ -140,7 +145,7 @@ class OracleModel:
         y = np.zeros(c.dim, F)
         for j, i in enumerate(ids):
             g_l, u_l, d_l = self.experts[l][i]
-            h = N.silu_mul(g_l(xq, s_x), u_l(xq, s_x))
+            h = N.gate_mul(g_l(xq, s_x), u_l(xq, s_x), c.act)
             hq, s_h = N.quant_act(h)
             y = (y + (w[j] * d_l(hq, s_h)).astype(F)).astype(F)
         self.last_route = (ids, w)
@@ -159,7 +164,7 @@ class OracleModel:
         if c.moe:
             y = np.stack([self.moe(l, xq[m], s_x[m]) for m in range(x.shape[0])])
         else:
-            u = N.silu_mul(self.w1[l](xq, s_x), self.w3[l](xq, s_x))
+            u = N.gate_mul(self.w1[l](xq, s_x), self.w3[l](xq, s_x), c.act)
             hq, s_h = N.quant_act(u)
             y = self.w2[l](hq, s_h)
         return (x + y).astype(F)

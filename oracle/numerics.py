@@ -302,6 +302,69 @@ def silu_mul(h1, h3):
     return ((h1 * sig).astype(F) * np.asarray(h3, F)).astype(F)
 
 
+# GELU's tanh approximation as the device computes it (compiler/frontend/hf_generic.py:840-852):
+# x * 0.5 * (1 + tanh(u)) = x * RECIP(F(EXP(z) + 1)), z = F(x * F(A + F(F(x * x) * B))),
+# u = sqrt(2 / pi) * (x + 0.044715 x^3), A = f32(-2 sqrt(2 / pi)), B = f32(A * 0.044715) (float64
+# constants rounded once).
+GELU_A = F(-2.0 * np.sqrt(2.0 / np.pi))
+GELU_B = F(-2.0 * np.sqrt(2.0 / np.pi) * 0.044715)
+
+
+def gelu_tanh(x):
+    """F(x * RECIP(F(EXP(z) + 1))) with z as above (hf_generic.py:848-852)."""
+    x = np.asarray(x, F)
+    with np.errstate(over="ignore", invalid="ignore"):     # |x| > 1.8e19: x * x -> inf, as on the device
+        z = (x * (GELU_A + ((x * x).astype(F) * GELU_B).astype(F)).astype(F)).astype(F)
+        return (x * sfu_recip((sfu_exp(z) + F(1)).astype(F))).astype(F)
+
+
+def gelu_mul(h1, h3):
+    """The GELU-tanh gate of a GeGLU FFN: u = F(gelu_tanh(h1) * h3) (the gate's activation in place of
+    SiLU, llm/ref_model.py:249-250's product order)."""
+    return (gelu_tanh(h1) * np.asarray(h3, F)).astype(F)
+
+
+def gate_mul(h1, h3, act):
+    """act "silu" (SwiGLU) or "gelu_tanh" (GeGLU)."""
+    return gelu_mul(h1, h3) if act == "gelu_tanh" else silu_mul(h1, h3)
+
+
+def attention(q, K, V, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None):
+    """One query row q [H * hd] against the int8 cache rows K, V [T, Hk * hd] (llm/ref_model.py:230-243,
+    GQA as compiler/frontend/qhf.py:304-319): per head quant_act(q), exact int32 scores
+    F(F(f32(dot) * s_q) * a_k), e = EXP(F(s - max)), then
+    - DeviceModel's form: pq = to_i8(F(F(e * RECIP(red_sum(e))) * 127)), out = F(f32(pq . V) * a_v);
+    - qsum (compiler/frontend/hf_generic.py:265-292): pq = to_i8(F(e * 127)),
+      out = F(F(f32(pq . V) * F(RECIP(f32(sum pq)) * 127)) * a_v).
+    ch_sk [Hk * hd]: K's per-channel scales, q = F(q * s_k) before its quant_act (hf_generic.py:252-254);
+    ch_av [Hk * hd]: a_v per output channel (hf_generic.py:183-186, 292)."""
+    T = K.shape[0]
+    hd = q.shape[-1] // H
+    G = H // Hk
+    per_head = lambda v: np.repeat(np.asarray(v, F).reshape(Hk, hd), G, axis=0)   # (H, hd)
+    Kh = np.repeat(np.asarray(K).reshape(T, Hk, hd).astype(np.int64), G, axis=1)    # (T, H, hd)
+    Vh = np.repeat(np.asarray(V).reshape(T, Hk, hd).astype(np.int64), G, axis=1)
+    qh = np.asarray(q, F).reshape(H, hd)
+    if ch_sk is not None:
+        qh = (qh * per_head(ch_sk)).astype(F)
+    qq, s_q = quant_act(qh)                                                          # (H, hd), (H,)
+    dots = np.einsum("thd,hd->ht", Kh, qq.astype(np.int64))                          # (H, T) exact
+    sc = (dots.astype(np.float64).astype(F) * s_q[:, None]).astype(F)
+    sc = (sc * F(a_k)).astype(F)
+    e = sfu_exp((sc - np.max(sc, axis=-1, keepdims=True)).astype(F))
+    if qsum:
+        pq = to_i8((e * F(127)).astype(F)).astype(np.int64)
+        rq = (sfu_recip(pq.sum(-1).astype(F)) * F(127)).astype(F)                   # (H,), the sum exact
+    else:
+        r = sfu_recip(red_sum(e, D))
+        pq = to_i8(((e * r[:, None]).astype(F) * F(127)).astype(F)).astype(np.int64)
+    att = np.einsum("ht,thd->hd", pq, Vh).astype(np.float64).astype(F)
+    if qsum:
+        att = (att * rq[:, None]).astype(F)
+    av = per_head(ch_av) if ch_av is not None else F(a_v)
+    return (att * av).astype(F).reshape(H * hd)
+
+
 def topk_desc(scores, k):
     """Top-k ids of a score vector: descending values, an equal value placed before a larger id, NaN
     never selected (compiler/tests/oracle.py:558-585). A stable sort on -value does exactly this."""

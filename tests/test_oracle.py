@@ -264,3 +264,150 @@ def test_moe_one_expert_collapses_to_dense():
     for p, t in enumerate(moe.prompt()):
         la, lb = a.forward(t, p), b.forward(t, p)
         assert sha(la) == sha(lb)
+
+
+# ------------------------------------------------------------------ the HF path's options
+# compiler/frontend/hf_generic.py computes these with torch operations; the device computes them with
+# its own EXP / RECIP and fp32 steps. They are pinned by what the mathematics fixes: GELU's tanh form
+# in float64, float64 softmax attention over the dequantised cache, and closed forms.
+
+def test_gelu_tanh_vs_float64():
+    """numerics.gelu_tanh (x RECIP(EXP(z) + 1), hf_generic.py:840-852) against torch's float64 GELU
+    tanh form: |err| <= 1e-5 |x| + 1e-7 over [-12, 12] (the SFU's EXP / RECIP error), exactly x once EXP
+    underflows (x >= 10.5) and a negative zero once it overflows (x <= -10.5)."""
+    import torch
+    x = np.linspace(-12, 12, 96001).astype(F)
+    got = N.gelu_tanh(x)
+    want = torch.nn.functional.gelu(torch.from_numpy(x.astype(np.float64)), approximate="tanh").numpy()
+    assert (np.abs(got - want) <= 1e-5 * np.abs(x) + 1e-7).all()
+    big = np.array([10.5, 11.0, 50.0, 1e4, 3e38], F)
+    assert np.array_equal(N.gelu_tanh(big), big)
+    neg = N.gelu_tanh(-big)
+    assert (neg == 0).all() and np.signbit(neg).all()
+    assert N.gelu_tanh(np.array([0.0], F))[0] == 0
+    # the gate: F(gelu(h1) * h3)
+    h1, h3 = np.array([1.5, -0.75], F), np.array([2.0, -3.0], F)
+    assert np.array_equal(N.gelu_mul(h1, h3), (N.gelu_tanh(h1) * h3).astype(F))
+    assert np.array_equal(N.gate_mul(h1, h3, "silu"), N.silu_mul(h1, h3))
+
+
+def _fp64_attention(q, Kd, Vd, H, Hk, scale):
+    T, hd, G = Kd.shape[0], q.size // H, H // Hk
+    out = np.zeros(H * hd)
+    for h in range(H):
+        g = h // G
+        s = (Kd[:, g * hd:(g + 1) * hd].astype(np.float64) @ q[h * hd:(h + 1) * hd].astype(np.float64)) * scale
+        p = np.exp(s - s.max())
+        out[h * hd:(h + 1) * hd] = (p / p.sum()) @ Vd[:, g * hd:(g + 1) * hd]
+    return out
+
+
+@pytest.mark.parametrize("qsum", [False, True])
+def test_attention_per_channel_vs_float64(qsum):
+    """Per-channel K and V scales (K's folded into q, hf_generic.py:153-187, 252-254): the int8 attention
+    against float64 softmax attention over the dequantised cache (k s_k[c], v s_v[c]) within 0.15 of each
+    channel's max |v| (int8 probabilities and q); the channel scales spread 150x, so a channel taken from
+    the wrong place (reversed, the q fold left out) is off by more than 1."""
+    rng = np.random.default_rng(1)
+    H, Hk, hd, T = 8, 2, 32, 200
+    for trial in range(4):
+        q = (rng.standard_normal(H * hd) * 6).astype(F)
+        kq = rng.integers(-127, 128, (T, Hk * hd)).astype(np.int8)
+        vq = rng.integers(-127, 128, (T, Hk * hd)).astype(np.int8)
+        sk = (np.exp(rng.uniform(-5, 0, Hk * hd)) * 0.05).astype(F)
+        sv = np.exp(rng.uniform(-6, -2, Hk * hd)).astype(F)
+        av = (sv * F(1.0 / 127.0)).astype(F)
+        want = _fp64_attention(q, kq * sk, vq * sv, H, Hk, 1 / np.sqrt(hd))
+        scale = np.abs(vq * sv).max(0).reshape(Hk, hd).repeat(H // Hk, axis=0).ravel()
+        got = N.attention(q, kq, vq, H, Hk, F(1 / np.sqrt(hd)), F(0), 16, qsum=qsum, ch_sk=sk, ch_av=av)
+        assert (np.abs(got - want) <= 0.15 * scale).all(), trial
+
+
+def test_qsum_weights_sum_to_one():
+    """qsum (hf_generic.py:265-292): the weights eq * 127 / sum(eq) sum to 1 exactly, so attention over
+    cache rows that all hold the same value returns that value up to the float32 rounding of the output
+    steps (a few ulps); DeviceModel's form, whose int8 p need not sum to 127, misses it by whole steps
+    of 1/127 on some rows."""
+    rng = np.random.default_rng(2)
+    H, Hk, hd = 4, 2, 16
+    worst_q, worst_d = 0.0, 0.0
+    for T in (1, 2, 7, 100, 1000):
+        q = (rng.standard_normal(H * hd) * 3).astype(F)
+        kq = rng.integers(-127, 128, (T, Hk * hd)).astype(np.int8)
+        row = rng.integers(-127, 128, Hk * hd).astype(np.int8)
+        vq = np.repeat(row[None], T, axis=0)
+        a_v = F(0.01 / 127)
+        want = np.repeat(row.reshape(Hk, hd), H // Hk, axis=0).ravel().astype(np.float64) * 127 * float(a_v)
+        for qsum in (True, False):
+            got = N.attention(q, kq, vq, H, Hk, F(0.05), a_v, 16, qsum=qsum)
+            rel = np.abs(got - want).max() / np.abs(want).max()
+            if qsum:
+                worst_q = max(worst_q, rel)
+            else:
+                worst_d = max(worst_d, rel)
+    assert worst_q < 4e-7
+    assert worst_d > 1e-3
+
+
+def test_per_layer_and_per_channel_constants():
+    """The per-channel constants (hf_generic.py:169-186): float32 division for the inverses, a float32
+    product for a_v; a_k = f32(1 / sqrt(hd)) on a K-per-channel layer; a layer whose row holds one value is
+    per layer, with the per-layer constants of llm/export_w8a8.py:68-72."""
+    cfg = C.TINY_GQA
+    L, kv = cfg.layers, cfg.kv_dim
+    rng = np.random.default_rng(3)
+    s = np.exp(rng.uniform(-6, -1, (L, 2, kv))).astype(F)
+    s[1, 1] = s[1, 1, 0]                                  # layer 1's V per layer
+    flags = W.kv_channel_flags(cfg, s)
+    assert flags.tolist() == [3, 1]
+    ch = W.kv_channel_constants(cfg, s)
+    assert np.array_equal(ch[:, 0], s[:, 0])
+    assert np.array_equal(ch[:, 1], (F(1) / s[:, 0]).astype(F))
+    assert np.array_equal(ch[:, 2], (F(1) / s[:, 1]).astype(F))
+    assert np.array_equal(ch[:, 3], (s[:, 1] * F(1 / 127)).astype(F))
+    kvc = W.kv_constants(cfg, s)
+    assert kvc[0, 2] == kvc[1, 2] == F(1 / np.sqrt(cfg.head_dim))
+    assert kvc[1, 3] == F(float(s[1, 1, 0]) / 127.0) and kvc[1, 1] == F(1.0 / float(s[1, 1, 0]))
+    assert W.kv_channel_constants(cfg, s[:, :, 0]) is None and not W.kv_channel_flags(cfg, s[:, :, 0]).any()
+
+
+def test_calibrate_kv_channel_rule():
+    """calibrate_kv(channel=...) (hf_generic.py:466-491): the chosen parts per channel, the others the
+    layer's single value, which is the per-layer calibration's."""
+    cfg = C.TINY_GQA
+    per_layer = W.calibrate_kv(cfg, channel="")
+    for channel in ("k", "v", "kv"):
+        s = W.calibrate_kv(cfg, channel=channel)
+        assert s.shape == (cfg.layers, 2, cfg.kv_dim)
+        for j, part in enumerate("kv"):
+            assert np.array_equal(s[:, j].max(-1), per_layer[:, j])
+            if part not in channel:
+                assert (s[:, j] == per_layer[:, j][:, None]).all()
+            else:
+                assert (s[:, j].min(-1) < s[:, j].max(-1)).all()
+
+
+def test_logits_scaling_fold_is_torch_division():
+    """The fold of hf_generic.py:913 is `s_w / float(ls)` on a float32 torch tensor: the float32 division
+    by f32(ls); fold_logits_scaling gives the same bits, including for an ls float32 cannot hold."""
+    import torch
+    s = (np.random.default_rng(4).random(5000).astype(F) * F(0.02)).astype(F)
+    for ls in (8.0, 3.0, 0.1, 12.345678901):
+        want = (torch.from_numpy(s) / float(ls)).numpy()
+        assert np.array_equal(W.fold_logits_scaling(s, ls).view(np.uint32), want.view(np.uint32))
+    assert W.fold_logits_scaling(s, 1.0) is s
+
+
+@pytest.mark.parametrize("name", ["tiny-hf", "tiny-hf-kv", "tiny-hf-v", "tiny-hf-moe"])
+def test_oracle_hf_prefill_equals_decode(name):
+    cfg = C.get(name)
+    qm = W.QuantModel(cfg)
+    om = OracleModel(qm)
+    toks = cfg.prompt()
+    for p, t in enumerate(toks):
+        dec = om.forward(t, p)
+    kc, vc = om.kc.copy(), om.vc.copy()
+    om.reset()
+    pre = om.prefill(toks)
+    assert sha(pre) == sha(dec)
+    assert np.array_equal(om.kc, kc) and np.array_equal(om.vc, vc)

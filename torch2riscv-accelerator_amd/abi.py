@@ -11,9 +11,10 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libt2r.so")
 
-T2R_ABI_VERSION = 1
+T2R_ABI_VERSION = 2
 T2R_OK, T2R_EINVAL, T2R_ESHAPE, T2R_ERANGE, T2R_EHIP, T2R_ENOMEM, T2R_ESTATE = 0, -1, -2, -3, -4, -5, -6
 T2R_ADVANCE_POS = 1
+T2R_ATTN_QSUM = 1
 
 c_int, c_int64, c_uint64, c_float, c_void_p = ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_void_p
 P = c_void_p    # every tensor argument is a raw device pointer
@@ -39,7 +40,9 @@ class ModelDesc(ctypes.Structure):
                                  "k_norm", "wqkv", "s_wqkv", "wo", "s_wo", "w1", "s_w1", "w3", "s_w3", "w2", "s_w2",
                                  "router", "s_router", "wg", "s_wg", "wu", "s_wu", "wd", "s_wd", "rope_cos",
                                  "rope_sin", "kv_consts", "k_cache", "v_cache", "workspace")] + \
-        [("workspace_bytes", c_int64), ("max_rows", ctypes.c_int32)]
+        [("workspace_bytes", c_int64), ("max_rows", ctypes.c_int32)] + \
+        [("attn_qsum", ctypes.c_int32), ("ffn_act", ctypes.c_int32), ("kv_channel", c_void_p),
+         ("kv_channel_flags", c_void_p)]
 
 
 # name: (restype, argtypes)
@@ -59,8 +62,12 @@ _SIGS = {
     "t2r_gemm_w8a8": (c_int, [P, P, P, P, c_int, c_int, c_int, P, P, P, P]),
     "t2r_rope": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
     "t2r_kv_append": (c_int, [P, P, c_float, c_float, P, P, P, c_int, c_int, c_int, P]),
+    "t2r_kv_append_ch": (c_int, [P, P, c_float, c_float, P, P, P, P, P, c_int, c_int, c_int, P]),
     "t2r_attn_decode": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int, P, P]),
+    "t2r_attn_decode_opt": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int, c_int, P, P,
+                                    P, P]),
     "t2r_swiglu_w8a8": (c_int, [P, P, P, P, P, P, c_int, c_int, P, P, P, P]),
+    "t2r_gated_ffn_w8a8": (c_int, [c_int, P, P, P, P, P, P, c_int, c_int, P, P, P, P]),
     "t2r_moe_route": (c_int, [P, c_int, c_int, c_int, c_int, P, P, P]),
     "t2r_argmax": (c_int, [P, c_int, c_int, P, P]),
     "t2r_model_workspace_bytes": (c_int64, [ctypes.POINTER(ModelDesc), c_int]),

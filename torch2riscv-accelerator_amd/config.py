@@ -15,6 +15,18 @@ the numerics choices the reference leaves to the caller:
   compiler/frontend/qhf.py:183-189.
 - MoE: `n_experts` experts with top-`top_k` routing; `hidden` is then the
   per-expert FFN width (compiler/frontend/hf_generic.py:602-663).
+- The HF path's numerics options (compiler/frontend/hf_generic.py), all off by
+  default (DeviceModel's form):
+  - `attn_norm` "qsum": int8 probabilities eq = to_i8(F(e * 127)) and the
+    output F(F(f32(sum eq V) * F(RECIP(f32(sum eq)) * 127)) * a_v) instead of
+    p = F(e * RECIP(red_sum(e))) (:265-292);
+  - `kv_channel` "k" / "v" / "kv": static K and / or V scales per cache channel
+    (calibrated per channel, :466-491); K's folded into q before its
+    quantisation, V's applied per output channel (:153-187);
+  - `act` "gelu_tanh": the FFN gate's activation is GELU's tanh approximation
+    from EXP and RECIP (GeGLU, :840-852) instead of SiLU;
+  - `logits_scaling`: the logits divided by it, folded into the classifier's
+    row scales as F(s / F(ls)) (:909-917).
 """
 from dataclasses import dataclass, replace
 
@@ -48,6 +60,10 @@ class ModelConfig:
     seed_p: int = 0
     prompt_len: int = 0
     decode_steps: int = 0
+    attn_norm: str = "device"
+    kv_channel: str = ""
+    act: str = "silu"
+    logits_scaling: float = 1.0
 
     @property
     def q_dim(self):
@@ -74,6 +90,14 @@ class ModelConfig:
             raise ValueError(f"{self.name}: D = {self.D} (8 or 16)")
         if self.rope_method not in ("f32", "f64"):
             raise ValueError(f"{self.name}: rope_method {self.rope_method!r}")
+        if self.attn_norm not in ("device", "qsum"):
+            raise ValueError(f"{self.name}: attn_norm {self.attn_norm!r} (device or qsum)")
+        if self.kv_channel not in ("", "k", "v", "kv"):
+            raise ValueError(f"{self.name}: kv_channel {self.kv_channel!r} ('', k, v or kv)")
+        if self.act not in ("silu", "gelu_tanh"):
+            raise ValueError(f"{self.name}: act {self.act!r} (silu or gelu_tanh)")
+        if not (np.isfinite(self.logits_scaling) and self.logits_scaling != 0):
+            raise ValueError(f"{self.name}: logits_scaling {self.logits_scaling}")
         if self.moe and not 1 <= self.top_k <= min(self.n_experts, 8):
             raise ValueError(f"{self.name}: top-{self.top_k} of {self.n_experts} experts")
         for n in ("dim", "hidden", "q_dim", "kv_dim"):
@@ -128,8 +152,23 @@ TINY_MOE = ModelConfig("tiny-moe", dim=32, hidden=32, layers=2, heads=4, kv_head
                        seq_len=24, theta=1e4, eps=1e-6, n_experts=8, top_k=4, weight_std=None, gain_std=0.1,
                        emb_scale=4.0, seed_w=31, seed_p=32, prompt_len=6, decode_steps=10)
 
+# the HF path's numerics options on tiny models: every option, and each kind of per-channel scale
+TINY_HF = TINY_QWEN.with_(name="tiny-hf", attn_norm="qsum", kv_channel="k", act="gelu_tanh", logits_scaling=8.0,
+                          seed_w=41)
+TINY_HF_KV = TINY_GQA.with_(name="tiny-hf-kv", attn_norm="qsum", kv_channel="kv", logits_scaling=3.0, seed_w=51)
+TINY_HF_V = TINY.with_(name="tiny-hf-v", kv_channel="v", act="gelu_tanh", seed_w=61)
+TINY_HF_MOE = TINY_MOE.with_(name="tiny-hf-moe", attn_norm="qsum", kv_channel="k", act="gelu_tanh", seed_w=71)
+
 CONFIGS = {c.name: c.validate() for c in (C1, C2, C3, C4, C5)}
-TINY_CONFIGS = {c.name: c.validate() for c in (TINY, TINY_GQA, TINY_QWEN, TINY_MOE)}
+TINY_CONFIGS = {c.name: c.validate() for c in (TINY, TINY_GQA, TINY_QWEN, TINY_MOE, TINY_HF, TINY_HF_KV, TINY_HF_V,
+                                                TINY_HF_MOE)}
+
+
+def hf_options(cfg, name=None):
+    """cfg with every HF-path option on (qsum, K per channel, GELU-tanh gate, logits scaling 8), as the
+    reference's HF builds compute (compiler/frontend/hf_generic.py); named name or cfg.name + "-hf"."""
+    return cfg.with_(name=name or cfg.name + "-hf", attn_norm="qsum", kv_channel="k", act="gelu_tanh",
+                     logits_scaling=8.0)
 
 
 def get(name):
@@ -139,4 +178,6 @@ def get(name):
     short = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5}
     if name in short:
         return short[name]
+    if name.endswith("-hf") and name[:-3] in CONFIGS:
+        return hf_options(CONFIGS[name[:-3]])
     raise KeyError(f"unknown config {name!r}")

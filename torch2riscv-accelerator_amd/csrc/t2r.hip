@@ -3,6 +3,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstddef>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -61,7 +62,9 @@ int ensure_init() {
   void* addr = nullptr;
   if (hipGetSymbolAddress(&addr, HIP_SYMBOL(c_sfu)) != hipSuccess || addr == nullptr) return T2R_EHIP;
   // the prefill attention keeps up to kPreMaxLds of score rows in LDS (160 KB per CU on gfx950)
-  const void* pre[] = {(const void*)k_attn_pre<32>, (const void*)k_attn_pre<64>, (const void*)k_attn_pre<128>};
+  const void* pre[] = {(const void*)k_attn_pre<32>, (const void*)k_attn_pre<64>, (const void*)k_attn_pre<128>,
+                       (const void*)k_attn_pre<32, true>, (const void*)k_attn_pre<64, true>,
+                       (const void*)k_attn_pre<128, true>};
   for (const void* f : pre)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPreMaxLds) != hipSuccess)
       return T2R_EHIP;
@@ -122,23 +125,39 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   const bool c16 = a.hd % 16 == 0;
   // batched decode: one workgroup per (row, KV head) for its group of 2..4 query heads
   const int G = a.H / a.Hk;
+  const bool opt = attn_opt(a);                 // the HF options: the kernels' OPT instantiations
   if (mode == ATTN_FUSED && rows > 1 && a.tab != nullptr && G >= 2 && G <= kGqaMaxG &&
       (a.hd == 64 || a.hd == 128) && attn_gqa_lds_bytes(a.S, a.D, G) <= 65536) {
     const dim3 gg(a.Hk, rows);
     const size_t gl = attn_gqa_lds_bytes(a.S, a.D, G);
-    if (a.hd == 64) launch((k_attn_gqa<4>), gg, dim3(kGqaThreads), gl, st, a);
-    else launch((k_attn_gqa<8>), gg, dim3(kGqaThreads), gl, st, a);
+    if (a.hd == 64) {
+      if (opt) launch((k_attn_gqa<4, true>), gg, dim3(kGqaThreads), gl, st, a);
+      else launch((k_attn_gqa<4>), gg, dim3(kGqaThreads), gl, st, a);
+    } else {
+      if (opt) launch((k_attn_gqa<8, true>), gg, dim3(kGqaThreads), gl, st, a);
+      else launch((k_attn_gqa<8>), gg, dim3(kGqaThreads), gl, st, a);
+    }
     return launched();
   }
   if (mode == ATTN_FUSED && a.tab != nullptr && a.hd % 16 == 0 &&
       (a.hd == 16 || a.hd == 32 || a.hd == 48 || a.hd == 64 || a.hd == 128)) {
     const size_t dl = attn_dec_lds_bytes(a.S, a.D);
-    switch (a.hd / 16) {
-      case 1: launch((k_attn_dec<1>), grid, block, dl, st, a); break;
-      case 2: launch((k_attn_dec<2>), grid, block, dl, st, a); break;
-      case 3: launch((k_attn_dec<3>), grid, block, dl, st, a); break;
-      case 4: launch((k_attn_dec<4>), grid, block, dl, st, a); break;
-      default: launch((k_attn_dec<8>), grid, block, dl, st, a); break;
+    if (opt) {
+      switch (a.hd / 16) {
+        case 1: launch((k_attn_dec<1, true>), grid, block, dl, st, a); break;
+        case 2: launch((k_attn_dec<2, true>), grid, block, dl, st, a); break;
+        case 3: launch((k_attn_dec<3, true>), grid, block, dl, st, a); break;
+        case 4: launch((k_attn_dec<4, true>), grid, block, dl, st, a); break;
+        default: launch((k_attn_dec<8, true>), grid, block, dl, st, a); break;
+      }
+    } else {
+      switch (a.hd / 16) {
+        case 1: launch((k_attn_dec<1>), grid, block, dl, st, a); break;
+        case 2: launch((k_attn_dec<2>), grid, block, dl, st, a); break;
+        case 3: launch((k_attn_dec<3>), grid, block, dl, st, a); break;
+        case 4: launch((k_attn_dec<4>), grid, block, dl, st, a); break;
+        default: launch((k_attn_dec<8>), grid, block, dl, st, a); break;
+      }
     }
   } else if (mode == ATTN_FUSED) {
     if (c16) launch((k_attn<ATTN_FUSED, 16>), grid, block, lds, st, a);
@@ -149,9 +168,15 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
     const int hdp = (a.hd + 31) & ~31;
     dim3 pg(a.H, cdiv(rows, kPreRows));
     const size_t pl = attn_pre_lds_bytes(pre_cap(a), hdp);
-    if (hdp == 32) launch((k_attn_pre<32>), pg, dim3(kPreThreads), pl, st, a, rows);
-    else if (hdp == 64) launch((k_attn_pre<64>), pg, dim3(kPreThreads), pl, st, a, rows);
-    else launch((k_attn_pre<128>), pg, dim3(kPreThreads), pl, st, a, rows);
+    if (opt) {
+      if (hdp == 32) launch((k_attn_pre<32, true>), pg, dim3(kPreThreads), pl, st, a, rows);
+      else if (hdp == 64) launch((k_attn_pre<64, true>), pg, dim3(kPreThreads), pl, st, a, rows);
+      else launch((k_attn_pre<128, true>), pg, dim3(kPreThreads), pl, st, a, rows);
+    } else {
+      if (hdp == 32) launch((k_attn_pre<32>), pg, dim3(kPreThreads), pl, st, a, rows);
+      else if (hdp == 64) launch((k_attn_pre<64>), pg, dim3(kPreThreads), pl, st, a, rows);
+      else launch((k_attn_pre<128>), pg, dim3(kPreThreads), pl, st, a, rows);
+    }
   } else {
     if (c16) launch((k_attn<ATTN_ONLY, 16>), grid, block, lds, st, a);
     else launch((k_attn<ATTN_ONLY, 8>), grid, block, lds, st, a);
@@ -163,6 +188,7 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
 struct Model {
   t2r_model_desc d;
   std::vector<float> kvc;           // [L, 4]
+  std::vector<int32_t> kv_flags;    // [L]: bit 0 K per channel, bit 1 V per channel
   int q_dim, kv_dim, qkv_dim, ffn_rows, max_in;
   int32_t* part;                    // split-K partial sums of the prefill linears
   int part_rows;
@@ -275,8 +301,25 @@ void model_dims(Model* m) {
   m->max_in = mi;
 }
 
+// the caller's descriptor as the current version: an ABI-1 descriptor ends before the HF options,
+// which are then off
+bool desc_read(const t2r_model_desc* in, t2r_model_desc* out) {
+  if (!in || (in->abi_version != 1 && in->abi_version != T2R_ABI_VERSION)) return false;
+  std::memset(out, 0, sizeof(*out));
+  std::memcpy(out, in, in->abi_version == 1 ? offsetof(t2r_model_desc, attn_qsum) : sizeof(*out));
+  out->abi_version = T2R_ABI_VERSION;
+  return true;
+}
+
 int validate(const t2r_model_desc* d) {
   if (!d || d->abi_version != T2R_ABI_VERSION) return T2R_EINVAL;
+  if ((d->attn_qsum != 0 && d->attn_qsum != 1) || (d->ffn_act != 0 && d->ffn_act != 1)) return T2R_EINVAL;
+  if (d->kv_channel_flags) {
+    for (int l = 0; l < d->layers; ++l) {
+      if (d->kv_channel_flags[l] & ~3) return T2R_EINVAL;
+      if (d->kv_channel_flags[l] && !d->kv_channel) return T2R_EINVAL;
+    }
+  }
   if (d->dim <= 0 || d->hidden <= 0 || d->layers <= 0 || d->heads <= 0 || d->kv_heads <= 0 || d->head_dim <= 0 ||
       d->vocab <= 0 || d->seq_len <= 0)
     return T2R_ESHAPE;
@@ -392,6 +435,7 @@ int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, c
   a.part = m->part;
   a.part_cap = 4LL * m->part_rows * (m->qkv_dim > m->d.dim ? m->qkv_dim : m->d.dim);
   a.tab = sfu_table_ptr();
+  a.act = m->d.ffn_act;
   if (m->pend_z > 1) return T2R_ESTATE;          // the partials buffer still holds an unfinished linear
   if (argmax_done) *argmax_done = false;
   if (argmax && EPI == EPI_STORE && rows <= kBgMaxRows) {
@@ -465,6 +509,12 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
   at.H = d.heads; at.Hk = d.kv_heads; at.hd = d.head_dim; at.D = d.D; at.S = d.seq_len;
   at.att = m->att; at.att_stride = m->q_dim;
   at.tab = sfu_table_ptr();
+  at.qsum = d.attn_qsum;
+  if (m->kv_flags[l]) {
+    const float* ch = d.kv_channel + (long long)l * 4 * m->kv_dim;   // s_k, 1/s_k, 1/s_v, a_v
+    if (m->kv_flags[l] & 1) { at.ch_sk = ch; at.ch_isk = ch + m->kv_dim; }
+    if (m->kv_flags[l] & 2) { at.ch_isv = ch + 2 * m->kv_dim; at.ch_av = ch + 3 * m->kv_dim; }
+  }
   if (qz > 1) {
     at.part = m->part; at.part_nz = qz; at.part_zstride = (long long)rows * m->qkv_dim;
     at.part_sw = a.s_w; at.part_sx = m->sx;
@@ -498,7 +548,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     a.w = d.w1 + (long long)l * d.hidden * d.dim; a.s_w = d.s_w1 + (long long)l * d.hidden;
     a.w3 = d.w3 + (long long)l * d.hidden * d.dim; a.s_w3 = d.s_w3 + (long long)l * d.hidden;
     a.x = m->x; a.x_stride = d.dim; a.g = d.rms_ffn + L_dim; a.inv_n = inv_d; a.eps = d.eps; a.D = d.D;
-    a.N = d.hidden; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows;
+    a.N = d.hidden; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows; a.act = d.ffn_act;
     if (decode) {
       ProfScope p(m, T2R_PROF_FFN_UP, st);
       if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_SWIGLU>(a, rows, st))) return rc;
@@ -543,7 +593,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     a.w3 = d.wu + (long long)l * E * Fe * d.dim; a.s_w3 = d.s_wu + (long long)l * E * Fe;
     a.xq = m->mxq; a.xq_stride = d.dim; a.s_x = m->msx;
     a.ids = m->ids; a.rows_per_id = Fe; a.ids_stride = k;
-    a.N = k * Fe; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows;
+    a.N = k * Fe; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows; a.act = d.ffn_act;
     {
       ProfScope p(m, T2R_PROF_FFN_UP, st);
       if ((rc = gemv_launch<PRO_XQ, EPI_SWIGLU>(a, rows, st))) return rc;
@@ -723,18 +773,27 @@ int t2r_rope(float* v, const float* cos_t, const float* sin_t, const int32_t* po
   return launched();
 }
 
-int t2r_kv_append(const float* k, const float* v, float inv_sk, float inv_sv, int8_t* kc, int8_t* vc,
-                  const int32_t* pos, int rows, int kv_dim, int S_, void* stream) {
+int t2r_kv_append_ch(const float* k, const float* v, float inv_sk, float inv_sv, const float* inv_sk_ch,
+                     const float* inv_sv_ch, int8_t* kc, int8_t* vc, const int32_t* pos, int rows, int kv_dim, int S_,
+                     void* stream) {
   if (!k || !v || !kc || !vc || !pos) return T2R_EINVAL;
   if (rows <= 0 || kv_dim <= 0 || S_ <= 0) return T2R_ESHAPE;
   T2R_INIT();
-  launch(k_kv_append, dim3(rows), dim3(256), 0, S(stream), k, v, inv_sk, inv_sv, kc, vc, pos, kv_dim, S_);
+  launch(k_kv_append, dim3(rows), dim3(256), 0, S(stream), k, v, inv_sk, inv_sv, inv_sk_ch, inv_sv_ch, kc, vc, pos,
+         kv_dim, S_);
   return launched();
 }
 
-int t2r_attn_decode(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H, int Hk,
-                    int hd, int S_, float a_k, float a_v, int D, float* att, void* stream) {
+int t2r_kv_append(const float* k, const float* v, float inv_sk, float inv_sv, int8_t* kc, int8_t* vc,
+                  const int32_t* pos, int rows, int kv_dim, int S_, void* stream) {
+  return t2r_kv_append_ch(k, v, inv_sk, inv_sv, nullptr, nullptr, kc, vc, pos, rows, kv_dim, S_, stream);
+}
+
+int t2r_attn_decode_opt(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H,
+                        int Hk, int hd, int S_, float a_k, float a_v, int D, int flags, const float* ch_sk,
+                        const float* ch_av, float* att, void* stream) {
   if (!q || !kc || !vc || !pos || !att) return T2R_EINVAL;
+  if (flags & ~T2R_ATTN_QSUM) return T2R_EINVAL;
   if (rows <= 0) return T2R_ESHAPE;
   T2R_INIT();
   AttnArgs a;
@@ -743,20 +802,34 @@ int t2r_attn_decode(const float* q, const int8_t* kc, const int8_t* vc, const in
   a.kc = (int8_t*)kc; a.vc = (int8_t*)vc; a.pos = pos;
   a.a_k = a_k; a.a_v = a_v; a.H = H; a.Hk = Hk; a.hd = hd; a.D = D; a.S = S_;
   a.att = att; a.att_stride = (long long)H * hd;
+  a.qsum = flags & T2R_ATTN_QSUM;
+  a.ch_sk = ch_sk; a.ch_av = ch_av;
   return attn_launch(ATTN_ONLY, a, rows, S(stream));
 }
 
-int t2r_swiglu_w8a8(const int8_t* w1, const float* s_w1, const int8_t* w3, const float* s_w3, const int8_t* xq,
-                    const float* s_x, int F, int K, float* u_out, int8_t* hq, float* s_h, void* stream) {
+int t2r_attn_decode(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H, int Hk,
+                    int hd, int S_, float a_k, float a_v, int D, float* att, void* stream) {
+  return t2r_attn_decode_opt(q, kc, vc, pos, rows, H, Hk, hd, S_, a_k, a_v, D, 0, nullptr, nullptr, att, stream);
+}
+
+int t2r_gated_ffn_w8a8(int act, const int8_t* w1, const float* s_w1, const int8_t* w3, const float* s_w3,
+                       const int8_t* xq, const float* s_x, int F, int K, float* u_out, int8_t* hq, float* s_h,
+                       void* stream) {
   if (!w1 || !s_w1 || !w3 || !s_w3 || !xq || !s_x || !u_out || !hq || !s_h) return T2R_EINVAL;
+  if (act != 0 && act != 1) return T2R_EINVAL;
   if (F <= 0 || F % 16 || F > kMaxK) return T2R_ESHAPE;
   T2R_INIT();
   GemvArgs a = gemv_args();
   a.w = w1; a.s_w = s_w1; a.w3 = w3; a.s_w3 = s_w3; a.xq = xq; a.xq_stride = K; a.s_x = s_x;
-  a.N = F; a.K = K; a.y = u_out; a.y_stride = F;
+  a.N = F; a.K = K; a.y = u_out; a.y_stride = F; a.act = act;
   int rc = gemv_launch<PRO_XQ, EPI_SWIGLU>(a, 1, S(stream));
   if (rc) return rc;
   return t2r_quant_act(u_out, 1, F, hq, s_h, stream);
+}
+
+int t2r_swiglu_w8a8(const int8_t* w1, const float* s_w1, const int8_t* w3, const float* s_w3, const int8_t* xq,
+                    const float* s_x, int F, int K, float* u_out, int8_t* hq, float* s_h, void* stream) {
+  return t2r_gated_ffn_w8a8(0, w1, s_w1, w3, s_w3, xq, s_x, F, K, u_out, hq, s_h, stream);
 }
 
 int t2r_moe_route(const float* scores, int rows, int E, int k, int D, int32_t* ids, float* weights, void* stream) {
@@ -777,9 +850,8 @@ int t2r_argmax(const float* x, int rows, int n, int32_t* idx, void* stream) {
 
 // ---------------------------------------------------------------- model level
 int64_t t2r_model_workspace_bytes(const t2r_model_desc* desc, int max_rows) {
-  if (!desc || max_rows < 1) return -1;
   Model m;
-  m.d = *desc;
+  if (!desc_read(desc, &m.d) || max_rows < 1) return -1;
   model_dims(&m);
   return carve(&m, nullptr, max_rows);
 }
@@ -787,12 +859,15 @@ int64_t t2r_model_workspace_bytes(const t2r_model_desc* desc, int max_rows) {
 int t2r_model_create(const t2r_model_desc* desc, void** model) {
   if (!model) return T2R_EINVAL;
   *model = nullptr;
-  int rc = validate(desc);
+  t2r_model_desc dv;
+  if (!desc_read(desc, &dv)) return T2R_EINVAL;
+  int rc = validate(&dv);
   if (rc) return rc;
   T2R_INIT();
   Model* m = new (std::nothrow) Model();
   if (!m) return T2R_ENOMEM;
-  m->d = *desc;
+  m->d = dv;
+  desc = &m->d;
   model_dims(m);
   if (carve(m, nullptr, desc->max_rows) > desc->workspace_bytes) {
     delete m;
@@ -800,7 +875,11 @@ int t2r_model_create(const t2r_model_desc* desc, void** model) {
   }
   carve(m, (char*)desc->workspace, desc->max_rows);
   m->kvc.assign(desc->kv_consts, desc->kv_consts + (size_t)desc->layers * 4);
+  m->kv_flags.assign((size_t)desc->layers, 0);
+  if (desc->kv_channel_flags)
+    m->kv_flags.assign(desc->kv_channel_flags, desc->kv_channel_flags + desc->layers);
   m->d.kv_consts = nullptr;
+  m->d.kv_channel_flags = nullptr;
   *model = m;
   return T2R_OK;
 }

@@ -16,6 +16,13 @@
 // Modes: ATTN_FUSED (decode: the stages, then attention), ATTN_PREP (prefill: the stages for every
 // row, q rotated in place: k_attn_prep), ATTN_ONLY (prefill: attention of rows whose q is rotated
 // and whose KV rows are all in the cache).
+// The HF path's options (compiler/frontend/hf_generic.py:153-187, 265-292), off by default:
+//   qsum:          pq[t] = to_i8(F(e[t] * 127)), att_h = F(F(f32(sum_t pq V) * rq) * a_v) with
+//                  rq = F(RECIP(f32(sum_t pq[t])) * 127) (an exact integer sum)
+//   K per channel: q = F(q * s_k[c]) before its quant_act; kc = to_i8(F(k * inv_sk[c]))
+//   V per channel: vc = to_i8(F(v * inv_sv[c])); att = F(... * a_v[c]) per output channel
+// (channel c = g hd + j of the cache row). The specialised kernels take them in a separate
+// instantiation (template flag OPT), so the default one is unchanged.
 #pragma once
 #include "t2r_device.h"
 
@@ -55,7 +62,18 @@ struct AttnArgs {
   int part_nz;
   const float* part_sw;
   const float* part_sx;
+  // the HF path's options (see above); nullptr / 0: off
+  int qsum;
+  const float* ch_sk;        // K per channel [kv_dim]: the q multiplier s_k
+  const float* ch_isk;       //   and 1 / s_k for the cache row
+  const float* ch_isv;       // V per channel [kv_dim]: 1 / s_v for the cache row
+  const float* ch_av;        //   and a_v per output channel
 };
+
+inline bool attn_opt(const AttnArgs& a) { return a.qsum || a.ch_sk || a.ch_isk || a.ch_isv || a.ch_av; }
+
+// qsum's output scale rq = F(RECIP(f32(sum of the int8 probabilities)) * 127)
+T2R_DEV float qsum_scale(int sum, const float* tab) { return sfu_recip((float)sum, tab) * 127.0f; }
 
 // RMSNorm (optional) and RoPE of one head vector v[0..hd) in LDS, by one wave.
 T2R_DEV void head_norm_rope(float* v, const float* gain, const AttnArgs& a, int pos, int lane) {
@@ -121,6 +139,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
   __shared__ int part[kAttnWaves][kMaxHd];
   __shared__ float red[64];
   __shared__ float s_sq, s_r;
+  __shared__ int s_qs[kAttnWaves];
 
   const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -145,8 +164,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     for (int j = lane; j < hd / 4; j += 64) {
       int k4[4], v4[4];
       for (int b = 0; b < 4; ++b) {
-        k4[b] = to_i8(s_k[4 * j + b] * a.inv_sk);
-        v4[b] = to_i8(s_v[4 * j + b] * a.inv_sv);
+        const int ch = g * hd + 4 * j + b;
+        k4[b] = to_i8(s_k[4 * j + b] * (a.ch_isk ? a.ch_isk[ch] : a.inv_sk));
+        v4[b] = to_i8(s_v[4 * j + b] * (a.ch_isv ? a.ch_isv[ch] : a.inv_sv));
       }
       const int kw = pack_i8x4(k4[0], k4[1], k4[2], k4[3]), vw = pack_i8x4(v4[0], v4[1], v4[2], v4[3]);
       s_kq[j] = kw;
@@ -161,6 +181,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     for (int j = lane; j < hd; j += 64) s_q[j] = qkv[h * hd + j];
     __builtin_amdgcn_wave_barrier();
     if (MODE != ATTN_ONLY) head_norm_rope(s_q, a.qn, a, pos, lane);
+    if (a.ch_sk) {                               // K per channel: its scales folded into q
+      for (int j = lane; j < hd; j += 64) s_q[j] = s_q[j] * a.ch_sk[g * hd + j];
+      __builtin_amdgcn_wave_barrier();
+    }
     // quant_act of the head
     float m = 0.0f;
     for (int j = lane; j < hd; j += 64) m = nanmax(m, fabsf(s_q[j]));
@@ -211,12 +235,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     float s = 0.0f;
     if (lane < D) s = ordered_sum_t<false>(sc, T, D, P, lane);
     s = __shfl(s, 0);
-    if (lane == 0) s_r = sfu_recip(s);
+    if (lane == 0) s_r = a.qsum ? 1.0f : sfu_recip(s);   // qsum: pq = to_i8(F(F(e * 1) * 127)), e * 1 = e
   }
   __syncthreads();
   int8_t* pq = (int8_t*)(dyn + D * P);
   const float r = s_r;
-  for (int t = tid; t < T; t += kAttnThreads) pq[t] = (int8_t)to_i8((sc[osum_index(t, D, P)] * r) * 127.0f);
+  int qs = 0;
+  for (int t = tid; t < T; t += kAttnThreads) {
+    const int p = to_i8((sc[osum_index(t, D, P)] * r) * 127.0f);
+    pq[t] = (int8_t)p;
+    qs += p;
+  }
+  if (a.qsum) {
+    qs = wave_sum_i32(qs);
+    if (lane == 0) s_qs[wave] = qs;
+  }
   __syncthreads();
 
   // ---- P.V: thread = (chunk slot c of CB columns, row slice ts); int32 partial sums, 4 rows in flight.
@@ -274,10 +307,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
     for (int b = 0; b < CB; ++b) part[wave][lane * CB + b] = acc[b];
   __syncthreads();
   float* out = a.att + row * a.att_stride;
+  float rq = 1.0f;
+  if (a.qsum) {
+    int tot = 0;
+    for (int w = 0; w < kAttnWaves; ++w) tot += s_qs[w];
+    rq = qsum_scale(tot, c_sfu);
+  }
   for (int j = tid; j < hd; j += kAttnThreads) {
     int s = 0;
     for (int w = 0; w < kAttnWaves; ++w) s += part[w][j];
-    out[h * hd + j] = (float)s * a.a_v;
+    float o = (float)s;
+    if (a.qsum) o = o * rq;
+    out[h * hd + j] = o * (a.ch_av ? a.ch_av[g * hd + j] : a.a_v);
   }
 }
 
@@ -321,7 +362,7 @@ T2R_DEV int slot_group_sum(int v) {
   return v;
 }
 
-template <int NCH>   // 16-byte chunks per head row: hd = 16 NCH
+template <int NCH, bool OPT = false>   // 16-byte chunks per head row: hd = 16 NCH; OPT: the HF options
 __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   constexpr int HD = 16 * NCH;
   constexpr int NCHP = NCH <= 1 ? 1 : (NCH <= 2 ? 2 : (NCH <= 4 ? 4 : 8));
@@ -337,6 +378,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   __shared__ int part[kAttnWaves * 4][HD];
   __shared__ float red[16];
   __shared__ float s_sq, s_r;
+  __shared__ int s_qs[kAttnWaves];
 
   const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -372,6 +414,20 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     xa[k] = va[j];
     xb[k] = vb[j];
     xg[k] = gn[j];
+  }
+  // OPT: per-channel scales of this KV head (wave 0: 1 / s_k, 1 / s_v; wave 1: the q multiplier s_k),
+  // loaded unconditionally from a readable address when absent
+  float xc1[NV], xc2[NV];
+  if constexpr (OPT) {
+    const float* c1 = wave == 0 ? a.ch_isk : a.ch_sk;
+    c1 = c1 ? c1 + (long long)g * HD : va;
+    const float* c2 = wave == 0 && a.ch_isv ? a.ch_isv + (long long)g * HD : va;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int j = min(lane + 64 * k, HD - 1);
+      xc1[k] = c1[j];
+      xc2[k] = c2[j];
+    }
   }
   float cs[NV], sn[NV];                          // RoPE of element j = lane + 64 k: pair j / 2
 #pragma unroll
@@ -424,7 +480,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         const int j = lane + 64 * k;
-        const int8_t kb = (int8_t)to_i8(xr[k] * a.inv_sk), vb8 = (int8_t)to_i8(xb[k] * a.inv_sv);
+        float isk = a.inv_sk, isv = a.inv_sv;
+        if constexpr (OPT) {
+          if (a.ch_isk) isk = xc1[k];
+          if (a.ch_isv) isv = xc2[k];
+        }
+        const int8_t kb = (int8_t)to_i8(xr[k] * isk), vb8 = (int8_t)to_i8(xb[k] * isv);
         if (j < HD) {
           kq8[j] = kb;
           vq8[j] = vb8;
@@ -435,6 +496,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
         }
       }
     } else {
+      if constexpr (OPT) {
+        if (a.ch_sk) {                           // K per channel: its scales folded into q
+#pragma unroll
+          for (int k = 0; k < NV; ++k) xr[k] = xr[k] * xc1[k];
+        }
+      }
       uint32_t am = 0;
 #pragma unroll
       for (int k = 0; k < NV; ++k)
@@ -526,10 +593,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   if (wave == 0) {
     float ssum = 0.0f;
     if (lane < D) ssum = ordered_sum_t<false>(sc, T, D, P, lane);
-    if (lane == 0) s_r = sfu_recip(ssum, tab);
+    if (lane == 0) s_r = (OPT && a.qsum) ? 1.0f : sfu_recip(ssum, tab);   // qsum: to_i8(F(F(e * 1) * 127))
   }
   __syncthreads();
   const float rr = s_r;
+  int qs = 0;                                    // qsum: the slot-0 lanes' probabilities (each row once)
 
   // ---- P.V over the thread's rows, four at a time: int8 p of the four rows against V transposed
   int acc[16];
@@ -554,6 +622,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) rw[u][w] = here ? vpos[w] : vw[i4 + u][w];
       }
+      if (OPT && c == 0) qs += (pk[0] + pk[1]) + (pk[2] + pk[3]);
       const int pp = pack_i8x4(pk[0], pk[1], pk[2], pk[3]);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -575,17 +644,34 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     if (NCHP <= 8) v += dpp_i<0x128>(v);                      // row_ror:8
     acc[b] = v;
   }
+  if (OPT && a.qsum) {
+    qs = wave_sum_i32(qs);
+    if (lane == 0) s_qs[wave] = qs;
+  }
   if ((lane & 15) < NCHP && cok) {
 #pragma unroll
     for (int b = 0; b < 16; ++b) part[wave * 4 + (lane >> 4)][16 * c + b] = acc[b];
   }
   __syncthreads();
   float* out = a.att + row * a.att_stride;
+  float rq = 1.0f;
+  if (OPT && a.qsum) {
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) tot += s_qs[w];
+    rq = qsum_scale(tot, tab);
+  }
   for (int j = tid; j < HD; j += kAttnThreads) {
     int ssum = 0;
 #pragma unroll
     for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
-    out[(long long)h * HD + j] = (float)ssum * a.a_v;
+    if constexpr (OPT) {
+      float o = (float)ssum;
+      if (a.qsum) o = o * rq;
+      out[(long long)h * HD + j] = o * (a.ch_av ? a.ch_av[(long long)g * HD + j] : a.a_v);
+    } else {
+      out[(long long)h * HD + j] = (float)ssum * a.a_v;
+    }
   }
 }
 
@@ -634,8 +720,9 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
   for (int j = lane; j < hd / 4; j += 64) {
     int k4[4], v4[4];
     for (int b = 0; b < 4; ++b) {
-      k4[b] = to_i8(v0[4 * j + b] * a.inv_sk);
-      v4[b] = to_i8(v1[4 * j + b] * a.inv_sv);
+      const int ch = g * hd + 4 * j + b;
+      k4[b] = to_i8(v0[4 * j + b] * (a.ch_isk ? a.ch_isk[ch] : a.inv_sk));
+      v4[b] = to_i8(v1[4 * j + b] * (a.ch_isv ? a.ch_isv[ch] : a.inv_sv));
     }
     *(int*)(kc + 4 * j) = pack_i8x4(k4[0], k4[1], k4[2], k4[3]);
     *(int*)(vc + 4 * j) = pack_i8x4(v4[0], v4[1], v4[2], v4[3]);
@@ -660,7 +747,7 @@ constexpr size_t kPreMaxLds = 136 * 1024;     // dynamic LDS the kernels are set
 
 T2R_DEV int pre_est(int S) { return (S + 16 + 31) & ~31; }   // row stride of the score / exp rows
 
-template <int HDP>   // head dim padded to a multiple of 32 (MFMA k-steps)
+template <int HDP, bool OPT = false>   // head dim padded to a multiple of 32 (MFMA k-steps); OPT: HF options
 __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   constexpr int KS = HDP / 32;                 // k-steps of the score MFMA; column tiles of P.V
   constexpr int NV = HDP > 64 ? 2 : 1;
@@ -670,6 +757,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   __shared__ __align__(16) int8_t VT[4][HDP][32];
   __shared__ float s_sq[kPreRows], s_r[kPreRows];
   __shared__ int s_T[kPreRows];
+  __shared__ int s_qs[4][kPreRows];
   // row blocks in reverse: a causal prompt's later rows attend to more positions, and the blocks
   // dispatched first should be the longest (the short ones then fill in behind them)
   const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kPreRows, tid = threadIdx.x;
@@ -692,6 +780,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
     for (int k = 0; k < NV; ++k) {
       const int j = lane + 64 * k;
       x[k] = q[min(j, HD - 1)];
+      if (OPT && a.ch_sk) x[k] = x[k] * a.ch_sk[(long long)g * HD + min(j, HD - 1)];   // K per channel
       if (j < HD) am = max(am, abs_bits(x[k]));
     }
     const float sq = fv(wave_max_u32(am)) * kInv127;
@@ -777,7 +866,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
     if (D > 4 && (l & 7) == 0) acc = acc + o;
     o = dpp_f<0x108>(acc);
     if (D > 8 && (l & 15) == 0) acc = acc + o;
-    if (l == 0) s_r[i] = sfu_recip(acc, tab);
+    if (l == 0) s_r[i] = (OPT && a.qsum) ? 1.0f : sfu_recip(acc, tab);   // qsum: to_i8(F(F(e * 1) * 127))
   }
   __syncthreads();
 
@@ -791,6 +880,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   const float rm = pm < kPreRows ? s_r[pm] : 0.0f;
   const int Tm = pm < kPreRows ? s_T[pm] : 0;
   int8_t* vt = &VT[wave][0][0];
+  int qs = 0;                                         // qsum: this lane's probabilities of row pm
   for (int c0 = wave; c0 < ntile; c0 += 4 * kPreTiles) {
     v4i_t vb[kPreTiles][HDP / 32];                    // V rows: lane takes row (lane & 31), half of the columns
 #pragma unroll
@@ -825,6 +915,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
           const float e = E[min(pm, kPreRows - 1) * est + t];
           bytes[b] = t < Tm ? to_i8((e * rm) * 127.0f) : 0;
         }
+        if (OPT) qs += (bytes[0] + bytes[1]) + (bytes[2] + bytes[3]);
         pw[w] = pack_i8x4(bytes[0], bytes[1], bytes[2], bytes[3]);
       }
       const v4i_t pa = {pw[0], pw[1], pw[2], pw[3]};
@@ -834,6 +925,10 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
         pv[jt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, fb, pv[jt], 0, 0, 0);
       }
     }
+  }
+  if (OPT && a.qsum) {                                // (row pm: lanes pm and pm + 32 of every wave)
+    qs += __shfl_xor(qs, 32);
+    if (lane < kPreRows) s_qs[wave][lane] = qs;
   }
   __syncthreads();                                    // E is free: partial sums of the four waves
   int* part = (int*)E;                                // [4][16][HDP]
@@ -850,7 +945,14 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
     if (s_T[m] == 0) continue;
     const int sum = part[(0 * kPreRows + m) * HDP + j] + part[(1 * kPreRows + m) * HDP + j] +
                     part[(2 * kPreRows + m) * HDP + j] + part[(3 * kPreRows + m) * HDP + j];
-    a.att[(long long)(r0 + m) * a.att_stride + (long long)h * HD + j] = (float)sum * a.a_v;
+    if constexpr (OPT) {
+      float o = (float)sum;
+      if (a.qsum) o = o * qsum_scale((s_qs[0][m] + s_qs[1][m]) + (s_qs[2][m] + s_qs[3][m]), tab);
+      a.att[(long long)(r0 + m) * a.att_stride + (long long)h * HD + j] =
+          o * (a.ch_av ? a.ch_av[(long long)g * HD + j] : a.a_v);
+    } else {
+      a.att[(long long)(r0 + m) * a.att_stride + (long long)h * HD + j] = (float)sum * a.a_v;
+    }
   }
 }
 
@@ -890,7 +992,7 @@ inline size_t attn_gqa_lds_bytes(int S, int D, int G) {
   return (size_t)G * ((size_t)D * osum_stride(S, D) + 64) * 4 + (size_t)G * ((S + 15) & ~15);
 }
 
-template <int NCH>   // 16-byte chunks per head row: hd = 16 NCH (64 or 128)
+template <int NCH, bool OPT = false>   // 16-byte chunks per head row: hd = 16 NCH (64 or 128); OPT: HF options
 __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   constexpr int HD = 16 * NCH, KS = HD / 32;                // MFMA k-steps per key tile
   constexpr int NCHP = NCH;                                 // (4 or 8: a power of two)
@@ -905,6 +1007,7 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   __shared__ __align__(16) float s_vec[kGqaWaves][HD];
   __shared__ float s_sq[kGqaMaxG], s_r[kGqaMaxG];
   __shared__ float red[kGqaWaves][kGqaMaxG];
+  __shared__ int s_qs[kGqaWaves][kGqaMaxG];
   __shared__ int part[kGqaWaves * 4][kGqaMaxG * HD];
 
   const int g = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
@@ -946,6 +1049,20 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
     const long long ip = (long long)pos * (HD / 2) + (j >> 1);
     cs[k] = a.cos_t[ip];
     sn[k] = a.sin_t[ip];
+  }
+  // OPT: per-channel scales of the KV head (job 0: 1 / s_k, 1 / s_v; query jobs: the q multiplier
+  // s_k), loaded unconditionally from a readable address when absent
+  float xc1[NV], xc2[NV];
+  if constexpr (OPT) {
+    const float* c1 = job == 0 ? a.ch_isk : a.ch_sk;
+    c1 = c1 ? c1 + (long long)g * HD : va;
+    const float* c2 = job == 0 && a.ch_isv ? a.ch_isv + (long long)g * HD : va;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int j = min(lane + 64 * k, HD - 1);
+      xc1[k] = c1[j];
+      xc2[k] = c2[j];
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   v4i_t kw[kGqaRK][KS];
@@ -999,7 +1116,12 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         const int j = lane + 64 * k;
-        const int8_t kb = (int8_t)to_i8(xr[k] * a.inv_sk), vb8 = (int8_t)to_i8(xb[k] * a.inv_sv);
+        float isk = a.inv_sk, isv = a.inv_sv;
+        if constexpr (OPT) {
+          if (a.ch_isk) isk = xc1[k];
+          if (a.ch_isv) isv = xc2[k];
+        }
+        const int8_t kb = (int8_t)to_i8(xr[k] * isk), vb8 = (int8_t)to_i8(xb[k] * isv);
         if (j < HD) {
           s_k8[j] = kb;
           s_v8[j] = vb8;
@@ -1008,6 +1130,12 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
         }
       }
     } else {
+      if constexpr (OPT) {
+        if (a.ch_sk) {                           // K per channel: its scales folded into q
+#pragma unroll
+          for (int k = 0; k < NV; ++k) xr[k] = xr[k] * xc1[k];
+        }
+      }
       uint32_t am = 0;
 #pragma unroll
       for (int k = 0; k < NV; ++k)
@@ -1101,7 +1229,7 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   if (wave < G) {
     float ssum = 0.0f;
     if (lane < D) ssum = ordered_sum_t<false>(dyn + wave * SH, T, D, P, lane);
-    if (lane == 0) s_r[wave] = sfu_recip(ssum, tab);
+    if (lane == 0) s_r[wave] = (OPT && a.qsum) ? 1.0f : sfu_recip(ssum, tab);   // qsum: to_i8(F(F(e * 1) * 127))
   }
   __syncthreads();
 
@@ -1110,6 +1238,7 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) rh[r] = s_r[r < G ? r : 0];
   const int T4 = (T + 3) & ~3;
+  int qs[4] = {0, 0, 0, 0};                      // qsum: the probabilities of the thread's keys, per head
   for (int t = tid; t < T4; t += kGqaThreads) {
     const int k = osum_index(min(t, T - 1), D, P);
     float ev[4];
@@ -1117,7 +1246,18 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
     for (int h = 0; h < 4; ++h) ev[h] = dyn[(h < G ? h : 0) * SH + k];
 #pragma unroll
     for (int h = 0; h < 4; ++h)
-      if (h < G) pq[h * SP + t] = (int8_t)(t < T ? to_i8((ev[h] * rh[h]) * 127.0f) : 0);
+      if (h < G) {
+        const int p = t < T ? to_i8((ev[h] * rh[h]) * 127.0f) : 0;
+        pq[h * SP + t] = (int8_t)p;
+        if (OPT) qs[h] += p;
+      }
+  }
+  if (OPT && a.qsum) {
+#pragma unroll
+    for (int h = 0; h < kGqaMaxG; ++h) {
+      const int v = wave_sum_i32(qs[h]);
+      if (lane == 0) s_qs[wave][h] = v;
+    }
   }
   __syncthreads();
 
@@ -1185,7 +1325,18 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
 #pragma unroll
     for (int w = 0; w < kGqaWaves * 4; ++w) ssum += part[w][idx];
     const int h = idx / HD, j = idx - h * HD;
-    out[(long long)(g * G + h) * HD + j] = (float)ssum * a.a_v;
+    if constexpr (OPT) {
+      float o = (float)ssum;
+      if (a.qsum) {
+        int tot = 0;
+#pragma unroll
+        for (int w = 0; w < kGqaWaves; ++w) tot += s_qs[w][h];
+        o = o * qsum_scale(tot, tab);
+      }
+      out[(long long)(g * G + h) * HD + j] = o * (a.ch_av ? a.ch_av[(long long)g * HD + j] : a.a_v);
+    } else {
+      out[(long long)(g * G + h) * HD + j] = (float)ssum * a.a_v;
+    }
   }
 }
 

@@ -272,6 +272,23 @@ T2R_DEV float silu_mul(float h1, float h3, const float* tab = c_sfu) {
   return a * h3;
 }
 
+// GELU-tanh gate (GeGLU; compiler/frontend/hf_generic.py:840-852): GELU's tanh approximation from EXP
+// and RECIP, x * 0.5 (1 + tanh(u)) = x * RECIP(F(EXP(z) + 1)) with z = F(x * F(A + F(F(x * x) * B))),
+// A = f32(-2 sqrt(2 / pi)), B = f32(-2 sqrt(2 / pi) 0.044715); then F(gelu * h3). Large negative x:
+// EXP gives +inf, RECIP 0, the product a signed zero.
+constexpr float kGeluA = -1.5957692f;     // the float32 values (shortest round-trip decimals)
+constexpr float kGeluB = -0.071354814f;
+T2R_DEV float gelu_mul(float h1, float h3, const float* tab = c_sfu) {
+  const float z = h1 * (kGeluA + (h1 * h1) * kGeluB);
+  const float a = h1 * sfu_recip(sfu_exp(z, tab) + 1.0f, tab);
+  return a * h3;
+}
+
+// the FFN gate: act 0 SiLU (SwiGLU), 1 GELU-tanh (GeGLU); act is uniform over the launch
+T2R_DEV float gate_mul(float h1, float h3, int act, const float* tab = c_sfu) {
+  return act ? gelu_mul(h1, h3, tab) : silu_mul(h1, h3, tab);
+}
+
 // 16 int8 products of a 128-bit weight chunk with a 128-bit activation chunk, accumulated
 T2R_DEV int dot16(int4 w, int4 x, int acc) {
   acc = __builtin_amdgcn_sdot4(w.x, x.x, acc, false);

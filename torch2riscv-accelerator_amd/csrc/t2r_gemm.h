@@ -117,6 +117,7 @@ struct GemmArgs {
   const float* tab;          // SFU tables (device copy of c_sfu; required for EPI_SWIGLU)
   unsigned long long* argmax_key;  // optional (k_bgemv, EPI_STORE): per row m the atomic max of
                                    // argmax_key(y, n), the greedy token of the row (keys zeroed before)
+  int act;                   // EPI_SWIGLU gate: 0 SiLU, 1 GELU-tanh (gate_mul)
 };
 
 // source row of tile column c (0 .. BN) for the block's column origin n0 (SwiGLU interleave)
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(GemmArgs a) {
         if (n >= a.N) continue;
         const int ac1 = acc[i][0][r], ac3 = acc[i][1][r];
         const float h1 = dequant(ac1, a.s_w[n], sx), h3 = dequant(ac3, a.s_w3[n], sx);
-        a.y[(long long)m * a.y_stride + n] = silu_mul(h1, h3);
+        a.y[(long long)m * a.y_stride + n] = gate_mul(h1, h3, a.act);
         if (a.acc_out) {
           a.acc_out[(long long)m * 2 * a.N + n] = ac1;
           a.acc_out[(long long)m * 2 * a.N + a.N + n] = ac3;
@@ -403,7 +404,7 @@ __global__ __launch_bounds__(256) void k_gemm_d(GemmArgs a, int ntile, int nz) {
         const int m = mrow(i, r);
         if (m >= a.M || n >= a.N) continue;
         const int ac1 = acc[i][0][r], ac3 = acc[i][1][r];
-        a.y[(long long)m * a.y_stride + n] = silu_mul(dequant(ac1, sw1, sx[i][r]), dequant(ac3, sw3, sx[i][r]), tab_lds);
+        a.y[(long long)m * a.y_stride + n] = gate_mul(dequant(ac1, sw1, sx[i][r]), dequant(ac3, sw3, sx[i][r]), a.act, tab_lds);
         if (a.acc_out) {
           a.acc_out[(long long)m * 2 * a.N + n] = ac1;
           a.acc_out[(long long)m * 2 * a.N + a.N + n] = ac3;
@@ -600,7 +601,8 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
     if constexpr (SPLIT) {
       a.part[((long long)z * a.M + m) * a.N + n] = s1;
     } else if constexpr (EPI == EPI_SWIGLU) {
-      a.y[(long long)m * a.y_stride + n] = silu_mul(dequant(s1, e_sw[i], e_sx[i]), dequant(s3, e_sw3[i], e_sx[i]), tab_lds);
+      a.y[(long long)m * a.y_stride + n] = gate_mul(dequant(s1, e_sw[i], e_sx[i]), dequant(s3, e_sw3[i], e_sx[i]), a.act,
+                                                 tab_lds);
       if (a.acc_out) {
         a.acc_out[(long long)m * 2 * a.N + n] = s1;
         a.acc_out[(long long)m * 2 * a.N + a.N + n] = s3;

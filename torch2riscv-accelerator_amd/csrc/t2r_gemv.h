@@ -51,6 +51,7 @@ struct GemvArgs {
   int rows_per_id;           //   ids[row * ids_stride + r / rows_per_id] * rows_per_id + r % rows_per_id
   int ids_stride;
   const float* tab;          // the SFU tables (kSfuWords floats, 16-byte aligned) in device memory
+  int act;                   // EPI_SWIGLU gate: 0 SiLU, 1 GELU-tanh (gate_mul)
 };
 
 T2R_DEV long long weight_row(const GemvArgs& a, int row_in, int row) {
@@ -329,7 +330,7 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs a) {
       const int row = r0 + lane;
       if (row < N) {
         float v = dequant(ac, w1s, s_x);
-        if (EPI == EPI_SWIGLU) v = silu_mul(v, dequant(ac3, w3s, s_x), tab_lds);
+        if (EPI == EPI_SWIGLU) v = gate_mul(v, dequant(ac3, w3s, s_x), a.act, tab_lds);
         if (EPI == EPI_RESID) v = rr + v;
         y[row] = v;
         if (a.acc_out != nullptr) {

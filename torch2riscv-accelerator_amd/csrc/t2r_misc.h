@@ -158,15 +158,18 @@ __global__ __launch_bounds__(256) void k_rope(float* v, const float* cos_t, cons
   }
 }
 
-// kc[pos[r]] = to_i8(F(k[r] * inv_sk)), vc[pos[r]] = to_i8(F(v[r] * inv_sv))
+// kc[pos[r]] = to_i8(F(k[r] * inv_sk)), vc[pos[r]] = to_i8(F(v[r] * inv_sv)); per channel c with
+// inv_sk_ch[c] / inv_sv_ch[c] when given
 __global__ __launch_bounds__(256) void k_kv_append(const float* k, const float* v, float inv_sk, float inv_sv,
-                                                   int8_t* kc, int8_t* vc, const int32_t* pos, int kv_dim, int S) {
+                                                   const float* inv_sk_ch, const float* inv_sv_ch, int8_t* kc,
+                                                   int8_t* vc, const int32_t* pos, int kv_dim, int S) {
   const int row = blockIdx.x;
   const long long p = pos[row];
   if (p < 0 || p >= S) return;
   for (int i = threadIdx.x; i < kv_dim; i += blockDim.x) {
-    kc[p * kv_dim + i] = (int8_t)to_i8(k[(long long)row * kv_dim + i] * inv_sk);
-    vc[p * kv_dim + i] = (int8_t)to_i8(v[(long long)row * kv_dim + i] * inv_sv);
+    const float isk = inv_sk_ch ? inv_sk_ch[i] : inv_sk, isv = inv_sv_ch ? inv_sv_ch[i] : inv_sv;
+    kc[p * kv_dim + i] = (int8_t)to_i8(k[(long long)row * kv_dim + i] * isk);
+    vc[p * kv_dim + i] = (int8_t)to_i8(v[(long long)row * kv_dim + i] * isv);
   }
 }
 

@@ -41,10 +41,16 @@ class ResidentModel:
 
         with torch.cuda.device(dev):
             up("emb_q", qm.emb_q); up("emb_s", qm.emb_s)
+            # a tied classifier shares the embedding's int8 rows; its scales are its own when the logits'
+            # scaling is folded into them
             if qm.cls_q is qm.emb_q:
-                keep["cls_q"], keep["cls_s"] = keep["emb_q"], keep["emb_s"]
+                keep["cls_q"] = keep["emb_q"]
             else:
-                up("cls_q", qm.cls_q); up("cls_s", qm.cls_s)
+                up("cls_q", qm.cls_q)
+            if qm.cls_s is qm.emb_s:
+                keep["cls_s"] = keep["emb_s"]
+            else:
+                up("cls_s", qm.cls_s)
             for n in ("rms_att", "rms_ffn", "rms_final", "wqkv", "s_wqkv", "wo", "s_wo"):
                 up(n, getattr(qm, n))
             if c.qk_norm:
@@ -54,6 +60,10 @@ class ResidentModel:
             for n in names:
                 up(n, getattr(qm, n))
             up("rope_cos", qm.cos); up("rope_sin", qm.sin)
+            kvch = getattr(qm, "kvch", None)
+            self.kv_flags = np.ascontiguousarray(getattr(qm, "kv_flags", np.zeros(c.layers)), np.int32)
+            if kvch is not None and self.kv_flags.any():
+                up("kv_channel", kvch)
             self.kc = torch.zeros((c.layers, c.seq_len, c.kv_dim), dtype=torch.int8, device=dev)
             self.vc = torch.zeros_like(self.kc)
             self.kv_consts = np.ascontiguousarray(qm.kvc, F)
@@ -67,6 +77,9 @@ class ResidentModel:
             for n, t in keep.items():
                 setattr(desc, n, t.data_ptr())
             desc.kv_consts = self.kv_consts.ctypes.data
+            desc.attn_qsum = int(c.attn_norm == "qsum")
+            desc.ffn_act = int(c.act == "gelu_tanh")
+            desc.kv_channel_flags = self.kv_flags.ctypes.data
             desc.k_cache, desc.v_cache = self.kc.data_ptr(), self.vc.data_ptr()
             desc.max_rows = self.max_rows
             nbytes = self.lib.t2r_model_workspace_bytes(ctypes.byref(desc), self.max_rows)

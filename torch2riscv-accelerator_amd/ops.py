@@ -115,6 +115,16 @@ def kv_append(k, v, inv_sk, inv_sv, kc, vc, pos):
              abi.ptr(pos), k.numel() // kv, kv, kc.shape[0], _s())
 
 
+def kv_append_ch(k, v, inv_sk, inv_sv, kc, vc, pos):
+    """KV append with per-channel inverse scales: inv_sk / inv_sv are [kv_dim] device tensors or scalars."""
+    _dev(k, v, kc, vc, pos)
+    kv = kc.shape[-1]
+    vec = lambda x: abi.ptr(x) if isinstance(x, torch.Tensor) else None
+    sca = lambda x: 0.0 if isinstance(x, torch.Tensor) else float(x)
+    abi.call("t2r_kv_append_ch", abi.ptr(k), abi.ptr(v), sca(inv_sk), sca(inv_sv), vec(inv_sk), vec(inv_sv),
+             abi.ptr(kc), abi.ptr(vc), abi.ptr(pos), k.numel() // kv, kv, kc.shape[0], _s())
+
+
 def attention(q, kc, vc, pos, H, Hk, a_k, a_v, D):
     """Attention of rows q [rows, H * hd] at positions pos over the int8 caches [S, Hk * hd]."""
     _dev(q, kc, vc, pos)
@@ -126,6 +136,19 @@ def attention(q, kc, vc, pos, H, Hk, a_k, a_v, D):
     return att
 
 
+def attention_opt(q, kc, vc, pos, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None):
+    """attention() with the HF path's options: qsum normalisation, K per channel (ch_sk [Hk * hd]: q
+    multiplied before its quantisation), V per channel (ch_av [Hk * hd] in place of a_v)."""
+    _dev(q, kc, vc, pos)
+    hd = q.shape[-1] // H
+    rows = q.numel() // q.shape[-1]
+    att = torch.empty_like(q)
+    abi.call("t2r_attn_decode_opt", abi.ptr(q), abi.ptr(kc), abi.ptr(vc), abi.ptr(pos), rows, H, Hk, hd,
+             kc.shape[0], float(a_k), float(a_v), int(D), abi.T2R_ATTN_QSUM if qsum else 0, abi.ptr(ch_sk),
+             abi.ptr(ch_av), abi.ptr(att), _s())
+    return att
+
+
 def swiglu(w1, s_w1, w3, s_w3, xq, s_x):
     _dev(w1, s_w1, w3, s_w3, xq, s_x)
     F_, K = w1.shape
@@ -134,6 +157,19 @@ def swiglu(w1, s_w1, w3, s_w3, xq, s_x):
     s_h = torch.empty(1, dtype=F32, device=w1.device)
     abi.call("t2r_swiglu_w8a8", abi.ptr(w1), abi.ptr(s_w1), abi.ptr(w3), abi.ptr(s_w3), abi.ptr(xq), abi.ptr(s_x),
              F_, K, abi.ptr(u), abi.ptr(hq), abi.ptr(s_h), _s())
+    return u, hq, s_h
+
+
+def gated_ffn(act, w1, s_w1, w3, s_w3, xq, s_x):
+    """The gated up-projection with gate activation act ("silu" or "gelu_tanh"), then quant_act."""
+    _dev(w1, s_w1, w3, s_w3, xq, s_x)
+    F_, K = w1.shape
+    u = torch.empty(F_, dtype=F32, device=w1.device)
+    hq = torch.empty(F_, dtype=I8, device=w1.device)
+    s_h = torch.empty(1, dtype=F32, device=w1.device)
+    code = {"silu": 0, "gelu_tanh": 1}[act]
+    abi.call("t2r_gated_ffn_w8a8", code, abi.ptr(w1), abi.ptr(s_w1), abi.ptr(w3), abi.ptr(s_w3), abi.ptr(xq),
+             abi.ptr(s_x), F_, K, abi.ptr(u), abi.ptr(hq), abi.ptr(s_h), _s())
     return u, hq, s_h
 
 

@@ -17,6 +17,16 @@ constants per layer.
 - KV constants per layer from the static scales (s_k, s_v):
   1/s_k, 1/s_v, a_k = s_k / sqrt(head_dim), a_v = s_v / 127, each computed in
   float64 and rounded once (llm/export_w8a8.py:68-72).
+- Per-channel KV scales (cfg.kv_channel; compiler/frontend/hf_generic.py:153-187,
+  466-491): scales [L, 2, kv_dim]; a layer whose K (or V) row holds one value is
+  per layer. A K-per-channel layer multiplies q by s_k per channel before its
+  quantisation and scales the scores by a_k = f32(1 / sqrt(head_dim)) only; the
+  cache takes to_i8(F(k * F(1 / s_k))) per channel (a float32 division). A
+  V-per-channel layer quantises with F(1 / s_v) per channel and scales the output
+  channel by a_v = F(s_v * f32(1 / 127)) (a float32 product).
+- logits_scaling: the classifier's row scales divided by it, F(s / f32(ls)) (the
+  float32 division of hf_generic.py:909-917); a tied classifier keeps the
+  embedding's int8 rows and gets scales of its own.
 """
 import hashlib
 import json
@@ -99,14 +109,51 @@ def rope_tables(cfg):
     return np.cos(val).astype(F), np.sin(val).astype(F)
 
 
+def kv_channel_flags(cfg, kv_scales):
+    """(L,) int32: bit 0 K per channel, bit 1 V per channel, for scales (L, 2) (none) or (L, 2, kv_dim):
+    a layer's row is per channel unless it holds one value (compiler/frontend/hf_generic.py:155-160)."""
+    kv = np.asarray(kv_scales, F)
+    flags = np.zeros(cfg.layers, np.int32)
+    if kv.ndim == 3:
+        for l in range(cfg.layers):
+            for j in (0, 1):
+                if not np.all(kv[l, j] == kv[l, j, 0]):
+                    flags[l] |= 1 << j
+    return flags
+
+
 def kv_constants(cfg, kv_scales):
-    """(L, 4) float32: 1/s_k, 1/s_v, s_k / sqrt(head_dim), s_v / 127 per layer."""
-    kv = np.asarray(kv_scales, F).reshape(cfg.layers, 2)
+    """(L, 4) float32 per layer: 1/s_k, 1/s_v, a_k, a_v. a_k = s_k / sqrt(head_dim), or 1 / sqrt(head_dim) on a
+    K-per-channel layer; a_v = s_v / 127 (hf_generic.py:172-186). With scales (L, 2, kv_dim) a layer's value is
+    its channel 0 (the per-layer case, every channel equal)."""
+    kv = np.asarray(kv_scales, F)
+    flags = kv_channel_flags(cfg, kv)
+    kv1 = kv[:, :, 0] if kv.ndim == 3 else kv.reshape(cfg.layers, 2)
     out = np.empty((cfg.layers, 4), F)
-    for l, (sk, sv) in enumerate(kv):
-        out[l] = [F(1.0 / float(sk)), F(1.0 / float(sv)), F(float(sk) / np.sqrt(cfg.head_dim)),
-                  F(float(sv) / 127.0)]
+    for l, (sk, sv) in enumerate(kv1):
+        a_k = F(1.0 / np.sqrt(cfg.head_dim)) if flags[l] & 1 else F(float(sk) / np.sqrt(cfg.head_dim))
+        out[l] = [F(1.0 / float(sk)), F(1.0 / float(sv)), a_k, F(float(sv) / 127.0)]
     return out
+
+
+def kv_channel_constants(cfg, kv_scales):
+    """(L, 4, kv_dim) float32 per cache channel: s_k (the q multiplier), F(1 / s_k), F(1 / s_v),
+    F(s_v * f32(1 / 127)) (float32 operations, hf_generic.py:169-186), or None for per-layer scales."""
+    kv = np.asarray(kv_scales, F)
+    if kv.ndim != 3:
+        return None
+    one = F(1.0)
+    with np.errstate(divide="ignore"):
+        out = np.stack([kv[:, 0], (one / kv[:, 0]).astype(F), (one / kv[:, 1]).astype(F),
+                        (kv[:, 1] * F(1.0 / 127.0)).astype(F)], axis=1)
+    return np.ascontiguousarray(out, F)
+
+
+def fold_logits_scaling(cls_s, ls):
+    """Classifier row scales with the logits' division folded in: F(s / f32(ls)) (hf_generic.py:909-917)."""
+    if ls == 1.0:
+        return cls_s
+    return (np.asarray(cls_s, F) / F(ls)).astype(F)
 
 
 class QuantModel:
@@ -155,12 +202,22 @@ class QuantModel:
             self.cls_q, self.cls_s = self.emb_q, self.emb_s
         else:
             self.cls_q, self.cls_s = cls.result()
+        self.cls_s = fold_logits_scaling(self.cls_s, c.logits_scaling)
         pool.shutdown()
         self.cos, self.sin = rope_tables(c)
         if kv_scales is None:
             kv_scales = stored_kv_scales(c)
-        self.kv_scales = np.asarray(kv_scales, F).reshape(L, 2)
+        self._set_kv(kv_scales)
+
+    def _set_kv(self, kv_scales):
+        c = self.cfg
+        kv = np.asarray(kv_scales, F)
+        self.kv_scales = kv if kv.ndim == 3 else kv.reshape(c.layers, 2)
+        if self.kv_scales.ndim == 3 and self.kv_scales.shape != (c.layers, 2, c.kv_dim):
+            raise ValueError(f"{c.name}: kv_scales shape {self.kv_scales.shape}")
         self.kvc = kv_constants(c, self.kv_scales)
+        self.kvch = kv_channel_constants(c, self.kv_scales)
+        self.kv_flags = kv_channel_flags(c, self.kv_scales)
 
     # the arrays a model consists of (dense; MoE replaces w1 / w3 / w2 with router / wg / wu / wd)
     DENSE = ("w1", "s_w1", "w3", "s_w3", "w2", "s_w2")
@@ -188,9 +245,10 @@ class QuantModel:
             setattr(self, k, np.ascontiguousarray(v))
         if getattr(self, "cos", None) is None or getattr(self, "sin", None) is None:
             self.cos, self.sin = rope_tables(c)
-        self.kv_scales = np.asarray(self.kv_scales, F).reshape(L, 2)
-        if getattr(self, "kvc", None) is None:
-            self.kvc = kv_constants(c, self.kv_scales)
+        kvc = getattr(self, "kvc", None)
+        self._set_kv(self.kv_scales)
+        if kvc is not None:
+            self.kvc = np.asarray(kvc, F)
         expect = {"emb_q": (c.vocab, c.dim), "wqkv": (L, c.q_dim + 2 * c.kv_dim, c.dim), "wo": (L, c.dim, c.q_dim),
                   "cls_q": (c.vocab, c.dim), "cos": (c.seq_len, hd // 2), "sin": (c.seq_len, hd // 2),
                   "kvc": (L, 4), "rms_att": (L, c.dim), "rms_ffn": (L, c.dim), "rms_final": (c.dim,)}
@@ -215,8 +273,9 @@ class QuantModel:
 # ------------------------------------------------------------------ KV calibration
 def _fp32_forward_rows(cfg, tokens, amax_out, weight=None):
     """Causal fp32 forward of `tokens` at positions 0.. (all rows at once, torch on the CPU),
-    recording max|k| and max|v| per layer (after RoPE for k). llama2.c run.c semantics
-    (llm/ref_model.py:45-91) generalised as compiler/frontend/qhf.py:206-243."""
+    recording max|k| and max|v| per layer and cache channel into amax_out [L, 2, kv_dim] (after RoPE for
+    k). llama2.c run.c semantics (llm/ref_model.py:45-91) generalised as compiler/frontend/qhf.py:206-243;
+    cfg.act "gelu_tanh" gates with GELU's tanh form."""
     import torch
     c = cfg
     fp32_tensor = weight if weight is not None else globals()["fp32_tensor"]
@@ -235,6 +294,11 @@ def _fp32_forward_rows(cfg, tokens, amax_out, weight=None):
         p = v.reshape(v.shape[:-1] + (-1, 2))
         return torch.stack((-p[..., 1], p[..., 0]), dim=-1).reshape(v.shape)
 
+    if c.act == "gelu_tanh":
+        act = lambda h: torch.nn.functional.gelu(h, approximate="tanh")
+    else:
+        act = torch.nn.functional.silu
+
     with torch.no_grad():
         x = t(fp32_tensor(c, "tok", -1))[torch.tensor(tokens)]
         mask = torch.tril(torch.ones(M, M, dtype=torch.bool))
@@ -248,8 +312,8 @@ def _fp32_forward_rows(cfg, tokens, amax_out, weight=None):
                 k = rms(k, t(fp32_tensor(c, "k_norm", l)))
             q = q * cos[:, None] + swapneg(q) * sin[:, None]
             k = k * cos[:, None] + swapneg(k) * sin[:, None]
-            amax_out[l, 0] = max(amax_out[l, 0], float(k.abs().max()))
-            amax_out[l, 1] = max(amax_out[l, 1], float(v.abs().max()))
+            amax_out[l, 0] = np.maximum(amax_out[l, 0], k.reshape(M, -1).abs().amax(0).double().numpy())
+            amax_out[l, 1] = np.maximum(amax_out[l, 1], v.abs().amax(0).double().numpy())
             kk = k.repeat_interleave(G, dim=1)                        # (M, H, hd)
             vv = v.reshape(M, Hk, hd).repeat_interleave(G, dim=1)
             s = torch.einsum("mhd,thd->hmt", q, kk) / np.sqrt(hd)
@@ -266,23 +330,32 @@ def _fp32_forward_rows(cfg, tokens, amax_out, weight=None):
                 for m in range(M):
                     for j in range(c.top_k):
                         e = int(ids[m, j])
-                        h = torch.nn.functional.silu(wg[e] @ xb[m]) * (wu[e] @ xb[m])
+                        h = act(wg[e] @ xb[m]) * (wu[e] @ xb[m])
                         y[m] += wts[m, j] * (wd[e] @ h)
                 x = x + y
             else:
-                h = torch.nn.functional.silu(xb @ t(fp32_tensor(c, "w1", l)).T) * (xb @ t(fp32_tensor(c, "w3", l)).T)
+                h = act(xb @ t(fp32_tensor(c, "w1", l)).T) * (xb @ t(fp32_tensor(c, "w3", l)).T)
                 x = x + h @ t(fp32_tensor(c, "w2", l)).T
 
 
-def calibrate_kv(cfg, tokens=None, chunk=None, weight=None):
-    """Static per-layer KV scales: max(absmax, 1e-8) / 127 over an fp32 run of the prompt
-    (llm/test_l4.py:51-55, compiler/frontend/qhf.py:246-251). weight(cfg, name, layer): the fp32
-    tensors (default: the synthetic ones of fp32_tensor)."""
+def calibrate_kv(cfg, tokens=None, chunk=None, weight=None, channel=None):
+    """Static KV scales: max(absmax, 1e-8) / 127 over an fp32 run of the prompt, per layer [L, 2]
+    (llm/test_l4.py:51-55, compiler/frontend/qhf.py:246-251), or with channel "k" / "v" / "kv"
+    (default cfg.kv_channel) those parts per cache channel [L, 2, kv_dim], the others' rows the layer's
+    single value (compiler/frontend/hf_generic.py:466-491). weight(cfg, name, layer): the fp32 tensors
+    (default: the synthetic ones of fp32_tensor)."""
+    channel = cfg.kv_channel if channel is None else channel
     tokens = cfg.prompt() if tokens is None else list(tokens)
     tokens = tokens[:cfg.seq_len]
-    amax = np.zeros((cfg.layers, 2), np.float64)
+    amax = np.zeros((cfg.layers, 2, cfg.kv_dim), np.float64)
     _fp32_forward_rows(cfg, tokens, amax, weight)
-    return (np.maximum(amax, 1e-8) / 127.0).astype(F)
+    if not channel:
+        return (np.maximum(amax.max(-1), 1e-8) / 127.0).astype(F)
+    out = np.repeat(amax.max(-1, keepdims=True), cfg.kv_dim, -1)
+    for j, part in enumerate("kv"):
+        if part in channel:
+            out[:, j] = amax[:, j]
+    return (np.maximum(out, 1e-8) / 127.0).astype(F)
 
 
 _KV_FILE = os.path.join(HERE, "kv_scales.json")
@@ -294,7 +367,7 @@ def stored_kv_scales(cfg):
     if os.path.exists(_KV_FILE):
         with open(_KV_FILE) as f:
             table = json.load(f)
-        if cfg.name in table and table[cfg.name]["seed_w"] == cfg.seed_w:
+        if cfg.name in table and table[cfg.name]["seed_w"] == cfg.seed_w and not cfg.kv_channel:
             return np.array(table[cfg.name]["bits"], np.uint32).view(F).reshape(cfg.layers, 2)
     if cfg.layers * cfg.dim <= 1 << 16:
         return calibrate_kv(cfg)
