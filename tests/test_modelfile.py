@@ -33,6 +33,7 @@ def same_model(a, b):
 
 
 @pytest.mark.parametrize("name,version", [("tiny", 1), ("tiny-gqa", 1), ("tiny-qwen", 2), ("tiny-moe", 2),
+                                          ("tiny-hf", 2), ("tiny-hf-kv", 2), ("tiny-hf-v", 2), ("tiny-hf-moe", 2),
                                           ("c1-stories15m", 1)])
 def test_w8a8_round_trip(tmp_path, name, version):
     cfg = C.get(name)
@@ -237,3 +238,23 @@ def test_hf_tokenizer(tmp_path):
     t2 = MF.open_tokenizer(str(tmp_path), len(vocab), bos_id=0)  # a directory; BOS on request
     assert t2.encode("hello") == [0, vocab["hello"]]
     assert t2.decode([0, vocab["hello"]]) == "<s>hello"
+
+
+@pytest.mark.parametrize("name", ["tiny-hf", "tiny-hf-kv", "tiny-hf-moe"])
+def test_w8a8_hf_options_round_trip(tmp_path, name):
+    """The HF options survive a version-2 file: the config fields, the per-channel KV scales (`kvch`) and
+    their constants, and a tied classifier's own folded scales beside the shared int8 rows."""
+    cfg = C.get(name)
+    qm = W.QuantModel(cfg)
+    p = str(tmp_path / "m.w8a8")
+    MF.write_w8a8(qm, p)
+    back = MF.read_w8a8(p)
+    for f in ("attn_norm", "act", "kv_channel", "logits_scaling"):
+        assert getattr(back.cfg, f) == getattr(cfg, f), f
+    assert back.kv_scales.shape == (cfg.layers, 2, cfg.kv_dim)
+    assert np.array_equal(back.kvch, qm.kvch) and np.array_equal(back.kv_flags, qm.kv_flags)
+    assert np.array_equal(back.kvc.view(np.uint32), qm.kvc.view(np.uint32))
+    assert np.array_equal(back.cls_s.view(np.uint32), qm.cls_s.view(np.uint32))
+    if cfg.tied:
+        assert back.cls_q is back.emb_q
+        assert (cfg.logits_scaling == 1.0) == (back.cls_s is back.emb_s)

@@ -6,8 +6,10 @@
   (out / D, in, D): tile t holds output rows [t D, (t + 1) D) transposed. Version 1 is the
   reference's llama2.c-shaped model. Version 2 (this package's extension, which a version-1 reader
   refuses) adds what version 1 cannot express: q_dim != dim, QK-norm, MoE, theta / eps, the RoPE
-  method and an untied classifier, in a `cfg` entry and extra named tensors; its linear weights
-  are row-major (out, in) int8 (the B tiles serve the reference's matrix engine, not this device).
+  method, an untied classifier and the HF path's numerics options (qsum, the GELU-tanh gate, the
+  logits scaling folded into s_wcls, per-channel KV scales as a per-layer `kvch` tensor), in a `cfg`
+  entry and extra named tensors; its linear weights are row-major (out, in) int8 (the B tiles serve
+  the reference's matrix engine, not this device).
 - llama2.c legacy fp32 checkpoints (llm/checkpoint.py:30-59): 7 int32 (dim, hidden, layers, heads,
   kv_heads, vocab, seq_len; vocab < 0: separate classifier), then the fp32 tensors in run.c's order.
 - `tokenizer.bin`, llama2.c's SentencePiece-style BPE (llm/tokenizer.py:10-67).
@@ -75,9 +77,10 @@ def _rope_head(wide, hd):
 
 
 def _kvp(qm):
-    """(L, 8) float32: s_k, s_v, 1/s_k, 1/s_v, s_k / sqrt(head_dim), s_v / 127, 0, 0 per layer."""
+    """(L, 8) float32: s_k, s_v, 1/s_k, 1/s_v, a_k, a_v, 0, 0 per layer (per-channel scales: channel 0's
+    values here, the rows in `kvch`)."""
     out = np.zeros((qm.cfg.layers, 8), F)
-    out[:, 0:2] = qm.kv_scales
+    out[:, 0:2] = qm.kv_scales[:, :, 0] if qm.kv_scales.ndim == 3 else qm.kv_scales
     out[:, 2:6] = qm.kvc
     return out
 
@@ -86,10 +89,16 @@ _CFG_WORDS = 16
 
 
 def _cfg_block(c):
+    """Words 0-5 head_dim, qk_norm, tied, n_experts, top_k, RoPE method; 6-9 eps, theta (float64);
+    10 qsum, 11 the gate (1 GELU-tanh), 12 per-channel KV (bit 0 K, bit 1 V), 13-14 logits_scaling
+    (float64; already folded into s_wcls)."""
     w = np.zeros(_CFG_WORDS, np.uint32)
     w[0:6] = [c.head_dim, int(c.qk_norm), int(c.tied), c.n_experts, c.top_k, 1 if c.rope_method == "f64" else 0]
     w[6:8] = np.array([c.eps], np.float64).view(np.uint32)       # float64: the config's values exactly
     w[8:10] = np.array([c.theta], np.float64).view(np.uint32)
+    w[10:13] = [int(c.attn_norm == "qsum"), int(c.act == "gelu_tanh"),
+                ("k" in c.kv_channel) | (("v" in c.kv_channel) << 1)]
+    w[13:15] = np.array([c.logits_scaling], np.float64).view(np.uint32)
     return w
 
 
@@ -98,7 +107,8 @@ def is_v1(cfg):
     head_dim = dim / heads, no QK-norm, no MoE)."""
     c = cfg
     return (c.q_dim == c.dim and c.head_dim * c.heads == c.dim and not c.qk_norm and not c.moe
-            and c.eps == 1e-5 and c.rope_method == "f32" and c.theta == 10000.0)
+            and c.eps == 1e-5 and c.rope_method == "f32" and c.theta == 10000.0 and c.attn_norm == "device"
+            and not c.kv_channel and c.act == "silu" and c.logits_scaling == 1.0)
 
 
 def write_w8a8(qm, path, d=None):
@@ -126,6 +136,8 @@ def write_w8a8(qm, path, d=None):
                   ("s_w13", np.concatenate([qm.s_w1[l], qm.s_w3[l]])),
                   ("w2", lin(qm.w2[l])), ("s_w2", qm.s_w2[l])]
         t.append(("kvp", kvp[l]))
+        if qm.kv_scales.ndim == 3:
+            t.append(("kvch", qm.kv_scales[l]))
         if c.qk_norm:
             t += [("q_norm", qm.q_norm[l]), ("k_norm", qm.k_norm[l])]
         return [(n, np.ascontiguousarray(a)) for n, a in t]
@@ -206,10 +218,14 @@ class W8A8File:
             return C.ModelConfig(head_dim=self.dim // self.heads, theta=10000.0, eps=1e-5, rope_method="f32",
                                  tied=False, **base)
         w = self.get("cfg")
+        ls = float(np.array(w[13:15]).view(np.float64)[0])
         return C.ModelConfig(head_dim=int(w[0]), qk_norm=bool(w[1]), tied=bool(w[2]), n_experts=int(w[3]),
                              top_k=int(w[4]), rope_method="f64" if w[5] else "f32",
                              eps=float(np.array(w[6:8]).view(np.float64)[0]),
-                             theta=float(np.array(w[8:10]).view(np.float64)[0]), **base)
+                             theta=float(np.array(w[8:10]).view(np.float64)[0]),
+                             attn_norm="qsum" if w[10] else "device", act="gelu_tanh" if w[11] else "silu",
+                             kv_channel=("k" if w[12] & 1 else "") + ("v" if w[12] & 2 else ""),
+                             logits_scaling=ls if ls else 1.0, **base)
 
     def quant_model(self, name=None):
         """The QuantModel (row-major int8 weights) of the file. A version-1 classifier equal to the
@@ -227,6 +243,8 @@ class W8A8File:
                 cls_s.view(np.uint32), a["emb_s"].view(np.uint32)):
             c = dataclasses.replace(c, tied=True)
         a["cls_q"], a["cls_s"] = (a["emb_q"], a["emb_s"]) if c.tied else (cls_q, cls_s)
+        if c.tied and not np.array_equal(cls_s.view(np.uint32), a["emb_s"].view(np.uint32)):
+            a["cls_s"] = cls_s                     # the embedding's rows with the logits scaling folded in
         a["cos"] = _rope_head(self.get("rope_cos").reshape(c.seq_len, -1), hd)
         a["sin"] = _rope_head(self.get("rope_sin").reshape(c.seq_len, -1), hd)
 
@@ -252,6 +270,8 @@ class W8A8File:
             a["s_w2"] = per("s_w2")
         kvp = per("kvp")
         a["kv_scales"], a["kvc"] = kvp[:, 0:2], kvp[:, 2:6]
+        if "kvch" in self.entries:
+            a["kv_scales"] = per("kvch", lambda x: x.reshape(2, c.kv_dim))
         if c.qk_norm:
             a["q_norm"], a["k_norm"] = per("q_norm"), per("k_norm")
         return W.QuantModel.from_arrays(c, a)

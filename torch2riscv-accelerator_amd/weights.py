@@ -243,6 +243,11 @@ class QuantModel:
             if v is None:
                 raise ValueError(f"{cfg.name}: array {k} missing")
             setattr(self, k, np.ascontiguousarray(v))
+        # a tied classifier stays the embedding's arrays (one copy on the device)
+        if arrays.get("cls_q") is arrays.get("emb_q"):
+            self.cls_q = self.emb_q
+        if arrays.get("cls_s") is arrays.get("emb_s"):
+            self.cls_s = self.emb_s
         if getattr(self, "cos", None) is None or getattr(self, "sin", None) is None:
             self.cos, self.sin = rope_tables(c)
         kvc = getattr(self, "kvc", None)
