@@ -342,14 +342,16 @@ def attention(q, K, V, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None):
     hd = q.shape[-1] // H
     G = H // Hk
     per_head = lambda v: np.repeat(np.asarray(v, F).reshape(Hk, hd), G, axis=0)   # (H, hd)
-    Kh = np.repeat(np.asarray(K).reshape(T, Hk, hd).astype(np.int64), G, axis=1)    # (T, H, hd)
-    Vh = np.repeat(np.asarray(V).reshape(T, Hk, hd).astype(np.int64), G, axis=1)
+    # int8 products summed in float64 are exact: |dot| <= 127^2 hd and |P.V| <= 127^2 T, far below 2^53
+    Kg = np.asarray(K).reshape(T, Hk, hd).transpose(1, 0, 2).astype(np.float64)      # (Hk, T, hd)
+    Vg = np.asarray(V).reshape(T, Hk, hd).transpose(1, 0, 2).astype(np.float64)
     qh = np.asarray(q, F).reshape(H, hd)
     if ch_sk is not None:
         qh = (qh * per_head(ch_sk)).astype(F)
     qq, s_q = quant_act(qh)                                                          # (H, hd), (H,)
-    dots = np.einsum("thd,hd->ht", Kh, qq.astype(np.int64))                          # (H, T) exact
-    sc = (dots.astype(np.float64).astype(F) * s_q[:, None]).astype(F)
+    qg = qq.astype(np.float64).reshape(Hk, G, hd)
+    dots = np.matmul(qg, Kg.transpose(0, 2, 1)).reshape(H, T)                        # (H, T) exact
+    sc = (dots.astype(F) * s_q[:, None]).astype(F)
     sc = (sc * F(a_k)).astype(F)
     e = sfu_exp((sc - np.max(sc, axis=-1, keepdims=True)).astype(F))
     if qsum:
@@ -358,7 +360,7 @@ def attention(q, K, V, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None):
     else:
         r = sfu_recip(red_sum(e, D))
         pq = to_i8(((e * r[:, None]).astype(F) * F(127)).astype(F)).astype(np.int64)
-    att = np.einsum("ht,thd->hd", pq, Vh).astype(np.float64).astype(F)
+    att = np.matmul(pq.astype(np.float64).reshape(Hk, G, T), Vg).reshape(H, hd).astype(F)   # exact sums
     if qsum:
         att = (att * rq[:, None]).astype(F)
     av = per_head(ch_av) if ch_av is not None else F(a_v)

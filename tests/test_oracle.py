@@ -411,3 +411,14 @@ def test_oracle_hf_prefill_equals_decode(name):
     pre = om.prefill(toks)
     assert sha(pre) == sha(dec)
     assert np.array_equal(om.kc, kc) and np.array_equal(om.vc, vc)
+
+
+def test_calibrate_kv_windows():
+    """Text longer than the cache (hf_generic.py:472-484): windows of seq_len, each from position 0, and the
+    max over them: equal to the max of calibrating each window alone."""
+    cfg = C.TINY_GQA
+    toks = list(np.random.default_rng(5).integers(0, cfg.vocab, 2 * cfg.seq_len + 5))
+    both = W.calibrate_kv(cfg, tokens=toks, channel="kv")
+    parts = [W.calibrate_kv(cfg, tokens=toks[w:w + cfg.seq_len], channel="kv") for w in range(0, len(toks), cfg.seq_len)]
+    assert np.array_equal(both, np.maximum.reduce(parts))
+    assert not np.array_equal(both, parts[0])

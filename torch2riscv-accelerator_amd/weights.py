@@ -347,13 +347,16 @@ def calibrate_kv(cfg, tokens=None, chunk=None, weight=None, channel=None):
     """Static KV scales: max(absmax, 1e-8) / 127 over an fp32 run of the prompt, per layer [L, 2]
     (llm/test_l4.py:51-55, compiler/frontend/qhf.py:246-251), or with channel "k" / "v" / "kv"
     (default cfg.kv_channel) those parts per cache channel [L, 2, kv_dim], the others' rows the layer's
-    single value (compiler/frontend/hf_generic.py:466-491). weight(cfg, name, layer): the fp32 tensors
-    (default: the synthetic ones of fp32_tensor)."""
+    single value (compiler/frontend/hf_generic.py:466-491). A text longer than seq_len is calibrated
+    window by window. weight(cfg, name, layer): the fp32 tensors (default: the synthetic ones of
+    fp32_tensor)."""
     channel = cfg.kv_channel if channel is None else channel
     tokens = cfg.prompt() if tokens is None else list(tokens)
-    tokens = tokens[:cfg.seq_len]
     amax = np.zeros((cfg.layers, 2, cfg.kv_dim), np.float64)
-    _fp32_forward_rows(cfg, tokens, amax, weight)
+    # tokens beyond seq_len: windows of seq_len, each from position 0 (a fresh cache), the max over them
+    # (compiler/frontend/hf_generic.py:472-484)
+    for w in range(0, max(len(tokens), 1), cfg.seq_len):
+        _fp32_forward_rows(cfg, tokens[w:w + cfg.seq_len], amax, weight)
     if not channel:
         return (np.maximum(amax.max(-1), 1e-8) / 127.0).astype(F)
     out = np.repeat(amax.max(-1, keepdims=True), cfg.kv_dim, -1)
