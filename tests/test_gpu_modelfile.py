@@ -79,3 +79,22 @@ def test_llamadevice_from_llama2c_checkpoint(tmp_path):
     assert [t for t, _ in dev.generate(prompt, steps=10)] == [t for t, _ in ref.generate(prompt, steps=10)]
     dev.close()
     ref.close()
+
+
+@pytest.mark.parametrize("kind", ["qwen3", "mixtral"])
+def test_hf_checkpoint_on_device(tmp_path, kind):
+    """An HF checkpoint directory (transformers' own tiny random model, saved as safetensors) through
+    LlamaDevice(path): the imported W8A8 model decodes on the device bit-identically to the oracle."""
+    from oracle import OracleModel
+    from t2r_amd.runtime import LlamaDevice
+    from test_hf_import import _build
+    model = _build(kind)
+    model.save_pretrained(str(tmp_path))
+    dev = LlamaDevice(str(tmp_path))
+    assert dev.cfg.qk_norm == (kind == "qwen3") and dev.cfg.moe == (kind == "mixtral")
+    om = OracleModel(dev.qm)
+    for pos, t in enumerate([1, 17, 5, 88, 42, 3, 9, 60]):
+        want = om.forward(t, pos)
+        got = dev.forward(t)
+        assert np.array_equal(np.asarray(got, np.float32).view(np.uint32), want.view(np.uint32)), f"pos {pos}"
+    dev.close()

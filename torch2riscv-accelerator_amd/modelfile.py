@@ -320,9 +320,12 @@ def read_llama2c(path):
 
 
 def quant_model_from_fp32(cfg, w, kv_scales=None, calib_tokens=None):
-    """Quantise fp32 llama2.c-named weights (read_llama2c) as the reference's exporter does
-    (llm/export_w8a8.py:75-95: per-row int8 of every linear, q | k | v rows stacked). kv_scales
-    (layers, 2) as the reference's --kv file; None: calibrated by an fp32 run of calib_tokens."""
+    """Quantise fp32 llama2.c-named weights (read_llama2c, hf_weights) as the reference's exporters do
+    (llm/export_w8a8.py:75-95, compiler/frontend/hf_generic.py:872-917: per-row int8 of every linear,
+    q | k | v rows stacked; MoE experts row by row; the logits scaling folded into the classifier's
+    scales). Extra names: q_norm / k_norm [L, hd] (QK-norm), router [L, E, d], wg / wu [L, E, F, d],
+    wd [L, E, d, F] (MoE). kv_scales (layers, 2) or (layers, 2, kv_dim) as the reference's --kv file;
+    None: calibrated by an fp32 run of calib_tokens (per channel as cfg.kv_channel says)."""
     L = cfg.layers
 
     def stack(fn):
@@ -334,20 +337,22 @@ def quant_model_from_fp32(cfg, w, kv_scales=None, calib_tokens=None):
         a["cls_q"], a["cls_s"] = a["emb_q"], a["emb_s"]
     else:
         a["cls_q"], a["cls_s"] = W.quantize_rows(w["wcls"])
+    a["cls_s"] = W.fold_logits_scaling(a["cls_s"], cfg.logits_scaling)
     a["rms_final"] = np.array(w["rms_final"], F)
     a["rms_att"], a["rms_ffn"] = np.array(w["rms_att"], F), np.array(w["rms_ffn"], F)
+    if cfg.qk_norm:
+        a["q_norm"], a["k_norm"] = np.array(w["q_norm"], F), np.array(w["k_norm"], F)
     a["wqkv"], a["s_wqkv"] = stack(lambda l: W.quantize_rows(np.concatenate([w["wq"][l], w["wk"][l], w["wv"][l]])))
-    for n in ("wo", "w1", "w3", "w2"):
+    for n in ("wo",) + (("router", "wg", "wu", "wd") if cfg.moe else ("w1", "w3", "w2")):
         a[n], a["s_" + n] = stack(lambda l, n=n: W.quantize_rows(w[n][l]))
     if kv_scales is None:
-        names = {"tok": "tok"}
-
         def weight(c, name, layer=-1):
-            v = w[names.get(name, name)]
-            return np.asarray(v if layer < 0 or name == "tok" else v[layer], F)
+            v = w[name]
+            return np.asarray(v if layer < 0 or name in ("tok", "wcls", "rms_final") else v[layer], F)
         toks = list(calib_tokens) if calib_tokens is not None else [BOS] + list(range(3, 3 + min(31, cfg.vocab - 3)))
         kv_scales = W.calibrate_kv(cfg, toks, weight=weight)
-    a["kv_scales"] = np.asarray(kv_scales, F).reshape(L, 2)
+    kv = np.asarray(kv_scales, F)
+    a["kv_scales"] = kv if kv.ndim == 3 else kv.reshape(L, 2)
     return W.QuantModel.from_arrays(cfg, a)
 
 
@@ -461,3 +466,123 @@ def open_tokenizer(path, vocab_size, bos_id=None):
     if os.path.isdir(path) or path.endswith(".json"):
         return HFTokenizer(path, bos_id=bos_id)
     return Llama2cTokenizer(path, vocab_size)
+
+
+# ------------------------------------------------------------------ HuggingFace checkpoints
+# A model directory with config.json and *.safetensors, as the reference's HF path reads it
+# (compiler/frontend/qhf.py:97-181): the fp32 weights (F32 / F16 / BF16 stored), q / k rows (and
+# QK-norm gains) reordered from HF's rotate-half halves to the interleaved RoPE pairs this datapath
+# rotates, then W8A8-quantised like every other source. Mixtral-style MoE blocks as
+# compiler/frontend/hf_generic.py:602-663 reads them.
+HF_ARCHS = ("LlamaForCausalLM", "MistralForCausalLM", "Qwen3ForCausalLM", "MixtralForCausalLM")
+_HF_ACT = {"silu": "silu", "swish": "silu", "gelu_pytorch_tanh": "gelu_tanh", "gelu_tanh": "gelu_tanh"}
+
+
+def read_safetensors(path):
+    """{name: float32 array} of a .safetensors file (8-byte little-endian header length, a JSON header,
+    the raw tensors; F32 kept memory-mapped, F16 / BF16 widened). Executes nothing from the file."""
+    import json
+    raw = np.memmap(path, dtype=np.uint8, mode="r")
+    n = int(raw[:8].view("<u8")[0])
+    header = json.loads(bytes(raw[8:8 + n]).decode("utf-8"))
+    base = 8 + n
+    out = {}
+    for name, info in header.items():
+        if name == "__metadata__":
+            continue
+        a, b = info["data_offsets"]
+        buf = raw[base + a:base + b]
+        dt = info["dtype"]
+        if dt == "F32":
+            v = buf.view("<f4")
+        elif dt == "F16":
+            v = buf.view("<f2").astype(F)
+        elif dt == "BF16":
+            v = (buf.view("<u2").astype(np.uint32) << 16).view(F)
+        else:
+            raise ValueError(f"{path}: {name} has dtype {dt} (F32, F16 or BF16)")
+        out[name] = v.reshape(info["shape"])
+    return out
+
+
+def hf_config(path, seq_len=2048, name=None, D=16, **options):
+    """The ModelConfig of an HF model directory (config.json; qhf.py:97-121). options: the HF path's
+    numerics options (attn_norm, kv_channel); act and logits_scaling come from the config."""
+    import json
+    c = json.load(open(os.path.join(path, "config.json")))
+    arch = (c.get("architectures") or ["LlamaForCausalLM"])[0]
+    if arch not in HF_ARCHS:
+        raise ValueError(f"{path}: architecture {arch} (supported: {', '.join(HF_ARCHS)})")
+    rp = c.get("rope_parameters") or {}
+    scaling = c.get("rope_scaling") or ({k: v for k, v in rp.items() if k != "rope_theta"}
+                                        if rp.get("rope_type", "default") != "default" else None)
+    if scaling:
+        raise ValueError(f"{path}: rope scaling {scaling} is not supported")
+    if c.get("attention_bias") or c.get("mlp_bias"):
+        raise ValueError(f"{path}: linear biases are not supported (W8A8 rows with one scale each)")
+    act = c.get("hidden_act", c.get("hidden_activation", "silu"))
+    if act not in _HF_ACT:
+        raise ValueError(f"{path}: activation {act} (supported: {', '.join(_HF_ACT)})")
+    heads = c["num_attention_heads"]
+    moe = arch == "MixtralForCausalLM"
+    cfg = C.ModelConfig(
+        name=name or os.path.basename(os.path.normpath(path)), dim=c["hidden_size"], hidden=c["intermediate_size"],
+        layers=c["num_hidden_layers"], heads=heads, kv_heads=c.get("num_key_value_heads") or heads,
+        head_dim=c.get("head_dim") or c["hidden_size"] // heads, vocab=c["vocab_size"],
+        seq_len=min(seq_len, c.get("max_position_embeddings", seq_len)),
+        theta=float(c.get("rope_theta", rp.get("rope_theta", 10000.0))), eps=float(c.get("rms_norm_eps", 1e-5)),
+        qk_norm=arch.startswith("Qwen3"), tied=bool(c.get("tie_word_embeddings", False)),
+        n_experts=c["num_local_experts"] if moe else 0, top_k=c["num_experts_per_tok"] if moe else 0,
+        rope_method="f64", D=D, act=_HF_ACT[act], logits_scaling=float(c.get("logits_scaling", 1.0) or 1.0),
+        **options)
+    return cfg.validate()
+
+
+def _interleave_rows(w, heads, hd):
+    """HF's rotate-half order (per head: the first halves of the pairs, then the second halves) -> the
+    interleaved pairs (x0, x1), (x2, x3), ... this datapath rotates (qhf.py:123-130)."""
+    w = np.asarray(w, F)
+    return np.ascontiguousarray(np.swapaxes(w.reshape(heads, 2, hd // 2, *w.shape[1:]), 1, 2).reshape(w.shape))
+
+
+def hf_weights(path, cfg):
+    """{llama2.c name: float32 array} of an HF model directory (qhf.py:159-181): tok, wcls, rms_final,
+    per layer (stacked) wq, wk, wv, wo, rms_att, rms_ffn, w1 / w3 / w2 (gate / up / down) or the MoE
+    router, wg, wu, wd, and q_norm / k_norm (QK-norm), q / k in interleaved pair order."""
+    t = {}
+    for f in sorted(os.listdir(path)):
+        if f.endswith(".safetensors"):
+            t.update(read_safetensors(os.path.join(path, f)))
+    if not t:
+        raise ValueError(f"{path}: no .safetensors files")
+    g = lambda n: np.asarray(t[n], F)
+    L, hd = cfg.layers, cfg.head_dim
+    w = {"tok": g("model.embed_tokens.weight"), "rms_final": g("model.norm.weight")}
+    w["wcls"] = w["tok"] if cfg.tied or "lm_head.weight" not in t else g("lm_head.weight")
+    names = {"wq": "self_attn.q_proj", "wk": "self_attn.k_proj", "wv": "self_attn.v_proj", "wo": "self_attn.o_proj",
+             "rms_att": "input_layernorm", "rms_ffn": "post_attention_layernorm"}
+    if cfg.qk_norm:
+        names.update({"q_norm": "self_attn.q_norm", "k_norm": "self_attn.k_norm"})
+    if not cfg.moe:
+        names.update({"w1": "mlp.gate_proj", "w3": "mlp.up_proj", "w2": "mlp.down_proj"})
+    for k, n in names.items():
+        w[k] = np.stack([g(f"model.layers.{l}.{n}.weight") for l in range(L)])
+    if cfg.moe:
+        E = cfg.n_experts
+        moe = lambda l, n: f"model.layers.{l}.block_sparse_moe.{n}.weight"
+        w["router"] = np.stack([g(moe(l, "gate")) for l in range(L)])
+        for k, n in (("wg", "w1"), ("wu", "w3"), ("wd", "w2")):
+            w[k] = np.stack([np.stack([g(moe(l, f"experts.{e}.{n}")) for e in range(E)]) for l in range(L)])
+    w["wq"] = np.stack([_interleave_rows(x, cfg.heads, hd) for x in w["wq"]])
+    w["wk"] = np.stack([_interleave_rows(x, cfg.kv_heads, hd) for x in w["wk"]])
+    if cfg.qk_norm:
+        w["q_norm"] = np.stack([_interleave_rows(x, 1, hd) for x in w["q_norm"]])
+        w["k_norm"] = np.stack([_interleave_rows(x, 1, hd) for x in w["k_norm"]])
+    return w
+
+
+def read_hf(path, seq_len=2048, kv_scales=None, calib_tokens=None, name=None, **options):
+    """QuantModel of an HF model directory: hf_config + hf_weights + quant_model_from_fp32 (KV scales
+    calibrated on calib_tokens unless given)."""
+    cfg = hf_config(path, seq_len=seq_len, name=name, **options)
+    return quant_model_from_fp32(cfg, hf_weights(path, cfg), kv_scales=kv_scales, calib_tokens=calib_tokens)

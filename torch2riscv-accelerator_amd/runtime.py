@@ -74,19 +74,34 @@ class Sampler:
         return int(cand[int(min(np.searchsorted(cdf[:last + 1], r, side="right"), last))])
 
 
+def _default_tokenizer(model_path):
+    """tokenizer.bin next to a model file (the reference's default, llm/runtime.py:80-84), or an HF model
+    directory's tokenizer.json."""
+    if not isinstance(model_path, str):
+        return None
+    if os.path.isdir(model_path):
+        return model_path if os.path.exists(os.path.join(model_path, "tokenizer.json")) else None
+    if os.path.isfile(model_path):
+        guess = os.path.join(os.path.dirname(os.path.abspath(model_path)), "tokenizer.bin")
+        return guess if os.path.exists(guess) else None
+    return None
+
+
 def _resolve_model(model):
     if isinstance(model, W.QuantModel):
         return model
     if isinstance(model, C.ModelConfig):
         return W.QuantModel(model)
     if isinstance(model, str):
+        if os.path.isdir(model) and os.path.exists(os.path.join(model, "config.json")):
+            return MF.read_hf(model)                       # HF checkpoint (compiler/frontend/qhf.py:97-181)
         if os.path.isfile(model):
             if model.endswith(".bin"):                     # llama2.c fp32 checkpoint: quantised here
                 cfg, w = MF.read_llama2c(model)
                 return MF.quant_model_from_fp32(cfg, w)
             return MF.read_w8a8(model)                      # the device file (llm/runtime.py:80)
         return W.QuantModel(C.get(model))
-    raise TypeError(f"model: a .w8a8 / llama2.c .bin path, a ModelConfig, a config name or a QuantModel, "
+    raise TypeError(f"model: a .w8a8 / llama2.c .bin path, an HF model directory, a ModelConfig, a config name or a QuantModel, "
                     f"not {type(model).__name__}")
 
 
@@ -97,9 +112,8 @@ class LlamaDevice:
         c = self.cfg = self.qm.cfg
         self.d = c.D
         self.tok = None
-        if tokenizer_path is None and isinstance(model_path, str) and os.path.isfile(model_path):
-            guess = os.path.join(os.path.dirname(os.path.abspath(model_path)), "tokenizer.bin")
-            tokenizer_path = guess if os.path.exists(guess) else None     # (the reference's default)
+        if tokenizer_path is None:
+            tokenizer_path = _default_tokenizer(model_path)
         if tokenizer_path is not None:
             self.tok = MF.open_tokenizer(tokenizer_path, c.vocab, bos_id=bos_id)
         self.m = ResidentModel(self.qm, device=device or "cuda:0", max_rows=max_rows)
@@ -228,9 +242,8 @@ class BatchLlamaDevice:
         c = self.cfg = self.qm.cfg
         self.d = int(slots or c.D)
         self.tok = None
-        if tokenizer_path is None and isinstance(model_path, str) and os.path.isfile(model_path):
-            guess = os.path.join(os.path.dirname(os.path.abspath(model_path)), "tokenizer.bin")
-            tokenizer_path = guess if os.path.exists(guess) else None
+        if tokenizer_path is None:
+            tokenizer_path = _default_tokenizer(model_path)
         if tokenizer_path is not None:
             self.tok = MF.open_tokenizer(tokenizer_path, c.vocab, bos_id=bos_id)
         self.m = ResidentModel(self.qm, device=device or "cuda:0", max_rows=self.d)

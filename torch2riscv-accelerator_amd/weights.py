@@ -279,13 +279,13 @@ class QuantModel:
 def _fp32_forward_rows(cfg, tokens, amax_out, weight=None):
     """Causal fp32 forward of `tokens` at positions 0.. (all rows at once, torch on the CPU),
     recording max|k| and max|v| per layer and cache channel into amax_out [L, 2, kv_dim] (after RoPE for
-    k). llama2.c run.c semantics (llm/ref_model.py:45-91) generalised as compiler/frontend/qhf.py:206-243;
-    cfg.act "gelu_tanh" gates with GELU's tanh form."""
+    k); returns the logits [M, vocab]. llama2.c run.c semantics (llm/ref_model.py:45-91) generalised as
+    compiler/frontend/qhf.py:206-243; cfg.act "gelu_tanh" gates with GELU's tanh form."""
     import torch
     c = cfg
     fp32_tensor = weight if weight is not None else globals()["fp32_tensor"]
     M = len(tokens)
-    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    t = lambda a: torch.from_numpy(np.require(a, F, requirements=["C", "W"]))   # (a read-only map: copied)
     H, Hk, hd = c.heads, c.kv_heads, c.head_dim
     G = H // Hk
     cos, sin = rope_tables(c)
@@ -341,6 +341,18 @@ def _fp32_forward_rows(cfg, tokens, amax_out, weight=None):
             else:
                 h = act(xb @ t(fp32_tensor(c, "w1", l)).T) * (xb @ t(fp32_tensor(c, "w3", l)).T)
                 x = x + h @ t(fp32_tensor(c, "w2", l)).T
+        cls = fp32_tensor(c, "wcls") if not c.tied else fp32_tensor(c, "tok")
+        logits = rms(x, t(fp32_tensor(c, "rms_final"))) @ t(cls).T
+        if c.logits_scaling != 1.0:
+            logits = logits / c.logits_scaling
+        return logits.numpy()
+
+
+def fp32_logits(cfg, tokens, weight=None):
+    """Logits [M, vocab] of the causal fp32 forward of `tokens` at positions 0.. (the calibration run's
+    model; weight(cfg, name, layer) as in calibrate_kv)."""
+    amax = np.zeros((cfg.layers, 2, cfg.kv_dim), np.float64)
+    return _fp32_forward_rows(cfg, list(tokens), amax, weight)
 
 
 def calibrate_kv(cfg, tokens=None, chunk=None, weight=None, channel=None):
