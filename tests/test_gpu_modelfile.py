@@ -98,3 +98,26 @@ def test_hf_checkpoint_on_device(tmp_path, kind):
         got = dev.forward(t)
         assert np.array_equal(np.asarray(got, np.float32).view(np.uint32), want.view(np.uint32)), f"pos {pos}"
     dev.close()
+
+
+@pytest.mark.parametrize("kind", ["llama", "mixtral"])
+def test_compressed_tensors_on_device(tmp_path, kind):
+    """A compressed-tensors W8A8 checkpoint (int8 rows with -128 values, kept as stored) decodes and
+    prefills on the device bit-identically to the oracle."""
+    from oracle import OracleModel
+    from t2r_amd.runtime import LlamaDevice
+    from test_hf_import import _build, _compressed
+    stored = _compressed(_build(kind), tmp_path)
+    assert any((q == -128).any() for q, _ in stored.values())
+    dev = LlamaDevice(str(tmp_path))
+    assert (dev.qm.wqkv == -128).any() or (dev.qm.wo == -128).any()
+    om = OracleModel(dev.qm)
+    toks = [1, 17, 5, 88, 42, 3, 9, 60, 11, 4]
+    for pos, t in enumerate(toks):
+        want = om.forward(t, pos)
+        got = dev.forward(t)
+        assert np.array_equal(np.asarray(got, np.float32).view(np.uint32), want.view(np.uint32)), f"pos {pos}"
+    dev.m.reset()
+    pre = dev.m.prefill(toks).cpu().numpy()
+    assert np.array_equal(pre.view(np.uint32), want.view(np.uint32))
+    dev.close()

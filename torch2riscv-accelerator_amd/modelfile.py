@@ -319,14 +319,22 @@ def read_llama2c(path):
     return cfg, w
 
 
-def quant_model_from_fp32(cfg, w, kv_scales=None, calib_tokens=None):
+def quant_model_from_fp32(cfg, w, kv_scales=None, calib_tokens=None, stored=None):
     """Quantise fp32 llama2.c-named weights (read_llama2c, hf_weights) as the reference's exporters do
     (llm/export_w8a8.py:75-95, compiler/frontend/hf_generic.py:872-917: per-row int8 of every linear,
     q | k | v rows stacked; MoE experts row by row; the logits scaling folded into the classifier's
     scales). Extra names: q_norm / k_norm [L, hd] (QK-norm), router [L, E, d], wg / wu [L, E, F, d],
     wd [L, E, d, F] (MoE). kv_scales (layers, 2) or (layers, 2, kv_dim) as the reference's --kv file;
-    None: calibrated by an fp32 run of calib_tokens (per channel as cfg.kv_channel says)."""
+    None: calibrated by an fp32 run of calib_tokens (per channel as cfg.kv_channel says). stored: int8 rows
+    and scales to take as they are instead of quantizing ({name: (q, s)}, a compressed-tensors checkpoint's)."""
     L = cfg.layers
+    stored = stored or {}
+
+    def quant(name, l=None):
+        if name in stored:
+            q, sc = stored[name]
+            return (q, sc) if l is None else (q[l], sc[l])
+        return W.quantize_rows(w[name] if l is None else w[name][l])
 
     def stack(fn):
         qs = [fn(l) for l in range(L)]
@@ -336,15 +344,18 @@ def quant_model_from_fp32(cfg, w, kv_scales=None, calib_tokens=None):
     if cfg.tied:
         a["cls_q"], a["cls_s"] = a["emb_q"], a["emb_s"]
     else:
-        a["cls_q"], a["cls_s"] = W.quantize_rows(w["wcls"])
+        a["cls_q"], a["cls_s"] = quant("wcls")
     a["cls_s"] = W.fold_logits_scaling(a["cls_s"], cfg.logits_scaling)
     a["rms_final"] = np.array(w["rms_final"], F)
     a["rms_att"], a["rms_ffn"] = np.array(w["rms_att"], F), np.array(w["rms_ffn"], F)
     if cfg.qk_norm:
         a["q_norm"], a["k_norm"] = np.array(w["q_norm"], F), np.array(w["k_norm"], F)
-    a["wqkv"], a["s_wqkv"] = stack(lambda l: W.quantize_rows(np.concatenate([w["wq"][l], w["wk"][l], w["wv"][l]])))
+    def qkv(l):
+        parts = [quant(n, l) for n in ("wq", "wk", "wv")]
+        return np.concatenate([q for q, _ in parts]), np.concatenate([s_ for _, s_ in parts])
+    a["wqkv"], a["s_wqkv"] = stack(qkv)
     for n in ("wo",) + (("router", "wg", "wu", "wd") if cfg.moe else ("w1", "w3", "w2")):
-        a[n], a["s_" + n] = stack(lambda l, n=n: W.quantize_rows(w[n][l]))
+        a[n], a["s_" + n] = stack(lambda l, n=n: quant(n, l))
     if kv_scales is None:
         def weight(c, name, layer=-1):
             v = w[name]
@@ -480,7 +491,8 @@ _HF_ACT = {"silu": "silu", "swish": "silu", "gelu_pytorch_tanh": "gelu_tanh", "g
 
 def read_safetensors(path):
     """{name: float32 array} of a .safetensors file (8-byte little-endian header length, a JSON header,
-    the raw tensors; F32 kept memory-mapped, F16 / BF16 widened). Executes nothing from the file."""
+    the raw tensors; F32 kept memory-mapped, F16 / BF16 widened; I8 (a compressed-tensors checkpoint's
+    weights) kept int8). Executes nothing from the file."""
     import json
     raw = np.memmap(path, dtype=np.uint8, mode="r")
     n = int(raw[:8].view("<u8")[0])
@@ -499,8 +511,10 @@ def read_safetensors(path):
             v = buf.view("<f2").astype(F)
         elif dt == "BF16":
             v = (buf.view("<u2").astype(np.uint32) << 16).view(F)
+        elif dt == "I8":
+            v = buf.view(np.int8)
         else:
-            raise ValueError(f"{path}: {name} has dtype {dt} (F32, F16 or BF16)")
+            raise ValueError(f"{path}: {name} has dtype {dt} (F32, F16, BF16 or I8)")
         out[name] = v.reshape(info["shape"])
     return out
 
@@ -523,6 +537,8 @@ def hf_config(path, seq_len=2048, name=None, D=16, **options):
     act = c.get("hidden_act", c.get("hidden_activation", "silu"))
     if act not in _HF_ACT:
         raise ValueError(f"{path}: activation {act} (supported: {', '.join(_HF_ACT)})")
+    if c.get("quantization_config") is not None:
+        CompressedScheme(c["quantization_config"])          # refuses what the datapath cannot take as it is
     heads = c["num_attention_heads"]
     moe = arch == "MixtralForCausalLM"
     cfg = C.ModelConfig(
@@ -545,44 +561,169 @@ def _interleave_rows(w, heads, hd):
     return np.ascontiguousarray(np.swapaxes(w.reshape(heads, 2, hd // 2, *w.shape[1:]), 1, 2).reshape(w.shape))
 
 
-def hf_weights(path, cfg):
+class CompressedScheme:
+    """A compressed-tensors quantization_config (llm-compressor W8A8, as the reference's
+    compiler/frontend/ct_import.py:1-27, 63-105 accepts it): int-quantized, compressed; weights int8
+    static per output channel, symmetric; input activations int8 dynamic per token, symmetric (the
+    datapath's own quant_act). Anything else raises. `quantized(module name)`: whether a Linear's weight
+    is stored as int8 rows with scales."""
+    WEIGHTS = {"type": "int", "num_bits": 8, "dynamic": False, "strategy": "channel", "symmetric": True}
+    INPUTS = {"type": "int", "num_bits": 8, "dynamic": True, "strategy": "token", "symmetric": True}
+    UNSET = ("group_size", "block_structure")
+
+    def __init__(self, qc):
+        bad = lambda what: ValueError(f"compressed-tensors: {what}")
+        if qc.get("quant_method") != "compressed-tensors":
+            raise bad(f"quant_method {qc.get('quant_method')!r} (supported: compressed-tensors)")
+        if qc.get("format") != "int-quantized":
+            raise bad(f"format {qc.get('format')!r} (supported: int-quantized)")
+        if qc.get("quantization_status", "compressed") != "compressed":
+            raise bad(f"quantization_status {qc.get('quantization_status')!r} (supported: compressed)")
+        if qc.get("kv_cache_scheme"):
+            raise bad("kv_cache_scheme set (the KV scales are calibrated here)")
+        self.targets = []
+        for name, g in (qc.get("config_groups") or {}).items():
+            for kind, want in (("weights", self.WEIGHTS), ("input_activations", self.INPUTS)):
+                a = g.get(kind)
+                if a is None:
+                    raise bad(f"group {name}: no {kind} scheme")
+                for k, v in want.items():
+                    if a.get(k) != v:
+                        raise bad(f"group {name}: {kind}.{k} = {a.get(k)!r} (supported: {v!r})")
+                for k in self.UNSET:
+                    if a.get(k) not in (None, False, {}):
+                        raise bad(f"group {name}: {kind}.{k} = {a.get(k)!r} (supported: unset)")
+                if kind == "weights" and a.get("actorder") not in (None, False, "static"):
+                    raise bad(f"group {name}: weights.actorder = {a.get('actorder')!r} (supported: none, static)")
+            if g.get("output_activations"):
+                raise bad(f"group {name}: output_activations set")
+            self.targets += g.get("targets") or []
+        if not self.targets:
+            raise bad("no config_groups with targets")
+        self.ignore = qc.get("ignore") or []
+
+    @staticmethod
+    def _match(name, pats):
+        return any(re.fullmatch(p[3:], name) if p.startswith("re:") else p in (name, "Linear") for p in pats)
+
+    def quantized(self, name):
+        return self._match(name, self.targets) and not self._match(name, self.ignore)
+
+
+def _stored_qs(t, name, shape):
+    """(int8 rows [N, K], fp32 scales [N]) of a compressed-tensors linear layer, checked
+    (ct_import.py:150-167): the int8 values as stored (-128 included)."""
+    q, sc = t.get(name + ".weight"), t.get(name + ".weight_scale")
+    if q is None or sc is None:
+        raise ValueError(f"compressed-tensors: {name}: weight / weight_scale missing")
+    if q.dtype != np.int8 or tuple(q.shape) != tuple(shape):
+        raise ValueError(f"compressed-tensors: {name}.weight: {q.dtype} {tuple(q.shape)}, expected int8 {tuple(shape)}")
+    if sc.size != shape[0] or (sc.ndim == 2 and sc.shape[1] != 1) or sc.ndim > 2:
+        raise ValueError(f"compressed-tensors: {name}.weight_scale: shape {tuple(sc.shape)}, expected ({shape[0]}, 1)")
+    zp = t.get(name + ".weight_zero_point")
+    if zp is not None and np.any(np.asarray(zp) != 0):
+        raise ValueError(f"compressed-tensors: {name}.weight_zero_point non-zero (supported: symmetric)")
+    for k in ("weight_g_idx", "input_scale", "input_zero_point"):
+        if name + "." + k in t:
+            raise ValueError(f"compressed-tensors: {name}.{k} present (supported: no act-order, dynamic inputs)")
+    return np.ascontiguousarray(q), np.ascontiguousarray(np.asarray(sc, F).reshape(shape[0]))
+
+
+def hf_weights(path, cfg, stored=None):
     """{llama2.c name: float32 array} of an HF model directory (qhf.py:159-181): tok, wcls, rms_final,
     per layer (stacked) wq, wk, wv, wo, rms_att, rms_ffn, w1 / w3 / w2 (gate / up / down) or the MoE
-    router, wg, wu, wd, and q_norm / k_norm (QK-norm), q / k in interleaved pair order."""
+    router, wg, wu, wd, and q_norm / k_norm (QK-norm), q / k in interleaved pair order. A compressed-tensors
+    checkpoint's quantized linears come as q * s (the fp32 model of the KV calibration); their int8 rows
+    and scales, reordered with them, go into `stored` (a dict): {name: (q [L, ...], s [L, ...])}."""
+    import json
     t = {}
     for f in sorted(os.listdir(path)):
         if f.endswith(".safetensors"):
             t.update(read_safetensors(os.path.join(path, f)))
     if not t:
         raise ValueError(f"{path}: no .safetensors files")
+    qc = json.load(open(os.path.join(path, "config.json"))).get("quantization_config")
+    scheme = CompressedScheme(qc) if qc is not None else None
+    L, hd, d = cfg.layers, cfg.head_dim, cfg.dim
+    shapes = {"self_attn.q_proj": (cfg.q_dim, d), "self_attn.k_proj": (cfg.kv_dim, d),
+              "self_attn.v_proj": (cfg.kv_dim, d), "self_attn.o_proj": (d, cfg.q_dim),
+              "mlp.gate_proj": (cfg.hidden, d), "mlp.up_proj": (cfg.hidden, d), "mlp.down_proj": (d, cfg.hidden),
+              "block_sparse_moe.gate": (cfg.n_experts, d), "w1": (cfg.hidden, d), "w3": (cfg.hidden, d),
+              "w2": (d, cfg.hidden)}
+    qs = {}
+
+    def lin(full, kind):
+        """fp32 weight of a Linear (dequantized when the checkpoint stores it as int8 rows)."""
+        if scheme is not None and scheme.quantized(full):
+            q, sc = _stored_qs(t, full, shapes[kind])
+            qs[full] = (q, sc)
+            return (q.astype(F) * sc[:, None]).astype(F)
+        if full + ".weight" not in t:
+            raise ValueError(f"{path}: tensor {full}.weight missing")
+        v = np.asarray(t[full + ".weight"])
+        if v.dtype == np.int8:
+            raise ValueError(f"{full}.weight is int8 but the scheme does not quantize it")
+        return np.asarray(v, F)
     g = lambda n: np.asarray(t[n], F)
-    L, hd = cfg.layers, cfg.head_dim
     w = {"tok": g("model.embed_tokens.weight"), "rms_final": g("model.norm.weight")}
-    w["wcls"] = w["tok"] if cfg.tied or "lm_head.weight" not in t else g("lm_head.weight")
-    names = {"wq": "self_attn.q_proj", "wk": "self_attn.k_proj", "wv": "self_attn.v_proj", "wo": "self_attn.o_proj",
-             "rms_att": "input_layernorm", "rms_ffn": "post_attention_layernorm"}
+    shapes["lm_head"] = (cfg.vocab, d)
+    w["wcls"] = w["tok"] if cfg.tied or "lm_head.weight" not in t else lin("lm_head", "lm_head")
+    gains = {"rms_att": "input_layernorm", "rms_ffn": "post_attention_layernorm"}
     if cfg.qk_norm:
-        names.update({"q_norm": "self_attn.q_norm", "k_norm": "self_attn.k_norm"})
-    if not cfg.moe:
-        names.update({"w1": "mlp.gate_proj", "w3": "mlp.up_proj", "w2": "mlp.down_proj"})
-    for k, n in names.items():
+        gains.update({"q_norm": "self_attn.q_norm", "k_norm": "self_attn.k_norm"})
+    for k, n in gains.items():
         w[k] = np.stack([g(f"model.layers.{l}.{n}.weight") for l in range(L)])
+    linears = {"wq": "self_attn.q_proj", "wk": "self_attn.k_proj", "wv": "self_attn.v_proj", "wo": "self_attn.o_proj"}
+    if not cfg.moe:
+        linears.update({"w1": "mlp.gate_proj", "w3": "mlp.up_proj", "w2": "mlp.down_proj"})
+    for k, n in linears.items():
+        w[k] = np.stack([lin(f"model.layers.{l}.{n}", n) for l in range(L)])
     if cfg.moe:
         E = cfg.n_experts
-        moe = lambda l, n: f"model.layers.{l}.block_sparse_moe.{n}.weight"
-        w["router"] = np.stack([g(moe(l, "gate")) for l in range(L)])
+        moe = lambda l, n: f"model.layers.{l}.block_sparse_moe.{n}"
+        w["router"] = np.stack([lin(moe(l, "gate"), "block_sparse_moe.gate") for l in range(L)])
         for k, n in (("wg", "w1"), ("wu", "w3"), ("wd", "w2")):
-            w[k] = np.stack([np.stack([g(moe(l, f"experts.{e}.{n}")) for e in range(E)]) for l in range(L)])
-    w["wq"] = np.stack([_interleave_rows(x, cfg.heads, hd) for x in w["wq"]])
-    w["wk"] = np.stack([_interleave_rows(x, cfg.kv_heads, hd) for x in w["wk"]])
+            w[k] = np.stack([np.stack([lin(moe(l, f"experts.{e}.{n}"), n) for e in range(E)]) for l in range(L)])
+    perm = lambda x, heads: _interleave_rows(x, heads, hd)
+    w["wq"] = np.stack([perm(x, cfg.heads) for x in w["wq"]])
+    w["wk"] = np.stack([perm(x, cfg.kv_heads) for x in w["wk"]])
     if cfg.qk_norm:
         w["q_norm"] = np.stack([_interleave_rows(x, 1, hd) for x in w["q_norm"]])
         w["k_norm"] = np.stack([_interleave_rows(x, 1, hd) for x in w["k_norm"]])
+    if stored is not None and qs:
+        # the stored int8 rows under this datapath's names (q / k rows and scales reordered like the weights)
+        def rows(names, heads=None):
+            q = np.stack([qs[n][0] for n in names])
+            sc = np.stack([qs[n][1] for n in names])
+            if heads is not None:
+                q = np.stack([_interleave_rows(x, heads, hd).astype(np.int8) for x in q.astype(F)]).astype(np.int8)
+                sc = np.stack([_interleave_rows(x[:, None], heads, hd)[:, 0] for x in sc])
+            return q, sc
+        for k, n in linears.items():
+            names = [f"model.layers.{l}.{n}" for l in range(L)]
+            if all(x in qs for x in names):
+                heads = cfg.heads if k == "wq" else cfg.kv_heads if k == "wk" else None
+                stored[k] = rows(names, heads)
+        if cfg.moe:
+            for k, n in (("wg", "w1"), ("wu", "w3"), ("wd", "w2")):
+                names = [[f"model.layers.{l}.block_sparse_moe.experts.{e}.{n}" for e in range(cfg.n_experts)]
+                         for l in range(L)]
+                if all(x in qs for r in names for x in r):
+                    stored[k] = (np.stack([np.stack([qs[x][0] for x in r]) for r in names]),
+                                 np.stack([np.stack([qs[x][1] for x in r]) for r in names]))
+            names = [f"model.layers.{l}.block_sparse_moe.gate" for l in range(L)]
+            if all(x in qs for x in names):
+                stored["router"] = rows(names)
+        if "lm_head" in qs:
+            stored["wcls"] = qs["lm_head"]
     return w
 
 
 def read_hf(path, seq_len=2048, kv_scales=None, calib_tokens=None, name=None, **options):
     """QuantModel of an HF model directory: hf_config + hf_weights + quant_model_from_fp32 (KV scales
-    calibrated on calib_tokens unless given)."""
+    calibrated on calib_tokens unless given). A compressed-tensors W8A8 checkpoint keeps its own int8
+    rows and scales; the layers its scheme ignores are quantized here."""
     cfg = hf_config(path, seq_len=seq_len, name=name, **options)
-    return quant_model_from_fp32(cfg, hf_weights(path, cfg), kv_scales=kv_scales, calib_tokens=calib_tokens)
+    stored = {}
+    w = hf_weights(path, cfg, stored)
+    return quant_model_from_fp32(cfg, w, kv_scales=kv_scales, calib_tokens=calib_tokens, stored=stored)
