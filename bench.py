@@ -120,7 +120,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the datapath runs on a single "
-              f"MI355X; DESIGN.md describes how it would shard)", file=sys.stderr)
+              f"MI355X; no multi-GPU path is built)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
