@@ -114,3 +114,49 @@ def test_kv_scales_recorded_for_every_config():
     kvc = W.kv_constants(C.C4, W.stored_kv_scales(C.C4))
     sk, sv = W.stored_kv_scales(C.C4)[0]
     assert kvc[0, 2] == np.float32(float(sk) / 8.0) and kvc[0, 3] == np.float32(float(sv) / 127.0)
+
+
+def test_hf_option_validation_before_launch():
+    """The HF-path options: bad flags / activations are refused before any HIP call; the ABI-2 model
+    descriptor's option fields are validated before the device is touched (a valid descriptor only then
+    fails, here, at device initialisation: no GPU), and an ABI-1 descriptor's bytes past max_rows are
+    ignored (read with the options off)."""
+    import numpy as np
+    lib = abi.load()
+    p = ctypes.c_void_p(16)
+    assert lib.t2r_attn_decode_opt(p, p, p, p, 1, 4, 2, 16, 32, 0.1, 0.1, 16, 2, None, None, p, None) == abi.T2R_EINVAL
+    assert lib.t2r_gated_ffn_w8a8(2, p, p, p, p, p, p, 64, 64, p, p, p, None) == abi.T2R_EINVAL
+    assert lib.t2r_gated_ffn_w8a8(1, p, p, p, p, p, p, 24, 64, p, p, p, None) == abi.T2R_ESHAPE     # F % 16
+    assert lib.t2r_kv_append_ch(p, p, 1.0, 1.0, None, None, p, p, p, 0, 64, 16, None) == abi.T2R_ESHAPE
+    import torch
+    if torch.cuda.device_count() > 0:                      # (counting devices does not initialise them)
+        pytest.skip("the descriptor cases rely on device initialisation failing: no GPU may be visible")
+    cfg = C.TINY_QWEN
+    flags = np.zeros(cfg.layers, np.int32)
+
+    def full(version, **opt):
+        d = _desc(cfg, 4)
+        d.abi_version = version
+        d.qk_norm, d.eps = 1, 1e-6
+        for n in ("emb_q", "emb_s", "cls_q", "cls_s", "rms_att", "rms_ffn", "rms_final", "q_norm", "k_norm", "wqkv",
+                  "s_wqkv", "wo", "s_wo", "w1", "s_w1", "w3", "s_w3", "w2", "s_w2", "rope_cos", "rope_sin",
+                  "kv_consts", "k_cache", "v_cache", "workspace"):
+            setattr(d, n, 16)
+        d.workspace_bytes = 1 << 40
+        for k, v in opt.items():
+            setattr(d, k, v)
+        return lib.t2r_model_create(ctypes.byref(d), ctypes.byref(ctypes.c_void_p()))
+    assert full(2) == abi.T2R_EHIP                                          # valid: only the device is missing
+    assert full(2, attn_qsum=2) == abi.T2R_EINVAL
+    assert full(2, ffn_act=3) == abi.T2R_EINVAL
+    flags[1] = 4
+    assert full(2, kv_channel=16, kv_channel_flags=flags.ctypes.data) == abi.T2R_EINVAL   # unknown flag bit
+    flags[1] = 1
+    assert full(2, kv_channel_flags=flags.ctypes.data) == abi.T2R_EINVAL                  # per channel, no table
+    assert full(2, kv_channel=16, kv_channel_flags=flags.ctypes.data) == abi.T2R_EHIP
+    assert full(1, attn_qsum=7, ffn_act=9, kv_channel_flags=16) == abi.T2R_EHIP           # ABI 1: options off
+    v1 = _desc(cfg, 4)
+    v1.abi_version = 1
+    v1.attn_qsum = 7
+    assert lib.t2r_model_workspace_bytes(ctypes.byref(v1), 4) == lib.t2r_model_workspace_bytes(
+        ctypes.byref(_desc(cfg, 4)), 4)
