@@ -121,15 +121,16 @@ def test_hf_decode_vs_oracle(name):
     rm.close()
 
 
-@pytest.mark.parametrize("name,steps", [("c2-smollm2-135m-hf", 6), ("c3-qwen3-0.6b-hf", 4)])
+@pytest.mark.parametrize("name,steps", [("c2-smollm2-135m-hf", 6), ("c3-qwen3-0.6b-hf", 4), ("c5-granite-1b-a400m-hf", 3)])
 def test_hf_full_shape_decode_vs_oracle(name, steps):
     """The full-size decode kernels with the options (head dims 64 and 128, groups of 3 and 2 query
-    heads, QK-norm) against the CPU restatement on the first positions."""
+    heads, QK-norm, and C5's 32-expert MoE with the GELU-tanh expert gate) against the CPU restatement
+    on the first positions."""
     import t2r_amd.config as C
     from oracle import OracleModel
     from t2r_amd.model import ResidentModel
     cfg = C.get(name)
-    qm = quant_model(cfg)
+    qm = quant_model(cfg, calib=16 if cfg.moe else 64)    # (the fp32 MoE calibration runs row by row)
     rm = ResidentModel(qm, max_rows=16)
     om = OracleModel(qm)
     toks = cfg.prompt()[:steps]
@@ -143,7 +144,7 @@ def test_hf_full_shape_decode_vs_oracle(name, steps):
     rm.close()
 
 
-@pytest.mark.parametrize("name,P", [("tiny-hf", 20), ("tiny-hf-kv", 16), ("tiny-hf-v", 16),
+@pytest.mark.parametrize("name,P", [("tiny-hf", 20), ("tiny-hf-kv", 16), ("tiny-hf-v", 16), ("tiny-hf-moe", 20),
                                     ("c2-smollm2-135m-hf", 40), ("c3-qwen3-0.6b-hf", 300)])
 def test_hf_prefill_equals_decode(name, P):
     """The prompt through t2r_prefill (all rows, and 8-row chunks) gives the decode-only logits and KV
@@ -168,7 +169,7 @@ def test_hf_prefill_equals_decode(name, P):
     rm.close()
 
 
-@pytest.mark.parametrize("name,B", [("tiny-hf", 4), ("tiny-hf-kv", 3), ("c2-smollm2-135m-hf", 4),
+@pytest.mark.parametrize("name,B", [("tiny-hf", 4), ("tiny-hf-kv", 3), ("tiny-hf-moe", 3), ("c2-smollm2-135m-hf", 4),
                                     ("c3-qwen3-0.6b-hf", 3)])
 def test_hf_decode_batch_equals_single(name, B):
     import torch
