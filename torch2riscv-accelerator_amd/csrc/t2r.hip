@@ -75,6 +75,9 @@ int ensure_init() {
   for (const void* f : deep)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmDDeepLds) != hipSuccess)
       return T2R_EHIP;
+  if (hipFuncSetAttribute((const void*)k_gemm_d<EPI_SWIGLU, false, 128, 3, 2 * kGT>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmDTallLds) != hipSuccess)
+    return T2R_EHIP;
   g_sfu_addr[dev] = (const float*)addr;
   g_inited[dev] = true;
   return T2R_OK;

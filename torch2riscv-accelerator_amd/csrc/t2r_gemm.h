@@ -271,30 +271,36 @@ T2R_DEV int xcd_order(int b, int n) {
 // `vmcnt((NST - 2) NI)` is always "this slab landed, NST - 2 newer in flight".
 // BKD: K bytes per slab (64 or 128: a 128-byte row segment is one cache line per request);
 // NST: LDS stages (NST - 1 slabs in flight). Stage bytes 2 * 128 * BKD.
-template <int BKD, int NST>
-constexpr size_t gemm_d_lds() { return (size_t)NST * 2 * kGT * BKD; }
+template <int BKD, int NST, int BM = kGT>
+constexpr size_t gemm_d_lds() { return (size_t)NST * (BM + kGT) * BKD; }
 // the two configurations launched: 128-byte slabs (one full cache line per row and request) double
 // buffered when K % 128 == 0, else 64-byte slabs four deep; both 64 KB of LDS, two workgroups per CU
 constexpr size_t kGemmDLds = gemm_d_lds<128, 2>();
 static_assert(gemm_d_lds<64, 4>() == kGemmDLds, "both GEMM configurations use the same LDS");
 // and the deep ring for grids of at most one workgroup per CU (needs the large-LDS launch attribute)
 constexpr size_t kGemmDDeepLds = gemm_d_lds<128, 4>();
+// and the 256-row tiles' ring (3 x 48 KB)
+constexpr size_t kGemmDTallLds = gemm_d_lds<128, 3, 2 * kGT>();
 
-template <int EPI, bool SPLIT, int BKD, int NST>
-__global__ __launch_bounds__(256) void k_gemm_d(GemmArgs a, int ntile, int nz) {
+// BM: tile rows (128: four waves, 2 x 2; 256: eight waves, 4 x 2), always 128 columns.
+template <int EPI, bool SPLIT, int BKD, int NST, int BM = kGT>
+__global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz) {
   constexpr int CPR = BKD / 16;                   // 16-byte chunks per row per slab
-  constexpr int NI = CPR;                         // DMA instructions per wave per slab (2 x 128 CPR / 64 / 4)
-  constexpr int OPB = kGT * BKD;                  // bytes of one operand per slab
-  constexpr int STB = 2 * OPB;
+  constexpr int NWAVE = 2 * BM / 64;
+  constexpr int NA = BM * CPR / 64;               // DMA instructions (1 KB each) of A per slab; B: 2 CPR
+  constexpr int NI = (NA + 2 * CPR) / NWAVE;      // DMA instructions per wave per slab
+  static_assert(NI * NWAVE == NA + 2 * CPR, "whole DMA instructions per wave");
+  constexpr int OPA = BM * BKD, OPB = kGT * BKD;  // bytes of A / B per slab
+  constexpr int STB = OPA + OPB;
   extern __shared__ __align__(16) int8_t lds[];   // NST stages
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   // work item w = (split z, tile): tiles of one split consecutive, M tiles fastest (weight slabs shared)
   const int w = xcd_order((int)blockIdx.x, ntile * nz);
   const int z = w / ntile, tile = w % ntile;
-  const int mtiles = cdiv_i(a.M, kGT);
+  const int mtiles = cdiv_i(a.M, BM);
   const int mt = tile % mtiles, nt = tile / mtiles;
-  const int m0 = mt * kGT, n0 = nt * kGT;
+  const int m0 = mt * BM, n0 = nt * kGT;
   const int K = a.K, nslab = K / BKD;
   const int per = cdiv_i(nslab, nz);
   const int s0 = z * per, nk = max(0, min(nslab, s0 + per) - s0);
@@ -303,13 +309,13 @@ __global__ __launch_bounds__(256) void k_gemm_d(GemmArgs a, int ntile, int nz) {
   // {0-3, 8-11, 20-23, 28-31} + {0, 4, 32, 36} (measured with the bank-conflict counter); the rows
   // one pass reads (lane % 32, one kc) then land in 16 distinct 16-byte bank groups
   auto swz = [](int r) { return CPR == 8 ? ((r ^ (r >> 3)) & 7) : ((r >> 2) & 3); };
-  // this lane's DMA sources (instructions NI wave + j: the first half of all instructions fill A)
+  // this lane's DMA sources (instructions NI wave + j: the first NA of all instructions fill A)
   const int8_t* src[NI];
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
-    const int i = NI * wave + j, ii = i % (2 * NI), pos = 64 * ii + lane;
+    const int i = NI * wave + j, ii = i < NA ? i : i - NA, pos = 64 * ii + lane;
     const int r = pos / CPR, kc = (pos % CPR) ^ swz(r);
-    if (i < 2 * NI) {
+    if (i < NA) {
       src[j] = a.xq + (long long)min(m0 + r, a.M - 1) * K + 16 * kc;
     } else {
       int n;
@@ -322,7 +328,7 @@ __global__ __launch_bounds__(256) void k_gemm_d(GemmArgs a, int ntile, int nz) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       const int i = NI * wave + j;
-      int8_t* dst = lds + stage * STB + (i >= 2 * NI ? OPB : 0) + 1024 * (i % (2 * NI));
+      int8_t* dst = lds + stage * STB + (i >= NA ? OPA + 1024 * (i - NA) : 1024 * i);
       __builtin_amdgcn_global_load_lds((const void*)(src[j] + k0), (void*)dst, 16, 0, 0);
     }
   };
@@ -349,7 +355,7 @@ __global__ __launch_bounds__(256) void k_gemm_d(GemmArgs a, int ntile, int nz) {
     asm volatile("" ::: "memory");
     issue(s + NST - 1, (s + NST - 1) % NST);
     const int8_t* As = lds + (s % NST) * STB;
-    const int8_t* Bs = As + OPB;
+    const int8_t* Bs = As + OPA;
 #pragma unroll
     for (int kk = 0; kk < BKD / 32; ++kk) {
       v4i_t fa[2], fb[2];
@@ -470,17 +476,17 @@ inline int gemm_splits(int M, int ncols, int K, int part_rows, int epi, bool def
 
 // defer_z (STORE / RESID): when the launch splits K, the int32 partials [z, M, N] are left in a.part
 // for the caller's own finishing pass and *defer_z = z; otherwise *defer_z = 1 (output written)
-template <int EPI, int BKD, int NST>
+template <int EPI, int BKD, int NST, int BM = kGT>
 int gemm_d_launch(const GemmArgs& a, hipStream_t st, int z, int* defer_z) {
   if (defer_z) *defer_z = z;
-  const long long nb = (long long)cdiv_i(a.M, kGT) * cdiv_i(EPI == EPI_SWIGLU ? 2 * a.N : a.N, kGT);
+  const long long nb = (long long)cdiv_i(a.M, BM) * cdiv_i(EPI == EPI_SWIGLU ? 2 * a.N : a.N, kGT);
   if (nb * z > 0x7FFFFFFF) return -2;
   const dim3 grid((unsigned)(nb * z));
-  const size_t lb = gemm_d_lds<BKD, NST>();
+  const size_t lb = gemm_d_lds<BKD, NST, BM>();
   if (z == 1) {
-    launch((k_gemm_d<EPI, false, BKD, NST>), grid, dim3(256), lb, st, a, (int)nb, z);
+    launch((k_gemm_d<EPI, false, BKD, NST, BM>), grid, dim3(2 * BM), lb, st, a, (int)nb, z);
   } else if constexpr (EPI != EPI_SWIGLU) {
-    launch((k_gemm_d<EPI, true, BKD, NST>), grid, dim3(256), lb, st, a, (int)nb, z);
+    launch((k_gemm_d<EPI, true, BKD, NST, BM>), grid, dim3(2 * BM), lb, st, a, (int)nb, z);
     const long long total = (long long)a.M * a.N;
     if (!defer_z) launch((k_gemm_fin<EPI>), dim3((unsigned)min(4096LL, (total + 255) / 256)), dim3(256), 0, st, a, z);
   }
@@ -674,6 +680,10 @@ int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0, int* defer
     // -> 14.0 / 12.8 / 42.0); larger grids two workgroups per CU with the double buffer
     const long long nwg = (long long)cdiv_i(a.M, kGT) * cdiv_i(ncols, kGT) * z;
     if (a.K % 128) return gemm_d_launch<EPI, 64, 4>(a, st, z, defer_z);
+    if constexpr (EPI == EPI_SWIGLU) {
+      // 256-row tiles (eight waves) with a 3 x 48 KB ring: two slabs in flight, one workgroup per CU
+      if (a.M >= 2 * kGT) return gemm_d_launch<EPI, 128, 3, 2 * kGT>(a, st, z, defer_z);
+    }
     return nwg <= 256 ? gemm_d_launch<EPI, 128, 4>(a, st, z, defer_z) : gemm_d_launch<EPI, 128, 2>(a, st, z, defer_z);
   }
   auto blocks = [&](int bm, int bn) { return (long long)cdiv_i(a.M, bm) * cdiv_i(ncols, bn); };
