@@ -745,7 +745,11 @@ constexpr int kPreThreads = 256;
 constexpr int kPreTiles = 8;                  // 32-row cache tiles a wave loads at once
 constexpr size_t kPreMaxLds = 136 * 1024;     // dynamic LDS the kernels are set up for (of 160 KB per CU)
 
-T2R_DEV int pre_est(int S) { return (S + 16 + 31) & ~31; }   // row stride of the score / exp rows
+// Row stride (floats) of the score / exp rows: at least S + 16, and 17 mod 64. The P.V pass reads one
+// key of all 16 rows per instruction (and, in lanes 32-63, the key 16 on): 32 distinct LDS banks. The
+// exp pass's 4 rows x 16 keys per wave overlap in 3 banks. (A stride of 0 or 32 mod 64 put the 16
+// rows of a key in 2 banks.)
+__host__ __device__ inline int pre_est(int S) { return ((S + 16 + 63) & ~63) + 17; }
 
 template <int HDP, bool OPT = false>   // head dim padded to a multiple of 32 (MFMA k-steps); OPT: HF options
 __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
@@ -958,7 +962,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
 
 // dynamic LDS bytes of k_attn_pre: 16 rows of scores / exps (also the partial sums afterwards)
 inline size_t attn_pre_lds_bytes(int S, int HDP) {
-  const size_t e = (size_t)kPreRows * ((S + 16 + 31) & ~31) * 4, p = (size_t)4 * kPreRows * HDP * 4;
+  const size_t e = (size_t)kPreRows * pre_est(S) * 4, p = (size_t)4 * kPreRows * HDP * 4;
   return e > p ? e : p;
 }
 
