@@ -996,7 +996,10 @@ inline size_t attn_gqa_lds_bytes(int S, int D, int G) {
   return (size_t)G * ((size_t)D * osum_stride(S, D) + 64) * 4 + (size_t)G * ((S + 15) & ~15);
 }
 
-template <int NCH, bool OPT = false>   // 16-byte chunks per head row: hd = 16 NCH (64 or 128); OPT: HF options
+// GW: query heads per workgroup. GW < kGqaMaxG (launched for G = kGqaMaxG only) splits a KV head's
+// group over kGqaMaxG / GW workgroups (blockIdx.x = KV head * splits + split); each computes the KV
+// head's new row for itself, and split 0 writes it to the cache.
+template <int NCH, bool OPT = false, int GW = kGqaMaxG>   // hd = 16 NCH (64 or 128); OPT: HF options
 __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   constexpr int HD = 16 * NCH, KS = HD / 32;                // MFMA k-steps per key tile
   constexpr int NCHP = NCH;                                 // (4 or 8: a power of two)
@@ -1014,11 +1017,15 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   __shared__ int s_qs[kGqaWaves][kGqaMaxG];
   __shared__ int part[kGqaWaves * 4][kGqaMaxG * HD];
 
-  const int g = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  const int row = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, lr = lane & 31, kh = lane >> 5;
   const int G = a.H / a.Hk, S = a.S, D = a.D, P = osum_stride(S, D), SH = D * P + 64;
+  constexpr int NSPL = kGqaMaxG / GW;           // workgroups per KV head
+  const int g = NSPL == 1 ? (int)blockIdx.x : (int)blockIdx.x / NSPL, spl = (int)blockIdx.x - g * NSPL;
+  const int GH = NSPL == 1 ? G : GW;             // query heads of this workgroup
+  const int h0 = g * G + spl * GW;               // its first query head
   const int SP = (S + 15) & ~15;                 // int8 p row stride
-  int8_t* pq = (int8_t*)(dyn + G * SH);
+  int8_t* pq = (int8_t*)(dyn + GH * SH);
   a.kc += row * a.kv_row_stride;                 // this row's sequence cache
   a.vc += row * a.kv_row_stride;
   const long long q_dim = (long long)a.H * HD;
@@ -1035,9 +1042,9 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   v4f_t tb[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) tb[k] = ((const v4f_t*)a.tab)[(lane + 64 * k) & (kSfuWords / 4 - 1)];
-  const int job = wave;                          // 0: the KV head, 1 .. G: query head job - 1 (G < waves)
-  const bool has_job = job <= G;
-  const int hq = g * G + (job - 1);              // global query head of job >= 1
+  const int job = wave;                          // 0: the KV head, 1 .. GH: query head job - 1 (GH < waves)
+  const bool has_job = job <= GH;
+  const int hq = h0 + (job - 1);                 // global query head of job >= 1
   const float* va = job == 0 ? qkv + q_dim + (long long)g * HD : qkv + (long long)(has_job ? hq : 0) * HD;
   const float* vb = job == 0 ? qkv + q_dim + kv_dim + (long long)g * HD : va;
   const float* gn = job == 0 ? a.kn : a.qn;
@@ -1129,8 +1136,10 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
         if (j < HD) {
           s_k8[j] = kb;
           s_v8[j] = vb8;
-          a.kc[crow + j] = kb;
-          a.vc[crow + j] = vb8;
+          if (spl == 0) {
+            a.kc[crow + j] = kb;
+            a.vc[crow + j] = vb8;
+          }
         }
       }
     } else {
@@ -1154,17 +1163,17 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   }
   __syncthreads();
 
-  // ---- scores of the G heads: C[head][key] = q8[head] . k8[key] on MFMA, 32 keys per tile.
+  // ---- scores of the workgroup's GH heads: C[head][key] = q8[head] . k8[key] on MFMA, 32 keys per tile.
   // Lane (lr, kh) holds key lr of the tile and heads 4 kh + r (r < 4) in acc[r].
   v4i_t qa[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     const v4i_t z = {0, 0, 0, 0};
-    qa[s] = lr < G ? *(const v4i_t*)(&s_q8[lr < G ? lr : 0][32 * s + 16 * kh]) : z;
+    qa[s] = lr < GH ? *(const v4i_t*)(&s_q8[lr < GH ? lr : 0][32 * s + 16 * kh]) : z;
   }
   float sqh[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) sqh[r] = s_sq[r < G ? r : 0];
+  for (int r = 0; r < 4; ++r) sqh[r] = s_sq[r < GH ? r : 0];
   const int ntile = (T + 31) >> 5;
   const int npk = (ntile + kGqaWaves * kGqaRK - 1) / (kGqaWaves * kGqaRK);
   float mloc[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
@@ -1186,9 +1195,9 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int h = 4 * kh + r;
-        const bool ok = h < G && t < T;
+        const bool ok = h < GH && t < T;
         const float sv = ((float)acc[r] * sqh[r]) * a.a_k;
-        dyn[ok ? h * SH + osum_index(t, D, P) : (r < G ? r : 0) * SH + D * P + lane] = sv;   // (spare slot)
+        dyn[ok ? h * SH + osum_index(t, D, P) : (r < GH ? r : 0) * SH + D * P + lane] = sv;   // (spare slot)
         mloc[r] = nanmax(mloc[r], ok ? sv : -__builtin_inff());
       }
     }
@@ -1203,16 +1212,16 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
     v = nanmax(v, dpp_f<kDppMirror>(v));
     const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
     const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    if (lane == 0 && r < G) red[wave][r] = nanmax(m0, m1);
+    if (lane == 0 && r < GH) red[wave][r] = nanmax(m0, m1);
   }
   __syncthreads();
 
   // ---- e = EXP(s - m) (+0 padding to a multiple of D), key t by thread t % 512, all heads at once
   const int Tpad = ((T + D - 1) / D) * D;
-  float mh[4];
+  float mh[GW];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int h = r < G ? r : 0;
+  for (int r = 0; r < GW; ++r) {
+    const int h = r < GH ? r : 0;
     float m = red[0][h];
 #pragma unroll
     for (int w = 1; w < kGqaWaves; ++w) m = nanmax(m, red[w][h]);
@@ -1220,17 +1229,17 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   }
   for (int t = tid; t < Tpad; t += kGqaThreads) {
     const int k = osum_index(t, D, P);
-    float sv[4], ev[4];
+    float sv[GW], ev[GW];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) sv[h] = dyn[(h < G ? h : 0) * SH + k];
+    for (int h = 0; h < GW; ++h) sv[h] = dyn[(h < GH ? h : 0) * SH + k];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) ev[h] = sfu_exp(sv[h] - mh[h], tab);
+    for (int h = 0; h < GW; ++h) ev[h] = sfu_exp(sv[h] - mh[h], tab);
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
-      if (h < G) dyn[h * SH + k] = t < T ? ev[h] : 0.0f;
+    for (int h = 0; h < GW; ++h)
+      if (h < GH) dyn[h * SH + k] = t < T ? ev[h] : 0.0f;
   }
   __syncthreads();
-  if (wave < G) {
+  if (wave < GH) {
     float ssum = 0.0f;
     if (lane < D) ssum = ordered_sum_t<false>(dyn + wave * SH, T, D, P, lane);
     if (lane == 0) s_r[wave] = (OPT && a.qsum) ? 1.0f : sfu_recip(ssum, tab);   // qsum: to_i8(F(F(e * 1) * 127))
@@ -1238,19 +1247,19 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   __syncthreads();
 
   // ---- the int8 probabilities p = to_i8(F(F(e r) 127)) of every (head, key) in [0, T4), zero past T
-  float rh[4];
+  float rh[GW];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) rh[r] = s_r[r < G ? r : 0];
+  for (int r = 0; r < GW; ++r) rh[r] = s_r[r < GH ? r : 0];
   const int T4 = (T + 3) & ~3;
   int qs[4] = {0, 0, 0, 0};                      // qsum: the probabilities of the thread's keys, per head
   for (int t = tid; t < T4; t += kGqaThreads) {
     const int k = osum_index(min(t, T - 1), D, P);
-    float ev[4];
+    float ev[GW];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) ev[h] = dyn[(h < G ? h : 0) * SH + k];
+    for (int h = 0; h < GW; ++h) ev[h] = dyn[(h < GH ? h : 0) * SH + k];
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
-      if (h < G) {
+    for (int h = 0; h < GW; ++h)
+      if (h < GH) {
         const int p = t < T ? to_i8((ev[h] * rh[h]) * 127.0f) : 0;
         pq[h * SP + t] = (int8_t)p;
         if (OPT) qs[h] += p;
@@ -1270,9 +1279,9 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   int vpos[4];
 #pragma unroll
   for (int w = 0; w < 4; ++w) vpos[w] = ((const int*)s_v8)[4 * c + w];
-  int acc[kGqaMaxG][16];
+  int acc[GW][16];
 #pragma unroll
-  for (int h = 0; h < kGqaMaxG; ++h)
+  for (int h = 0; h < GW; ++h)
 #pragma unroll
     for (int b = 0; b < 16; ++b) acc[h][b] = 0;
   const int npv = (T + 4 * TS * RQ - 1) / (4 * TS * RQ);
@@ -1291,11 +1300,11 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
         int col[4][4];
 #pragma unroll
         for (int w = 0; w < 4; ++w) transpose4x4(rw[0][w], rw[1][w], rw[2][w], rw[3][w], col[w]);
-        int pp[4];
+        int pp[GW];
 #pragma unroll
-        for (int h = 0; h < 4; ++h) pp[h] = *(const int*)(pq + (h < G ? h : 0) * SP + t0);
+        for (int h = 0; h < GW; ++h) pp[h] = *(const int*)(pq + (h < GH ? h : 0) * SP + t0);
 #pragma unroll
-        for (int h = 0; h < kGqaMaxG; ++h)
+        for (int h = 0; h < GW; ++h)
 #pragma unroll
           for (int w = 0; w < 4; ++w)
 #pragma unroll
@@ -1306,7 +1315,7 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   // lanes of a 16-lane row with the same chunk rotate-and-add over the row-slice bits; then one
   // partial row per (wave, row of 16 lanes) in LDS, summed by (head, column)
 #pragma unroll
-  for (int h = 0; h < kGqaMaxG; ++h)
+  for (int h = 0; h < GW; ++h)
 #pragma unroll
     for (int b = 0; b < 16; ++b) {
       int v = acc[h][b];
@@ -1317,14 +1326,14 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
     }
   if ((lane & 15) < NCHP) {
 #pragma unroll
-    for (int h = 0; h < kGqaMaxG; ++h)
-      if (h < G)
+    for (int h = 0; h < GW; ++h)
+      if (h < GH)
 #pragma unroll
         for (int b = 0; b < 16; ++b) part[wave * 4 + (lane >> 4)][h * HD + 16 * c + b] = acc[h][b];
   }
   __syncthreads();
   float* out = a.att + row * a.att_stride;
-  for (int idx = tid; idx < G * HD; idx += kGqaThreads) {
+  for (int idx = tid; idx < GH * HD; idx += kGqaThreads) {
     int ssum = 0;
 #pragma unroll
     for (int w = 0; w < kGqaWaves * 4; ++w) ssum += part[w][idx];
@@ -1337,9 +1346,9 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
         for (int w = 0; w < kGqaWaves; ++w) tot += s_qs[w][h];
         o = o * qsum_scale(tot, tab);
       }
-      out[(long long)(g * G + h) * HD + j] = o * (a.ch_av ? a.ch_av[(long long)g * HD + j] : a.a_v);
+      out[(long long)(h0 + h) * HD + j] = o * (a.ch_av ? a.ch_av[(long long)g * HD + j] : a.a_v);
     } else {
-      out[(long long)(g * G + h) * HD + j] = (float)ssum * a.a_v;
+      out[(long long)(h0 + h) * HD + j] = (float)ssum * a.a_v;
     }
   }
 }
