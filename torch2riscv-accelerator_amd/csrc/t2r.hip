@@ -131,17 +131,26 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   const bool opt = attn_opt(a);                 // the HF options: the kernels' OPT instantiations
   if (mode == ATTN_FUSED && rows > 1 && a.tab != nullptr && G >= 2 && G <= kGqaMaxG &&
       (a.hd == 64 || a.hd == 128) && attn_gqa_lds_bytes(a.S, a.D, G) <= 65536) {
-    if (G == kGqaMaxG) {
-      // four query heads per KV head: two workgroups of two heads each (twice the grid)
-      constexpr int GW = kGqaMaxG / 2;
-      const dim3 gs(a.Hk * (kGqaMaxG / GW), rows);
-      const size_t gl = attn_gqa_lds_bytes(a.S, a.D, GW);
-      if (a.hd == 64) {
-        if (opt) launch((k_attn_gqa<4, true, GW>), gs, dim3(kGqaThreads), gl, st, a);
-        else launch((k_attn_gqa<4, false, GW>), gs, dim3(kGqaThreads), gl, st, a);
+    if (G == 4 || G == 2) {
+      // an even group: G / 2 query heads per workgroup, two workgroups per KV head (twice the grid)
+      const dim3 gs(a.Hk * 2, rows);
+      const size_t gl = attn_gqa_lds_bytes(a.S, a.D, G / 2);
+      if (G == 4) {
+        if (a.hd == 64) {
+          if (opt) launch((k_attn_gqa<4, true, 2>), gs, dim3(kGqaThreads), gl, st, a);
+          else launch((k_attn_gqa<4, false, 2>), gs, dim3(kGqaThreads), gl, st, a);
+        } else {
+          if (opt) launch((k_attn_gqa<8, true, 2>), gs, dim3(kGqaThreads), gl, st, a);
+          else launch((k_attn_gqa<8, false, 2>), gs, dim3(kGqaThreads), gl, st, a);
+        }
       } else {
-        if (opt) launch((k_attn_gqa<8, true, GW>), gs, dim3(kGqaThreads), gl, st, a);
-        else launch((k_attn_gqa<8, false, GW>), gs, dim3(kGqaThreads), gl, st, a);
+        if (a.hd == 64) {
+          if (opt) launch((k_attn_gqa<4, true, 1>), gs, dim3(kGqaThreads), gl, st, a);
+          else launch((k_attn_gqa<4, false, 1>), gs, dim3(kGqaThreads), gl, st, a);
+        } else {
+          if (opt) launch((k_attn_gqa<8, true, 1>), gs, dim3(kGqaThreads), gl, st, a);
+          else launch((k_attn_gqa<8, false, 1>), gs, dim3(kGqaThreads), gl, st, a);
+        }
       }
       return launched();
     }
