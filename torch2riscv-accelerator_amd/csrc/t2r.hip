@@ -126,42 +126,32 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   const size_t lds = mode == ATTN_PREP ? 0 : attn_lds_bytes(a.S, a.D);
   dim3 grid(a.H, rows), block(kAttnThreads);
   const bool c16 = a.hd % 16 == 0;
-  // batched decode: one workgroup per (row, KV head) for its group of 2..4 query heads
+  // batched decode: per (row, KV head) its group of 2..4 query heads, over G / gw workgroups
   const int G = a.H / a.Hk;
   const bool opt = attn_opt(a);                 // the HF options: the kernels' OPT instantiations
   if (mode == ATTN_FUSED && rows > 1 && a.tab != nullptr && G >= 2 && G <= kGqaMaxG &&
       (a.hd == 64 || a.hd == 128) && attn_gqa_lds_bytes(a.S, a.D, G) <= 65536) {
-    if (G == 4 || G == 2) {
-      // an even group: G / 2 query heads per workgroup, two workgroups per KV head (twice the grid)
-      const dim3 gs(a.Hk * 2, rows);
-      const size_t gl = attn_gqa_lds_bytes(a.S, a.D, G / 2);
-      if (G == 4) {
-        if (a.hd == 64) {
-          if (opt) launch((k_attn_gqa<4, true, 2>), gs, dim3(kGqaThreads), gl, st, a);
-          else launch((k_attn_gqa<4, false, 2>), gs, dim3(kGqaThreads), gl, st, a);
-        } else {
-          if (opt) launch((k_attn_gqa<8, true, 2>), gs, dim3(kGqaThreads), gl, st, a);
-          else launch((k_attn_gqa<8, false, 2>), gs, dim3(kGqaThreads), gl, st, a);
-        }
+    // the group split over workgroups: two query heads each for four-head groups, else one
+    // (G / gw workgroups per KV head; the lds bound above holds a fortiori)
+    const int gw = G == 4 ? 2 : 1;
+    const dim3 gs(a.Hk * (G / gw), rows);
+    const size_t gl = attn_gqa_lds_bytes(a.S, a.D, gw);
+    if (gw == 2) {
+      if (a.hd == 64) {
+        if (opt) launch((k_attn_gqa<4, true, 2>), gs, dim3(kGqaThreads), gl, st, a);
+        else launch((k_attn_gqa<4, false, 2>), gs, dim3(kGqaThreads), gl, st, a);
       } else {
-        if (a.hd == 64) {
-          if (opt) launch((k_attn_gqa<4, true, 1>), gs, dim3(kGqaThreads), gl, st, a);
-          else launch((k_attn_gqa<4, false, 1>), gs, dim3(kGqaThreads), gl, st, a);
-        } else {
-          if (opt) launch((k_attn_gqa<8, true, 1>), gs, dim3(kGqaThreads), gl, st, a);
-          else launch((k_attn_gqa<8, false, 1>), gs, dim3(kGqaThreads), gl, st, a);
-        }
+        if (opt) launch((k_attn_gqa<8, true, 2>), gs, dim3(kGqaThreads), gl, st, a);
+        else launch((k_attn_gqa<8, false, 2>), gs, dim3(kGqaThreads), gl, st, a);
       }
-      return launched();
-    }
-    const dim3 gg(a.Hk, rows);
-    const size_t gl = attn_gqa_lds_bytes(a.S, a.D, G);
-    if (a.hd == 64) {
-      if (opt) launch((k_attn_gqa<4, true>), gg, dim3(kGqaThreads), gl, st, a);
-      else launch((k_attn_gqa<4>), gg, dim3(kGqaThreads), gl, st, a);
     } else {
-      if (opt) launch((k_attn_gqa<8, true>), gg, dim3(kGqaThreads), gl, st, a);
-      else launch((k_attn_gqa<8>), gg, dim3(kGqaThreads), gl, st, a);
+      if (a.hd == 64) {
+        if (opt) launch((k_attn_gqa<4, true, 1>), gs, dim3(kGqaThreads), gl, st, a);
+        else launch((k_attn_gqa<4, false, 1>), gs, dim3(kGqaThreads), gl, st, a);
+      } else {
+        if (opt) launch((k_attn_gqa<8, true, 1>), gs, dim3(kGqaThreads), gl, st, a);
+        else launch((k_attn_gqa<8, false, 1>), gs, dim3(kGqaThreads), gl, st, a);
+      }
     }
     return launched();
   }

@@ -996,10 +996,10 @@ inline size_t attn_gqa_lds_bytes(int S, int D, int G) {
   return (size_t)G * ((size_t)D * osum_stride(S, D) + 64) * 4 + (size_t)G * ((S + 15) & ~15);
 }
 
-// GW: query heads per workgroup. GW < kGqaMaxG (launched for G a multiple of GW, G > GW) splits a KV
-// head's group over G / GW workgroups (blockIdx.x = KV head * splits + split); each computes the KV
-// head's new row for itself, and split 0 writes it to the cache.
-template <int NCH, bool OPT = false, int GW = kGqaMaxG>   // hd = 16 NCH (64 or 128); OPT: HF options
+// GW: query heads per workgroup (G a multiple of GW): a KV head's group is split over G / GW
+// workgroups (blockIdx.x = KV head * splits + split); each computes the KV head's new row for
+// itself, and split 0 writes it to the cache.
+template <int NCH, bool OPT, int GW>   // hd = 16 NCH (64 or 128); OPT: HF options
 __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   constexpr int HD = 16 * NCH, KS = HD / 32;                // MFMA k-steps per key tile
   constexpr int NCHP = NCH;                                 // (4 or 8: a power of two)
@@ -1020,9 +1020,9 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   const int row = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, lr = lane & 31, kh = lane >> 5;
   const int G = a.H / a.Hk, S = a.S, D = a.D, P = osum_stride(S, D), SH = D * P + 64;
-  const int NSPL = GW == kGqaMaxG ? 1 : G / GW;  // workgroups per KV head
-  const int g = GW == kGqaMaxG ? (int)blockIdx.x : (int)blockIdx.x / NSPL, spl = (int)blockIdx.x - g * NSPL;
-  const int GH = GW == kGqaMaxG ? G : GW;        // query heads of this workgroup
+  const int NSPL = G / GW;                       // workgroups per KV head
+  const int g = (int)blockIdx.x / NSPL, spl = (int)blockIdx.x - g * NSPL;
+  const int GH = GW;                             // query heads of this workgroup
   const int h0 = g * G + spl * GW;               // its first query head
   const int SP = (S + 15) & ~15;                 // int8 p row stride
   int8_t* pq = (int8_t*)(dyn + GH * SH);
