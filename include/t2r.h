@@ -130,6 +130,16 @@ int t2r_moe_route(const float* scores, int rows, int E, int k, int D, int32_t* i
 int t2r_attn_decode_opt(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H,
                         int Hk, int hd, int S, float a_k, float a_v, int D, int flags, const float* ch_sk,
                         const float* ch_av, float* att, void* stream);
+/* Prefill attention of M prompt rows q[M, H * hd] (already rotated, their KV rows already in the cache)
+ * at positions pos[M], each row over the cache rows 0..pos[r] (the prompt chunk's attention:
+ * expandAttnChunkBlocked, compiler/plugins/sa/transforms/SahlExpandKernels.cpp:1702; QModel.prefill's
+ * per-row attention, compiler/frontend/qhf.py:356-409). Each row's result is t2r_attn_decode_opt's for
+ * that row, bit for bit; rows run 16 at a time per query head on int8 MFMA where hd is a multiple of 16
+ * (<= 128) and a row's scores fit in LDS, else row by row. Flags and per-channel scales as
+ * t2r_attn_decode_opt. S = cache rows <= 8192. */
+int t2r_attn_prefill(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int M, int H, int Hk,
+                     int hd, int S, float a_k, float a_v, int D, int flags, const float* ch_sk, const float* ch_av,
+                     float* att, void* stream);
 /* KV append with per-channel inverse scales inv_sk[kv_dim], inv_sv[kv_dim] (hf_generic.py:203-218):
  * kc[pos[r]][c] = to_i8(F(k[r][c] * inv_sk[c])); either vector may be NULL for the scalar one. */
 int t2r_kv_append_ch(const float* k, const float* v, float inv_sk, float inv_sv, const float* inv_sk_ch,

@@ -66,6 +66,8 @@ _SIGS = {
     "t2r_attn_decode": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int, P, P]),
     "t2r_attn_decode_opt": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int, c_int, P, P,
                                     P, P]),
+    "t2r_attn_prefill": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int, c_int, P, P,
+                                 P, P]),
     "t2r_swiglu_w8a8": (c_int, [P, P, P, P, P, P, c_int, c_int, P, P, P, P]),
     "t2r_gated_ffn_w8a8": (c_int, [c_int, P, P, P, P, P, P, c_int, c_int, P, P, P, P]),
     "t2r_moe_route": (c_int, [P, c_int, c_int, c_int, c_int, P, P, P]),

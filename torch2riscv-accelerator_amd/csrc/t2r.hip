@@ -75,6 +75,14 @@ int ensure_init() {
   for (const void* f : deep)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmDDeepLds) != hipSuccess)
       return T2R_EHIP;
+  // the grouped decode attention: score rows of caches up to kMaxS positions
+  const void* gqa[] = {(const void*)k_attn_gqa<4, false, 1>, (const void*)k_attn_gqa<4, true, 1>,
+                       (const void*)k_attn_gqa<4, false, 2>, (const void*)k_attn_gqa<4, true, 2>,
+                       (const void*)k_attn_gqa<8, false, 1>, (const void*)k_attn_gqa<8, true, 1>,
+                       (const void*)k_attn_gqa<8, false, 2>, (const void*)k_attn_gqa<8, true, 2>};
+  for (const void* f : gqa)
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGqaMaxLds) != hipSuccess)
+      return T2R_EHIP;
   if (hipFuncSetAttribute((const void*)k_gemm_d<EPI_SWIGLU, false, 128, 3, 2 * kGT>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmDTallLds) != hipSuccess)
     return T2R_EHIP;
@@ -129,11 +137,11 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   // batched decode: per (row, KV head) its group of 2..4 query heads, over G / gw workgroups
   const int G = a.H / a.Hk;
   const bool opt = attn_opt(a);                 // the HF options: the kernels' OPT instantiations
+  // the group split over workgroups: two query heads each for four-head groups, else one
+  // (G / gw workgroups per KV head), each with its gw heads' score rows in LDS
+  const int gw = G == 4 ? 2 : 1;
   if (mode == ATTN_FUSED && rows > 1 && a.tab != nullptr && G >= 2 && G <= kGqaMaxG &&
-      (a.hd == 64 || a.hd == 128) && attn_gqa_lds_bytes(a.S, a.D, G) <= 65536) {
-    // the group split over workgroups: two query heads each for four-head groups, else one
-    // (G / gw workgroups per KV head; the lds bound above holds a fortiori)
-    const int gw = G == 4 ? 2 : 1;
+      (a.hd == 64 || a.hd == 128) && attn_gqa_lds_bytes(a.S, a.D, gw) <= kGqaMaxLds) {
     const dim3 gs(a.Hk * (G / gw), rows);
     const size_t gl = attn_gqa_lds_bytes(a.S, a.D, gw);
     if (gw == 2) {
@@ -649,6 +657,22 @@ int run_final(Model* m, int row, float* logits, int32_t* next_token, int32_t* po
   return T2R_OK;
 }
 
+// the model's state from a validated descriptor (its workspace in dv)
+int model_init(Model* m, const t2r_model_desc& dv) {
+  m->d = dv;
+  const t2r_model_desc* desc = &m->d;
+  model_dims(m);
+  if (carve(m, nullptr, desc->max_rows) > desc->workspace_bytes) return T2R_ENOMEM;
+  carve(m, (char*)desc->workspace, desc->max_rows);
+  m->kvc.assign(desc->kv_consts, desc->kv_consts + (size_t)desc->layers * 4);
+  m->kv_flags.assign((size_t)desc->layers, 0);
+  if (desc->kv_channel_flags)
+    m->kv_flags.assign(desc->kv_channel_flags, desc->kv_channel_flags + desc->layers);
+  m->d.kv_consts = nullptr;
+  m->d.kv_channel_flags = nullptr;
+  return T2R_OK;
+}
+
 }  // namespace
 
 // ================================================================== C-ABI
@@ -823,6 +847,25 @@ int t2r_attn_decode_opt(const float* q, const int8_t* kc, const int8_t* vc, cons
   return attn_launch(ATTN_ONLY, a, rows, S(stream));
 }
 
+int t2r_attn_prefill(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int M, int H, int Hk,
+                     int hd, int S_, float a_k, float a_v, int D, int flags, const float* ch_sk, const float* ch_av,
+                     float* att, void* stream) {
+  if (!q || !kc || !vc || !pos || !att) return T2R_EINVAL;
+  if (flags & ~T2R_ATTN_QSUM) return T2R_EINVAL;
+  if (M <= 0) return T2R_ESHAPE;
+  T2R_INIT();
+  AttnArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.qkv = (float*)q; a.qkv_stride = (long long)H * hd;
+  a.kc = (int8_t*)kc; a.vc = (int8_t*)vc; a.pos = pos;
+  a.a_k = a_k; a.a_v = a_v; a.H = H; a.Hk = Hk; a.hd = hd; a.D = D; a.S = S_;
+  a.att = att; a.att_stride = (long long)H * hd;
+  a.qsum = flags & T2R_ATTN_QSUM;
+  a.ch_sk = ch_sk; a.ch_av = ch_av;
+  a.tab = sfu_table_ptr();                       // the multi-row kernel (k_attn_pre) where it takes the shape
+  return attn_launch(ATTN_ONLY, a, M, S(stream));
+}
+
 int t2r_attn_decode(const float* q, const int8_t* kc, const int8_t* vc, const int32_t* pos, int rows, int H, int Hk,
                     int hd, int S_, float a_k, float a_v, int D, float* att, void* stream) {
   return t2r_attn_decode_opt(q, kc, vc, pos, rows, H, Hk, hd, S_, a_k, a_v, D, 0, nullptr, nullptr, att, stream);
@@ -882,20 +925,10 @@ int t2r_model_create(const t2r_model_desc* desc, void** model) {
   T2R_INIT();
   Model* m = new (std::nothrow) Model();
   if (!m) return T2R_ENOMEM;
-  m->d = dv;
-  desc = &m->d;
-  model_dims(m);
-  if (carve(m, nullptr, desc->max_rows) > desc->workspace_bytes) {
+  if ((rc = model_init(m, dv))) {
     delete m;
-    return T2R_ENOMEM;
+    return rc;
   }
-  carve(m, (char*)desc->workspace, desc->max_rows);
-  m->kvc.assign(desc->kv_consts, desc->kv_consts + (size_t)desc->layers * 4);
-  m->kv_flags.assign((size_t)desc->layers, 0);
-  if (desc->kv_channel_flags)
-    m->kv_flags.assign(desc->kv_channel_flags, desc->kv_channel_flags + desc->layers);
-  m->d.kv_consts = nullptr;
-  m->d.kv_channel_flags = nullptr;
   *model = m;
   return T2R_OK;
 }

@@ -973,16 +973,16 @@ inline size_t attn_lds_bytes(int S, int D) { return (size_t)D * osum_stride(S, D
 inline size_t attn_dec_lds_bytes(int S, int D) { return ((size_t)D * osum_stride(S, D) + 64) * 4; }
 
 // ------------------------------------------------------------------ grouped decode attention
-// Decode attention with one workgroup per (row, KV head g) for the G <= 4 query heads that share
-// the KV head, instead of one per query head: the numerics are k_attn_dec's step for step, the work
-// is split differently.
+// Decode attention of the G <= 4 query heads that share a KV head, split over G / GW workgroups per
+// (row, KV head g), each taking GW of the group's query heads (2 for four-head groups, else 1): the
+// numerics are k_attn_dec's step for step, the work is split differently.
 //  - Vector jobs, one per wave: the KV head (k: QK-norm, RoPE, int8; v: int8; the cache row) and
-//    the G query heads (QK-norm, RoPE, quant_act). This workgroup is the row's only writer of its
-//    KV head's cache row.
-//  - Scores: the K rows are read once for the group, straight into the MFMA B layout (lane = key
-//    row, 16 k-bytes), and v_mfma_i32_32x32x32_i8 takes the G int8 q vectors as its A rows (rows
-//    past G zero): exact int32 dot products of all G heads, 32 keys per instruction pair.
-//  - Per key, the G heads' EXPs side by side (independent table-lookup chains); per head the
+//    the workgroup's GW query heads (QK-norm, RoPE, quant_act). Every workgroup of the KV head forms
+//    its new row; split 0 is the only one that writes it to the cache.
+//  - Scores: the K rows are read once per workgroup, straight into the MFMA B layout (lane = key
+//    row, 16 k-bytes), and v_mfma_i32_32x32x32_i8 takes the GW int8 q vectors as its A rows (rows
+//    past GW zero): exact int32 dot products of its heads, 32 keys per instruction pair.
+//  - Per key, the GW heads' EXPs side by side (independent table-lookup chains); per head the
 //    D-lane ordered sum (one wave each) and RECIP; then the int8 probabilities of every (head, key)
 //    into LDS rows, so P.V reads one word per four consecutive keys and head.
 //  - P.V: a thread takes four consecutive V rows of one 16-byte chunk, transposes them once
@@ -991,7 +991,9 @@ inline size_t attn_dec_lds_bytes(int S, int D) { return ((size_t)D * osum_stride
 constexpr int kGqaThreads = 512, kGqaWaves = kGqaThreads / 64, kGqaMaxG = 4;   // G + 1 <= 8 vector jobs
 constexpr int kGqaRK = 4;                        // key tiles (32 rows) per wave per pass
 
-// dynamic LDS: per head the lane-major scores (D P floats + 64 spare), then per head S int8 p
+// dynamic LDS: per head the lane-major scores (D P floats + 64 spare), then per head S int8 p; the
+// kernels are set up for up to kGqaMaxLds (two heads of an 8192-position cache)
+constexpr size_t kGqaMaxLds = 96 * 1024;
 inline size_t attn_gqa_lds_bytes(int S, int D, int G) {
   return (size_t)G * ((size_t)D * osum_stride(S, D) + 64) * 4 + (size_t)G * ((S + 15) & ~15);
 }
@@ -1009,13 +1011,14 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   static_assert(HD == 64 || HD == 128, "k_attn_gqa: hd 64 or 128");
   extern __shared__ __align__(16) float dyn[];
   __shared__ __align__(16) float tab[kSfuWords];
-  __shared__ __align__(16) int8_t s_q8[kGqaMaxG][HD];
+  static_assert(GW >= 1 && GW <= kGqaMaxG, "k_attn_gqa: 1..4 query heads per workgroup");
+  __shared__ __align__(16) int8_t s_q8[GW][HD];
   __shared__ __align__(16) int8_t s_k8[HD], s_v8[HD];
   __shared__ __align__(16) float s_vec[kGqaWaves][HD];
-  __shared__ float s_sq[kGqaMaxG], s_r[kGqaMaxG];
-  __shared__ float red[kGqaWaves][kGqaMaxG];
-  __shared__ int s_qs[kGqaWaves][kGqaMaxG];
-  __shared__ int part[kGqaWaves * 4][kGqaMaxG * HD];
+  __shared__ float s_sq[GW], s_r[GW];
+  __shared__ float red[kGqaWaves][GW];
+  __shared__ int s_qs[kGqaWaves][GW];
+  __shared__ int part[kGqaWaves * 4][GW * HD];
 
   const int row = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, lr = lane & 31, kh = lane >> 5;
@@ -1251,7 +1254,9 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
 #pragma unroll
   for (int r = 0; r < GW; ++r) rh[r] = s_r[r < GH ? r : 0];
   const int T4 = (T + 3) & ~3;
-  int qs[4] = {0, 0, 0, 0};                      // qsum: the probabilities of the thread's keys, per head
+  int qs[GW];                                    // qsum: the probabilities of the thread's keys, per head
+#pragma unroll
+  for (int h = 0; h < GW; ++h) qs[h] = 0;
   for (int t = tid; t < T4; t += kGqaThreads) {
     const int k = osum_index(min(t, T - 1), D, P);
     float ev[GW];
@@ -1267,7 +1272,7 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   }
   if (OPT && a.qsum) {
 #pragma unroll
-    for (int h = 0; h < kGqaMaxG; ++h) {
+    for (int h = 0; h < GW; ++h) {
       const int v = wave_sum_i32(qs[h]);
       if (lane == 0) s_qs[wave][h] = v;
     }

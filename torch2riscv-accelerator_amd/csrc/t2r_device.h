@@ -300,17 +300,10 @@ T2R_DEV int dot16(int4 w, int4 x, int acc) {
 
 
 
-#ifndef T2R_NT_LOADS
-#define T2R_NT_LOADS 1
-#endif
 // 16-byte streaming load (non-temporal hint: weights are read once per token)
 T2R_DEV int4 load_nt16(const int8_t* p) {
-#if T2R_NT_LOADS
   const v4i_t v = __builtin_nontemporal_load((const v4i_t*)p);
   return make_int4(v.x, v.y, v.z, v.w);
-#else
-  return *(const int4*)p;
-#endif
 }
 
 T2R_DEV int pack_i8x4(int a, int b, int c, int d) {

@@ -85,10 +85,10 @@ class ResidentModel:
             nbytes = self.lib.t2r_model_workspace_bytes(ctypes.byref(desc), self.max_rows)
             if nbytes <= 0:
                 raise ValueError("t2r_model_workspace_bytes rejected the model description")
-            self.workspace = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
-            desc.workspace, desc.workspace_bytes = self.workspace.data_ptr(), int(nbytes)
             self.desc = desc
             handle = ctypes.c_void_p()
+            self.workspace = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
+            desc.workspace, desc.workspace_bytes = self.workspace.data_ptr(), int(nbytes)
             abi.check("t2r_model_create", self.lib.t2r_model_create(ctypes.byref(desc), ctypes.byref(handle)))
             self.handle = handle
             self.tok = torch.zeros(1, dtype=torch.int32, device=dev)

@@ -386,7 +386,7 @@ class Llama2cTokenizer:
     length and the piece's bytes. encode() follows run.c (llm/tokenizer.py:24-52): BOS, a " " dummy
     prefix for non-empty text, one piece per UTF-8 code point (else its bytes, id = byte + 3), then
     repeatedly the adjacent pair whose merged piece has the highest score (the leftmost such pair
-    on ties) is merged. decode() prints as run.c: the space after BOS dropped, <0xNN> pieces as
+    on ties) is merged, while one scores above -1e10. decode() prints as run.c: the space after BOS dropped, <0xNN> pieces as
     their byte, other single bytes only when printable or whitespace."""
 
     def __init__(self, path, vocab_size):
@@ -422,14 +422,15 @@ class Llama2cTokenizer:
             out.extend([tid] if tid is not None else [b + 3 for b in cp])
             i = j
         while len(out) > 1:                       # over the whole list, BOS included, as run.c
-            best = None                            # (score, position, id)
+            # a merge must score above run.c's floor of -1e10 (a NaN score never does)
+            best = (-1e10, -1, -1)                 # (score, position, id)
             for k in range(len(out) - 1):
                 tid = self.ids.get(self.pieces[out[k]] + self.pieces[out[k + 1]])
-                if tid is not None and (best is None or self.scores[tid] > best[0]):
+                if tid is not None and self.scores[tid] > best[0]:
                     best = (self.scores[tid], k, tid)
-            if best is None:
-                break
             _, k, tid = best
+            if k < 0:
+                break
             out[k:k + 2] = [tid]
         if eos:
             out.append(EOS)

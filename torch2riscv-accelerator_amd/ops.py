@@ -149,6 +149,19 @@ def attention_opt(q, kc, vc, pos, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch
     return att
 
 
+def attention_prefill(q, kc, vc, pos, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None):
+    """Prefill attention of prompt rows q [M, H * hd] at positions pos [M] (t2r_attn_prefill): each row
+    as attention_opt computes it, the rows on the multi-row kernel where the shape allows."""
+    _dev(q, kc, vc, pos)
+    hd = q.shape[-1] // H
+    rows = q.numel() // q.shape[-1]
+    att = torch.empty_like(q)
+    abi.call("t2r_attn_prefill", abi.ptr(q), abi.ptr(kc), abi.ptr(vc), abi.ptr(pos), rows, H, Hk, hd,
+             kc.shape[0], float(a_k), float(a_v), int(D), abi.T2R_ATTN_QSUM if qsum else 0, abi.ptr(ch_sk),
+             abi.ptr(ch_av), abi.ptr(att), _s())
+    return att
+
+
 def swiglu(w1, s_w1, w3, s_w3, xq, s_x):
     _dev(w1, s_w1, w3, s_w3, xq, s_x)
     F_, K = w1.shape
