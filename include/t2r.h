@@ -233,6 +233,11 @@ int t2r_prefill_at(void* model, const int32_t* tokens, int start, int M, float* 
 int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* positions, int B, int8_t* k_caches,
                      int8_t* v_caches, int64_t cache_stride, float* logits, int32_t* next_tokens, void* stream);
 
+/* The model's status word (the reference's per-list status, llm/runtime.py:116-119): bit 0 a token
+ * outside [0, vocab) was embedded (row 0 read instead). Waits for the device; clear != 0 then zeroes
+ * the word. */
+int t2r_model_status(void* model, int32_t* out, int clear);
+
 /* Kernel timing of a resident model with HIP events on the launch stream (the GPU counterpart of
  * the reference's event counters and per-list cycle counts: rtl/sysarray/sa_perf.v,
  * driver/pynq_matmul.py:969-981, 1029-1066). t2r_model_profile creates 2 * max_launches events

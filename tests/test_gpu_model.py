@@ -165,3 +165,29 @@ def test_prefill_at_equals_prefill_with_positions(name):
     with pytest.raises(ValueError):
         rm.prefill([1] * 4, start=cfg.seq_len - 2)
     rm.close()
+
+
+def test_status_word_and_token_range():
+    """Token ids outside the vocabulary: the host calls refuse them (ValueError, as the reference's
+    runtime raises for bad arguments); one that reaches the device anyway (through the step's device
+    token) reads row 0 and sets bit 0 of the model's status word, which t2r_model_status reports and
+    clears."""
+    import t2r_amd.config as C
+    from t2r_amd import weights as W
+    from t2r_amd.model import ResidentModel
+    cfg = C.get("tiny-qwen")
+    rm = ResidentModel(W.QuantModel(cfg), max_rows=8)
+    with pytest.raises(ValueError):
+        rm.decode(cfg.vocab, 0)
+    with pytest.raises(ValueError):
+        rm.prefill([1, -1, 3])
+    with pytest.raises(ValueError):
+        rm.decode_batch([2, cfg.vocab + 7], [0, 0], *rm.batch_caches(2))
+    rm.decode(3, 0)
+    assert rm.status() == 0
+    rm.tok.fill_(cfg.vocab + 5)
+    rm.pos.fill_(1)
+    rm.step()
+    assert rm.status() == 1
+    assert rm.status() == 0
+    rm.close()

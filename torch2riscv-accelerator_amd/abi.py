@@ -79,6 +79,7 @@ _SIGS = {
     "t2r_prefill": (c_int, [c_void_p, P, P, c_int, P, P, P]),
     "t2r_prefill_at": (c_int, [c_void_p, P, c_int, c_int, P, P, P]),
     "t2r_decode_batch": (c_int, [c_void_p, P, P, c_int, P, P, c_int64, P, P, P]),
+    "t2r_model_status": (c_int, [c_void_p, P, c_int]),
     "t2r_model_profile": (c_int, [c_void_p, c_int, c_int]),
     "t2r_model_profile_read": (c_int, [c_void_p, P, P, c_int]),
 }

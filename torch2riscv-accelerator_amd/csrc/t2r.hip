@@ -491,31 +491,10 @@ int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, c
 // own position and cache, m->kcb / m->vcb), the MFMA GEMMs and the fused per-row attention.
 enum { RUN_DECODE = 0, RUN_PREFILL = 1, RUN_BATCH = 2 };
 
-int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream_t st) {
+// the attention launch arguments of layer l (its cache, constants and options)
+AttnArgs layer_attn_args(Model* m, int l, const int32_t* pos, int mode) {
   const t2r_model_desc& d = m->d;
-  const bool decode = mode == RUN_DECODE, batch = mode == RUN_BATCH;
-  const long long L_dim = (long long)l * d.dim;
-  const float inv_d = (float)(1.0 / d.dim);
-  int rc;
-  // Wqkv: RMSNorm + quant_act + linear
-  GemvArgs a = gemv_args();
-  a.w = d.wqkv + (long long)l * m->qkv_dim * d.dim;
-  a.s_w = d.s_wqkv + (long long)l * m->qkv_dim;
-  a.x = m->x; a.x_stride = d.dim; a.g = d.rms_att + L_dim; a.inv_n = inv_d; a.eps = d.eps; a.D = d.D;
-  a.N = m->qkv_dim; a.K = d.dim; a.y = m->qkv; a.y_stride = m->qkv_dim;
-  int qz = 1;                                       // prefill: Wqkv's split finished by the prep kernel
-  // (the timed class of a multi-row linear is the GEMM alone: its row norm/quant runs before the scope)
-  if (decode) {
-    ProfScope p(m, T2R_PROF_QKV, st);
-    if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
-  } else {
-    if ((rc = rows_quant(m, m->x, d.dim, d.rms_att + L_dim, d.dim, rows, st))) return rc;
-    ProfScope p(m, T2R_PROF_QKV, st);
-    if ((rc = rows_linear<EPI_STORE>(m, a.w, a.s_w, nullptr, nullptr, m->qkv_dim, d.dim, rows, m->qkv, m->qkv_dim, st,
-                                     mode == RUN_PREFILL ? &qz : nullptr)))
-      return rc;
-  }
-  // attention (QK-norm, RoPE, KV append fused for decode)
+  const bool batch = mode == RUN_BATCH;
   AttnArgs at;
   std::memset(&at, 0, sizeof(at));
   at.qkv = m->qkv; at.qkv_stride = m->qkv_dim;
@@ -539,6 +518,43 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     if (m->kv_flags[l] & 1) { at.ch_sk = ch; at.ch_isk = ch + m->kv_dim; }
     if (m->kv_flags[l] & 2) { at.ch_isv = ch + 2 * m->kv_dim; at.ch_av = ch + 3 * m->kv_dim; }
   }
+  return at;
+}
+
+// the decode Wqkv GEMV of layer l: RMSNorm + quant_act of x, the q | k | v rows
+GemvArgs layer_qkv_args(Model* m, int l) {
+  const t2r_model_desc& d = m->d;
+  GemvArgs a = gemv_args();
+  a.w = d.wqkv + (long long)l * m->qkv_dim * d.dim;
+  a.s_w = d.s_wqkv + (long long)l * m->qkv_dim;
+  a.x = m->x; a.x_stride = d.dim; a.g = d.rms_att + (long long)l * d.dim; a.inv_n = (float)(1.0 / d.dim);
+  a.eps = d.eps; a.D = d.D;
+  a.N = m->qkv_dim; a.K = d.dim; a.y = m->qkv; a.y_stride = m->qkv_dim;
+  return a;
+}
+
+int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream_t st) {
+  const t2r_model_desc& d = m->d;
+  const bool decode = mode == RUN_DECODE, batch = mode == RUN_BATCH;
+  const long long L_dim = (long long)l * d.dim;
+  const float inv_d = (float)(1.0 / d.dim);
+  int rc;
+  // Wqkv: RMSNorm + quant_act + linear
+  GemvArgs a = layer_qkv_args(m, l);
+  int qz = 1;                                       // prefill: Wqkv's split finished by the prep kernel
+  // (the timed class of a multi-row linear is the GEMM alone: its row norm/quant runs before the scope)
+  if (decode) {
+    ProfScope p(m, T2R_PROF_QKV, st);
+    if ((rc = gemv_launch<PRO_NORM_QUANT, EPI_STORE>(a, rows, st))) return rc;
+  } else {
+    if ((rc = rows_quant(m, m->x, d.dim, d.rms_att + L_dim, d.dim, rows, st))) return rc;
+    ProfScope p(m, T2R_PROF_QKV, st);
+    if ((rc = rows_linear<EPI_STORE>(m, a.w, a.s_w, nullptr, nullptr, m->qkv_dim, d.dim, rows, m->qkv, m->qkv_dim, st,
+                                     mode == RUN_PREFILL ? &qz : nullptr)))
+      return rc;
+  }
+  // attention (QK-norm, RoPE, KV append fused for decode)
+  AttnArgs at = layer_attn_args(m, l, pos, mode);
   if (qz > 1) {
     at.part = m->part; at.part_nz = qz; at.part_zstride = (long long)rows * m->qkv_dim;
     at.part_sw = a.s_w; at.part_sx = m->sx;
@@ -664,6 +680,8 @@ int model_init(Model* m, const t2r_model_desc& dv) {
   model_dims(m);
   if (carve(m, nullptr, desc->max_rows) > desc->workspace_bytes) return T2R_ENOMEM;
   carve(m, (char*)desc->workspace, desc->max_rows);
+  // the status word starts clear
+  if (hipMemset(m->status, 0, sizeof(int32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return T2R_EHIP;
   m->kvc.assign(desc->kv_consts, desc->kv_consts + (size_t)desc->layers * 4);
   m->kv_flags.assign((size_t)desc->layers, 0);
   if (desc->kv_channel_flags)
@@ -940,6 +958,14 @@ void t2r_model_destroy(void* model) {
   delete m;
 }
 
+int t2r_model_status(void* model, int32_t* out, int clear) {
+  Model* m = (Model*)model;
+  if (!m || !out) return T2R_EINVAL;
+  if (hipMemcpy(out, m->status, sizeof(int32_t), hipMemcpyDeviceToHost) != hipSuccess) return T2R_EHIP;
+  if (clear && hipMemset(m->status, 0, sizeof(int32_t)) != hipSuccess) return T2R_EHIP;
+  return T2R_OK;
+}
+
 int t2r_model_profile(void* model, int mask, int max_launches) {
   Model* m = (Model*)model;
   if (!m || mask < 0 || max_launches < 0 || (mask && max_launches == 0)) return T2R_EINVAL;
@@ -974,6 +1000,7 @@ int t2r_decode_step(void* model, const int32_t* token, int32_t* pos, float* logi
                     void* stream) {
   Model* m = (Model*)model;
   if (!m || !token || !pos) return T2R_EINVAL;
+  if (flags & ~T2R_ADVANCE_POS) return T2R_EINVAL;
   T2R_INIT();
   m->pend_z = 0;
   hipStream_t st = S(stream);

@@ -299,7 +299,6 @@ T2R_DEV int dot16(int4 w, int4 x, int acc) {
 }
 
 
-
 // 16-byte streaming load (non-temporal hint: weights are read once per token)
 T2R_DEV int4 load_nt16(const int8_t* p) {
   const v4i_t v = __builtin_nontemporal_load((const v4i_t*)p);

@@ -128,10 +128,23 @@ class ResidentModel:
         """Logits (device tensor, valid until the next call) of `token` at `pos`."""
         if not 0 <= pos < self.cfg.seq_len:
             raise ValueError(f"position {pos} outside [0, {self.cfg.seq_len})")
+        self._check_tokens([token])
         self.tok.fill_(int(token))
         self.pos.fill_(int(pos))
         self.step()
         return self.logits
+
+    def _check_tokens(self, tokens):
+        bad = [int(t) for t in tokens if not 0 <= int(t) < self.cfg.vocab]
+        if bad:
+            raise ValueError(f"token {bad[0]} outside [0, {self.cfg.vocab})")
+
+    def status(self, clear=True):
+        """The device status word (bit 0: a token outside the vocabulary was embedded); waits for the
+        device."""
+        out = np.zeros(1, np.int32)
+        abi.check("t2r_model_status", self.lib.t2r_model_status(self.handle, out.ctypes.data, int(clear)))
+        return int(out[0])
 
     def prefill(self, tokens, start=0, logits=True):
         """Rows tokens at positions start.. as one call per max_rows chunk; logits of the last row."""
@@ -141,6 +154,7 @@ class ResidentModel:
             raise ValueError(f"positions {start}..{start + len(toks) - 1} outside [0, {self.cfg.seq_len})")
         if not toks:
             raise ValueError("empty prompt")
+        self._check_tokens(toks)
         i = 0
         while i < len(toks):
             chunk = toks[i:i + self.max_rows]
@@ -176,6 +190,7 @@ class ResidentModel:
         pos = [int(p) for p in positions]
         if min(pos) < 0 or max(pos) >= c.seq_len:
             raise ValueError(f"positions outside [0, {c.seq_len})")
+        self._check_tokens(tokens)
         self.rows_tok[:B].copy_(torch.tensor([int(t) for t in tokens], dtype=torch.int32))
         self.rows_pos[:B].copy_(torch.tensor(pos, dtype=torch.int32))
         out = logits if logits is not None else torch.empty((B, c.vocab), dtype=torch.float32, device=self.device)
