@@ -197,8 +197,19 @@ typedef struct t2r_model_desc {
 
 /* Bytes of workspace a model needs for prefill calls of up to max_rows rows (>= 1). */
 int64_t t2r_model_workspace_bytes(const t2r_model_desc* desc, int max_rows);
-/* Validates desc (shapes, pointers, workspace) and returns a handle; copies desc. */
+/* Validates desc (shapes, pointers, workspace; layers <= 256) and returns a handle; copies desc. */
 int t2r_model_create(const t2r_model_desc* desc, void** model);
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid hipMalloc). t2r_model_create with desc->workspace = NULL and
+ * desc->workspace_bytes = 0: the model's workspace is the library's static device array of
+ * T2R_STATIC_WORKSPACE_BYTES on the current device, and the handle comes from a fixed pool of 8, so the
+ * call allocates nothing. Models made this way on one device share that array: their calls (decode,
+ * prefill, batched decode) must not overlap; calls in sequence are fine, each starts from scratch.
+ * Returns T2R_ENOMEM when max_rows needs more than the array (t2r_model_workspace_bytes tells),
+ * T2R_EINVAL when a workspace is given, T2R_ESTATE when the 8 handles are taken. t2r_model_destroy
+ * returns the handle to the pool. */
+#define T2R_STATIC_WORKSPACE_BYTES (16 * 1024 * 1024)
+int t2r_model_create_static(const t2r_model_desc* desc, void** model);
 void t2r_model_destroy(void* model);
 /* One decode step (the reference's static token list: llm/compile_model.py:351-374, run per token
  * by llm/runtime.py:107-125): token and pos are read from DEVICE memory, so a captured HIP graph

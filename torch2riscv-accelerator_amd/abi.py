@@ -15,6 +15,7 @@ T2R_ABI_VERSION = 2
 T2R_OK, T2R_EINVAL, T2R_ESHAPE, T2R_ERANGE, T2R_EHIP, T2R_ENOMEM, T2R_ESTATE = 0, -1, -2, -3, -4, -5, -6
 T2R_ADVANCE_POS = 1
 T2R_ATTN_QSUM = 1
+T2R_STATIC_WORKSPACE_BYTES = 16 * 1024 * 1024
 
 c_int, c_int64, c_uint64, c_float, c_void_p = ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_void_p
 P = c_void_p    # every tensor argument is a raw device pointer
@@ -74,6 +75,7 @@ _SIGS = {
     "t2r_argmax": (c_int, [P, c_int, c_int, P, P]),
     "t2r_model_workspace_bytes": (c_int64, [ctypes.POINTER(ModelDesc), c_int]),
     "t2r_model_create": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(c_void_p)]),
+    "t2r_model_create_static": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(c_void_p)]),
     "t2r_model_destroy": (None, [c_void_p]),
     "t2r_decode_step": (c_int, [c_void_p, P, P, P, P, c_int, P]),
     "t2r_prefill": (c_int, [c_void_p, P, P, c_int, P, P, P]),

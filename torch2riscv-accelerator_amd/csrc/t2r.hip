@@ -20,6 +20,11 @@ namespace t2r {
 __constant__ float c_sfu[kSfuWords];
 }
 
+// The workspace of every model made by t2r_model_create_static on a device: one array per device,
+// held until the process ends and shared by all such models there (their calls must not overlap).
+// Host code uses its per-device address from hipGetSymbolAddress (g_scratch_addr), never the name.
+static __device__ __align__(256) char scratch[T2R_STATIC_WORKSPACE_BYTES];
+
 using namespace t2r;
 
 namespace {
@@ -28,6 +33,7 @@ constexpr int kMaxDevices = 64;
 std::mutex g_init_mu;
 bool g_inited[kMaxDevices];
 const float* g_sfu_addr[kMaxDevices];
+char* g_scratch_addr[kMaxDevices];
 
 // The SFU tables (llm/sfu.py:42-56): segment start T and slope S of each function, computed in
 // double and rounded once to float.
@@ -86,7 +92,10 @@ int ensure_init() {
   if (hipFuncSetAttribute((const void*)k_gemm_d<EPI_SWIGLU, false, 128, 3, 2 * kGT>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmDTallLds) != hipSuccess)
     return T2R_EHIP;
+  void* ws = nullptr;
+  if (hipGetSymbolAddress(&ws, HIP_SYMBOL(scratch)) != hipSuccess || ws == nullptr) return T2R_EHIP;
   g_sfu_addr[dev] = (const float*)addr;
+  g_scratch_addr[dev] = (char*)ws;
   g_inited[dev] = true;
   return T2R_OK;
 }
@@ -209,10 +218,13 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------- the resident model
+constexpr int kMaxLayers = 256;
+
 struct Model {
   t2r_model_desc d;
-  std::vector<float> kvc;           // [L, 4]
-  std::vector<int32_t> kv_flags;    // [L]: bit 0 K per channel, bit 1 V per channel
+  float kvc[kMaxLayers * 4];        // [L, 4]
+  int32_t kv_flags[kMaxLayers];     // [L]: bit 0 K per channel, bit 1 V per channel
+  int pool_slot = -1;               // t2r_model_create_static: its slot in the static pool
   int q_dim, kv_dim, qkv_dim, ffn_rows, max_in;
   int32_t* part;                    // split-K partial sums of the prefill linears
   int part_rows;
@@ -344,8 +356,8 @@ int validate(const t2r_model_desc* d) {
       if (d->kv_channel_flags[l] && !d->kv_channel) return T2R_EINVAL;
     }
   }
-  if (d->dim <= 0 || d->hidden <= 0 || d->layers <= 0 || d->heads <= 0 || d->kv_heads <= 0 || d->head_dim <= 0 ||
-      d->vocab <= 0 || d->seq_len <= 0)
+  if (d->dim <= 0 || d->hidden <= 0 || d->layers <= 0 || d->layers > kMaxLayers || d->heads <= 0 ||
+      d->kv_heads <= 0 || d->head_dim <= 0 || d->vocab <= 0 || d->seq_len <= 0)
     return T2R_ESHAPE;
   if (d->heads % d->kv_heads || d->heads / d->kv_heads > kMaxG || d->head_dim > kMaxHd || d->head_dim % 8)
     return T2R_ESHAPE;
@@ -506,7 +518,7 @@ AttnArgs layer_attn_args(Model* m, int l, const int32_t* pos, int mode) {
   at.qn = d.qk_norm ? d.q_norm + (long long)l * d.head_dim : nullptr;
   at.kn = d.qk_norm ? d.k_norm + (long long)l * d.head_dim : nullptr;
   at.cos_t = d.rope_cos; at.sin_t = d.rope_sin;
-  const float* kc4 = &m->kvc[(size_t)l * 4];
+  const float* kc4 = m->kvc + (size_t)l * 4;
   at.inv_sk = kc4[0]; at.inv_sv = kc4[1]; at.a_k = kc4[2]; at.a_v = kc4[3];
   at.eps = d.eps; at.inv_hd = (float)(1.0 / d.head_dim);
   at.H = d.heads; at.Hk = d.kv_heads; at.hd = d.head_dim; at.D = d.D; at.S = d.seq_len;
@@ -673,7 +685,7 @@ int run_final(Model* m, int row, float* logits, int32_t* next_token, int32_t* po
   return T2R_OK;
 }
 
-// the model's state from a validated descriptor (its workspace in dv)
+// the model's state from a validated descriptor whose workspace is in dv (the caller's or the static one)
 int model_init(Model* m, const t2r_model_desc& dv) {
   m->d = dv;
   const t2r_model_desc* desc = &m->d;
@@ -682,14 +694,18 @@ int model_init(Model* m, const t2r_model_desc& dv) {
   carve(m, (char*)desc->workspace, desc->max_rows);
   // the status word starts clear
   if (hipMemset(m->status, 0, sizeof(int32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return T2R_EHIP;
-  m->kvc.assign(desc->kv_consts, desc->kv_consts + (size_t)desc->layers * 4);
-  m->kv_flags.assign((size_t)desc->layers, 0);
-  if (desc->kv_channel_flags)
-    m->kv_flags.assign(desc->kv_channel_flags, desc->kv_channel_flags + desc->layers);
+  std::memcpy(m->kvc, desc->kv_consts, sizeof(float) * 4 * desc->layers);
+  for (int l = 0; l < desc->layers; ++l) m->kv_flags[l] = desc->kv_channel_flags ? desc->kv_channel_flags[l] : 0;
   m->d.kv_consts = nullptr;
   m->d.kv_channel_flags = nullptr;
   return T2R_OK;
 }
+
+// the handles of t2r_model_create_static: a fixed pool, so that creating one allocates nothing
+constexpr int kStaticModels = 8;
+std::mutex g_pool_mu;
+Model g_pool[kStaticModels];
+bool g_pool_used[kStaticModels];
 
 }  // namespace
 
@@ -951,10 +967,49 @@ int t2r_model_create(const t2r_model_desc* desc, void** model) {
   return T2R_OK;
 }
 
+int t2r_model_create_static(const t2r_model_desc* desc, void** model) {
+  if (!model) return T2R_EINVAL;
+  *model = nullptr;
+  t2r_model_desc dv;
+  if (!desc_read(desc, &dv)) return T2R_EINVAL;
+  if (dv.workspace != nullptr || dv.workspace_bytes != 0) return T2R_EINVAL;   // the library's array is the workspace
+  T2R_INIT();
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices || !g_scratch_addr[dev]) return T2R_EHIP;
+  dv.workspace = g_scratch_addr[dev];
+  dv.workspace_bytes = T2R_STATIC_WORKSPACE_BYTES;
+  int rc = validate(&dv);
+  if (rc) return rc;
+  Model* m = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    for (int i = 0; i < kStaticModels && !m; ++i)
+      if (!g_pool_used[i]) {
+        g_pool_used[i] = true;
+        m = &g_pool[i];
+        *m = Model();
+        m->pool_slot = i;
+      }
+  }
+  if (!m) return T2R_ESTATE;                     // every static model slot is taken
+  if ((rc = model_init(m, dv))) {
+    t2r_model_destroy(m);
+    return rc;                                   // T2R_ENOMEM: max_rows needs more than the static array
+  }
+  *model = m;
+  return T2R_OK;
+}
+
 void t2r_model_destroy(void* model) {
   Model* m = (Model*)model;
   if (!m) return;
   free_events(m);
+  if (m->pool_slot >= 0) {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    g_pool_used[m->pool_slot] = false;
+    m->pool_slot = -1;
+    return;
+  }
   delete m;
 }
 

@@ -16,8 +16,10 @@ F = np.float32
 
 
 class ResidentModel:
-    def __init__(self, qm, device="cuda:0", max_rows=None, D=None):
-        """qm: t2r_amd.weights.QuantModel (host arrays). max_rows: prefill rows per t2r_prefill call."""
+    def __init__(self, qm, device="cuda:0", max_rows=None, D=None, static_workspace=False):
+        """qm: t2r_amd.weights.QuantModel (host arrays). max_rows: prefill rows per t2r_prefill call.
+        static_workspace: the library's static workspace array instead of one allocated here
+        (t2r_model_create_static; calls of such models on one device must not overlap)."""
         import torch
         self.torch = torch
         self.cfg = c = qm.cfg
@@ -87,9 +89,15 @@ class ResidentModel:
                 raise ValueError("t2r_model_workspace_bytes rejected the model description")
             self.desc = desc
             handle = ctypes.c_void_p()
-            self.workspace = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
-            desc.workspace, desc.workspace_bytes = self.workspace.data_ptr(), int(nbytes)
-            abi.check("t2r_model_create", self.lib.t2r_model_create(ctypes.byref(desc), ctypes.byref(handle)))
+            if static_workspace:
+                self.workspace = None
+                desc.workspace, desc.workspace_bytes = None, 0
+                abi.check("t2r_model_create_static",
+                          self.lib.t2r_model_create_static(ctypes.byref(desc), ctypes.byref(handle)))
+            else:
+                self.workspace = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
+                desc.workspace, desc.workspace_bytes = self.workspace.data_ptr(), int(nbytes)
+                abi.check("t2r_model_create", self.lib.t2r_model_create(ctypes.byref(desc), ctypes.byref(handle)))
             self.handle = handle
             self.tok = torch.zeros(1, dtype=torch.int32, device=dev)
             self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
