@@ -72,33 +72,59 @@ def measured_traffic(kind, cfg_name):
     return None
 
 
-def cpu_baseline(qm, prompt, seconds):
-    """The oracle (NumPy restatement, bit-exact with the reference) decoding on this host's cores."""
-    import numpy as np
-    from oracle import OracleModel
+def host_cpu():
+    """This host's CPU model, logical cores, and the BLAS threads the oracle's matrix products use."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     try:
         from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+        blas = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
     except Exception:
-        cores = 1
+        blas = 1
+    return model, os.cpu_count() or 1, int(blas)
+
+
+def oracle_on_gpu_cache(qm, rm, P):
+    """The oracle holding the KV rows 0..P-1 that the GPU prefill wrote (bit-identical to the oracle's own
+    prefill of the prompt, which its tests check), so the CPU is timed at the GPU run's positions."""
+    from oracle import OracleModel
     om = OracleModel(qm)
-    P = 8
-    om.prefill(prompt[:P])
-    tok = prompt[P]
-    om.forward(tok, P)                                 # untimed: converts the weights to the matmul layout
-    om.reset()
-    om.prefill(prompt[:P])
-    n, t0 = 0, time.perf_counter()
-    logits = []
-    while time.perf_counter() - t0 < seconds and n < 64:
+    om.kc[:, :P] = rm.kc[:, :P].cpu().numpy()
+    om.vc[:, :P] = rm.vc[:, :P].cpu().numpy()
+    return om
+
+
+def cpu_decode(om, tok, P, seconds, max_steps=64):
+    """Greedy decode steps of the oracle at positions P, P + 1, ... for about `seconds` (the first step
+    untimed: it converts the weights to the matrix-product layout). Returns (tok/s, steps, logits)."""
+    import numpy as np
+    snap = (om.kc[:, P].copy(), om.vc[:, P].copy())
+    om.forward(tok, P)
+    om.kc[:, P], om.vc[:, P] = snap
+    n, logits, t0 = 0, [], time.perf_counter()
+    while time.perf_counter() - t0 < seconds and n < max_steps and P + n < om.cfg.seq_len:
         lg = om.forward(tok, P + n)
         logits.append(lg)
         tok = int(np.argmax(lg))
         n += 1
     dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": int(cores), "kind": "port",
-            "sample": f"{n} greedy decode steps at positions {P}..{P + n - 1} after an {P}-token prefill "
-                      f"({dt:.1f} s)"}, logits
+    return n / dt, n, dt, logits
+
+
+def cpu_prefill(om, prompt, P, rows):
+    """The oracle's prefill of the prompt's last `rows` rows (positions P - rows .. P - 1, attending to the
+    cache rows before them): rows/s at the prompt's longest contexts."""
+    rows = min(rows, P)
+    t0 = time.perf_counter()
+    om.prefill(prompt[P - rows:P], start=P - rows)
+    dt = time.perf_counter() - t0
+    return rows / dt, rows, dt
 
 
 def main():
@@ -114,6 +140,9 @@ def main():
     ap.add_argument("--batch", default="4,8,16",
                     help="batched-decode sizes to time (t2r_decode_batch; '' to skip)")
     ap.add_argument("--batch-steps", type=int, default=32)
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5",
+                    help="configs whose GPU and CPU decode / prefill rates go into the line's `configs` ('' to skip)")
+    ap.add_argument("--config-cpu-seconds", type=float, default=4.0)
     ap.add_argument("--copy-calib-mb", type=int, default=0,
                     help="first copy this many MiB device to device (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -341,22 +370,100 @@ def main():
                      "launches": dom.get("launches"), "traffic": measured_traffic("ffn_up", cfg.name)},
     }
 
-    # ---- CPU baseline (+ a bit-exactness spot check of the same positions on the GPU)
+    # ---- CPU baseline at the GPU run's positions (+ a bit-exactness spot check of those positions)
     if not args.no_cpu_baseline:
-        cb, cpu_logits = cpu_baseline(qm, prompt, args.cpu_seconds)
-        out["cpu_baseline"] = cb
+        cpu_model, ncpu, blas = host_cpu()
         rm.reset()
-        rm.prefill(prompt[:8])
-        tok = prompt[8]
-        same = True
+        rm.prefill(prompt)
+        tok0 = int(rm.next.item())
+        om = oracle_on_gpu_cache(qm, rm, P)
+        rate, n, cdt, cpu_logits = cpu_decode(om, tok0, P, args.cpu_seconds)
+        out["cpu_baseline"] = {"value": round(rate, 3), "unit": "tok/s", "cores": blas, "kind": "port",
+                               "sample": f"{n} greedy decode steps of the NumPy restatement at positions {P}.."
+                                         f"{P + n - 1} after the {P}-token prompt ({cdt:.1f} s)",
+                               "cpu": cpu_model, "host_logical_cores": ncpu}
+        tok, same = tok0, True
         for i, lg in enumerate(cpu_logits[:4]):
-            g = rm.decode(tok, 8 + i).cpu().numpy()
+            g = rm.decode(tok, P + i).cpu().numpy()
             same &= bool(np.array_equal(g.view(np.uint32), lg.view(np.uint32)))
             tok = int(np.argmax(lg))
-        out["parity_spot_check"] = {"positions": min(4, len(cpu_logits)), "bit_exact": same}
-        log(f"cpu baseline: {cb['value']} tok/s on {cb['cores']} cores; GPU == CPU logits: {same}")
+        out["parity_spot_check"] = {"positions": f"{P}..{P + min(4, len(cpu_logits)) - 1}", "bit_exact": same}
+        log(f"cpu baseline: {rate:.2f} tok/s on {blas} BLAS threads ({cpu_model}); GPU == CPU logits: {same}")
     rm.close()
+    del rm
+
+    # ---- every config: GPU decode (HIP graph) and prefill, CPU decode and prefill samples
+    if args.configs:
+        out["configs"] = per_config(args, out if not args.no_cpu_baseline else None)
     print(json.dumps(out), flush=True)
+
+
+def per_config(args, c4_out):
+    """Decode and prefill tok/s of each BASELINE.json config on the GPU and of the CPU restatement on this
+    host (BLAS threads stated), at the config's own prompt length; bounded samples. The headline config
+    reuses the numbers measured above."""
+    import numpy as np
+    import torch
+    import t2r_amd.config as C
+    from t2r_amd import weights as W
+    from t2r_amd.model import ResidentModel
+    cpu_model, ncpu, blas = host_cpu()
+    table = {"cpu": cpu_model, "host_logical_cores": ncpu, "blas_threads": blas}
+    for key in [k.strip() for k in args.configs.split(",") if k.strip()]:
+        cfg = C.get(key)
+        if c4_out is not None and cfg.name == args.config:
+            table[cfg.name] = {"gpu_decode_tok_s": c4_out["value"], "gpu_prefill_tok_s": c4_out["prefill_tok_s"],
+                               "cpu_decode_tok_s": c4_out["cpu_baseline"]["value"],
+                               "decode_positions": f"{cfg.prompt_len}..", "prompt": cfg.prompt_len}
+            continue
+        t0 = time.time()
+        qm = W.QuantModel(cfg)
+        prompt = cfg.prompt()
+        P = len(prompt)
+        rm = ResidentModel(qm, device="cuda:0", max_rows=min(P, 2048))
+        # GPU prefill: the whole prompt in one call (median of 3)
+        ts = []
+        for _ in range(4):
+            rm.reset()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            rm.prefill(prompt)
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t)
+        pre = float(np.median(ts[1:]))
+        tok0 = int(rm.next.item())
+        # GPU decode: a HIP graph of the config's decode steps (at most 64) from the prompt's end
+        K = max(1, min(cfg.decode_steps, 64, cfg.seq_len - P))
+        rm.tok.fill_(tok0)
+        rm.pos.fill_(P)
+        g = rm.capture_decode(K)
+        rm.tok.fill_(tok0)
+        rm.pos.fill_(P)
+        g.replay()
+        rm.tok.fill_(tok0)
+        rm.pos.fill_(P)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        gdt = time.perf_counter() - t
+        del g
+        rec = {"prompt": P, "gpu_prefill_tok_s": round(P / pre, 1), "gpu_decode_tok_s": round(K / gdt, 1),
+               "gpu_decode_steps": K, "decode_positions": f"{P}..{P + K - 1}"}
+        if c4_out is not None:
+            rm.reset()
+            rm.prefill(prompt)
+            om = oracle_on_gpu_cache(qm, rm, P)
+            rate, n, cdt, _ = cpu_decode(om, tok0, P, args.config_cpu_seconds, max_steps=32)
+            prate, rows, pdt = cpu_prefill(om, prompt, P, 16 if P <= 512 else 4)
+            rec.update({"cpu_decode_tok_s": round(rate, 3), "cpu_decode_steps": n,
+                        "cpu_prefill_tok_s": round(prate, 3),
+                        "cpu_prefill_sample": f"rows {P - rows}..{P - 1} ({pdt:.1f} s)"})
+        rm.close()
+        del rm, qm
+        table[cfg.name] = rec
+        log(f"{cfg.name}: {rec} ({time.time() - t0:.0f} s)")
+    return table
 
 
 if __name__ == "__main__":
