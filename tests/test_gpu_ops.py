@@ -249,13 +249,21 @@ def test_moe_route(env):
     sc[1, [3, 9, 20]] = 2.5                                                  # ties: lower id first
     sc[2, :] = 1.0
     sc[3, 5] = np.nan                                                        # NaN after every number
-    for k, D in ((8, 16), (2, 8), (1, 16)):
-        ids, w = ops.moe_route(T(sc), k, D)
+    sc[4, 30] = -0.0
+    sc[4, 2] = 0.0
+    wide = rng.standard_normal((4, 64)).astype(F)                            # E = 64: every lane an expert
+    wide[0, [1, 40, 63]] = np.nan
+    wide[1, :] = np.nan                                                      # all NaN: ids in order
+    wide[2, ::3] = 7.0
+    wide[3, 60:] = np.inf
+    for scores, k, D in ((sc, 8, 16), (sc, 2, 8), (sc, 1, 16), (wide, 8, 16), (wide, 5, 8), (sc[:, :8], 8, 16)):
+        scores = np.ascontiguousarray(scores)
+        ids, w = ops.moe_route(T(scores), k, D)
         ids, w = H(ids), H(w)
-        for r in range(sc.shape[0]):
-            want = N.topk_desc(sc[r], k)
+        for r in range(scores.shape[0]):
+            want = N.topk_desc(scores[r], k)
             assert list(ids[r]) == list(want)
-            v = sc[r][want]
+            v = scores[r][want]
             e = N.sfu_exp((v - v[0]).astype(F))
             ww = (e * N.sfu_recip(N.red_sum(e, D))).astype(F)
             assert np.array_equal(w[r].view(np.uint32), ww.view(np.uint32))

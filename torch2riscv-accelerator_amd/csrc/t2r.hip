@@ -636,7 +636,12 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     ra.k = k; ra.ids = m->ids; ra.wts = m->wts;
     {
       ProfScope p(m, T2R_PROF_ROUTE, st);
-      launch(k_moe_route, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+      if (!gemv_operands_ok<PRO_NORM_QUANT, EPI_STORE>(ra.a) || d.dim % d.D) return T2R_ESHAPE;
+      const int nc = cdiv(d.dim, 1024);
+      if (nc <= 1) launch(k_moe_route<1>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+      else if (nc <= 2) launch(k_moe_route<2>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+      else if (nc <= 4) launch(k_moe_route<4>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+      else launch(k_moe_route<8>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
       if ((rc = launched())) return rc;
     }
     // expert gate / up of the k selected experts (rows j * Fe + n of the selected tables)
@@ -653,8 +658,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     MoeDownArgs md;
     md.u = m->u; md.wd = d.wd + (long long)l * E * d.dim * Fe; md.s_wd = d.s_wd + (long long)l * E * d.dim;
     md.ids = m->ids; md.wts = m->wts; md.x = m->x; md.k = k; md.F = Fe; md.dim = d.dim; md.x_stride = d.dim;
-    int blocks = cdiv(d.dim, 4);
-    if (blocks > 512) blocks = 512;
+    const int blocks = cdiv(d.dim, 4);
     {
       ProfScope p(m, T2R_PROF_FFN_DOWN, st);
       launch(k_moe_down, dim3(blocks, rows), dim3(256), 0, st, md);

@@ -184,66 +184,83 @@ T2R_DEV bool route_before(float a, int ia, float b, int ib) {
   return ia < ib;
 }
 
-T2R_DEV void route_topk(const float* sc, int E, int k, int D, int lane, int32_t* ids, float* w, float* ev) {
-  if (lane == 0) {
-    int sel[8];
-    for (int j = 0; j < k; ++j) {
-      int best = -1;
-      for (int e = 0; e < E; ++e) {
-        bool used = false;
-        for (int q = 0; q < j; ++q) used |= sel[q] == e;
-        if (used) continue;
-        if (best < 0 || route_before(sc[e], e, sc[best], best)) best = e;
-      }
-      sel[j] = best;
-      ids[j] = best;
-    }
-    const float v0 = sc[sel[0]];
-    for (int j = 0; j < k; ++j) ev[j] = sfu_exp(sc[sel[j]] - v0);
+T2R_DEV void route_topk(const float* sc, int E, int k, int D, int lane, int32_t* ids, float* w, float* ev,
+                        const float* tab = c_sfu) {
+  // lane e's rank: how many experts come before it under route_before (a total order: ids differ)
+  const float v = lane < E ? sc[lane] : 0.0f;
+  int rank = 0;
+  for (int j = 0; j < E; ++j) rank += route_before(sc[j], j, v, lane) ? 1 : 0;
+  const bool sel = lane < E && rank < k;
+  if (sel && rank == 0) ev[8] = v;                 // the top score v0
+  __builtin_amdgcn_wave_barrier();
+  const float v0 = ev[8];
+  if (sel) {
+    ids[rank] = lane;
+    ev[rank] = sfu_exp(v - v0, tab);
   }
   __builtin_amdgcn_wave_barrier();
   float s = 0.0f;
   if (lane < D) s = ordered_sum<false>(ev, k, D, lane);
   s = __shfl(s, 0);
-  const float r = sfu_recip(s);
+  const float r = sfu_recip(s, tab);
   if (lane < k) w[lane] = ev[lane] * r;
 }
 
 // The MoE router of rows: RMSNorm + quant_act of x (the activations every expert shares), the
-// router's W8A8 scores, top-k and weights. One block per row.
+// router's W8A8 scores, top-k and weights. One block per row; K <= 1024 * NCB. The prologue's inputs
+// and the router's first 1024 columns are requested together, before the prologue runs, and the SFU
+// tables are read from LDS (the decode GEMV's staged prologue).
 struct RouteArgs {
-  GemvArgs a;                 // x, g, inv_n, eps, D, router weights (w, s_w; N = E, K = dim)
+  GemvArgs a;                 // x, g, inv_n, eps, D, router weights (w, s_w; N = E, K = dim), tab
   int k;
   int32_t* ids;               // [rows, k]
   float* wts;                 // [rows, k]
   float* scores;              // optional [rows, E]
 };
+template <int NCB>
 __global__ __launch_bounds__(kGemvThreads) void k_moe_route(RouteArgs ra) {
-  __shared__ __align__(16) int8_t xq_lds[kMaxK];
-  __shared__ __align__(16) float xf_lds[kMaxK + kOsumLds];
+  constexpr int NT = kGemvThreads, kWaves = NT / 64, kPerWave = 64 / kWaves;   // E <= 64 over the waves
+  __shared__ __align__(16) int8_t xq_lds[NCB * 1024];
+  __shared__ __align__(16) float xf_lds[kOsumLds];
+  __shared__ __align__(16) float tab_lds[kSfuWords];
   __shared__ float red[64];
   __shared__ float sc[64];
   __shared__ float ev[16];
   const GemvArgs& a = ra.a;
   const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int norm = a.g != nullptr;
-  const float s_x = norm ? gemv_prologue<PRO_NORM_QUANT>(a, row, xq_lds, xf_lds, red)
-                         : gemv_prologue<PRO_XQ>(a, row, xq_lds, xf_lds, red);
+  XStage<PRO_NORM_QUANT, EPI_STORE, NCB, NT> st;
+  stage_load(st, a, row);
+  __builtin_amdgcn_sched_barrier(0);
+  const int col0 = lane * 16;
+  int4 w0[kPerWave];
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const int e = min(wave + kWaves * i, a.N - 1);
+    w0[i] = load_nt16(a.w + (long long)e * a.K + min(col0, a.K - 16));
+  }
+  const float sw = a.s_w[min(lane, a.N - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  const float s_x = stage_finish(st, a, row, xq_lds, xf_lds, tab_lds, red);
   if (a.xq_out) {
-    for (int i = threadIdx.x; i < a.K; i += kGemvThreads) a.xq_out[row * a.xq_stride + i] = xq_lds[i];
+    for (int i = threadIdx.x; i < a.K; i += NT) a.xq_out[row * a.xq_stride + i] = xq_lds[i];
     if (threadIdx.x == 0) a.sx_out[row] = s_x;
   }
-  for (int e = wave; e < a.N; e += kGemvThreads / 64) {
-    int acc = 0;
-    for (int col = lane * 16; col < a.K; col += 1024)
-      acc = dot16(*(const int4*)(a.w + (long long)e * a.K + col), *(const int4*)(xq_lds + col), acc);
+  const int4 x0 = col0 < a.K ? *(const int4*)(xq_lds + col0) : make_int4(0, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const int e = wave + kWaves * i;
+    if (e >= a.N) break;
+    int acc = dot16(w0[i], x0, 0);
+    for (int col = col0 + 1024; col < a.K; col += 1024)
+      acc = dot16(load_nt16(a.w + (long long)e * a.K + col), *(const int4*)(xq_lds + col), acc);
     acc = wave_sum_i32(acc);
-    if (lane == 0) sc[e] = dequant(acc, a.s_w[e], s_x);
+    const float s_e = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw), e));
+    if (lane == 0) sc[e] = dequant(acc, s_e, s_x);
   }
   __syncthreads();
   if (ra.scores)
-    for (int e = threadIdx.x; e < a.N; e += kGemvThreads) ra.scores[row * a.N + e] = sc[e];
-  if (wave == 0) route_topk(sc, a.N, ra.k, a.D, lane, ra.ids + row * ra.k, ra.wts + row * ra.k, ev);
+    for (int e = threadIdx.x; e < a.N; e += NT) ra.scores[row * a.N + e] = sc[e];
+  if (wave == 0) route_topk(sc, a.N, ra.k, a.D, lane, ra.ids + row * ra.k, ra.wts + row * ra.k, ev, tab_lds);
 }
 
 // top-k + weights from given scores (the op-level ABI)
@@ -260,7 +277,7 @@ __global__ __launch_bounds__(64) void k_route_scores(const float* scores, int E,
 //   hq_j, s_j = quant_act(u_j)                           per selected expert j
 //   y_j[n]    = F(F(f32(wd[id_j][n] . hq_j) * s_wd) * s_j)
 //   y[n] = +0; y[n] = F(y[n] + F(w_j * y_j[n])) for j = 0..k-1 in order; x[n] = F(x[n] + y[n])
-// One wave per output row n at a time; u rows [k, F] (F <= 1024).
+// One wave per output row n (the grid covers dim); u rows [k, F] (F <= 1024, F % 16 == 0).
 struct MoeDownArgs {
   const float* u;             // [rows, k, F]
   const int8_t* wd;           // [E, dim, F]
@@ -273,46 +290,66 @@ struct MoeDownArgs {
 };
 __global__ __launch_bounds__(256) void k_moe_down(MoeDownArgs m) {
   __shared__ __align__(16) int8_t hq[8 * 1024];
-  __shared__ float red[64];
   __shared__ float s_h[8];
-  __shared__ int s_id[8];
-  __shared__ float s_w[8];
   const int row = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int k = m.k, F = m.F;
+  const int n = blockIdx.x * 4 + wave;
+  const bool live = n < m.dim;
+  const int32_t* idr = m.ids + row * k;
+  // everything this wave's row needs, requested at once: the k weight rows (16 columns a lane), lane j's
+  // expert scale and route weight, and x[n]
+  const int col = lane * 16;
+  int4 wv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int id = j < k ? idr[j] : 0;
+    wv[j] = (j < k && live && col < F) ? load_nt16(m.wd + ((long long)id * m.dim + n) * F + col)
+                                       : make_int4(0, 0, 0, 0);
+  }
+  float swd = 0.0f, wj = 0.0f;
+  if (lane < k && live) {
+    swd = m.s_wd[(long long)idr[lane] * m.dim + n];
+    wj = m.wts[row * k + lane];
+  }
+  float* xr = m.x + row * m.x_stride;
+  const float x_old = live ? xr[n] : 0.0f;
+  // quant_act of each selected expert's u (one wave per expert, the values kept in registers)
   const float* u = m.u + (long long)row * k * F;
-  // quant_act of each expert's u (one wave per expert)
   for (int j = wave; j < k; j += 4) {
+    float4 uv[4];
     uint32_t am = 0;
-    for (int i = lane; i < F; i += 64) am = max(am, abs_bits(u[j * F + i]));
-    const float s = fv(wave_max_u32(am)) * kInv127, inv = sfu_recip(s);
-    for (int i = lane; i < F; i += 64) hq[j * 1024 + i] = (int8_t)to_i8(u[j * F + i] * inv);
-    if (lane == 0) {
-      s_h[j] = s;
-      s_id[j] = m.ids[row * k + j];
-      s_w[j] = m.wts[row * k + j];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int i = c * 256 + lane * 4;
+      uv[c] = i < F ? *(const float4*)(u + j * F + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      am = max(am, max(max(abs_bits(uv[c].x), abs_bits(uv[c].y)), max(abs_bits(uv[c].z), abs_bits(uv[c].w))));
     }
+    const float sj = fv(wave_max_u32(am)) * kInv127, inv = sfu_recip(sj);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int i = c * 256 + lane * 4;
+      if (i < F)
+        *(int*)(hq + j * 1024 + i) = pack_i8x4(to_i8(uv[c].x * inv), to_i8(uv[c].y * inv), to_i8(uv[c].z * inv),
+                                               to_i8(uv[c].w * inv));
+    }
+    if (lane == 0) s_h[j] = sj;
   }
   __syncthreads();
-  const int col = lane * 16;
-  int4 xr[8];
-  for (int j = 0; j < 8; ++j) xr[j] = (j < k && col < F) ? *(const int4*)(hq + j * 1024 + col) : make_int4(0, 0, 0, 0);
-  const int nwaves = gridDim.x * 4;
-  for (int n = blockIdx.x * 4 + wave; n < m.dim; n += nwaves) {
-    int4 wv[8];
-    for (int j = 0; j < 8; ++j)
-      wv[j] = (j < k && col < F) ? *(const int4*)(m.wd + ((long long)s_id[j] * m.dim + n) * F + col) : make_int4(0, 0, 0, 0);
-    int acc[8];
-    for (int j = 0; j < 8; ++j) acc[j] = wave_sum_i32(dot16(wv[j], xr[j], 0));
-    if (lane == 0) {
-      float y = 0.0f;
-      for (int j = 0; j < k; ++j) {
-        const float yj = dequant(acc[j], m.s_wd[(long long)s_id[j] * m.dim + n], s_h[j]);
-        y = y + s_w[j] * yj;
-      }
-      float* x = m.x + row * m.x_stride;
-      x[n] = x[n] + y;
-    }
+  if (!live) return;
+  int acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int4 xq = (j < k && col < F) ? *(const int4*)(hq + j * 1024 + col) : make_int4(0, 0, 0, 0);
+    acc[j] = wave_sum_i32(dot16(wv[j], xq, 0));
   }
+  // lane j: F(w_j * y_j), y_j the dequantised expert output; then the sum in route order
+  int aj = acc[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) aj = lane == j ? acc[j] : aj;
+  const float t = lane < k ? wj * dequant(aj, swd, s_h[lane < k ? lane : 0]) : 0.0f;
+  float y = 0.0f;
+  for (int j = 0; j < k; ++j) y = y + __shfl(t, j);
+  if (lane == 0) xr[n] = x_old + y;
 }
 
 // argmax of rows (first index of the largest value; NaN counts as the largest): one block per row
