@@ -127,6 +127,28 @@ def cpu_prefill(om, prompt, P, rows):
     return rows / dt, rows, dt
 
 
+def prefill_gemm_rates(rm, cfg, prompt):
+    """The prompt prefilled once more with HIP events around each GEMM launch (the per-class scopes of a
+    multi-row linear cover the GEMM alone): per class and overall int8 TOPS at M = len(prompt) rows."""
+    P = len(prompt)
+    rm.reset()
+    rm.profile(kinds=("qkv", "wo", "ffn_up", "ffn_down"), max_launches=4 * cfg.layers + 8)
+    rm.prefill(prompt)
+    pprof = rm.profile_read()
+    rm.profile(kinds=())
+    gemm_ops = {k: 2 * P * v for k, v in gemm_weights(cfg).items()}
+    g_ops = sum(gemm_ops[k] * len(v) for k, v in pprof.items() if k in gemm_ops)
+    g_ms = sum(sum(v) for k, v in pprof.items() if k in gemm_ops)
+    rates = {k: {"launches": len(v), "avg_us": round(sum(v) / len(v) * 1e3, 3),
+                 "TOPS": round(gemm_ops[k] / (sum(v) / len(v) * 1e-3) * 1e-12, 1)}
+             for k, v in pprof.items() if k in gemm_ops and v}
+    g_tops = g_ops / (g_ms * 1e-3) * 1e-12 if g_ms > 0 else None
+    if g_tops:
+        rates["all"] = {"rows": P, "TOPS": round(g_tops, 1), "frac": round(g_tops / MFMA_INT8_PEAK_TOPS, 4),
+                        "peak_TOPS": MFMA_INT8_PEAK_TOPS, "total_us": round(g_ms * 1e3, 1)}
+    return rates, g_ms, g_tops
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -187,22 +209,8 @@ def main():
     prefill_s = float(np.median(times[1:])) if len(times) > 1 else times[0]
     log(f"prefill {P} rows: {prefill_s * 1e3:.2f} ms ({P / prefill_s:.0f} tok/s)")
     # the prefill GEMMs' int8 MFMA rate: one more prefill with HIP events around each GEMM launch
-    # (the per-class scopes of a multi-row linear cover the GEMM alone)
-    rm.reset()
-    rm.profile(kinds=("qkv", "wo", "ffn_up", "ffn_down"), max_launches=4 * cfg.layers + 8)
-    rm.prefill(prompt)
-    pprof = rm.profile_read()
-    rm.profile(kinds=())
-    gemm_ops = {k: 2 * P * v for k, v in gemm_weights(cfg).items()}
-    g_ops = sum(gemm_ops[k] * len(v) for k, v in pprof.items() if k in gemm_ops)
-    g_ms = sum(sum(v) for k, v in pprof.items() if k in gemm_ops)
-    prefill_gemm = {k: {"launches": len(v), "avg_us": round(sum(v) / len(v) * 1e3, 3),
-                        "TOPS": round(gemm_ops[k] / (sum(v) / len(v) * 1e-3) * 1e-12, 1)}
-                    for k, v in pprof.items() if k in gemm_ops and v}
-    g_tops = g_ops / (g_ms * 1e-3) * 1e-12 if g_ms > 0 else None
+    prefill_gemm, g_ms, g_tops = prefill_gemm_rates(rm, cfg, prompt)
     if g_tops:
-        prefill_gemm["all"] = {"TOPS": round(g_tops, 1), "frac": round(g_tops / MFMA_INT8_PEAK_TOPS, 4),
-                               "peak_TOPS": MFMA_INT8_PEAK_TOPS, "total_us": round(g_ms * 1e3, 1)}
         log(f"prefill GEMMs: {g_ms * 1e3:.0f} us, {g_tops:.0f} int8 TOPS ({g_tops / MFMA_INT8_PEAK_TOPS:.3f} of peak)")
     after_prompt = rm.next.clone()
 
@@ -413,6 +421,8 @@ def per_config(args, c4_out):
         cfg = C.get(key)
         if c4_out is not None and cfg.name == args.config:
             table[cfg.name] = {"gpu_decode_tok_s": c4_out["value"], "gpu_prefill_tok_s": c4_out["prefill_tok_s"],
+                               "prefill_gemm_TOPS": c4_out["prefill_gemm"].get("all", {}).get("TOPS"),
+                               "prefill_gemm_frac": c4_out["prefill_gemm"].get("all", {}).get("frac"),
                                "cpu_decode_tok_s": c4_out["cpu_baseline"]["value"],
                                "decode_positions": f"{cfg.prompt_len}..", "prompt": cfg.prompt_len}
             continue
@@ -432,6 +442,7 @@ def per_config(args, c4_out):
             ts.append(time.perf_counter() - t)
         pre = float(np.median(ts[1:]))
         tok0 = int(rm.next.item())
+        gemm, _, g_tops = prefill_gemm_rates(rm, cfg, prompt)
         # GPU decode: a HIP graph of the config's decode steps (at most 64) from the prompt's end
         K = max(1, min(cfg.decode_steps, 64, cfg.seq_len - P))
         rm.tok.fill_(tok0)
@@ -449,7 +460,8 @@ def per_config(args, c4_out):
         gdt = time.perf_counter() - t
         del g
         rec = {"prompt": P, "gpu_prefill_tok_s": round(P / pre, 1), "gpu_decode_tok_s": round(K / gdt, 1),
-               "gpu_decode_steps": K, "decode_positions": f"{P}..{P + K - 1}"}
+               "gpu_decode_steps": K, "decode_positions": f"{P}..{P + K - 1}",
+               "prefill_gemm_TOPS": gemm.get("all", {}).get("TOPS"), "prefill_gemm_frac": gemm.get("all", {}).get("frac")}
         if c4_out is not None:
             rm.reset()
             rm.prefill(prompt)

@@ -731,37 +731,43 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
 
 // ------------------------------------------------------------------ prefill attention
 // ATTN_ONLY for many rows at once (rows whose q is rotated and whose KV rows are in the cache), one
-// workgroup per (query head, 16 consecutive rows). Scores and P.V run on the int8 matrix cores
-// (v_mfma_i32_32x32x32_i8, query rows 16..31 of each tile zero): every lane feeds 16 consecutive
-// k-bytes of its A row and of its B row, the same k for both, so each int32 is the exact dot
-// product. The softmax is per row and follows the decode numerics exactly:
-//  - thread (row i, lane l < D) scans the row's scores t = l, l + D, ... in order;
-//  - it forms EXP(s - max) and keeps that chain of adds, which is the lane chain of the D-lane
-//    ordered sum;
-//  - DPP then pairs the D lanes, and RECIP gives r.
-// P.V packs to_i8(e r 127) of 16 t per lane against V transposed in LDS (wave-private tiles).
+// workgroup of eight waves per (query head, 16 consecutive rows). Scores and P.V run on the int8
+// matrix cores (v_mfma_i32_32x32x32_i8, query rows 16..31 of each tile zero): every lane feeds 16
+// consecutive k-bytes of its A row and of its B row, the same k for both, so each int32 is the exact
+// dot product. The softmax is per row and follows the decode numerics exactly:
+//  - the row maximum (order-free) and e = EXP(s - max) (+0 padding to a multiple of D), 32 threads
+//    per row, every element independent;
+//  - thread (row i, lane l < D) then adds the row's e[t], t = l, l + D, ... in order: the lane
+//    chain of the D-lane ordered sum; DPP pairs the D lanes, and RECIP gives r.
+// P.V packs to_i8(e r 127) of 16 t per lane against V transposed in LDS (wave-private tiles, 64
+// columns at a time).
 constexpr int kPreRows = 16;
-constexpr int kPreThreads = 256;
+constexpr int kPreThreads = 512;
+constexpr int kPreWaves = kPreThreads / 64;
 constexpr int kPreTiles = 8;                  // 32-row cache tiles a wave loads at once
 constexpr size_t kPreMaxLds = 136 * 1024;     // dynamic LDS the kernels are set up for (of 160 KB per CU)
 
 // Row stride (floats) of the score / exp rows: at least S + 16, and 17 mod 64. The P.V pass reads one
-// key of all 16 rows per instruction (and, in lanes 32-63, the key 16 on): 32 distinct LDS banks. The
-// exp pass's 4 rows x 16 keys per wave overlap in 3 banks. (A stride of 0 or 32 mod 64 put the 16
-// rows of a key in 2 banks.)
+// key of all 16 rows per instruction (and, in lanes 32-63, the key 16 on): 32 distinct LDS banks.
+// (A stride of 0 or 32 mod 64 put the 16 rows of a key in 2 banks.)
 __host__ __device__ inline int pre_est(int S) { return ((S + 16 + 63) & ~63) + 17; }
 
 template <int HDP, bool OPT = false>   // head dim padded to a multiple of 32 (MFMA k-steps); OPT: HF options
 __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   constexpr int KS = HDP / 32;                 // k-steps of the score MFMA; column tiles of P.V
   constexpr int NV = HDP > 64 ? 2 : 1;
+  constexpr int NW = kPreWaves;
+  constexpr int VTC = HDP < 64 ? HDP : 64;     // V columns transposed per pass
+  constexpr int PT = kPreTiles / 2;             // tiles in flight per wave (registers: two workgroups per
+                                               // CU at head dim 64)
+  constexpr int NPASS = HDP / VTC, QP = VTC / 32;   // V transpose passes; 16-byte chunks a lane per pass
   extern __shared__ __align__(16) float E[];   // [16][est] scores, then exps; then partial P.V sums
   __shared__ __align__(16) float tab[kSfuWords];
   __shared__ __align__(16) int8_t Q8[kPreRows][HDP];
-  __shared__ __align__(16) int8_t VT[4][HDP][32];
+  __shared__ __align__(16) int8_t VT[NW][VTC][32];
   __shared__ float s_sq[kPreRows], s_r[kPreRows];
   __shared__ int s_T[kPreRows];
-  __shared__ int s_qs[4][kPreRows];
+  __shared__ int s_qs[NW][kPreRows];
   // row blocks in reverse: a causal prompt's later rows attend to more positions, and the blocks
   // dispatched first should be the longest (the short ones then fill in behind them)
   const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kPreRows, tid = threadIdx.x;
@@ -772,8 +778,8 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = ((const v4f_t*)a.tab)[tid];
   __syncthreads();
 
-  // ---- q of the block's rows to int8 (one wave per 4 rows); rows without a valid position: T = 0
-  for (int i = wave; i < kPreRows; i += 4) {
+  // ---- q of the block's rows to int8 (one wave per 2 rows); rows without a valid position: T = 0
+  for (int i = wave; i < kPreRows; i += NW) {
     const int r = min(r0 + i, M - 1);
     const int pos = a.pos[r];
     const bool ok = r0 + i < M && pos >= 0 && pos < S;
@@ -808,22 +814,22 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc, (uint32_t)S * kv_dim);
   const int lr = lane & 31, lk = (lane >> 5) * 16;
 
-  // ---- scores of the wave's tiles (t = 32 tile + n), kPreTiles tiles' K rows in flight at a time
+  // ---- scores of the wave's tiles (t = 32 tile + n), PT tiles' K rows in flight at a time
   v4i_t qa[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
     qa[ks] = lr < kPreRows ? *(const v4i_t*)&Q8[lr][32 * ks + lk] : v4i_t{0, 0, 0, 0};
-  for (int c0 = wave; c0 < ntile; c0 += 4 * kPreTiles) {
-    v4i_t kb[kPreTiles][KS];
+  for (int c0 = wave; c0 < ntile; c0 += NW * PT) {
+    v4i_t kb[PT][KS];
 #pragma unroll
-    for (int u = 0; u < kPreTiles; ++u) {
-      const uint32_t off = (uint32_t)(32 * (c0 + 4 * u) + lr) * kv_dim + g * HD + lk;
+    for (int u = 0; u < PT; ++u) {
+      const uint32_t off = (uint32_t)(32 * (c0 + NW * u) + lr) * kv_dim + g * HD + lk;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kb[u][ks] = buffer_load16(krs, off + 32 * ks);
     }
 #pragma unroll
-    for (int u = 0; u < kPreTiles; ++u) {
-      const int ti = c0 + 4 * u;
+    for (int u = 0; u < PT; ++u) {
+      const int ti = c0 + NW * u;
       if (ti >= ntile) break;
       v16i_t acc;
 #pragma unroll
@@ -839,38 +845,65 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   }
   __syncthreads();
 
-  // ---- per row: max, e = EXP(s - max) (+0 padding), the D-lane ordered sum, RECIP
+  // ---- per row (32 threads of one wave each): max, e = EXP(s - max) with +0 padding to a multiple
+  // of D; then the D-lane ordered sum and RECIP
   {
-    const int i = tid >> 4, l = tid & 15;
+    const int i = tid >> 5, sub = tid & 31;
     const int T = s_T[i];
     float* row = E + i * est;
     float mx = -__builtin_inff();
-    if (l < D)
-      for (int t = l; t < T; t += D) mx = nanmax(mx, row[t]);
+    for (int t = sub; t < T; t += 32 * 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = t + 32 * j < T ? row[t + 32 * j] : -__builtin_inff();
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = nanmax(mx, v[j]);
+    }
     mx = nanmax(mx, dpp_f<kDppXor1>(mx));
     mx = nanmax(mx, dpp_f<kDppXor2>(mx));
     mx = nanmax(mx, dpp_f<kDppHalfMirror>(mx));
     mx = nanmax(mx, dpp_f<kDppMirror>(mx));
+    mx = nanmax(mx, __shfl_xor(mx, 16));           // the row's two 16-lane halves
+    const int groups = T > 0 ? (T + D - 1) / D : 0, Tpad = groups * D;
+    for (int t = sub; t < Tpad; t += 32 * 4) {
+      float e[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[j] = t + 32 * j < T ? row[t + 32 * j] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[j] = t + 32 * j < T ? sfu_exp(e[j] - mx, tab) : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (t + 32 * j < Tpad) row[t + 32 * j] = e[j];
+    }
+    // the row's exps were written by this wave's lanes: wait for them, then the lane chains
+    __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
     float acc = 0.0f;
-    const int groups = T > 0 ? (T + D - 1) / D : 0;
-    if (l < D) {
-      for (int gi = 0; gi < groups; ++gi) {
-        const int t = l + gi * D;
-        const float e = t < T ? sfu_exp(row[t] - mx, tab) : 0.0f;
-        row[t] = e;
+    if (sub < D) {
+      int gi = 0;
+      for (; gi + 8 <= groups; gi += 8) {
+        float e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e[j] = row[sub + (gi + j) * D];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = gi + j == 0 ? e[j] : acc + e[j];
+      }
+      for (; gi < groups; ++gi) {
+        const float e = row[sub + gi * D];
         acc = gi == 0 ? e : acc + e;
       }
     }
-    // pairwise tree over the D lanes of the row group (lane l, l % 2s == 0, takes lane l + s)
+    // pairwise tree over the D lanes of the row (lane l, l % 2s == 0, takes lane l + s); the row's
+    // lanes sub 0..15 are one 16-lane DPP row
     float o = dpp_f<0x101>(acc);
-    if (D > 1 && (l & 1) == 0) acc = acc + o;
+    if (D > 1 && (sub & 1) == 0) acc = acc + o;
     o = dpp_f<0x102>(acc);
-    if (D > 2 && (l & 3) == 0) acc = acc + o;
+    if (D > 2 && (sub & 3) == 0) acc = acc + o;
     o = dpp_f<0x104>(acc);
-    if (D > 4 && (l & 7) == 0) acc = acc + o;
+    if (D > 4 && (sub & 7) == 0) acc = acc + o;
     o = dpp_f<0x108>(acc);
-    if (D > 8 && (l & 15) == 0) acc = acc + o;
-    if (l == 0) s_r[i] = (OPT && a.qsum) ? 1.0f : sfu_recip(acc, tab);   // qsum: to_i8(F(F(e * 1) * 127))
+    if (D > 8 && (sub & 15) == 0) acc = acc + o;
+    if (sub == 0) s_r[i] = (OPT && a.qsum) ? 1.0f : sfu_recip(acc, tab);   // qsum: to_i8(F(F(e * 1) * 127))
   }
   __syncthreads();
 
@@ -885,29 +918,21 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   const int Tm = pm < kPreRows ? s_T[pm] : 0;
   int8_t* vt = &VT[wave][0][0];
   int qs = 0;                                         // qsum: this lane's probabilities of row pm
-  for (int c0 = wave; c0 < ntile; c0 += 4 * kPreTiles) {
-    v4i_t vb[kPreTiles][HDP / 32];                    // V rows: lane takes row (lane & 31), half of the columns
+  for (int c0 = wave; c0 < ntile; c0 += NW * PT) {
+    // V rows: lane takes row (lane & 31); in pass p the columns p VTC + (lane / 32) VTC / 2 + 16 q
+    v4i_t vb[PT][NPASS][QP];
 #pragma unroll
-    for (int u = 0; u < kPreTiles; ++u) {
-      const uint32_t off = (uint32_t)(32 * (c0 + 4 * u) + lr) * kv_dim + g * HD + (lane >> 5) * (HDP / 2);
+    for (int u = 0; u < PT; ++u) {
+      const uint32_t off = (uint32_t)(32 * (c0 + NW * u) + lr) * kv_dim + g * HD + (lane >> 5) * (VTC / 2);
 #pragma unroll
-      for (int q = 0; q < HDP / 32; ++q) vb[u][q] = buffer_load16(vrs, off + 16 * q);
+      for (int p = 0; p < NPASS; ++p)
+#pragma unroll
+        for (int q = 0; q < QP; ++q) vb[u][p][q] = buffer_load16(vrs, off + p * VTC + 16 * q);
     }
 #pragma unroll
-    for (int u = 0; u < kPreTiles; ++u) {
-      const int ti = c0 + 4 * u;
+    for (int u = 0; u < PT; ++u) {
+      const int ti = c0 + NW * u;
       if (ti >= ntile) break;
-      // V tile transposed: VT[j][tt] for the 32 rows tt of the tile
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int q = 0; q < HDP / 32; ++q) {
-        const int jb = (lane >> 5) * (HDP / 2) + 16 * q;
-        const int w4[4] = {vb[u][q].x, vb[u][q].y, vb[u][q].z, vb[u][q].w};
-#pragma unroll
-        for (int b = 0; b < 16; ++b) vt[(jb + b) * 32 + lr] = (int8_t)(w4[b >> 2] >> (8 * (b & 3)));
-      }
-      __builtin_amdgcn_s_waitcnt(0xc07f);
-      __builtin_amdgcn_wave_barrier();
       // A: p of row pm, t = 32 ti + lk + 0..15
       int pw[4];
 #pragma unroll
@@ -923,10 +948,33 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
         pw[w] = pack_i8x4(bytes[0], bytes[1], bytes[2], bytes[3]);
       }
       const v4i_t pa = {pw[0], pw[1], pw[2], pw[3]};
+      // V tile transposed, VTC columns a pass: VT[j][tt] for the 32 rows tt. The four lanes of a quad
+      // hold four consecutive rows; two exchanges (lane ^ 1, lane ^ 2) with byte selects leave lane
+      // 4k + c holding column c of each 4-column group for the quad's rows, one word of VT.
 #pragma unroll
-      for (int jt = 0; jt < KS; ++jt) {
-        const v4i_t fb = *(const v4i_t*)&vt[(32 * jt + lr) * 32 + lk];
-        pv[jt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, fb, pv[jt], 0, 0, 0);
+      for (int p = 0; p < NPASS; ++p) {
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int q = 0; q < QP; ++q) {
+          const int w4[4] = {vb[u][p][q].x, vb[u][p][q].y, vb[u][p][q].z, vb[u][p][q].w};
+          const int jb = (lane >> 5) * (VTC / 2) + 16 * q;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t x = (uint32_t)w4[d];
+            const uint32_t y = (uint32_t)dpp_i<kDppXor1>((int)x);
+            const uint32_t s1 = __builtin_amdgcn_perm(y, x, (lane & 1) ? 0x03070105u : 0x06020400u);
+            const uint32_t y2 = (uint32_t)dpp_i<kDppXor2>((int)s1);
+            const uint32_t col = __builtin_amdgcn_perm(y2, s1, (lane & 2) ? 0x03020706u : 0x05040100u);
+            *(uint32_t*)&vt[(jb + 4 * d + (lane & 3)) * 32 + 4 * (lr >> 2)] = col;
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int jt = p * VTC / 32; jt < (p + 1) * VTC / 32; ++jt) {
+          const v4i_t fb = *(const v4i_t*)&vt[(32 * jt - p * VTC + lr) * 32 + lk];
+          pv[jt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, fb, pv[jt], 0, 0, 0);
+        }
       }
     }
   }
@@ -934,8 +982,8 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
     qs += __shfl_xor(qs, 32);
     if (lane < kPreRows) s_qs[wave][lane] = qs;
   }
-  __syncthreads();                                    // E is free: partial sums of the four waves
-  int* part = (int*)E;                                // [4][16][HDP]
+  __syncthreads();                                    // E is free: partial sums of the waves
+  int* part = (int*)E;                                // [NW][16][HDP]
 #pragma unroll
   for (int jt = 0; jt < KS; ++jt)
 #pragma unroll
@@ -947,11 +995,17 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   for (int k = tid; k < kPreRows * HD; k += kPreThreads) {
     const int m = k / HD, j = k % HD;
     if (s_T[m] == 0) continue;
-    const int sum = part[(0 * kPreRows + m) * HDP + j] + part[(1 * kPreRows + m) * HDP + j] +
-                    part[(2 * kPreRows + m) * HDP + j] + part[(3 * kPreRows + m) * HDP + j];
+    int sum = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) sum += part[(w * kPreRows + m) * HDP + j];
     if constexpr (OPT) {
       float o = (float)sum;
-      if (a.qsum) o = o * qsum_scale((s_qs[0][m] + s_qs[1][m]) + (s_qs[2][m] + s_qs[3][m]), tab);
+      if (a.qsum) {
+        int tot = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) tot += s_qs[w][m];
+        o = o * qsum_scale(tot, tab);
+      }
       a.att[(long long)(r0 + m) * a.att_stride + (long long)h * HD + j] =
           o * (a.ch_av ? a.ch_av[(long long)g * HD + j] : a.a_v);
     } else {
@@ -962,7 +1016,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
 
 // dynamic LDS bytes of k_attn_pre: 16 rows of scores / exps (also the partial sums afterwards)
 inline size_t attn_pre_lds_bytes(int S, int HDP) {
-  const size_t e = (size_t)kPreRows * pre_est(S) * 4, p = (size_t)4 * kPreRows * HDP * 4;
+  const size_t e = (size_t)kPreRows * pre_est(S) * 4, p = (size_t)kPreWaves * kPreRows * HDP * 4;
   return e > p ? e : p;
 }
 
