@@ -210,8 +210,8 @@ def main():
         return
     runs, fsim = [], []
     plan = [(C.TINY, 8, None, True), (C.TINY, 16, None, True), (C.TINY_GQA, 8, None, True),
-            (C.TINY_GQA, 16, None, False), (C.C1, 16, C.C1.prompt_len + C.C1.decode_steps, 3),
-            (C.C1, 8, 40, 0)]
+            (C.TINY_GQA, 16, None, False), (C.C1, 16, C.C1.prompt_len + C.C1.decode_steps, True),
+            (C.C1, 8, 40, True)]
     for cfg, D, steps, do_fsim in plan:
         kv = W.stored_kv_scales(cfg) if cfg.name in C.CONFIGS else W.calibrate_kv(cfg)
         steps = steps or cfg.prompt_len + cfg.decode_steps
