@@ -282,6 +282,77 @@ constexpr size_t kGemmDDeepLds = gemm_d_lds<128, 4>();
 // and the 256-row tiles' ring (3 x 48 KB)
 constexpr size_t kGemmDTallLds = gemm_d_lds<128, 3, 2 * kGT>();
 
+// The LDS epilogue of k_gemm_d. C (int32) of the 64-row band b is staged as ct[64][kEpiCS] (SwiGLU:
+// the W1 and the W3 sums, 64 output columns each, then the SFU tables); then row mr, columns
+// 4 c .. 4 c + 3 are finished by one thread.
+constexpr int kEpiCS = kGT + 4;                   // staged row stride (ints): 16-byte aligned rows
+template <int EPI, bool SPLIT, int BM>
+T2R_DEV void gemm_d_epilogue_vec(const GemmArgs& a, const v16i_t (&acc)[2][2], int8_t* lds, int m0, int n0, int z,
+                                 int wm, int wn, int lane, int tid) {
+  constexpr int NT = 2 * BM, NB = BM / 64;
+  constexpr int OC = EPI == EPI_SWIGLU ? kGT / 2 : kGT;          // output columns of the tile
+  constexpr int CS = EPI == EPI_SWIGLU ? OC + 4 : kEpiCS;
+  int* c1 = (int*)lds;                                            // [64][CS]
+  int* c3 = c1 + 64 * CS;                                         // SwiGLU: W3 sums [64][CS]
+  float* tab_lds = (float*)(c3 + (EPI == EPI_SWIGLU ? 64 * CS : 0));
+  const int lr = lane & 31, kh = lane >> 5;
+  __syncthreads();                                                // every wave is done with the ring
+  if constexpr (EPI == EPI_SWIGLU) {
+    v4f_t t4 = {0.f, 0.f, 0.f, 0.f};
+    if (tid < kSfuWords / 4) t4 = ((const v4f_t*)a.tab)[tid];
+    sfu_store(tab_lds, t4);
+  }
+  const int nbase = EPI == EPI_SWIGLU ? (n0 >> 1) : n0;           // first output column of the tile
+  for (int b = 0; b < NB; ++b) {
+    if (wm == b) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int mr = 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
+          if constexpr (EPI == EPI_SWIGLU) {
+            c1[mr * CS + wn * 32 + lr] = acc[i][0][r];
+            c3[mr * CS + wn * 32 + lr] = acc[i][1][r];
+          } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) c1[mr * CS + wn * 64 + j * 32 + lr] = acc[i][j][r];
+          }
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < 64 * (OC / 4); e += NT) {
+      const int mr = e / (OC / 4), nc = 4 * (e % (OC / 4));
+      const int m = m0 + 64 * b + mr, n = nbase + nc;
+      if (m < a.M && n < a.N) {                                   // (N % 4 == 0: all four columns)
+        const v4i_t v = *(const v4i_t*)&c1[mr * CS + nc];
+        if constexpr (SPLIT) {
+          *(v4i_t*)&a.part[((long long)z * a.M + m) * a.N + n] = v;
+        } else {
+          const float sx = a.s_x[m];
+          const v4f_t sw = *(const v4f_t*)&a.s_w[n];
+          v4f_t y;
+          if constexpr (EPI == EPI_SWIGLU) {
+            const v4i_t v3 = *(const v4i_t*)&c3[mr * CS + nc];
+            const v4f_t sw3 = *(const v4f_t*)&a.s_w3[n];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) y[q] = gate_mul(dequant(v[q], sw[q], sx), dequant(v3[q], sw3[q], sx), a.act, tab_lds);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) y[q] = dequant(v[q], sw[q], sx);
+            if constexpr (EPI == EPI_RESID) {
+              const v4f_t rv = *(const v4f_t*)&a.res[(long long)m * a.y_stride + n];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) y[q] = rv[q] + y[q];
+            }
+          }
+          *(v4f_t*)&a.y[(long long)m * a.y_stride + n] = y;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // BM: tile rows (128: four waves, 2 x 2; 256: eight waves, 4 x 2), always 128 columns.
 template <int EPI, bool SPLIT, int BKD, int NST, int BM = kGT>
 __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz) {
@@ -323,8 +394,11 @@ __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz
       src[j] = b_row<EPI>(a, n0, r, n, ok) + 16 * kc;
     }
   }
+  // Each workgroup walks its K range from a different slab (the int32 sums are exact in any order):
+  // the workgroups that share an A or B tile then do not request the same lines at the same time.
+  const int rot = nk > 0 ? (mt + 3 * nt) % nk : 0;
   auto issue = [&](int s, int stage) {
-    const long long k0 = (long long)min(s0 + s, nslab - 1) * BKD;
+    const long long k0 = (long long)(nk > 0 ? s0 + (min(s, nk - 1) + rot) % nk : min(s0, nslab - 1)) * BKD;
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       const int i = NI * wave + j;
@@ -370,6 +444,21 @@ __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz
     }
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): no DMA into LDS outlives the workgroup
+
+  // Epilogue through LDS (16-byte aligned operands, no int32 copy requested): the tile's int32 sums go
+  // to LDS a 64-row band at a time (written by the band's two waves, read back by every thread), and
+  // each thread then finishes four consecutive columns of a row with one 16-byte load per operand
+  // (scales, residual) and one 16-byte store, instead of the MFMA layout's 4-byte accesses.
+  {
+    const bool vec = a.acc_out == nullptr && a.N % 4 == 0 && a.y_stride % 4 == 0 &&
+                     ((uintptr_t)a.s_w & 15) == 0 && (EPI != EPI_SWIGLU || ((uintptr_t)a.s_w3 & 15) == 0) &&
+                     (SPLIT ? ((uintptr_t)a.part & 15) == 0 : ((uintptr_t)a.y & 15) == 0) &&
+                     (EPI != EPI_RESID || SPLIT || ((uintptr_t)a.res & 15) == 0);
+    if (vec) {
+      gemm_d_epilogue_vec<EPI, SPLIT, BM>(a, acc, lds, m0, n0, z, wm, wn, lane, tid);
+      return;
+    }
+  }
 
   // Epilogue. Lane holds C[m][n] for n = lane % 32 of each 32 x 32 tile, m = 8 (r / 4) + 4 (lane / 32)
   // + r % 4. Every load it needs (scales, residual, SFU table) is issued before its first store:
