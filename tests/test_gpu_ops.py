@@ -143,6 +143,30 @@ def test_linear_exact(env, N_, K, M):
     y2 = ops.linear(T(w), T(s_w), xin, T(s_x), residual=T(res if M > 1 else res[0]))
     want = (res + N.dequant(acc_want, s_w, s_x)).astype(F)
     assert np.array_equal(H(y2).reshape(M, N_).view(np.uint32), want.view(np.uint32))
+    y3 = ops.linear(T(w), T(s_w), xin, T(s_x))           # no int32 copy: the GEMM's staged epilogue
+    assert np.array_equal(H(y3).reshape(M, N_).view(np.uint32), N.dequant(acc_want, s_w, s_x).view(np.uint32))
+
+
+@pytest.mark.parametrize("N_,K,M", [(64, 256, 1), (64, 256, 40), (512, 2048, 300)])
+def test_linear_residual_signed_zeros(env, N_, K, M):
+    """Residual rows of -0 with products of +0 and of -0 (zero weight rows, negative scales): IEEE gives
+    -0 + +0 = +0 and -0 + -0 = -0, as NumPy's float32 does."""
+    torch, N, ops, T, H = env
+    rng = np.random.default_rng(N_ + M)
+    w = rng.integers(-127, 128, (N_, K)).astype(np.int8)
+    w[::3] = 0                                            # acc = 0: the product is +-0 by the scale's sign
+    s_w = rng.uniform(1e-4, 1e-2, N_).astype(F)
+    s_w[::2] *= -1
+    xq = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    s_x = rng.uniform(1e-3, 1e-1, M).astype(F)
+    res = rng.standard_normal((M, N_)).astype(F)
+    res[:, ::3] = -0.0
+    acc_want = xq.astype(np.int64) @ w.astype(np.int64).T
+    want = (res + N.dequant(acc_want, s_w, s_x)).astype(F)
+    assert (want.view(np.uint32) == 0x80000000).any() and ((want == 0) & (want.view(np.uint32) == 0)).any()
+    xin = T(xq) if M > 1 else T(xq[0])
+    got = ops.linear(T(w), T(s_w), xin, T(s_x), residual=T(res if M > 1 else res[0]))
+    assert np.array_equal(H(got).reshape(M, N_).view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("n", [16, 288, 2048, 8192])
