@@ -532,6 +532,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   constexpr int RM = R / NCHP;                   // rows a lane keeps per pass: i = j NCHP + c
   const int dummy = D * P + lane;                // per-lane LDS slot for stores that keep nothing
   float mloc = -__builtin_inff();
+  // row pos lies past the buffer range (its K and V chunks load as zero); its slot's dot product comes
+  // from the LDS copy of the new row, formed once
+  int dpos = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) dpos = __builtin_amdgcn_sdot4(kpos[w], qw[w], dpos, false);
   for (int pass = 0; pass < npass; ++pass) {
     const int base = pass * TS * R;
     if (pass > 0) {
@@ -541,11 +546,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     int dots[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const bool here = base + ts + TS * i == pos;
       int dot = 0;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) dot = __builtin_amdgcn_sdot4(here ? kpos[w] : kw[i][w], qw[w], dot, false);
-      dots[i] = dot;
+      for (int w = 0; w < 4; ++w) dot = __builtin_amdgcn_sdot4(kw[i][w], qw[w], dot, false);
+      dots[i] = base + ts + TS * i == pos ? dpos : dot;
     }
     // the slot group's partial sums, the DPP steps of all rows interleaved
     if (NCHP >= 2) {
@@ -616,11 +620,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int t = base + ts + TS * (i4 + u);
-        const bool here = t == pos;
         const float ev = sc[osum_index(min(t, T - 1), D, P)];
         pk[u] = t < T ? to_i8((ev * rr) * 127.0f) : 0;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) rw[u][w] = here ? vpos[w] : vw[i4 + u][w];
+        for (int w = 0; w < 4; ++w) rw[u][w] = vw[i4 + u][w];   // row pos: zero here, added below
       }
       if (OPT && c == 0) qs += (pk[0] + pk[1]) + (pk[2] + pk[3]);
       const int pp = pack_i8x4(pk[0], pk[1], pk[2], pk[3]);
@@ -632,6 +635,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
         for (int k = 0; k < 4; ++k) acc[4 * w + k] = __builtin_amdgcn_sdot4(col[k], pp, acc[4 * w + k], false);
       }
     }
+  }
+  // row pos's term, p(pos) times the new V row (from LDS), in the threads whose slot holds row pos
+  // (exact int32 either way)
+  if (ts == pos % TS && cok) {
+    const int ppos = to_i8((sc[osum_index(pos, D, P)] * rr) * 127.0f);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[4 * w + k] += ppos * (int)(int8_t)(vpos[w] >> (8 * k));
   }
   // ---- partial sums: lanes of a 16-lane row with the same slot rotate-and-add over the row-slice
   // bits, then one partial per row of lanes and wave meets in LDS
