@@ -601,7 +601,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   }
   __syncthreads();
   const float rr = s_r;
-  int qs = 0;                                    // qsum: the slot-0 lanes' probabilities (each row once)
+  // int8 probabilities, once per row (not once per slot lane), in the order P.V reads them: word
+  // (pass R / 4 + i / 4) TS + ts holds rows base + ts + TS (i - i % 4 + u), u = 0..3; +0 past T
+  int8_t* pq = (int8_t*)(dyn + D * P + 64);
+  int qs = 0;                                    // qsum: the probabilities of the rows this thread forms
+  for (int t = tid; t < npass * TS * R; t += kAttnThreads) {
+    const int ps = t / (TS * R), rem = t % (TS * R), i = rem / TS, tsl = rem % TS;
+    const int p8 = t < T ? to_i8((sc[osum_index(t, D, P)] * rr) * 127.0f) : 0;
+    if (OPT) qs += p8;
+    pq[((ps * (R / 4) + (i >> 2)) * TS + tsl) * 4 + (i & 3)] = (int8_t)p8;
+  }
+  __syncthreads();
 
   // ---- P.V over the thread's rows, four at a time: int8 p of the four rows against V transposed
   int acc[16];
@@ -616,17 +626,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 #pragma unroll
     for (int i4 = 0; i4 < R; i4 += 4) {
       if (base + TS * i4 >= T) break;
-      int pk[4], rw[4][4];
+      int rw[4][4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int t = base + ts + TS * (i4 + u);
-        const float ev = sc[osum_index(min(t, T - 1), D, P)];
-        pk[u] = t < T ? to_i8((ev * rr) * 127.0f) : 0;
+      for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int w = 0; w < 4; ++w) rw[u][w] = vw[i4 + u][w];   // row pos: zero here, added below
-      }
-      if (OPT && c == 0) qs += (pk[0] + pk[1]) + (pk[2] + pk[3]);
-      const int pp = pack_i8x4(pk[0], pk[1], pk[2], pk[3]);
+        for (int w = 0; w < 4; ++w) rw[u][w] = vw[i4 + u][w];     // row pos: zero here, added below
+      const int pp = ((const int*)pq)[(pass * (R / 4) + (i4 >> 2)) * TS + ts];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         int col[4];
@@ -1035,8 +1040,9 @@ inline size_t attn_pre_lds_bytes(int S, int HDP) {
 // dynamic LDS bytes of k_attn: the scores (lane-major, D * osum_stride(S, D) floats) and the int8
 // probabilities of S cache rows
 inline size_t attn_lds_bytes(int S, int D) { return (size_t)D * osum_stride(S, D) * 4 + (size_t)S; }
-// dynamic LDS bytes of k_attn_dec: the scores (lane-major) and one spare slot per lane
-inline size_t attn_dec_lds_bytes(int S, int D) { return ((size_t)D * osum_stride(S, D) + 64) * 4; }
+// dynamic LDS bytes of k_attn_dec: the scores (lane-major), one spare slot per lane, then the int8
+// probabilities of every row slot of the passes (S rounded up to a pass, <= S + 4096)
+inline size_t attn_dec_lds_bytes(int S, int D) { return ((size_t)D * osum_stride(S, D) + 64) * 4 + (size_t)S + 4096; }
 
 // ------------------------------------------------------------------ grouped decode attention
 // Decode attention of the G <= 4 query heads that share a KV head, split over G / GW workgroups per
