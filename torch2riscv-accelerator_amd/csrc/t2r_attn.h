@@ -564,12 +564,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < R; ++i) dots[i] += dpp_i<kDppHalfMirror>(dots[i]);
     }
+    // every lane of a slot group now holds its rows' sums; lane c keeps rows i = j NCHP + c
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const int t = base + ts + TS * i;
-      const float sv = ((float)dots[i] * sq) * a.a_k;
+    for (int j = 0; j < RM; ++j) {
+      int dk = dots[j * NCHP];
+#pragma unroll
+      for (int q = 1; q < NCHP; ++q) dk = c == q ? dots[j * NCHP + q] : dk;
+      const int t = base + ts + TS * (j * NCHP + c);
+      const float sv = ((float)dk * sq) * a.a_k;
       const bool ok = t < T;
-      sc[ok && c == (i & (NCHP - 1)) ? osum_index(t, D, P) : dummy] = sv;   // one lane per row keeps it
+      sc[ok ? osum_index(t, D, P) : dummy] = sv;
       mloc = nanmax(mloc, ok ? sv : -__builtin_inff());
     }
   }
