@@ -928,6 +928,41 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   }
   __syncthreads();
 
+  // ---- int8 probabilities p = to_i8(F(F(e r) 127)), once per (row, key), written over the exps:
+  // row i's bytes from byte ((4 i est + 15) & ~15) of E, zero from its T to the tiles' end. Keys go
+  // in blocks of 512: every thread reads its 16 exps of the block, then (after a barrier) writes their
+  // bytes, which land on exps of this block or of earlier ones, all read by then.
+  const int nkey = 32 * ntile;
+  {
+    const int i = tid >> 5, sub = tid & 31;
+    const float ri = s_r[i];
+    const int Ti = s_T[i];
+    const float* erow = E + i * est;
+    int8_t* prow = (int8_t*)E + (((long long)i * est * 4 + 15) & ~15LL);
+    int qsr = 0;                                      // qsum: the row's probabilities (exact)
+    for (int c0 = 0; c0 < nkey; c0 += 512) {
+      float e[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int t = c0 + sub + 32 * j;
+        e[j] = t < Ti ? erow[t] : 0.0f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int t = c0 + sub + 32 * j;
+        const int p8 = t < Ti ? to_i8((e[j] * ri) * 127.0f) : 0;
+        if (OPT) qsr += p8;
+        if (t < nkey) prow[t] = (int8_t)p8;
+      }
+    }
+    if (OPT && a.qsum) {                              // the row's 32 threads: one half-wave
+      qsr = wave_half_sum_i32(qsr);
+      if (sub == 0) s_qs[0][i] = qsr;
+    }
+  }
+  __syncthreads();
+
   // ---- P.V: per tile, int8 p of 16 t per lane (A) against V transposed (B), exact int32
   v16i_t pv[KS];
 #pragma unroll
@@ -935,10 +970,8 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) pv[jt][r] = 0;
   const int pm = lr;                                  // A row of this lane
-  const float rm = pm < kPreRows ? s_r[pm] : 0.0f;
-  const int Tm = pm < kPreRows ? s_T[pm] : 0;
+  const int8_t* pmrow = (const int8_t*)E + (((long long)min(pm, kPreRows - 1) * est * 4 + 15) & ~15LL);
   int8_t* vt = &VT[wave][0][0];
-  int qs = 0;                                         // qsum: this lane's probabilities of row pm
   for (int c0 = wave; c0 < ntile; c0 += NW * PT) {
     // V rows: lane takes row (lane & 31); in pass p the columns p VTC + (lane / 32) VTC / 2 + 16 q
     v4i_t vb[PT][NPASS][QP];
@@ -954,21 +987,8 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
     for (int u = 0; u < PT; ++u) {
       const int ti = c0 + NW * u;
       if (ti >= ntile) break;
-      // A: p of row pm, t = 32 ti + lk + 0..15
-      int pw[4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        int bytes[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int t = 32 * ti + lk + 4 * w + b;
-          const float e = E[min(pm, kPreRows - 1) * est + t];
-          bytes[b] = t < Tm ? to_i8((e * rm) * 127.0f) : 0;
-        }
-        if (OPT) qs += (bytes[0] + bytes[1]) + (bytes[2] + bytes[3]);
-        pw[w] = pack_i8x4(bytes[0], bytes[1], bytes[2], bytes[3]);
-      }
-      const v4i_t pa = {pw[0], pw[1], pw[2], pw[3]};
+      // A: p of row pm, t = 32 ti + lk + 0..15 (rows 16..31 of the tile zero)
+      const v4i_t pa = pm < kPreRows ? *(const v4i_t*)(pmrow + 32 * ti + lk) : v4i_t{0, 0, 0, 0};
       // V tile transposed, VTC columns a pass: VT[j][tt] for the 32 rows tt. The four lanes of a quad
       // hold four consecutive rows; two exchanges (lane ^ 1, lane ^ 2) with byte selects leave lane
       // 4k + c holding column c of each 4-column group for the quad's rows, one word of VT.
@@ -999,10 +1019,6 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
       }
     }
   }
-  if (OPT && a.qsum) {                                // (row pm: lanes pm and pm + 32 of every wave)
-    qs += __shfl_xor(qs, 32);
-    if (lane < kPreRows) s_qs[wave][lane] = qs;
-  }
   __syncthreads();                                    // E is free: partial sums of the waves
   int* part = (int*)E;                                // [NW][16][HDP]
 #pragma unroll
@@ -1021,12 +1037,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
     for (int w = 0; w < NW; ++w) sum += part[(w * kPreRows + m) * HDP + j];
     if constexpr (OPT) {
       float o = (float)sum;
-      if (a.qsum) {
-        int tot = 0;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) tot += s_qs[w][m];
-        o = o * qsum_scale(tot, tab);
-      }
+      if (a.qsum) o = o * qsum_scale(s_qs[0][m], tab);
       a.att[(long long)(r0 + m) * a.att_stride + (long long)h * HD + j] =
           o * (a.ch_av ? a.ch_av[(long long)g * HD + j] : a.a_v);
     } else {

@@ -329,6 +329,14 @@ T2R_DEV int wave_sum_i32(int v) {
   return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
          (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
+// every lane returns the sum over its half-wave (lanes 0-31 or 32-63)
+T2R_DEV int wave_half_sum_i32(int v) {
+  v += dpp_i<kDppXor1>(v);
+  v += dpp_i<kDppXor2>(v);
+  v += dpp_i<kDppHalfMirror>(v);
+  v += dpp_i<kDppMirror>(v);
+  return v + __shfl_xor(v, 16);
+}
 T2R_DEV float wave_max(float v) {
   v = nanmax(v, dpp_f<kDppXor1>(v));
   v = nanmax(v, dpp_f<kDppXor2>(v));
