@@ -771,7 +771,7 @@ int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0, int* defer
     if (a.K % 128) return gemm_d_launch<EPI, 64, 4>(a, st, z, defer_z);
     if constexpr (EPI == EPI_SWIGLU) {
       // 256-row tiles (eight waves) with a 3 x 48 KB ring: two slabs in flight, one workgroup per CU
-      if (a.M >= 2 * kGT) return gemm_d_launch<EPI, 128, 3, 2 * kGT>(a, st, z, defer_z);
+      if (a.M >= 2 * kGT && a.M <= 1024) return gemm_d_launch<EPI, 128, 3, 2 * kGT>(a, st, z, defer_z);
     }
     return nwg <= 256 ? gemm_d_launch<EPI, 128, 4>(a, st, z, defer_z) : gemm_d_launch<EPI, 128, 2>(a, st, z, defer_z);
   }
