@@ -439,11 +439,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   // unconditional: a branch around a load would make the compiler's wait counts path-dependent
   // (it then waits for every later load too); rows past pos read as zero
+  // (the V rows follow after the first barrier: nothing before P.V needs them, and the barriers up to
+  // P.V order LDS only, so they stay in flight meanwhile)
   v4i_t kw[R], vw[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) kw[i] = buffer_load16(krs, chunk_off(ts + TS * i));
-#pragma unroll
-  for (int i = 0; i < R; ++i) vw[i] = buffer_load16(vrs, chunk_off(ts + TS * i));
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- tables to LDS; wave 0: k (norm, RoPE), k / v to int8 (+ cache row); wave 1: q to int8.
@@ -515,6 +515,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     }
   }
   __syncthreads();
+#pragma unroll
+  for (int i = 0; i < R; ++i) vw[i] = buffer_load16(vrs, chunk_off(ts + TS * i));
 
   // ---- scores: slot c's partial dot products of the thread's rows, summed over the slot group
   float* sc = dyn;
@@ -579,7 +581,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   }
   mloc = wave_max(mloc);
   if (lane == 0) red[wave] = mloc;
-  __syncthreads();
+  lds_barrier();
   float m = red[0];
 #pragma unroll
   for (int w = 1; w < kAttnWaves; ++w) m = nanmax(m, red[w]);
@@ -597,13 +599,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
       sc[k] = t < T ? ev : 0.0f;
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {
     float ssum = 0.0f;
     if (lane < D) ssum = ordered_sum_t<false>(sc, T, D, P, lane);
     if (lane == 0) s_r = (OPT && a.qsum) ? 1.0f : sfu_recip(ssum, tab);   // qsum: to_i8(F(F(e * 1) * 127))
   }
-  __syncthreads();
+  lds_barrier();
   const float rr = s_r;
   // int8 probabilities, once per row (not once per slot lane), in the order P.V reads them: word
   // (pass R / 4 + i / 4) TS + ts holds rows base + ts + TS (i - i % 4 + u), u = 0..3; +0 past T
@@ -615,7 +617,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     if (OPT) qs += p8;
     pq[((ps * (R / 4) + (i >> 2)) * TS + tsl) * 4 + (i & 3)] = (int8_t)p8;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- P.V over the thread's rows, four at a time: int8 p of the four rows against V transposed
   int acc[16];

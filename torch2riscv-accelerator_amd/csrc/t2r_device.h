@@ -329,6 +329,15 @@ T2R_DEV int wave_sum_i32(int v) {
   return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
          (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
+// A workgroup barrier that orders LDS only: this wave's LDS accesses complete, then s_barrier. Unlike
+// __syncthreads it leaves the wave's global loads in flight (no wait on their counter).
+T2R_DEV void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // every lane returns the sum over its half-wave (lanes 0-31 or 32-63)
 T2R_DEV int wave_half_sum_i32(int v) {
   v += dpp_i<kDppXor1>(v);
