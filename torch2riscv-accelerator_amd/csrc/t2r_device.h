@@ -145,17 +145,21 @@ T2R_DEV float ldexp_norm(float y, int n) {
 // (frac & 0x1FFFF) / 2^17, exact
 T2R_DEV float frac17(uint32_t frac) { return (float)(int)(frac & 0x1FFFFu) * 0x1p-17f; }
 
-// EXP (llm/sfu.py:7-11, 69-82)
+// EXP (llm/sfu.py:7-11, 69-82). Wherever the final selects do not replace the result, -104 < x < 89,
+// so |t| < 151: floor(t) converts to int without saturation (and the clamp of n to [-300, 300] is a
+// no-op), f = t - floor(t) is exact and in [0, 1), and u = 64 f is exact and in [0, 64). The clamp of
+// t to [-160, 160] changes nothing there; it keeps the conversions defined (and the table index in
+// range) for the inputs whose result the selects replace: NaN and out-of-range x.
 T2R_DEV float sfu_exp(float xin, const float* tab = c_sfu) {
   const float x = ftz(vreg(xin));
   const float t = x * (float)1.4426950408889634;
-  const int n = floor_sat(t);
-  const float f = t - (float)n;
+  const float tf = floorf(fminf(fmaxf(t, -160.0f), 160.0f));
+  const float f = fminf(fmaxf(t, -160.0f), 160.0f) - tf;
   const float u = f * 64.0f;
-  const int i = min(max(floor_sat(u), 0), 63);
+  const int i = min(max((int)floorf(u), 0), 63);
   const float r = u - (float)i;
   const float y = tab[kSfuExpT + i] + r * tab[kSfuExpS + i];
-  float out = ldexp_norm(y, min(max(n, -300), 300));
+  float out = ldexp_norm(y, (int)tf);
   out = x <= -104.0f ? 0.0f : out;
   out = x >= 89.0f ? fv(kPInf) : out;
   return x != x ? fv(kQNaN) : out;
