@@ -202,13 +202,13 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
     dim3 pg(a.H, cdiv(rows, kPreRows));
     const size_t pl = attn_pre_lds_bytes(pre_cap(a), hdp);
     if (opt) {
-      if (hdp == 32) launch((k_attn_pre<32, true>), pg, dim3(kPreThreads), pl, st, a, rows);
-      else if (hdp == 64) launch((k_attn_pre<64, true>), pg, dim3(kPreThreads), pl, st, a, rows);
-      else launch((k_attn_pre<128, true>), pg, dim3(kPreThreads), pl, st, a, rows);
+      if (hdp == 32) launch((k_attn_pre<32, true>), pg, dim3(pre_threads(hdp)), pl, st, a, rows);
+      else if (hdp == 64) launch((k_attn_pre<64, true>), pg, dim3(pre_threads(hdp)), pl, st, a, rows);
+      else launch((k_attn_pre<128, true>), pg, dim3(pre_threads(hdp)), pl, st, a, rows);
     } else {
-      if (hdp == 32) launch((k_attn_pre<32>), pg, dim3(kPreThreads), pl, st, a, rows);
-      else if (hdp == 64) launch((k_attn_pre<64>), pg, dim3(kPreThreads), pl, st, a, rows);
-      else launch((k_attn_pre<128>), pg, dim3(kPreThreads), pl, st, a, rows);
+      if (hdp == 32) launch((k_attn_pre<32>), pg, dim3(pre_threads(hdp)), pl, st, a, rows);
+      else if (hdp == 64) launch((k_attn_pre<64>), pg, dim3(pre_threads(hdp)), pl, st, a, rows);
+      else launch((k_attn_pre<128>), pg, dim3(pre_threads(hdp)), pl, st, a, rows);
     }
   } else {
     if (c16) launch((k_attn<ATTN_ONLY, 16>), grid, block, lds, st, a);

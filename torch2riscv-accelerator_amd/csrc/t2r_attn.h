@@ -754,21 +754,23 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
 
 // ------------------------------------------------------------------ prefill attention
 // ATTN_ONLY for many rows at once (rows whose q is rotated and whose KV rows are in the cache), one
-// workgroup of eight waves per (query head, 16 consecutive rows). Scores and P.V run on the int8
+// workgroup of 8 or 16 waves per (query head, 16 consecutive rows). Scores and P.V run on the int8
 // matrix cores (v_mfma_i32_32x32x32_i8, query rows 16..31 of each tile zero): every lane feeds 16
 // consecutive k-bytes of its A row and of its B row, the same k for both, so each int32 is the exact
 // dot product. The softmax is per row and follows the decode numerics exactly:
-//  - the row maximum (order-free) and e = EXP(s - max) (+0 padding to a multiple of D), 32 threads
-//    per row, every element independent;
+//  - the row maximum (order-free) and e = EXP(s - max) (+0 padding to a multiple of D), 32 or 64
+//    threads per row, every element independent;
 //  - thread (row i, lane l < D) then adds the row's e[t], t = l, l + D, ... in order: the lane
 //    chain of the D-lane ordered sum; DPP pairs the D lanes, and RECIP gives r.
-// P.V packs to_i8(e r 127) of 16 t per lane against V transposed in LDS (wave-private tiles, 64
-// columns at a time).
+// P.V packs to_i8(e r 127) of 16 t per lane against V transposed in LDS (wave-private tiles, 32 or
+// 64 columns at a time).
 constexpr int kPreRows = 16;
-constexpr int kPreThreads = 512;
-constexpr int kPreWaves = kPreThreads / 64;
-constexpr int kPreTiles = 8;                  // 32-row cache tiles a wave loads at once
 constexpr size_t kPreMaxLds = 136 * 1024;     // dynamic LDS the kernels are set up for (of 160 KB per CU)
+// Threads of k_attn_pre: 1024 (16 waves; a wave per row in the softmax) at head dims over 64, where
+// the registers (<= 128 a lane) and long caches' score rows leave one workgroup per CU: twice the
+// waves per SIMD to hide the EXP's table reads and the phases' barriers. 512 (8 waves, half a wave
+// per row) at head dims <= 64, where two or more workgroups share a CU.
+__host__ __device__ constexpr int pre_threads(int HDP) { return HDP > 64 ? 1024 : 512; }
 
 // Row stride (floats) of the score / exp rows: at least S + 16, and 17 mod 64. The P.V pass reads one
 // key of all 16 rows per instruction (and, in lanes 32-63, the key 16 on): 32 distinct LDS banks.
@@ -776,21 +778,21 @@ constexpr size_t kPreMaxLds = 136 * 1024;     // dynamic LDS the kernels are set
 __host__ __device__ inline int pre_est(int S) { return ((S + 16 + 63) & ~63) + 17; }
 
 template <int HDP, bool OPT = false>   // head dim padded to a multiple of 32 (MFMA k-steps); OPT: HF options
-__global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
+__global__ __launch_bounds__(pre_threads(HDP)) void k_attn_pre(AttnArgs a, int M) {
+  constexpr int NT = pre_threads(HDP), NW = NT / 64;
+  constexpr int TPR = NT / kPreRows;           // softmax threads per row: 32 or 64, all in one wave
   constexpr int KS = HDP / 32;                 // k-steps of the score MFMA; column tiles of P.V
   constexpr int NV = HDP > 64 ? 2 : 1;
-  constexpr int NW = kPreWaves;
-  constexpr int VTC = HDP < 64 ? HDP : 64;     // V columns transposed per pass
-  constexpr int PT = kPreTiles / 2;             // tiles in flight per wave (registers: two workgroups per
-                                               // CU at head dim 64)
+  constexpr int VTC = NW > 8 ? 32 : (HDP < 64 ? HDP : 64);   // V columns transposed per pass (16 KB of VT)
+  constexpr int PT = NW > 8 ? 2 : 4;           // cache tiles in flight per wave (32 per workgroup)
   constexpr int NPASS = HDP / VTC, QP = VTC / 32;   // V transpose passes; 16-byte chunks a lane per pass
-  extern __shared__ __align__(16) float E[];   // [16][est] scores, then exps; then partial P.V sums
+  extern __shared__ __align__(16) float E[];   // [16][est] scores, then exps; then the P.V sums
   __shared__ __align__(16) float tab[kSfuWords];
   __shared__ __align__(16) int8_t Q8[kPreRows][HDP];
   __shared__ __align__(16) int8_t VT[NW][VTC][32];
   __shared__ float s_sq[kPreRows], s_r[kPreRows];
   __shared__ int s_T[kPreRows];
-  __shared__ int s_qs[NW][kPreRows];
+  __shared__ int s_qs[kPreRows];
   // row blocks in reverse: a causal prompt's later rows attend to more positions, and the blocks
   // dispatched first should be the longest (the short ones then fill in behind them)
   const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kPreRows, tid = threadIdx.x;
@@ -801,7 +803,7 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = ((const v4f_t*)a.tab)[tid];
   __syncthreads();
 
-  // ---- q of the block's rows to int8 (one wave per 2 rows); rows without a valid position: T = 0
+  // ---- q of the block's rows to int8 (a wave per row or per 2 rows); rows without a valid position: T = 0
   for (int i = wave; i < kPreRows; i += NW) {
     const int r = min(r0 + i, M - 1);
     const int pos = a.pos[r];
@@ -868,17 +870,17 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   }
   __syncthreads();
 
-  // ---- per row (32 threads of one wave each): max, e = EXP(s - max) with +0 padding to a multiple
+  // ---- per row (TPR threads of one wave each): max, e = EXP(s - max) with +0 padding to a multiple
   // of D; then the D-lane ordered sum and RECIP
   {
-    const int i = tid >> 5, sub = tid & 31;
+    const int i = tid / TPR, sub = tid % TPR;
     const int T = s_T[i];
     float* row = E + i * est;
     float mx = -__builtin_inff();
-    for (int t = sub; t < T; t += 32 * 8) {
+    for (int t = sub; t < T; t += TPR * 8) {
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = t + 32 * j < T ? row[t + 32 * j] : -__builtin_inff();
+      for (int j = 0; j < 8; ++j) v[j] = t + TPR * j < T ? row[t + TPR * j] : -__builtin_inff();
 #pragma unroll
       for (int j = 0; j < 8; ++j) mx = nanmax(mx, v[j]);
     }
@@ -886,17 +888,18 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
     mx = nanmax(mx, dpp_f<kDppXor2>(mx));
     mx = nanmax(mx, dpp_f<kDppHalfMirror>(mx));
     mx = nanmax(mx, dpp_f<kDppMirror>(mx));
-    mx = nanmax(mx, __shfl_xor(mx, 16));           // the row's two 16-lane halves
+    mx = nanmax(mx, __shfl_xor(mx, 16));           // the row's 16-lane rows
+    if (TPR == 64) mx = nanmax(mx, __shfl_xor(mx, 32));
     const int groups = T > 0 ? (T + D - 1) / D : 0, Tpad = groups * D;
-    for (int t = sub; t < Tpad; t += 32 * 4) {
+    for (int t = sub; t < Tpad; t += TPR * 4) {
       float e[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) e[j] = t + 32 * j < T ? row[t + 32 * j] : 0.0f;
+      for (int j = 0; j < 4; ++j) e[j] = t + TPR * j < T ? row[t + TPR * j] : 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) e[j] = t + 32 * j < T ? sfu_exp(e[j] - mx, tab) : 0.0f;
+      for (int j = 0; j < 4; ++j) e[j] = t + TPR * j < T ? sfu_exp(e[j] - mx, tab) : 0.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (t + 32 * j < Tpad) row[t + 32 * j] = e[j];
+        if (t + TPR * j < Tpad) row[t + TPR * j] = e[j];
     }
     // the row's exps were written by this wave's lanes: wait for them, then the lane chains
     __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0)
@@ -932,35 +935,36 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
 
   // ---- int8 probabilities p = to_i8(F(F(e r) 127)), once per (row, key), written over the exps:
   // row i's bytes from byte ((4 i est + 15) & ~15) of E, zero from its T to the tiles' end. Keys go
-  // in blocks of 512: every thread reads its 16 exps of the block, then (after a barrier) writes their
-  // bytes, which land on exps of this block or of earlier ones, all read by then.
+  // in blocks of 512: every thread reads its 512 / TPR exps of the block, then (after a barrier)
+  // writes their bytes, which land on exps of this block or of earlier ones, all read by then.
   const int nkey = 32 * ntile;
   {
-    const int i = tid >> 5, sub = tid & 31;
+    constexpr int PE = 512 / TPR;
+    const int i = tid / TPR, sub = tid % TPR;
     const float ri = s_r[i];
     const int Ti = s_T[i];
     const float* erow = E + i * est;
     int8_t* prow = (int8_t*)E + (((long long)i * est * 4 + 15) & ~15LL);
     int qsr = 0;                                      // qsum: the row's probabilities (exact)
     for (int c0 = 0; c0 < nkey; c0 += 512) {
-      float e[16];
+      float e[PE];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int t = c0 + sub + 32 * j;
+      for (int j = 0; j < PE; ++j) {
+        const int t = c0 + sub + TPR * j;
         e[j] = t < Ti ? erow[t] : 0.0f;
       }
       __syncthreads();
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int t = c0 + sub + 32 * j;
+      for (int j = 0; j < PE; ++j) {
+        const int t = c0 + sub + TPR * j;
         const int p8 = t < Ti ? to_i8((e[j] * ri) * 127.0f) : 0;
         if (OPT) qsr += p8;
         if (t < nkey) prow[t] = (int8_t)p8;
       }
     }
-    if (OPT && a.qsum) {                              // the row's 32 threads: one half-wave
-      qsr = wave_half_sum_i32(qsr);
-      if (sub == 0) s_qs[0][i] = qsr;
+    if (OPT && a.qsum) {                              // the row's TPR threads: half a wave or a wave
+      qsr = TPR == 64 ? wave_sum_i32(qsr) : wave_half_sum_i32(qsr);
+      if (sub == 0) s_qs[i] = qsr;
     }
   }
   __syncthreads();
@@ -1021,25 +1025,27 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
       }
     }
   }
-  __syncthreads();                                    // E is free: partial sums of the waves
-  int* part = (int*)E;                                // [NW][16][HDP]
+  // E is free: the waves' P.V partials are added into sums [16][HDP] by LDS integer atomics (int32
+  // adds: exact in any order; |sum| <= 127 * 127 * T < 2^31)
+  __syncthreads();
+  int* part = (int*)E;
+  for (int k = tid; k < kPreRows * HDP; k += NT) part[k] = 0;
+  __syncthreads();
 #pragma unroll
   for (int jt = 0; jt < KS; ++jt)
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int m = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-      part[(wave * kPreRows + m) * HDP + 32 * jt + lr] = pv[jt][r];
+      atomicAdd(&part[m * HDP + 32 * jt + lr], pv[jt][r]);
     }
   __syncthreads();
-  for (int k = tid; k < kPreRows * HD; k += kPreThreads) {
+  for (int k = tid; k < kPreRows * HD; k += NT) {
     const int m = k / HD, j = k % HD;
     if (s_T[m] == 0) continue;
-    int sum = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) sum += part[(w * kPreRows + m) * HDP + j];
+    const int sum = part[m * HDP + j];
     if constexpr (OPT) {
       float o = (float)sum;
-      if (a.qsum) o = o * qsum_scale(s_qs[0][m], tab);
+      if (a.qsum) o = o * qsum_scale(s_qs[m], tab);
       a.att[(long long)(r0 + m) * a.att_stride + (long long)h * HD + j] =
           o * (a.ch_av ? a.ch_av[(long long)g * HD + j] : a.a_v);
     } else {
@@ -1048,9 +1054,9 @@ __global__ __launch_bounds__(kPreThreads) void k_attn_pre(AttnArgs a, int M) {
   }
 }
 
-// dynamic LDS bytes of k_attn_pre: 16 rows of scores / exps (also the partial sums afterwards)
+// dynamic LDS bytes of k_attn_pre: 16 rows of scores / exps (also the P.V sums afterwards)
 inline size_t attn_pre_lds_bytes(int S, int HDP) {
-  const size_t e = (size_t)kPreRows * pre_est(S) * 4, p = (size_t)kPreWaves * kPreRows * HDP * 4;
+  const size_t e = (size_t)kPreRows * pre_est(S) * 4, p = (size_t)kPreRows * HDP * 4;
   return e > p ? e : p;
 }
 
