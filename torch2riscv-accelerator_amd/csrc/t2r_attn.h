@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
   const int Tpad = ((T + D - 1) / D) * D;
   for (int t = tid; t < Tpad; t += kAttnThreads) {
     const int i = osum_index(t, D, P);
-    sc[i] = t < T ? sfu_exp(sc[i] - m) : 0.0f;
+    sc[i] = t < T ? sfu_exp_np(sc[i] - m) : 0.0f;
   }
   __syncthreads();
   if (wave == 0) {
@@ -595,7 +595,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     for (int j = 0; j < RM; ++j) {
       const int t = base + ts + TS * (j * NCHP + c);
       const int k = t < Tpad ? osum_index(t, D, P) : dummy;
-      const float ev = sfu_exp(sc[k] - m, tab);
+      const float ev = sfu_exp_np(sc[k] - m, tab);
       sc[k] = t < T ? ev : 0.0f;
     }
   }
@@ -784,15 +784,19 @@ __global__ __launch_bounds__(pre_threads(HDP)) void k_attn_pre(AttnArgs a, int M
   constexpr int KS = HDP / 32;                 // k-steps of the score MFMA; column tiles of P.V
   constexpr int NV = HDP > 64 ? 2 : 1;
   constexpr int VTC = NW > 8 ? 32 : (HDP < 64 ? HDP : 64);   // V columns transposed per pass (16 KB of VT)
-  constexpr int PT = NW > 8 ? 2 : 4;           // cache tiles in flight per wave (32 per workgroup)
+  // cache tiles in flight per wave: the score pass 4 (all 64 tiles of a 2048-key block at 16 waves);
+  // P.V at 16 waves 8 (a wave takes one 32-column quarter of V: 16 bytes a lane per tile; 16 spill),
+  // else 4
+  constexpr int PTS = 4, PTV = NW > 8 ? 8 : 4;
   constexpr int NPASS = HDP / VTC, QP = VTC / 32;   // V transpose passes; 16-byte chunks a lane per pass
   extern __shared__ __align__(16) float E[];   // [16][est] scores, then exps; then the P.V sums
   __shared__ __align__(16) float tab[kSfuWords];
   __shared__ __align__(16) int8_t Q8[kPreRows][HDP];
   __shared__ __align__(16) int8_t VT[NW][VTC][32];
-  __shared__ float s_sq[kPreRows], s_r[kPreRows];
+  __shared__ float s_sq[kPreRows];
   __shared__ int s_T[kPreRows];
   __shared__ int s_qs[kPreRows];
+  __shared__ float s_mx[NW][kPreRows];          // each wave's maximum of each row's scores
   // row blocks in reverse: a causal prompt's later rows attend to more positions, and the blocks
   // dispatched first should be the longest (the short ones then fill in behind them)
   const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kPreRows, tid = threadIdx.x;
@@ -839,21 +843,29 @@ __global__ __launch_bounds__(pre_threads(HDP)) void k_attn_pre(AttnArgs a, int M
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc, (uint32_t)S * kv_dim);
   const int lr = lane & 31, lk = (lane >> 5) * 16;
 
-  // ---- scores of the wave's tiles (t = 32 tile + n), PT tiles' K rows in flight at a time
+  // ---- scores of the wave's tiles (t = 32 tile + n), PTS tiles' K rows in flight at a time. A tile
+  // past the block's last gets an offset outside the buffer: zeros, with no memory access. Each lane
+  // also keeps the maximum of the scores it writes of each of its 8 rows (keys t < T of the row;
+  // smax: order-free, NaN winning).
+  constexpr uint32_t kNoRow = 0x80000000u;      // beyond every cache (S kv_dim < 2^31)
   v4i_t qa[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
     qa[ks] = lr < kPreRows ? *(const v4i_t*)&Q8[lr][32 * ks + lk] : v4i_t{0, 0, 0, 0};
-  for (int c0 = wave; c0 < ntile; c0 += NW * PT) {
-    v4i_t kb[PT][KS];
+  float rmx[8];
 #pragma unroll
-    for (int u = 0; u < PT; ++u) {
-      const uint32_t off = (uint32_t)(32 * (c0 + NW * u) + lr) * kv_dim + g * HD + lk;
+  for (int r = 0; r < 8; ++r) rmx[r] = -__builtin_inff();
+  for (int c0 = wave; c0 < ntile; c0 += NW * PTS) {
+    v4i_t kb[PTS][KS];
+#pragma unroll
+    for (int u = 0; u < PTS; ++u) {
+      const int ti = c0 + NW * u;
+      const uint32_t off = ti < ntile ? (uint32_t)(32 * ti + lr) * kv_dim + g * HD + lk : kNoRow;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kb[u][ks] = buffer_load16(krs, off + 32 * ks);
     }
 #pragma unroll
-    for (int u = 0; u < PT; ++u) {
+    for (int u = 0; u < PTS; ++u) {
       const int ti = c0 + NW * u;
       if (ti >= ntile) break;
       v16i_t acc;
@@ -864,39 +876,42 @@ __global__ __launch_bounds__(pre_threads(HDP)) void k_attn_pre(AttnArgs a, int M
 #pragma unroll
       for (int r = 0; r < 8; ++r) {                   // output rows m < 16
         const int m = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        E[m * est + 32 * ti + lr] = ((float)acc[r] * s_sq[m]) * a.a_k;
+        const float sv = ((float)acc[r] * s_sq[m]) * a.a_k;
+        E[m * est + 32 * ti + lr] = sv;
+        rmx[r] = smax(rmx[r], 32 * ti + lr < s_T[m] ? sv : -__builtin_inff());
       }
     }
   }
+  // the wave's maximum of each row: over the 32 lanes of a half (which share their 8 rows)
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    float v = rmx[r];
+    v = smax(v, dpp_f<kDppXor1>(v));
+    v = smax(v, dpp_f<kDppXor2>(v));
+    v = smax(v, dpp_f<kDppHalfMirror>(v));
+    v = smax(v, dpp_f<kDppMirror>(v));
+    v = smax(v, __shfl_xor(v, 16));
+    if (lr == 0) s_mx[wave][(r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)] = v;
+  }
   __syncthreads();
 
-  // ---- per row (TPR threads of one wave each): max, e = EXP(s - max) with +0 padding to a multiple
-  // of D; then the D-lane ordered sum and RECIP
+  // ---- per row (TPR threads of one wave each): the row maximum from the waves' maxima, e = EXP(s -
+  // max) (s <= max: the softmax form of EXP) with +0 padding to a multiple of D; the D-lane ordered
+  // sum and RECIP; then the row's int8 probabilities
   {
     const int i = tid / TPR, sub = tid % TPR;
     const int T = s_T[i];
     float* row = E + i * est;
-    float mx = -__builtin_inff();
-    for (int t = sub; t < T; t += TPR * 8) {
-      float v[8];
+    float mx = s_mx[0][i];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = t + TPR * j < T ? row[t + TPR * j] : -__builtin_inff();
-#pragma unroll
-      for (int j = 0; j < 8; ++j) mx = nanmax(mx, v[j]);
-    }
-    mx = nanmax(mx, dpp_f<kDppXor1>(mx));
-    mx = nanmax(mx, dpp_f<kDppXor2>(mx));
-    mx = nanmax(mx, dpp_f<kDppHalfMirror>(mx));
-    mx = nanmax(mx, dpp_f<kDppMirror>(mx));
-    mx = nanmax(mx, __shfl_xor(mx, 16));           // the row's 16-lane rows
-    if (TPR == 64) mx = nanmax(mx, __shfl_xor(mx, 32));
+    for (int w = 1; w < NW; ++w) mx = smax(mx, s_mx[w][i]);
     const int groups = T > 0 ? (T + D - 1) / D : 0, Tpad = groups * D;
     for (int t = sub; t < Tpad; t += TPR * 4) {
       float e[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) e[j] = t + TPR * j < T ? row[t + TPR * j] : 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) e[j] = t + TPR * j < T ? sfu_exp(e[j] - mx, tab) : 0.0f;
+      for (int j = 0; j < 4; ++j) e[j] = t + TPR * j < T ? sfu_exp_np(e[j] - mx, tab) : 0.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (t + TPR * j < Tpad) row[t + TPR * j] = e[j];
@@ -929,37 +944,33 @@ __global__ __launch_bounds__(pre_threads(HDP)) void k_attn_pre(AttnArgs a, int M
     if (D > 4 && (sub & 7) == 0) acc = acc + o;
     o = dpp_f<0x108>(acc);
     if (D > 8 && (sub & 15) == 0) acc = acc + o;
-    if (sub == 0) s_r[i] = (OPT && a.qsum) ? 1.0f : sfu_recip(acc, tab);   // qsum: to_i8(F(F(e * 1) * 127))
-  }
-  __syncthreads();
+    // r (qsum: 1, so p = to_i8(F(F(e * 1) * 127))) from the row's first lane to all of its lanes
+    const uint32_t rb = fb((OPT && a.qsum) ? 1.0f : sfu_recip(acc, tab));
+    const float ri = fv((uint32_t)(TPR == 64 || lane < 32 ? __builtin_amdgcn_readlane((int)rb, 0)
+                                                          : __builtin_amdgcn_readlane((int)rb, 32)));
 
-  // ---- int8 probabilities p = to_i8(F(F(e r) 127)), once per (row, key), written over the exps:
-  // row i's bytes from byte ((4 i est + 15) & ~15) of E, zero from its T to the tiles' end. Keys go
-  // in blocks of 512: every thread reads its 512 / TPR exps of the block, then (after a barrier)
-  // writes their bytes, which land on exps of this block or of earlier ones, all read by then.
-  const int nkey = 32 * ntile;
-  {
+    // int8 probabilities p = to_i8(F(F(e r) 127)), once per (row, key), written over the row's own
+    // exps: bytes from byte ((4 i est + 15) & ~15) of E (inside row i's floats), zero from T to the
+    // tiles' end. Keys go in blocks of 512: the row's lanes read their exps of the block, then write
+    // the bytes, which land on exps of this block or of earlier ones: the row is this wave's alone,
+    // and a wave's LDS accesses complete in order, so no workgroup barrier is needed.
     constexpr int PE = 512 / TPR;
-    const int i = tid / TPR, sub = tid % TPR;
-    const float ri = s_r[i];
-    const int Ti = s_T[i];
-    const float* erow = E + i * est;
     int8_t* prow = (int8_t*)E + (((long long)i * est * 4 + 15) & ~15LL);
     int qsr = 0;                                      // qsum: the row's probabilities (exact)
-    for (int c0 = 0; c0 < nkey; c0 += 512) {
+    for (int c0 = 0; c0 < 32 * ntile; c0 += 512) {
       float e[PE];
 #pragma unroll
       for (int j = 0; j < PE; ++j) {
         const int t = c0 + sub + TPR * j;
-        e[j] = t < Ti ? erow[t] : 0.0f;
+        e[j] = t < T ? row[t] : 0.0f;
       }
-      __syncthreads();
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int j = 0; j < PE; ++j) {
         const int t = c0 + sub + TPR * j;
-        const int p8 = t < Ti ? to_i8((e[j] * ri) * 127.0f) : 0;
+        const int p8 = t < T ? to_i8((e[j] * ri) * 127.0f) : 0;
         if (OPT) qsr += p8;
-        if (t < nkey) prow[t] = (int8_t)p8;
+        if (t < 32 * ntile) prow[t] = (int8_t)p8;
       }
     }
     if (OPT && a.qsum) {                              // the row's TPR threads: half a wave or a wave
@@ -970,74 +981,116 @@ __global__ __launch_bounds__(pre_threads(HDP)) void k_attn_pre(AttnArgs a, int M
   __syncthreads();
 
   // ---- P.V: per tile, int8 p of 16 t per lane (A) against V transposed (B), exact int32
-  v16i_t pv[KS];
-#pragma unroll
-  for (int jt = 0; jt < KS; ++jt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) pv[jt][r] = 0;
   const int pm = lr;                                  // A row of this lane
   const int8_t* pmrow = (const int8_t*)E + (((long long)min(pm, kPreRows - 1) * est * 4 + 15) & ~15LL);
   int8_t* vt = &VT[wave][0][0];
-  for (int c0 = wave; c0 < ntile; c0 += NW * PT) {
-    // V rows: lane takes row (lane & 31); in pass p the columns p VTC + (lane / 32) VTC / 2 + 16 q
-    v4i_t vb[PT][NPASS][QP];
+  // V tile transposed, 32 x 16 bytes (lane: row lr, 16 columns from jb) into VT[j][tt] for the 32 rows
+  // tt. The four lanes of a quad hold four consecutive rows; two exchanges (lane ^ 1, lane ^ 2) with
+  // byte selects leave lane 4k + c holding column c of each 4-column group for the quad's rows, one
+  // word of VT.
+  auto v_transpose = [&](const v4i_t v, int jb) {
+    const int w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int u = 0; u < PT; ++u) {
-      const uint32_t off = (uint32_t)(32 * (c0 + NW * u) + lr) * kv_dim + g * HD + (lane >> 5) * (VTC / 2);
-#pragma unroll
-      for (int p = 0; p < NPASS; ++p)
-#pragma unroll
-        for (int q = 0; q < QP; ++q) vb[u][p][q] = buffer_load16(vrs, off + p * VTC + 16 * q);
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t x = (uint32_t)w4[d];
+      const uint32_t y = (uint32_t)dpp_i<kDppXor1>((int)x);
+      const uint32_t s1 = __builtin_amdgcn_perm(y, x, (lane & 1) ? 0x03070105u : 0x06020400u);
+      const uint32_t y2 = (uint32_t)dpp_i<kDppXor2>((int)s1);
+      const uint32_t col = __builtin_amdgcn_perm(y2, s1, (lane & 2) ? 0x03020706u : 0x05040100u);
+      *(uint32_t*)&vt[(jb + 4 * d + (lane & 3)) * 32 + 4 * (lr >> 2)] = col;
     }
+  };
+  int* part = (int*)E;
+  if constexpr (NW > 8) {
+    // a wave per (32-column quarter q of V, tile group tg): the quarter's 32 x 32 bytes of each of the
+    // group's tiles, up to PTV tiles in flight
+    constexpr int NG = NW / KS;                       // tile groups (KS = 4 at these head dims)
+    const int q = wave % KS, tg = wave / KS;
+    v16i_t pv;
 #pragma unroll
-    for (int u = 0; u < PT; ++u) {
-      const int ti = c0 + NW * u;
-      if (ti >= ntile) break;
-      // A: p of row pm, t = 32 ti + lk + 0..15 (rows 16..31 of the tile zero)
-      const v4i_t pa = pm < kPreRows ? *(const v4i_t*)(pmrow + 32 * ti + lk) : v4i_t{0, 0, 0, 0};
-      // V tile transposed, VTC columns a pass: VT[j][tt] for the 32 rows tt. The four lanes of a quad
-      // hold four consecutive rows; two exchanges (lane ^ 1, lane ^ 2) with byte selects leave lane
-      // 4k + c holding column c of each 4-column group for the quad's rows, one word of VT.
+    for (int r = 0; r < 16; ++r) pv[r] = 0;
+    for (int c0 = tg; tg < NG && c0 < ntile; c0 += NG * PTV) {
+      v4i_t vb[PTV];
 #pragma unroll
-      for (int p = 0; p < NPASS; ++p) {
+      for (int u = 0; u < PTV; ++u) {
+        const int ti = c0 + NG * u;
+        vb[u] = buffer_load16(vrs, ti < ntile ? (uint32_t)(32 * ti + lr) * kv_dim + g * HD + 32 * q + lk : kNoRow);
+      }
+#pragma unroll
+      for (int u = 0; u < PTV; ++u) {
+        const int ti = c0 + NG * u;
+        if (ti >= ntile) break;
+        // A: p of row pm, t = 32 ti + lk + 0..15 (rows 16..31 of the tile zero)
+        const v4i_t pa = pm < kPreRows ? *(const v4i_t*)(pmrow + 32 * ti + lk) : v4i_t{0, 0, 0, 0};
         __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int q = 0; q < QP; ++q) {
-          const int w4[4] = {vb[u][p][q].x, vb[u][p][q].y, vb[u][p][q].z, vb[u][p][q].w};
-          const int jb = (lane >> 5) * (VTC / 2) + 16 * q;
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const uint32_t x = (uint32_t)w4[d];
-            const uint32_t y = (uint32_t)dpp_i<kDppXor1>((int)x);
-            const uint32_t s1 = __builtin_amdgcn_perm(y, x, (lane & 1) ? 0x03070105u : 0x06020400u);
-            const uint32_t y2 = (uint32_t)dpp_i<kDppXor2>((int)s1);
-            const uint32_t col = __builtin_amdgcn_perm(y2, s1, (lane & 2) ? 0x03020706u : 0x05040100u);
-            *(uint32_t*)&vt[(jb + 4 * d + (lane & 3)) * 32 + 4 * (lr >> 2)] = col;
-          }
-        }
+        v_transpose(vb[u], lk);
         __builtin_amdgcn_s_waitcnt(0xc07f);
         __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int jt = p * VTC / 32; jt < (p + 1) * VTC / 32; ++jt) {
-          const v4i_t fb = *(const v4i_t*)&vt[(32 * jt - p * VTC + lr) * 32 + lk];
-          pv[jt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, fb, pv[jt], 0, 0, 0);
-        }
+        const v4i_t fb = *(const v4i_t*)&vt[lr * 32 + lk];
+        pv = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, fb, pv, 0, 0, 0);
       }
     }
-  }
-  // E is free: the waves' P.V partials are added into sums [16][HDP] by LDS integer atomics (int32
-  // adds: exact in any order; |sum| <= 127 * 127 * T < 2^31)
-  __syncthreads();
-  int* part = (int*)E;
-  for (int k = tid; k < kPreRows * HDP; k += NT) part[k] = 0;
-  __syncthreads();
-#pragma unroll
-  for (int jt = 0; jt < KS; ++jt)
+    // E is free: the waves' P.V partials are added into sums [16][HDP] by LDS integer atomics (int32
+    // adds: exact in any order; |sum| <= 127 * 127 * T < 2^31)
+    __syncthreads();
+    for (int k = tid; k < kPreRows * HDP; k += NT) part[k] = 0;
+    __syncthreads();
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const int m = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-      atomicAdd(&part[m * HDP + 32 * jt + lr], pv[jt][r]);
+      if (tg < NG) atomicAdd(&part[m * HDP + 32 * q + lr], pv[r]);
     }
+  } else {
+    v16i_t pv[KS];
+#pragma unroll
+    for (int jt = 0; jt < KS; ++jt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pv[jt][r] = 0;
+    for (int c0 = wave; c0 < ntile; c0 += NW * PTV) {
+      // V rows: lane takes row (lane & 31); in pass p the columns p VTC + (lane / 32) VTC / 2 + 16 q
+      v4i_t vb[PTV][NPASS][QP];
+#pragma unroll
+      for (int u = 0; u < PTV; ++u) {
+        const int ti = c0 + NW * u;
+        const uint32_t off = ti < ntile ? (uint32_t)(32 * ti + lr) * kv_dim + g * HD + (lane >> 5) * (VTC / 2) : kNoRow;
+#pragma unroll
+        for (int p = 0; p < NPASS; ++p)
+#pragma unroll
+          for (int q = 0; q < QP; ++q) vb[u][p][q] = buffer_load16(vrs, off + p * VTC + 16 * q);
+      }
+#pragma unroll
+      for (int u = 0; u < PTV; ++u) {
+        const int ti = c0 + NW * u;
+        if (ti >= ntile) break;
+        const v4i_t pa = pm < kPreRows ? *(const v4i_t*)(pmrow + 32 * ti + lk) : v4i_t{0, 0, 0, 0};
+#pragma unroll
+        for (int p = 0; p < NPASS; ++p) {
+          __builtin_amdgcn_wave_barrier();
+#pragma unroll
+          for (int q = 0; q < QP; ++q) v_transpose(vb[u][p][q], (lane >> 5) * (VTC / 2) + 16 * q);
+          __builtin_amdgcn_s_waitcnt(0xc07f);
+          __builtin_amdgcn_wave_barrier();
+#pragma unroll
+          for (int jt = p * VTC / 32; jt < (p + 1) * VTC / 32; ++jt) {
+            const v4i_t fb = *(const v4i_t*)&vt[(32 * jt - p * VTC + lr) * 32 + lk];
+            pv[jt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, fb, pv[jt], 0, 0, 0);
+          }
+        }
+      }
+    }
+    // E is free: the waves' P.V partials are added into sums [16][HDP] by LDS integer atomics (int32
+    // adds: exact in any order; |sum| <= 127 * 127 * T < 2^31)
+    __syncthreads();
+    for (int k = tid; k < kPreRows * HDP; k += NT) part[k] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int jt = 0; jt < KS; ++jt)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int m = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        atomicAdd(&part[m * HDP + 32 * jt + lr], pv[jt][r]);
+      }
+  }
   __syncthreads();
   for (int k = tid; k < kPreRows * HD; k += NT) {
     const int m = k / HD, j = k % HD;
@@ -1331,7 +1384,7 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
 #pragma unroll
     for (int h = 0; h < GW; ++h) sv[h] = dyn[(h < GH ? h : 0) * SH + k];
 #pragma unroll
-    for (int h = 0; h < GW; ++h) ev[h] = sfu_exp(sv[h] - mh[h], tab);
+    for (int h = 0; h < GW; ++h) ev[h] = sfu_exp_np(sv[h] - mh[h], tab);
 #pragma unroll
     for (int h = 0; h < GW; ++h)
       if (h < GH) dyn[h * SH + k] = t < T ? ev[h] : 0.0f;

@@ -413,6 +413,9 @@ __global__ void k_sfu_check(int fn, unsigned long long first, unsigned long long
     uint32_t a, b;
     if (fn == 0) {
       a = fb(sfu_exp(v)); b = fb(seq::sfu_exp(v, c_sfu));
+    } else if (fn == 3) {                       // the softmax form, on its domain (x <= 0, NaN)
+      if (v > 0.0f) continue;
+      a = fb(sfu_exp_np(v)); b = fb(seq::sfu_exp(v, c_sfu));
     } else if (fn == 1) {
       a = fb(sfu_recip(v)); b = fb(seq::sfu_recip(v, c_sfu));
     } else {
