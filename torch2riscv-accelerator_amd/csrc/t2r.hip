@@ -752,7 +752,7 @@ int t2r_sfu(int fn, const uint32_t* x, uint32_t* y, int64_t n, void* stream) {
 }
 
 int t2r_sfu_check(int fn, uint64_t first, uint64_t count, uint32_t* out, void* stream) {
-  if (fn < 0 || fn > 3 || !out || first > 0xFFFFFFFFull || count > 0x100000000ull - first) return T2R_EINVAL;
+  if (fn < 0 || fn > 4 || !out || first > 0xFFFFFFFFull || count > 0x100000000ull - first) return T2R_EINVAL;
   T2R_INIT();
   launch(k_sfu_check_init, dim3(1), dim3(64), 0, S(stream), out);
   if (count > 0) launch(k_sfu_check, dim3(8192), dim3(256), 0, S(stream), fn, (unsigned long long)first,

@@ -416,6 +416,9 @@ __global__ void k_sfu_check(int fn, unsigned long long first, unsigned long long
     } else if (fn == 3) {                       // the softmax form, on its domain (x <= 0, NaN)
       if (v > 0.0f) continue;
       a = fb(sfu_exp_np(v)); b = fb(seq::sfu_exp(v, c_sfu));
+    } else if (fn == 4) {                       // the gate form, on its domain (x >= 1, NaN)
+      if (v < 1.0f) continue;
+      a = fb(sfu_recip_ge1(v)); b = fb(seq::sfu_recip(v, c_sfu));
     } else if (fn == 1) {
       a = fb(sfu_recip(v)); b = fb(seq::sfu_recip(v, c_sfu));
     } else {
