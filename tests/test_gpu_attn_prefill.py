@@ -102,6 +102,31 @@ def test_attention_exp_underflow(env, H_, Hk, hd, S):
         assert np.array_equal(dec[i].view(np.uint32), want[i].view(np.uint32)), f"decode row {i}"
 
 
+@pytest.mark.parametrize("H_,Hk,hd,S", [(32, 8, 64, 512), (16, 8, 128, 512)])
+def test_attention_special_scores(env, H_, Hk, hd, S):
+    """Rows whose q holds NaN or +-inf (NaN scores: every EXP NaN, every probability 0) beside finite
+    rows, through the prefill kernel (eight and sixteen waves: the row maximum folded into the score
+    pass, the softmax form of EXP) and the decode op, against the oracle (np.max: NaN propagates)."""
+    torch, N, ops, T, H = env
+    rng = np.random.default_rng(11 * hd + H_)
+    kc, vc = caches(rng, S, Hk * hd)
+    M = 20
+    pos = np.arange(S - M, S, dtype=np.int32)
+    q = (rng.standard_normal((M, H_ * hd)) * 2).astype(F)
+    q[2, 5] = np.nan                                  # head 0 of row 2
+    q[7, hd + 1] = np.inf                             # head 1 of row 7
+    q[11, :] = -np.inf                                # every head of row 11
+    q[15, 3 * hd:4 * hd] = np.nan                     # a whole head of row 15
+    a_k, a_v = F(0.5 / np.sqrt(hd)), F(0.03 / 127)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = [N.attention(q[i], kc[:p + 1], vc[:p + 1], H_, Hk, a_k, a_v, 16) for i, p in enumerate(pos)]
+    pre = H(ops.attention_prefill(T(q), T(kc), T(vc), T(pos), H_, Hk, a_k, a_v, 16))
+    dec = H(ops.attention(T(q), T(kc), T(vc), T(pos), H_, Hk, a_k, a_v, 16))
+    for i in range(M):
+        assert np.array_equal(pre[i].view(np.uint32), want[i].view(np.uint32)), f"prefill row {i}"
+        assert np.array_equal(dec[i].view(np.uint32), want[i].view(np.uint32)), f"decode row {i}"
+
+
 @pytest.mark.parametrize("name", ["c4-llama3.2-1b", "c2-smollm2-135m", "c3-qwen3-0.6b"])
 def test_model_exp_underflow(name):
     """The fused decode attention (k_attn_dec), the grouped batched kernel (k_attn_gqa) and the prefill
