@@ -318,9 +318,9 @@ long long carve(Model* m, char* base, int M) {
   m->msx = c.take<float>(M);
   m->status = c.take<int32_t>(1);
   m->pos_rows = c.take<int32_t>(M);
-  // split-K partial sums of the prefill linears: 4 splits of up to 512 rows of the widest
-  // STORE / RESID output
-  m->part_rows = M < 512 ? M : 512;
+  // split-K partial sums of the prefill linears: 4 splits of up to 2048 rows of the widest
+  // STORE / RESID output (C3's 2032-row prompt: 133 MB)
+  m->part_rows = M < 2048 ? M : 2048;
   m->part = c.take<int32_t>(4LL * m->part_rows * (m->qkv_dim > d.dim ? m->qkv_dim : d.dim));
   return c.off;
 }
