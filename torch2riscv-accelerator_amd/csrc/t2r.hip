@@ -634,16 +634,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     ra.a.x = m->x; ra.a.x_stride = d.dim; ra.a.g = d.rms_ffn + L_dim; ra.a.inv_n = inv_d; ra.a.eps = d.eps;
     ra.a.D = d.D; ra.a.N = E; ra.a.K = d.dim; ra.a.xq_out = m->mxq; ra.a.xq_stride = d.dim; ra.a.sx_out = m->msx;
     ra.k = k; ra.ids = m->ids; ra.wts = m->wts;
-    {
-      ProfScope p(m, T2R_PROF_ROUTE, st);
-      if (!gemv_operands_ok<PRO_NORM_QUANT, EPI_STORE>(ra.a) || d.dim % d.D) return T2R_ESHAPE;
-      const int nc = cdiv(d.dim, 1024);
-      if (nc <= 1) launch(k_moe_route<1>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
-      else if (nc <= 2) launch(k_moe_route<2>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
-      else if (nc <= 4) launch(k_moe_route<4>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
-      else launch(k_moe_route<8>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
-      if ((rc = launched())) return rc;
-    }
+    if (!gemv_operands_ok<PRO_NORM_QUANT, EPI_STORE>(ra.a) || d.dim % d.D) return T2R_ESHAPE;
     // expert gate / up of the k selected experts (rows j * Fe + n of the selected tables)
     a = gemv_args();
     a.w = d.wg + (long long)l * E * Fe * d.dim; a.s_w = d.s_wg + (long long)l * E * Fe;
@@ -651,7 +642,26 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     a.xq = m->mxq; a.xq_stride = d.dim; a.s_x = m->msx;
     a.ids = m->ids; a.rows_per_id = Fe; a.ids_stride = k;
     a.N = k * Fe; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows; a.act = d.ffn_act;
-    {
+    if (d.dim <= 1024 && k <= 8) {
+      // the router fused into the gate / up GEMV: every block routes its row, then its tiles
+      MoeUpArgs mu;
+      mu.r = ra;
+      mu.up = a;
+      const GemvShape g = gemv_shape<1>(a.N);
+      ProfScope p(m, T2R_PROF_FFN_UP, st);
+      if (g.ru >= 4) launch((k_moe_up<1, 4>), dim3(g.blocks, rows), dim3(kGemvThreads), 0, st, mu);
+      else if (g.ru == 2) launch((k_moe_up<1, 2>), dim3(g.blocks, rows), dim3(kGemvThreads), 0, st, mu);
+      else launch((k_moe_up<1, 1>), dim3(g.blocks, rows), dim3(kGemvThreads), 0, st, mu);
+      if ((rc = launched())) return rc;
+    } else {
+      {
+        ProfScope p(m, T2R_PROF_ROUTE, st);
+        const int nc = cdiv(d.dim, 1024);
+        if (nc <= 2) launch(k_moe_route<2>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+        else if (nc <= 4) launch(k_moe_route<4>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+        else launch(k_moe_route<8>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+        if ((rc = launched())) return rc;
+      }
       ProfScope p(m, T2R_PROF_FFN_UP, st);
       if ((rc = gemv_launch<PRO_XQ, EPI_SWIGLU>(a, rows, st))) return rc;
     }

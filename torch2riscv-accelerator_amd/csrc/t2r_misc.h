@@ -263,6 +263,131 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_route(RouteArgs ra) {
   if (wave == 0) route_topk(sc, a.N, ra.k, a.D, lane, ra.ids + row * ra.k, ra.wts + row * ra.k, ev, tab_lds);
 }
 
+// The router fused with the selected experts' gate / up GEMV (rows on grid y): every block repeats
+// its row's routing (the router's staged prologue, the E scores, top-k and weights: the same bits in
+// every block, with the same numerics as k_moe_route) and then computes its waves' tiles of the k Fe
+// selected W1 / W3 rows with the SwiGLU gate (k_gemv's int8-input path: the tile rows through the ids
+// in LDS). One launch instead of the router's single block followed by the GEMV, whose weight
+// requests had to wait for the router kernel to end. Block 0 of the row writes the ids and weights
+// for the down projections (and the int8 activations when xq_out is set).
+struct MoeUpArgs {
+  RouteArgs r;                // the router (r.a: x, g, inv_n, eps, D, w / s_w with N = E, K = dim, tab)
+  GemvArgs up;                // gate / up: w, s_w, w3, s_w3, N = k Fe, K = dim, y, y_stride, act, rows_per_id = Fe
+};
+template <int NCB, int RU>
+__global__ __launch_bounds__(kGemvThreads) void k_moe_up(MoeUpArgs m) {
+  constexpr int NT = kGemvThreads, kWaves = NT / 64, kPerWave = 64 / kWaves;   // E <= 64 over the waves
+  __shared__ __align__(16) int8_t xq_lds[NCB * 1024];
+  __shared__ __align__(16) float xf_lds[kOsumLds];
+  __shared__ __align__(16) float tab_lds[kSfuWords];
+  __shared__ float red[64];
+  __shared__ float sc[64];
+  __shared__ float ev[16];
+  __shared__ int32_t ids_l[16];
+  __shared__ float wts_l[16];
+  const GemvArgs& ra = m.r.a;
+  const GemvArgs& a = m.up;
+  const int row = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int k = m.r.k, Fe = a.rows_per_id, N = a.N, K = a.K;
+  // ---- routing (k_moe_route's steps)
+  XStage<PRO_NORM_QUANT, EPI_STORE, NCB, NT> st;
+  stage_load(st, ra, row);
+  __builtin_amdgcn_sched_barrier(0);
+  const int col0 = lane * 16;
+  int4 w0[kPerWave];
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const int e = min(wave + kWaves * i, ra.N - 1);
+    w0[i] = load_nt16(ra.w + (long long)e * ra.K + min(col0, ra.K - 16));
+  }
+  const float sw_r = ra.s_w[min(lane, ra.N - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  const float s_x = stage_finish(st, ra, row, xq_lds, xf_lds, tab_lds, red);
+  if (ra.xq_out && blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < ra.K; i += NT) ra.xq_out[row * ra.xq_stride + i] = xq_lds[i];
+    if (threadIdx.x == 0) ra.sx_out[row] = s_x;
+  }
+  const int4 x0 = col0 < ra.K ? *(const int4*)(xq_lds + col0) : make_int4(0, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const int e = wave + kWaves * i;
+    if (e >= ra.N) break;
+    int acc = dot16(w0[i], x0, 0);
+    for (int col = col0 + 1024; col < ra.K; col += 1024)
+      acc = dot16(load_nt16(ra.w + (long long)e * ra.K + col), *(const int4*)(xq_lds + col), acc);
+    acc = wave_sum_i32(acc);
+    const float s_e = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw_r), e));
+    if (lane == 0) sc[e] = dequant(acc, s_e, s_x);
+  }
+  __syncthreads();
+  if (wave == 0) route_topk(sc, ra.N, k, ra.D, lane, ids_l, wts_l, ev, tab_lds);
+  __syncthreads();
+  if (blockIdx.x == 0 && threadIdx.x < k) {
+    m.r.ids[row * k + threadIdx.x] = ids_l[threadIdx.x];
+    m.r.wts[row * k + threadIdx.x] = wts_l[threadIdx.x];
+  }
+  // ---- the gate / up rows of the selected experts: tile row r reads weight row ids[r / Fe] Fe + r % Fe
+  const int nwaves = gridDim.x * (NT / 64);
+  int r0 = (blockIdx.x * (NT / 64) + wave) * RU;
+  WTile<EPI_SWIGLU, NCB, RU> t;
+  auto tile = [&](int rb) {
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const int rc = min(rb + u, N - 1), j = rc / Fe;
+      const long long wr = (long long)ids_l[j] * Fe + (rc - j * Fe);
+#pragma unroll
+      for (int c = 0; c < NCB; ++c) {
+        const int col = min(lane * 16 + c * 1024, K - 16);
+        t.w[u][c] = load_nt16(a.w + wr * K + col);
+        t.w3[u][c] = load_nt16(a.w3 + wr * K + col);
+      }
+      t.sw[u] = a.s_w[wr];
+      t.sw3[u] = a.s_w3[wr];
+    }
+  };
+  tile(r0);
+  int4 xr[NCB];
+#pragma unroll
+  for (int c = 0; c < NCB; ++c) {
+    const int col = lane * 16 + c * 1024;
+    xr[c] = col < K ? *(const int4*)(xq_lds + col) : make_int4(0, 0, 0, 0);
+  }
+  float* y = a.y + row * a.y_stride;
+  for (; r0 < N; r0 += nwaves * RU) {
+    int acc[RU], acc3[RU];
+    float sw[RU], sw3[RU];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      acc[u] = 0;
+      acc3[u] = 0;
+#pragma unroll
+      for (int c = 0; c < NCB; ++c) {
+        acc[u] = dot16(t.w[u][c], xr[c], acc[u]);
+        acc3[u] = dot16(t.w3[u][c], xr[c], acc3[u]);
+      }
+      sw[u] = t.sw[u];
+      sw3[u] = t.sw3[u];
+    }
+    if (r0 + nwaves * RU < N) tile(r0 + nwaves * RU);
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      acc[u] = wave_sum_i32(acc[u]);
+      acc3[u] = wave_sum_i32(acc3[u]);
+    }
+    if (lane < RU) {                                  // lane u finishes row r0 + u
+      int ac = acc[0], ac3 = acc3[0];
+      float w1s = sw[0], w3s = sw3[0];
+#pragma unroll
+      for (int u = 1; u < RU; ++u)
+        if (lane == u) {
+          ac = acc[u]; ac3 = acc3[u]; w1s = sw[u]; w3s = sw3[u];
+        }
+      const int r = r0 + lane;
+      if (r < N) y[r] = gate_mul(dequant(ac, w1s, s_x), dequant(ac3, w3s, s_x), a.act, tab_lds);
+    }
+  }
+}
+
 // top-k + weights from given scores (the op-level ABI)
 __global__ __launch_bounds__(64) void k_route_scores(const float* scores, int E, int k, int D, int32_t* ids, float* wts) {
   __shared__ float sc[64];
