@@ -247,8 +247,9 @@ int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* position
                      int8_t* v_caches, int64_t cache_stride, float* logits, int32_t* next_tokens, void* stream);
 
 /* The model's status word (the reference's per-list status, llm/runtime.py:116-119): bit 0 a token
- * outside [0, vocab) was embedded (row 0 read instead). Waits for the device; clear != 0 then zeroes
- * the word. */
+ * outside [0, vocab) was embedded (row 0 read instead); bit 1 a bounded wait between the workgroups of
+ * a head's decode attention ran out (its output is then not to be trusted). Waits for the device;
+ * clear != 0 then zeroes the word. */
 int t2r_model_status(void* model, int32_t* out, int clear);
 
 /* Kernel timing of a resident model with HIP events on the launch stream (the GPU counterpart of

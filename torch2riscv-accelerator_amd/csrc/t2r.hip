@@ -175,7 +175,11 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   if (mode == ATTN_FUSED && a.tab != nullptr && a.hd % 16 == 0 &&
       (a.hd == 16 || a.hd == 32 || a.hd == 48 || a.hd == 64 || a.hd == 128)) {
     const size_t dl = attn_dec_lds_bytes(a.S, a.D);
-    if (opt) {
+    if (a.nsplit > 1 && rows == 1 && a.hd == 128 && a.sp_s && a.sp_o && a.sp_sync) {
+      const dim3 gs(a.H, a.nsplit);
+      if (opt) launch((k_attn_dec<8, true, true>), gs, block, dl, st, a);
+      else launch((k_attn_dec<8, false, true>), gs, block, dl, st, a);
+    } else if (opt) {
       switch (a.hd / 16) {
         case 1: launch((k_attn_dec<1, true>), grid, block, dl, st, a); break;
         case 2: launch((k_attn_dec<2, true>), grid, block, dl, st, a); break;
@@ -246,6 +250,11 @@ struct Model {
   int8_t* mxq;
   float* msx;
   int32_t* status;
+  // batch-1 decode attention split over workgroups per head: published scores [H, S], P.V sums
+  // [H, kMaxHd] and arrival counters [H, 2] (the last two zero between launches)
+  float* sp_s;
+  int32_t* sp_o;
+  uint32_t* sp_sync;
   // batched decode (t2r_decode_batch): the caches of the step's sequences, kv_rs bytes apart
   int8_t* kcb = nullptr;
   int8_t* vcb = nullptr;
@@ -318,6 +327,9 @@ long long carve(Model* m, char* base, int M) {
   m->msx = c.take<float>(M);
   m->status = c.take<int32_t>(1);
   m->pos_rows = c.take<int32_t>(M);
+  m->sp_s = c.take<float>((long long)d.heads * d.seq_len);
+  m->sp_o = c.take<int32_t>((long long)d.heads * kMaxHd);
+  m->sp_sync = c.take<uint32_t>(2LL * d.heads);
   // split-K partial sums of the prefill linears: 4 splits of up to 2048 rows of the widest
   // STORE / RESID output (C3's 2032-row prompt: 133 MB)
   m->part_rows = M < 2048 ? M : 2048;
@@ -525,6 +537,12 @@ AttnArgs layer_attn_args(Model* m, int l, const int32_t* pos, int mode) {
   at.att = m->att; at.att_stride = m->q_dim;
   at.tab = sfu_table_ptr();
   at.qsum = d.attn_qsum;
+  // batch-1 decode at head dim 128 over caches of more than 512 rows: each head's keys over 4
+  // workgroups (k_attn_dec's SPLIT form); at most 256 workgroups, so all of them are resident at once
+  if (mode == RUN_DECODE && d.head_dim == 128 && d.seq_len > 512 && d.heads * 4 <= 256) {
+    at.nsplit = 4;
+    at.sp_s = m->sp_s; at.sp_o = m->sp_o; at.sp_sync = m->sp_sync; at.sp_status = m->status;
+  }
   if (m->kv_flags[l]) {
     const float* ch = d.kv_channel + (long long)l * 4 * m->kv_dim;   // s_k, 1/s_k, 1/s_v, a_v
     if (m->kv_flags[l] & 1) { at.ch_sk = ch; at.ch_isk = ch + m->kv_dim; }
@@ -706,8 +724,12 @@ int model_init(Model* m, const t2r_model_desc& dv) {
   model_dims(m);
   if (carve(m, nullptr, desc->max_rows) > desc->workspace_bytes) return T2R_ENOMEM;
   carve(m, (char*)desc->workspace, desc->max_rows);
-  // the status word starts clear
-  if (hipMemset(m->status, 0, sizeof(int32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return T2R_EHIP;
+  // the status word, the split attention's sums and counters start clear
+  if (hipMemset(m->status, 0, sizeof(int32_t)) != hipSuccess ||
+      hipMemset(m->sp_o, 0, sizeof(int32_t) * (size_t)desc->heads * kMaxHd) != hipSuccess ||
+      hipMemset(m->sp_sync, 0, sizeof(uint32_t) * 2 * (size_t)desc->heads) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess)
+    return T2R_EHIP;
   std::memcpy(m->kvc, desc->kv_consts, sizeof(float) * 4 * desc->layers);
   for (int l = 0; l < desc->layers; ++l) m->kv_flags[l] = desc->kv_channel_flags ? desc->kv_channel_flags[l] : 0;
   m->d.kv_consts = nullptr;

@@ -68,7 +68,29 @@ struct AttnArgs {
   const float* ch_isk;       //   and 1 / s_k for the cache row
   const float* ch_isv;       // V per channel [kv_dim]: 1 / s_v for the cache row
   const float* ch_av;        //   and a_v per output channel
+  // batch-1 decode with a head's keys split over nsplit workgroups (grid y; k_attn_dec's SPLIT form,
+  // nsplit > 1): the scores published [H, S], the P.V sums [H, kMaxHd] (int32) and arrival counters
+  // [H, 2] (both zero between launches: the last workgroup of a head clears them), the status word
+  // (bit 1: a bounded wait ran out)
+  float* sp_s;
+  int32_t* sp_o;
+  uint32_t* sp_sync;
+  int32_t* sp_status;
+  int nsplit;
 };
+
+// A bounded wait for *p >= want at device scope (one lane polls); on running out it sets bit 1 of
+// *status and returns, so every workgroup reaches its end whatever happens.
+T2R_DEV void split_wait(uint32_t* p, uint32_t want, int32_t* status) {
+  for (int it = 0; it < (1 << 20); ++it) {
+    if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= want) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  if (status) atomicOr(status, 2);
+}
 
 inline bool attn_opt(const AttnArgs& a) { return a.qsum || a.ch_sk || a.ch_isk || a.ch_isv || a.ch_av; }
 
@@ -362,7 +384,15 @@ T2R_DEV int slot_group_sum(int v) {
   return v;
 }
 
-template <int NCH, bool OPT = false>   // 16-byte chunks per head row: hd = 16 NCH; OPT: the HF options
+// SPLIT (batch-1 decode of long caches): grid y splits a head's keys, workgroup j taking passes
+// j, j + n, ... (n = min(nsplit, passes); the others end at once). One CU streams a head's K and V
+// at most ~95 GB/s (522 KB at head dim 128 and T = 2048), so more CUs per head shorten that part.
+// Each split publishes its scores with device-coherent stores and arrives once; after one bounded
+// wait every split reads all T scores and forms the max, the EXPs, the ordered sum and RECIP itself
+// (the same bits in each), then the probabilities and P.V of its own passes; the P.V sums meet as
+// exact int32 device atomics, and the head's last split to arrive writes the output and clears the
+// sums and counters for the next launch.
+template <int NCH, bool OPT = false, bool SPLIT = false>   // 16-byte chunks per head row: hd = 16 NCH; OPT: the HF options
 __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   constexpr int HD = 16 * NCH;
   constexpr int NCHP = NCH <= 1 ? 1 : (NCH <= 2 ? 2 : (NCH <= 4 ? 4 : 8));
@@ -379,8 +409,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   __shared__ float red[16];
   __shared__ float s_sq, s_r;
   __shared__ int s_qs[kAttnWaves];
+  __shared__ int s_last;
 
-  const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  const int h = blockIdx.x, row = SPLIT ? 0 : blockIdx.y, tid = threadIdx.x;
+  const int sj = SPLIT ? blockIdx.y : 0;         // this workgroup's split
   const int lane = tid & 63, wave = tid >> 6;
   const int G = a.H / a.Hk, g = h / G, S = a.S;
   a.kc += row * a.kv_row_stride;                 // this row's sequence cache
@@ -390,6 +422,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   const int pos = a.pos[row];
   if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
   const int T = pos + 1;
+  // SPLIT: splits past the number of passes end here (all of a launch's workgroups agree on it)
+  const int nsp = SPLIT ? min(a.nsplit, (T + TS * R - 1) / (TS * R)) : 1;
+  if (SPLIT && sj >= nsp) return;
   const float* qkv = a.qkv + row * a.qkv_stride;
   const int c = tid & (NCHP - 1), ts = tid / NCHP;
   const bool cok = c < NCH;
@@ -443,7 +478,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   // P.V order LDS only, so they stay in flight meanwhile)
   v4i_t kw[R], vw[R];
 #pragma unroll
-  for (int i = 0; i < R; ++i) kw[i] = buffer_load16(krs, chunk_off(ts + TS * i));
+  for (int i = 0; i < R; ++i) kw[i] = buffer_load16(krs, chunk_off(sj * TS * R + ts + TS * i));
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- tables to LDS; wave 0: k (norm, RoPE), k / v to int8 (+ cache row); wave 1: q to int8.
@@ -489,7 +524,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
         if (j < HD) {
           kq8[j] = kb;
           vq8[j] = vb8;
-          if (h % G == 0) {
+          if (h % G == 0 && sj == 0) {
             a.kc[crow + j] = kb;
             a.vc[crow + j] = vb8;
           }
@@ -516,7 +551,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < R; ++i) vw[i] = buffer_load16(vrs, chunk_off(ts + TS * i));
+  for (int i = 0; i < R; ++i) vw[i] = buffer_load16(vrs, chunk_off(sj * TS * R + ts + TS * i));
 
   // ---- scores: slot c's partial dot products of the thread's rows, summed over the slot group
   float* sc = dyn;
@@ -539,9 +574,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   int dpos = 0;
 #pragma unroll
   for (int w = 0; w < 4; ++w) dpos = __builtin_amdgcn_sdot4(kpos[w], qw[w], dpos, false);
-  for (int pass = 0; pass < npass; ++pass) {
+  for (int pass = sj; pass < npass; pass += nsp) {
     const int base = pass * TS * R;
-    if (pass > 0) {
+    if (pass > sj) {
 #pragma unroll
       for (int i = 0; i < R; ++i) kw[i] = buffer_load16(krs, chunk_off(base + ts + TS * i));
     }
@@ -577,6 +612,35 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
       const bool ok = t < T;
       sc[ok ? osum_index(t, D, P) : dummy] = sv;
       mloc = nanmax(mloc, ok ? sv : -__builtin_inff());
+      if (SPLIT && ok) __hip_atomic_store(a.sp_s + (long long)h * S + t, sv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if constexpr (SPLIT) {
+    // every split's scores published (this workgroup's stores done at the barrier), then all T of
+    // them into sc from the published copy (the own ones read back unchanged); the max over them
+    __syncthreads();
+    uint32_t* arrive = a.sp_sync + 2 * h;
+    if (tid == 0) {
+      __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      split_wait(arrive, (uint32_t)nsp, a.sp_status);
+    }
+    __syncthreads();
+    mloc = -__builtin_inff();
+    const float* pub = a.sp_s + (long long)h * S;
+    for (int t0 = 0; t0 < T; t0 += 4 * kAttnThreads) {   // four loads in flight per thread
+      float sv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        sv[u] = __hip_atomic_load(pub + min(t0 + u * kAttnThreads + tid, T - 1), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = t0 + u * kAttnThreads + tid;
+        if (t < T) {
+          sc[osum_index(t, D, P)] = sv[u];
+          mloc = nanmax(mloc, sv[u]);
+        }
+      }
     }
   }
   mloc = wave_max(mloc);
@@ -587,16 +651,25 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   for (int w = 1; w < kAttnWaves; ++w) m = nanmax(m, red[w]);
 
   // ---- e = EXP(s - m) by the row's keeping lane (+0 padding to a multiple of D), ordered sum, RECIP
+  // (four of the lane's rows loaded ahead of their EXPs and stores: distinct LDS words, or the dummy)
   const int Tpad = ((T + D - 1) / D) * D;
-  const int epass = (Tpad + TS * R - 1) / (TS * R);
-  for (int pass = 0; pass < epass; ++pass) {
-    const int base = pass * TS * R;
+  const int erows = ((Tpad + TS * R - 1) / (TS * R)) * RM;
+  for (int q0 = 0; q0 < erows; q0 += 4) {
+    int kk[4];
+    float sv[4];
+    bool live[4];
 #pragma unroll
-    for (int j = 0; j < RM; ++j) {
-      const int t = base + ts + TS * (j * NCHP + c);
-      const int k = t < Tpad ? osum_index(t, D, P) : dummy;
-      const float ev = sfu_exp_np(sc[k] - m, tab);
-      sc[k] = t < T ? ev : 0.0f;
+    for (int u = 0; u < 4; ++u) {
+      const int q = q0 + u, j = q % RM;
+      const int t = (q / RM) * TS * R + ts + TS * (j * NCHP + c);
+      kk[u] = q < erows && t < Tpad ? osum_index(t, D, P) : dummy;
+      live[u] = q < erows && t < T;
+      sv[u] = sc[kk[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float ev = sfu_exp_np(sv[u] - m, tab);
+      sc[kk[u]] = live[u] ? ev : 0.0f;
     }
   }
   lds_barrier();
@@ -609,13 +682,34 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   const float rr = s_r;
   // int8 probabilities, once per row (not once per slot lane), in the order P.V reads them: word
   // (pass R / 4 + i / 4) TS + ts holds rows base + ts + TS (i - i % 4 + u), u = 0..3; +0 past T
+  // (SPLIT: the split's own passes, or all of them for qsum's total; four rows' loads ahead)
   int8_t* pq = (int8_t*)(dyn + D * P + 64);
   int qs = 0;                                    // qsum: the probabilities of the rows this thread forms
-  for (int t = tid; t < npass * TS * R; t += kAttnThreads) {
-    const int ps = t / (TS * R), rem = t % (TS * R), i = rem / TS, tsl = rem % TS;
-    const int p8 = t < T ? to_i8((sc[osum_index(t, D, P)] * rr) * 127.0f) : 0;
-    if (OPT) qs += p8;
-    pq[((ps * (R / 4) + (i >> 2)) * TS + tsl) * 4 + (i & 3)] = (int8_t)p8;
+  {
+    const bool all = !SPLIT || (OPT && a.qsum);
+    const int p0 = all ? 0 : sj, pst = all ? 1 : nsp;
+    const int nq = ((npass - p0 + pst - 1) / pst) * TS * R;
+    for (int q0 = 0; q0 < nq; q0 += 4 * kAttnThreads) {
+      int tt[4];
+      float sv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = q0 + u * kAttnThreads + tid;
+        const int t = (p0 + (q / (TS * R)) * pst) * TS * R + q % (TS * R);
+        tt[u] = q < nq ? t : -1;
+        sv[u] = sc[q < nq && t < T ? osum_index(t, D, P) : dummy];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = tt[u];
+        if (t >= 0) {
+          const int ps = t / (TS * R), rem = t % (TS * R), i = rem / TS, tsl = rem % TS;
+          const int p8 = t < T ? to_i8((sv[u] * rr) * 127.0f) : 0;
+          if (OPT) qs += p8;
+          pq[((ps * (R / 4) + (i >> 2)) * TS + tsl) * 4 + (i & 3)] = (int8_t)p8;
+        }
+      }
+    }
   }
   lds_barrier();
 
@@ -623,9 +717,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   int acc[16];
 #pragma unroll
   for (int b = 0; b < 16; ++b) acc[b] = 0;
-  for (int pass = 0; pass < npass; ++pass) {
+  for (int pass = sj; pass < npass; pass += nsp) {
     const int base = pass * TS * R;
-    if (pass > 0) {
+    if (pass > sj) {
 #pragma unroll
       for (int i = 0; i < R; ++i) vw[i] = buffer_load16(vrs, chunk_off(base + ts + TS * i));
     }
@@ -649,7 +743,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   }
   // row pos's term, p(pos) times the new V row (from LDS), in the threads whose slot holds row pos
   // (exact int32 either way)
-  if (ts == pos % TS && cok) {
+  if (ts == pos % TS && cok && (pos / (TS * R)) % nsp == sj) {
     const int ppos = to_i8((sc[osum_index(pos, D, P)] * rr) * 127.0f);
 #pragma unroll
     for (int w = 0; w < 4; ++w)
@@ -684,10 +778,32 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     for (int w = 0; w < kAttnWaves; ++w) tot += s_qs[w];
     rq = qsum_scale(tot, tab);
   }
+  if constexpr (SPLIT) {
+    // this split's sums into the head's (exact int32 device atomics); the last split to arrive
+    // finishes the output from them and clears them and the counters for the next launch
+    for (int j = tid; j < HD; j += kAttnThreads) {
+      int ssum = 0;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
+      __hip_atomic_fetch_add(a.sp_o + (long long)h * kMaxHd + j, ssum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(a.sp_sync + 2 * h + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)(nsp - 1);
+    __syncthreads();
+    if (!s_last) return;
+  }
   for (int j = tid; j < HD; j += kAttnThreads) {
     int ssum = 0;
+    if constexpr (SPLIT) {
+      int* o = a.sp_o + (long long)h * kMaxHd + j;
+      ssum = __hip_atomic_load(o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(o, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
 #pragma unroll
-    for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
+      for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
+    }
     if constexpr (OPT) {
       float o = (float)ssum;
       if (a.qsum) o = o * rq;
@@ -695,6 +811,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     } else {
       out[(long long)h * HD + j] = (float)ssum * a.a_v;
     }
+  }
+  if (SPLIT && tid == 0) {
+    __hip_atomic_store(a.sp_sync + 2 * h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.sp_sync + 2 * h + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
