@@ -611,7 +611,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
       const float sv = ((float)dk * sq) * a.a_k;
       const bool ok = t < T;
       sc[ok ? osum_index(t, D, P) : dummy] = sv;
-      mloc = nanmax(mloc, ok ? sv : -__builtin_inff());
+      mloc = smax(mloc, ok ? sv : -__builtin_inff());
       if (SPLIT && ok) __hip_atomic_store(a.sp_s + (long long)h * S + t, sv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -638,38 +638,35 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
         const int t = t0 + u * kAttnThreads + tid;
         if (t < T) {
           sc[osum_index(t, D, P)] = sv[u];
-          mloc = nanmax(mloc, sv[u]);
+          mloc = smax(mloc, sv[u]);
         }
       }
     }
   }
-  mloc = wave_max(mloc);
+  mloc = wave_smax(mloc);
   if (lane == 0) red[wave] = mloc;
   lds_barrier();
   float m = red[0];
 #pragma unroll
-  for (int w = 1; w < kAttnWaves; ++w) m = nanmax(m, red[w]);
+  for (int w = 1; w < kAttnWaves; ++w) m = smax(m, red[w]);
 
   // ---- e = EXP(s - m) by the row's keeping lane (+0 padding to a multiple of D), ordered sum, RECIP
-  // (four of the lane's rows loaded ahead of their EXPs and stores: distinct LDS words, or the dummy)
-  const int Tpad = ((T + D - 1) / D) * D;
-  const int erows = ((Tpad + TS * R - 1) / (TS * R)) * RM;
-  for (int q0 = 0; q0 < erows; q0 += 4) {
-    int kk[4];
-    float sv[4];
-    bool live[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int q = q0 + u, j = q % RM;
-      const int t = (q / RM) * TS * R + ts + TS * (j * NCHP + c);
-      kk[u] = q < erows && t < Tpad ? osum_index(t, D, P) : dummy;
-      live[u] = q < erows && t < T;
-      sv[u] = sc[kk[u]];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float ev = sfu_exp_np(sv[u] - m, tab);
-      sc[kk[u]] = live[u] ? ev : 0.0f;
+  // over the lane-major copy itself: wave w takes its rows d = w, w + 8 of it (D is 8 or 16),
+  // lanes the groups g < Tpad / D (row t = g D + d; +0 at t >= T), conflict-free runs of words
+  const int Gt = (T + D - 1) / D;
+  const bool two = D > kAttnWaves;
+  for (int g0 = 0; g0 < Gt; g0 += 64) {
+    const int gg = g0 + lane;
+    if (gg < Gt) {
+      float* p0 = sc + wave * P + gg;
+      float* p1 = p0 + kAttnWaves * P;
+      const float v0 = *p0, v1 = two ? *p1 : 0.0f;
+      const float e0 = sfu_exp_np(v0 - m, tab);
+      *p0 = gg * D + wave < T ? e0 : 0.0f;
+      if (two) {
+        const float e1 = sfu_exp_np(v1 - m, tab);
+        *p1 = gg * D + wave + kAttnWaves < T ? e1 : 0.0f;
+      }
     }
   }
   lds_barrier();
@@ -682,33 +679,29 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   const float rr = s_r;
   // int8 probabilities, once per row (not once per slot lane), in the order P.V reads them: word
   // (pass R / 4 + i / 4) TS + ts holds rows base + ts + TS (i - i % 4 + u), u = 0..3; +0 past T
-  // (SPLIT: the split's own passes, or all of them for qsum's total; four rows' loads ahead)
+  // (a thread forms one word, its four rows; SPLIT: the split's own passes, or all of them for
+  // qsum's total)
   int8_t* pq = (int8_t*)(dyn + D * P + 64);
   int qs = 0;                                    // qsum: the probabilities of the rows this thread forms
   {
+    constexpr int WP = (R / 4) * TS;             // words per pass
     const bool all = !SPLIT || (OPT && a.qsum);
     const int p0 = all ? 0 : sj, pst = all ? 1 : nsp;
-    const int nq = ((npass - p0 + pst - 1) / pst) * TS * R;
-    for (int q0 = 0; q0 < nq; q0 += 4 * kAttnThreads) {
-      int tt[4];
+    const int nw = ((npass - p0 + pst - 1) / pst) * WP;
+    for (int q = tid; q < nw; q += kAttnThreads) {
+      const int ps = p0 + (q / WP) * pst, r = q % WP;
+      const int t0 = ps * TS * R + r % TS + 4 * TS * (r / TS);
       float sv[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int q = q0 + u * kAttnThreads + tid;
-        const int t = (p0 + (q / (TS * R)) * pst) * TS * R + q % (TS * R);
-        tt[u] = q < nq ? t : -1;
-        sv[u] = sc[q < nq && t < T ? osum_index(t, D, P) : dummy];
-      }
+      for (int u = 0; u < 4; ++u) sv[u] = sc[t0 + TS * u < T ? osum_index(t0 + TS * u, D, P) : dummy];
+      int word = 0;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int t = tt[u];
-        if (t >= 0) {
-          const int ps = t / (TS * R), rem = t % (TS * R), i = rem / TS, tsl = rem % TS;
-          const int p8 = t < T ? to_i8((sv[u] * rr) * 127.0f) : 0;
-          if (OPT) qs += p8;
-          pq[((ps * (R / 4) + (i >> 2)) * TS + tsl) * 4 + (i & 3)] = (int8_t)p8;
-        }
+        const int p8 = t0 + TS * u < T ? to_i8((sv[u] * rr) * 127.0f) : 0;
+        if (OPT) qs += p8;
+        word |= (p8 & 0xFF) << (8 * u);
       }
+      ((int*)pq)[ps * WP + r] = word;
     }
   }
   lds_barrier();

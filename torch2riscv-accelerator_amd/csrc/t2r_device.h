@@ -396,6 +396,19 @@ T2R_DEV int wave_half_sum_i32(int v) {
   v += dpp_i<kDppMirror>(v);
   return v + __shfl_xor(v, 16);
 }
+// wave_max with smax: the maximum of the wave's 64 values, NaN winning, to every lane
+T2R_DEV float wave_smax(float v) {
+  v = smax(v, dpp_f<kDppXor1>(v));
+  v = smax(v, dpp_f<kDppXor2>(v));
+  v = smax(v, dpp_f<kDppHalfMirror>(v));
+  v = smax(v, dpp_f<kDppMirror>(v));
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return smax(smax(a, b), smax(c, d));
+}
+
 T2R_DEV float wave_max(float v) {
   v = nanmax(v, dpp_f<kDppXor1>(v));
   v = nanmax(v, dpp_f<kDppXor2>(v));
