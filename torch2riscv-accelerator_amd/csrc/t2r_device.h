@@ -379,6 +379,47 @@ T2R_DEV int wave_sum_i32(int v) {
   return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
          (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
+// The wave sums of NV values at once (NV = 1, 2, 4 or 8; exact int32 in any order). Halving steps
+// first: each sends half of the lane's values to its partner (lane bit 2, then 1, then 0) and keeps
+// the other half, adding what the partner sent; then single-value steps over the remaining lane
+// bits (row_ror:8 for bit 3, the gfx950 permlane swaps for bits 4 and 5, each swap of a register
+// with itself leaving v(L) and v(L ^ 16) or v(L ^ 32) in the pair it returns). Lane L ends with the
+// total of value (L >> (3 - log2 NV)) & (NV - 1).
+template <int M, int CTRL>
+T2R_DEV void wave_halve(int* c, int hi) {
+#pragma unroll
+  for (int j = 0; j < M / 2; ++j) {
+    const int send = hi ? c[j] : c[j + M / 2];
+    const int keep = hi ? c[j + M / 2] : c[j];
+    c[j] = keep + dpp_i<CTRL>(send);
+  }
+}
+template <int NV>
+T2R_DEV int wave_sum_multi(const int (&v)[NV]) {
+  static_assert(NV == 1 || NV == 2 || NV == 4 || NV == 8, "1, 2, 4 or 8 values");
+  const int lane = threadIdx.x & 63;
+  int c[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) c[j] = v[j];
+  if constexpr (NV >= 2) wave_halve<NV, kDppHalfMirror>(c, (lane >> 2) & 1);   // partner lane ^ 7
+  if constexpr (NV >= 4) wave_halve<NV / 2, kDppXor2>(c, (lane >> 1) & 1);
+  if constexpr (NV >= 8) wave_halve<NV / 4, kDppXor1>(c, lane & 1);
+  int t = c[0];
+  if constexpr (NV < 8) t += dpp_i<kDppXor1>(t);
+  if constexpr (NV < 4) t += dpp_i<kDppXor2>(t);
+  if constexpr (NV < 2) t += dpp_i<kDppHalfMirror>(t);
+  t += dpp_i<0x128>(t);                                                     // row_ror:8 = lane ^ 8
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)t, (unsigned)t, false, false);
+    t = (int)(r[0] + r[1]);
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)t, (unsigned)t, false, false);
+    t = (int)(r[0] + r[1]);
+  }
+  return t;
+}
+
 // A workgroup barrier that orders LDS only: this wave's LDS accesses complete, then s_barrier. Unlike
 // __syncthreads it leaves the wave's global loads in flight (no wait on their counter).
 T2R_DEV void lds_barrier() {

@@ -313,21 +313,35 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs a) {
       rs[u] = EPI == EPI_RESID ? t.res[u] : 0.0f;
     }
     if (r0 + nwaves * RU < N) load_tile<EPI, NCB, RU, IDX>(t, a, res, row_in, r0 + nwaves * RU, lane);
+    // the tile's RU row sums (and W3's) in one multi-value reduction: lane L ends with sum
+    // (L >> SH) & (NV - 1) of vv; the lanes holding W1's sum of row u (and, beside them, W3's)
+    // finish row r0 + u
+    constexpr int NV = EPI == EPI_SWIGLU ? 2 * RU : RU;
+    constexpr int SH = NV == 8 ? 0 : NV == 4 ? 1 : NV == 2 ? 2 : 3;
+    int vv[NV];
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
-      acc[u] = wave_sum_i32(acc[u]);
-      if (EPI == EPI_SWIGLU) acc3[u] = wave_sum_i32(acc3[u]);
+      if (EPI == EPI_SWIGLU) {
+        vv[2 * u] = acc[u];
+        vv[2 * u + 1] = acc3[u];
+      } else {
+        vv[u] = acc[u];
+      }
     }
-    // every lane holds the RU sums (xor butterflies): lane u finishes row r0 + u
-    if (lane < RU) {
-      int ac = acc[0], ac3 = acc3[0];
+    const int tot = wave_sum_multi<NV>(vv);
+    int tot3 = 0;                                   // W3's sum: the lane holding value idx + 1
+    if constexpr (EPI == EPI_SWIGLU) tot3 = dpp_i<SH == 0 ? kDppXor1 : SH == 1 ? kDppXor2 : kDppHalfMirror>(tot);
+    const int idx = (lane >> SH) & (NV - 1);
+    const int ul = EPI == EPI_SWIGLU ? idx >> 1 : idx;
+    if (lane < 8 && (lane & ((1 << SH) - 1)) == 0 && (EPI != EPI_SWIGLU || (idx & 1) == 0)) {
+      int ac = tot, ac3 = tot3;
       float w1s = sw[0], w3s = sw3[0], rr = rs[0];
 #pragma unroll
       for (int u = 1; u < RU; ++u)
-        if (lane == u) {
-          ac = acc[u]; ac3 = acc3[u]; w1s = sw[u]; w3s = sw3[u]; rr = rs[u];
+        if (ul == u) {
+          w1s = sw[u]; w3s = sw3[u]; rr = rs[u];
         }
-      const int row = r0 + lane;
+      const int row = r0 + ul;
       if (row < N) {
         float v = dequant(ac, w1s, s_x);
         if (EPI == EPI_SWIGLU) v = gate_mul(v, dequant(ac3, w3s, s_x), a.act, tab_lds);
