@@ -369,21 +369,28 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_up(MoeUpArgs m) {
       sw3[u] = t.sw3[u];
     }
     if (r0 + nwaves * RU < N) tile(r0 + nwaves * RU);
+    // the RU row sums and W3's in one multi-value reduction (as in k_gemv): lane L holds sum
+    // (L >> SH) & (NV - 1) of vv, W3's beside it; the lanes holding W1's sum of row u finish it
+    constexpr int NV = 2 * RU;
+    constexpr int SH = NV == 8 ? 0 : NV == 4 ? 1 : 2;
+    int vv[NV];
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
-      acc[u] = wave_sum_i32(acc[u]);
-      acc3[u] = wave_sum_i32(acc3[u]);
+      vv[2 * u] = acc[u];
+      vv[2 * u + 1] = acc3[u];
     }
-    if (lane < RU) {                                  // lane u finishes row r0 + u
-      int ac = acc[0], ac3 = acc3[0];
+    const int tot = wave_sum_multi<NV>(vv);
+    const int tot3 = dpp_i<SH == 0 ? kDppXor1 : SH == 1 ? kDppXor2 : kDppHalfMirror>(tot);
+    const int idx = (lane >> SH) & (NV - 1), ul = idx >> 1;
+    if (lane < 8 && (lane & ((1 << SH) - 1)) == 0 && (idx & 1) == 0) {
       float w1s = sw[0], w3s = sw3[0];
 #pragma unroll
       for (int u = 1; u < RU; ++u)
-        if (lane == u) {
-          ac = acc[u]; ac3 = acc3[u]; w1s = sw[u]; w3s = sw3[u];
+        if (ul == u) {
+          w1s = sw[u]; w3s = sw3[u];
         }
-      const int r = r0 + lane;
-      if (r < N) y[r] = gate_mul(dequant(ac, w1s, s_x), dequant(ac3, w3s, s_x), a.act, tab_lds);
+      const int r = r0 + ul;
+      if (r < N) y[r] = gate_mul(dequant(tot, w1s, s_x), dequant(tot3, w3s, s_x), a.act, tab_lds);
     }
   }
 }
@@ -465,12 +472,11 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeDownArgs m) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int4 xq = (j < k && col < F) ? *(const int4*)(hq + j * 1024 + col) : make_int4(0, 0, 0, 0);
-    acc[j] = wave_sum_i32(dot16(wv[j], xq, 0));
+    acc[j] = dot16(wv[j], xq, 0);
   }
+  // the 8 sums in one multi-value reduction: lane j (< 8) holds expert j's;
   // lane j: F(w_j * y_j), y_j the dequantised expert output; then the sum in route order
-  int aj = acc[0];
-#pragma unroll
-  for (int j = 1; j < 8; ++j) aj = lane == j ? acc[j] : aj;
+  const int aj = wave_sum_multi<8>(acc);
   const float t = lane < k ? wj * dequant(aj, swd, s_h[lane < k ? lane : 0]) : 0.0f;
   float y = 0.0f;
   for (int j = 0; j < k; ++j) y = y + __shfl(t, j);
