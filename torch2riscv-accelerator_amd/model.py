@@ -148,8 +148,8 @@ class ResidentModel:
             raise ValueError(f"token {bad[0]} outside [0, {self.cfg.vocab})")
 
     def status(self, clear=True):
-        """The device status word (bit 0: a token outside the vocabulary was embedded); waits for the
-        device."""
+        """The device status word (bit 0: a token outside the vocabulary was embedded; bit 1: a bounded
+        wait between the workgroups of a head's split decode attention ran out); waits for the device."""
         out = np.zeros(1, np.int32)
         abi.check("t2r_model_status", self.lib.t2r_model_status(self.handle, out.ctypes.data, int(clear)))
         return int(out[0])
