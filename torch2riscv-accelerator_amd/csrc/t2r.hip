@@ -5,6 +5,7 @@
 #include <cstdint>
 #include <cstddef>
 #include <cstring>
+#include <type_traits>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -255,6 +256,13 @@ struct Model {
   float* sp_s;
   int32_t* sp_o;
   uint32_t* sp_sync;
+  // MoE over many rows, grouped by expert: route lists, the routes' int8 expert outputs and scales,
+  // and their weighted down projections (MoE models only)
+  int32_t* moe_off = nullptr;
+  int32_t* moe_list = nullptr;
+  int8_t* moe_hq = nullptr;
+  float* moe_sh = nullptr;
+  float* moe_t = nullptr;
   // batched decode (t2r_decode_batch): the caches of the step's sequences, kv_rs bytes apart
   int8_t* kcb = nullptr;
   int8_t* vcb = nullptr;
@@ -330,6 +338,14 @@ long long carve(Model* m, char* base, int M) {
   m->sp_s = c.take<float>((long long)d.heads * d.seq_len);
   m->sp_o = c.take<int32_t>((long long)d.heads * kMaxHd);
   m->sp_sync = c.take<uint32_t>(2LL * d.heads);
+  if (d.n_experts > 0) {
+    const long long routes = (long long)M * k;
+    m->moe_off = c.take<int32_t>(d.n_experts + 1);
+    m->moe_list = c.take<int32_t>(routes);
+    m->moe_hq = c.take<int8_t>(routes * d.hidden);
+    m->moe_sh = c.take<float>(routes);
+    m->moe_t = c.take<float>(routes * d.dim);
+  }
   // split-K partial sums of the prefill linears: 4 splits of up to 2048 rows of the widest
   // STORE / RESID output (C3's 2032-row prompt: 133 MB)
   m->part_rows = M < 2048 ? M : 2048;
@@ -660,6 +676,56 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     a.xq = m->mxq; a.xq_stride = d.dim; a.s_x = m->msx;
     a.ids = m->ids; a.rows_per_id = Fe; a.ids_stride = k;
     a.N = k * Fe; a.K = d.dim; a.y = m->u; a.y_stride = m->ffn_rows; a.act = d.ffn_act;
+    auto route_rows = [&]() {
+      const int nc = cdiv(d.dim, 1024);
+      if (nc <= 2) launch(k_moe_route<2>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+      else if (nc <= 4) launch(k_moe_route<4>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+      else launch(k_moe_route<8>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+    };
+    const bool grouped = rows >= 8 && m->moe_t != nullptr && E <= 64 && k <= 8 && Fe % 32 == 0 && Fe <= 1024 &&
+                         d.dim % 32 == 0 && ((uintptr_t)a.w & 15) == 0 && ((uintptr_t)a.w3 & 15) == 0 &&
+                         ((uintptr_t)d.wd & 15) == 0;
+    if (grouped) {
+      // many rows: every row routed, the routes listed per expert, then each expert's linears over
+      // its routes (its weights read once per 32 routes), the routes' quant_act, and the ordered combine
+      {
+        ProfScope p(m, T2R_PROF_ROUTE, st);
+        route_rows();
+        launch(k_moe_lists, dim3(1), dim3(256), 0, st, (const int32_t*)m->ids, rows * k, E, m->moe_off, m->moe_list);
+        if ((rc = launched())) return rc;
+      }
+      MoeGemmArgs g;
+      std::memset(&g, 0, sizeof(g));
+      g.off = m->moe_off; g.list = m->moe_list; g.k = k; g.tab = sfu_table_ptr(); g.act = d.ffn_act;
+      g.ngrp = cdiv(rows, 32);                      // an expert takes at most one route of each row
+      auto go = [&](auto mode, int K) {
+        constexpr int MODE = decltype(mode)::value;
+        const int nw = cdiv(K, kBgWin);
+        const dim3 grid((unsigned)((long long)E * g.ntile * g.ngrp));
+        if (nw >= 8) launch((k_moe_gemm<MODE, 8>), grid, dim3(512), 8 * kBgWaveLds, st, g);
+        else if (nw >= 4) launch((k_moe_gemm<MODE, 4>), grid, dim3(256), 4 * kBgWaveLds, st, g);
+        else if (nw >= 2) launch((k_moe_gemm<MODE, 2>), grid, dim3(128), 2 * kBgWaveLds, st, g);
+        else launch((k_moe_gemm<MODE, 1>), grid, dim3(64), kBgWaveLds, st, g);
+      };
+      {
+        ProfScope p(m, T2R_PROF_FFN_UP, st);
+        g.xq = m->mxq; g.s_x = m->msx; g.w = a.w; g.s_w = a.s_w; g.w3 = a.w3; g.s_w3 = a.s_w3; g.y = m->u;
+        g.N = Fe; g.K = d.dim; g.ntile = cdiv(Fe, 16);
+        go(std::integral_constant<int, MOE_GU>(), g.K);
+        if ((rc = launched())) return rc;
+      }
+      {
+        ProfScope p(m, T2R_PROF_FFN_DOWN, st);
+        launch(k_moe_hq, dim3(cdiv(rows * k, 4)), dim3(256), 0, st, (const float*)m->u, rows * k, Fe, m->moe_hq, m->moe_sh);
+        g.xq = m->moe_hq; g.s_x = m->moe_sh; g.w = d.wd + (long long)l * E * d.dim * Fe; g.s_w = d.s_wd + (long long)l * E * d.dim;
+        g.w3 = nullptr; g.s_w3 = nullptr; g.wts = m->wts; g.y = m->moe_t; g.N = d.dim; g.K = Fe; g.ntile = cdiv(d.dim, 32);
+        go(std::integral_constant<int, MOE_DN>(), g.K);
+        launch(k_moe_combine, dim3(cdiv(d.dim, 256), rows), dim3(256), 0, st, (const float*)m->moe_t, k, d.dim, m->x,
+               (long long)d.dim);
+        if ((rc = launched())) return rc;
+      }
+      return T2R_OK;
+    }
     if (d.dim <= 1024 && k <= 8) {
       // the router fused into the gate / up GEMV: every block routes its row, then its tiles
       MoeUpArgs mu;
@@ -674,10 +740,7 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     } else {
       {
         ProfScope p(m, T2R_PROF_ROUTE, st);
-        const int nc = cdiv(d.dim, 1024);
-        if (nc <= 2) launch(k_moe_route<2>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
-        else if (nc <= 4) launch(k_moe_route<4>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
-        else launch(k_moe_route<8>, dim3(rows), dim3(kGemvThreads), 0, st, ra);
+        route_rows();
         if ((rc = launched())) return rc;
       }
       ProfScope p(m, T2R_PROF_FFN_UP, st);

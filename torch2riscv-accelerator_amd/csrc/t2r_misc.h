@@ -2,6 +2,7 @@
 // RoPE, KV append, the MoE router / expert combine, argmax, and the element-wise hooks that let
 // the tests see the SFU and the flush-to-zero primitives bit for bit.
 #pragma once
+#include "t2r_gemm.h"
 #include "t2r_gemv.h"
 
 namespace t2r {
@@ -393,6 +394,173 @@ __global__ __launch_bounds__(kGemvThreads) void k_moe_up(MoeUpArgs m) {
       if (r < N) y[r] = gate_mul(dequant(tot, w1s, s_x), dequant(tot3, w3s, s_x), a.act, tab_lds);
     }
   }
+}
+
+// ---- MoE over many rows (prefill): the experts' linears grouped by expert. The per-row kernels
+// (k_moe_up, k_moe_down) stream each row's k experts for that row alone; here the step's routes
+// (row r, slot j: entry r k + j) are listed per expert and every expert's weights are read once per
+// 32 routes by an int8 MFMA tile (k_bgemv's main loop with the activation rows gathered through the
+// list). The int32 sums are exact, and every float step is the per-row kernels' own, in their order.
+
+// list[off[e] .. off[e + 1]) = the entries routed to expert e (in no particular order: each entry's
+// result is computed on its own). One workgroup; E <= 64.
+__global__ __launch_bounds__(256) void k_moe_lists(const int32_t* ids, int n, int E, int32_t* off, int32_t* list) {
+  __shared__ int cnt[64], fill[64];
+  const int tid = threadIdx.x;
+  if (tid < 64) cnt[tid] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += 256) atomicAdd(&cnt[min(max(ids[i], 0), E - 1)], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int o = 0;
+    for (int e = 0; e < E; ++e) {
+      off[e] = o;
+      fill[e] = o;
+      o += cnt[e];
+    }
+    off[E] = o;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += 256) list[atomicAdd(&fill[min(max(ids[i], 0), E - 1)], 1)] = i;
+}
+
+// quant_act of every route's expert output u_j (one wave per entry; k_moe_down's prologue): hq [n, F]
+// int8, s_h [n]. F <= 1024.
+__global__ __launch_bounds__(256) void k_moe_hq(const float* u, int n, int F, int8_t* hq, float* s_h) {
+  const int lane = threadIdx.x & 63, ent = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (ent >= n) return;                           // (wave-uniform)
+  const float* ur = u + (long long)ent * F;
+  float4 uv[4];
+  uint32_t am = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int i = c * 256 + lane * 4;
+    uv[c] = i < F ? *(const float4*)(ur + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    am = max(am, max(max(abs_bits(uv[c].x), abs_bits(uv[c].y)), max(abs_bits(uv[c].z), abs_bits(uv[c].w))));
+  }
+  const float sj = fv(wave_max_u32(am)) * kInv127, inv = sfu_recip(sj);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int i = c * 256 + lane * 4;
+    if (i < F)
+      *(int*)(hq + (long long)ent * F + i) = pack_i8x4(to_i8(uv[c].x * inv), to_i8(uv[c].y * inv),
+                                                       to_i8(uv[c].z * inv), to_i8(uv[c].w * inv));
+  }
+  if (lane == 0) s_h[ent] = sj;
+}
+
+// The grouped expert linear. Block b = (expert e, weight tile, route group g) takes the routes
+// list[off[e] + 32 g ..] (at most 32; a group past the expert's routes ends at once):
+//   MOE_GU (gate / up): X = mxq[r] (K = dim), tiles of 16 gate + the same 16 up rows of expert e,
+//          u[r][j F + n] = gate(F(F(f32(s1) s_wg) s_x[r]), F(F(f32(s3) s_wu) s_x[r]))
+//   MOE_DN (down): X = hq[r k + j] (K = F), tiles of 32 rows of wd[e] (dim x F),
+//          t[r k + j][n] = F(w[r k + j] F(F(f32(s) s_wd) s_h[r k + j]))
+enum { MOE_GU = 0, MOE_DN = 1 };
+struct MoeGemmArgs {
+  const int32_t* off;
+  const int32_t* list;
+  const int8_t* xq;           // GU: mxq [rows, dim] (row r = entry / k); DN: hq [rows k, F] (row = entry)
+  const float* s_x;           // GU: msx [rows]; DN: s_h [rows k]
+  const int8_t* w;            // GU: wg [E, F, dim]; DN: wd [E, dim, F]
+  const float* s_w;           // [E, N]
+  const int8_t* w3;           // GU: wu [E, F, dim]
+  const float* s_w3;
+  const float* wts;           // DN: route weights [rows k]
+  float* y;                   // GU: u [rows, k F]; DN: t [rows k, dim]
+  const float* tab;           // SFU tables (GU's gate)
+  int act;
+  int k, N, K;                // N: weight rows per expert (GU: F; DN: dim), K: their length
+  int ntile, ngrp;            // weight tiles per expert, route groups per expert
+};
+template <int MODE, int KW>
+__global__ __launch_bounds__(64 * KW) void k_moe_gemm(MoeGemmArgs a) {
+  extern __shared__ __align__(16) int8_t lds[];    // KW x kBgWaveLds
+  __shared__ __align__(16) float tab_lds[MODE == MOE_GU ? kSfuWords : 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, kh = lane >> 5;
+  const int per_e = a.ntile * a.ngrp;
+  const int e = blockIdx.x / per_e, tile = (blockIdx.x % per_e) / a.ngrp, grp = blockIdx.x % a.ngrp;
+  const int beg = a.off[e] + 32 * grp, cnt = min(32, a.off[e + 1] - beg);
+  if (cnt <= 0) return;                           // (block-uniform: before any barrier)
+  constexpr int NT = MODE == MOE_GU ? 16 : 32;    // output columns per tile
+  const int n0 = tile * NT, K = a.K, N = a.N;
+  const int nwin = cdiv_i(K, kBgWin);
+  int8_t* wl = lds + wave * kBgWaveLds;
+  if (MODE == MOE_GU && tid < kSfuWords / 4) ((v4f_t*)tab_lds)[tid] = ((const v4f_t*)a.tab)[tid];
+  const int8_t* we = a.w + (long long)e * N * K;
+  const int8_t* we3 = MODE == MOE_GU ? a.w3 + (long long)e * N * K : we;
+  const int8_t* rowp[8];
+  int qo[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane >> 4);
+    qo[i] = 16 * ((lane & 15) ^ (r & 15));
+    if (MODE == MOE_GU) rowp[i] = (r < 16 ? we : we3) + (long long)min(n0 + (r & 15), N - 1) * K;
+    else rowp[i] = we + (long long)min(n0 + r, N - 1) * K;
+  }
+  // lane lr's activation row: route lr of the group (routes past cnt repeat the last one, unused)
+  const int ent = a.list[beg + min(lr, cnt - 1)];
+  const int8_t* xrow = a.xq + (long long)(MODE == MOE_GU ? ent / a.k : ent) * K + 16 * kh;
+  v16i_t acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0;
+  for (int w = wave; w < nwin; w += KW) {
+    const int k0 = w * kBgWin, nst = min(kBgWin, K - k0) >> 5;
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(rowp[i] + min(k0 + qo[i], K - 16)), (void*)(wl + 1024 * i), 16, 0, 0);
+    v4i_t xv[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) xv[st] = *(const v4i_t*)(xrow + min(k0 + 32 * st, K - 32));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      if (st < nst) {
+        const v4i_t wv = *(const v4i_t*)(wl + 256 * lr + 16 * ((2 * st + kh) ^ (lr & 15)));
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[st], wv, acc, 0, 0, 0);
+      }
+    }
+  }
+  asm volatile("" ::: "memory");
+  int* red = (int*)wl;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[((r >> 2) * 8 + kh * 4 + (r & 3)) * 33 + lr] = acc[r];
+  __syncthreads();
+  constexpr int OPT = (32 * NT + 64 * KW - 1) / (64 * KW);
+#pragma unroll
+  for (int i = 0; i < OPT; ++i) {
+    const int o = tid + i * 64 * KW, m = o / NT, j = o % NT, n = n0 + j;
+    if (m >= cnt || n >= N) continue;
+    int s1 = 0, s3 = 0;
+#pragma unroll
+    for (int v = 0; v < KW; ++v) {
+      const int* rv = (const int*)(lds + v * kBgWaveLds);
+      s1 += rv[m * 33 + j];
+      if (MODE == MOE_GU) s3 += rv[m * 33 + 16 + j];
+    }
+    const int em = a.list[beg + m];
+    if constexpr (MODE == MOE_GU) {
+      const int r = em / a.k, slot = em - r * a.k;
+      const float sx = a.s_x[r];
+      a.y[((long long)r * a.k + slot) * N + n] =
+          gate_mul(dequant(s1, a.s_w[(long long)e * N + n], sx), dequant(s3, a.s_w3[(long long)e * N + n], sx), a.act, tab_lds);
+    } else {
+      a.y[(long long)em * N + n] = a.wts[em] * dequant(s1, a.s_w[(long long)e * N + n], a.s_x[em]);
+    }
+  }
+}
+
+// x[r][n] = F(x[r][n] + y), y = +0 then y = F(y + t[r k + j][n]) for j = 0..k-1 in route order
+// (k_moe_down's combine). Grid (dim / 256 blocks, rows).
+__global__ __launch_bounds__(256) void k_moe_combine(const float* t, int k, int dim, float* x, long long x_stride) {
+  const int r = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= dim) return;
+  float y = 0.0f;
+  for (int j = 0; j < k; ++j) y = y + t[((long long)r * k + j) * dim + n];
+  float* xr = x + (long long)r * x_stride + n;
+  *xr = *xr + y;
 }
 
 // top-k + weights from given scores (the op-level ABI)
