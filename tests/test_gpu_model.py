@@ -104,6 +104,32 @@ def test_prefill_equals_decode(name):
         assert np.array_equal(kc[0], kd[0]) and np.array_equal(kc[1], kd[1])
 
 
+def test_moe_grouped_prefill_many_routes():
+    """The grouped MoE prefill (routes listed per expert, each expert's linears over its routes in
+    groups of 32) with more routes than 32 per expert: 160 rows x 8 routes over 32 experts puts at
+    least 33 on some expert in every layer, so second groups run. Prefill (one call, and 64-row
+    chunks) gives the decode-only logits and KV cache bit for bit."""
+    import t2r_amd.config as C
+    cfg = C.C5.with_(name="c5-2l-160", layers=2, prompt_len=160)
+    assert cfg.prompt_len * cfg.top_k > 32 * cfg.n_experts
+    qm, rm = resident(cfg, max_rows=160)
+    toks = cfg.prompt()
+    P = len(toks)
+    print(f"{cfg.name}: {P} rows", flush=True)
+    for p, t in enumerate(toks):
+        dec = rm.decode(t, p).cpu().numpy()
+    kd = kv_host(rm, P)
+    rm.reset()
+    pre = rm.prefill(toks).cpu().numpy()
+    assert sha(pre) == sha(dec)
+    kp = kv_host(rm, P)
+    assert np.array_equal(kp[0], kd[0]) and np.array_equal(kp[1], kd[1])
+    rm.reset()
+    ch = rm.prefill_chunks(toks, M=64).cpu().numpy()
+    assert sha(ch) == sha(dec)
+    rm.close()
+
+
 def test_greedy_on_device_c1(gold):
     """The config-1 run as LlamaDevice.greedy_on_device does it (prefill, then argmax and pos += 1 on the
     device, no host round trip): the same 160 tokens as the reference's run."""
