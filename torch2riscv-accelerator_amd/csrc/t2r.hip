@@ -137,6 +137,13 @@ bool pre_ok(const AttnArgs& a) {
   return a.hd % 16 == 0 && a.hd <= 128 && attn_pre_lds_bytes(pre_cap(a), (a.hd + 31) & ~31) <= kPreMaxLds;
 }
 
+// batch-1 decode attention split over workgroups per head (k_attn_dec's SPLIT forms)
+inline bool attn_split(const AttnArgs& a, int rows) {
+  return a.nsplit > 1 && rows == 1 && a.hd == 128 && a.sp_s && a.sp_o && a.sp_sync;
+}
+// ... and whether it leaves its int32 P.V sums per split for the next linear (SPLIT 2) instead of att
+inline bool attn_split_to_linear(const AttnArgs& a, int rows) { return attn_split(a, rows) && !attn_opt(a); }
+
 int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   if (a.H <= 0 || a.Hk <= 0 || a.H % a.Hk || a.hd <= 0 || a.hd > kMaxHd || a.hd % 8 || a.S <= 0 || a.S > kMaxS ||
       (a.D != 8 && a.D != 16))
@@ -176,10 +183,11 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   if (mode == ATTN_FUSED && a.tab != nullptr && a.hd % 16 == 0 &&
       (a.hd == 16 || a.hd == 32 || a.hd == 48 || a.hd == 64 || a.hd == 128)) {
     const size_t dl = attn_dec_lds_bytes(a.S, a.D);
-    if (a.nsplit > 1 && rows == 1 && a.hd == 128 && a.sp_s && a.sp_o && a.sp_sync) {
+    if (attn_split(a, rows)) {
+      // (without the HF options the next linear adds the splits' sums: attn_split_to_linear)
       const dim3 gs(a.H, a.nsplit);
-      if (opt) launch((k_attn_dec<8, true, true>), gs, block, dl, st, a);
-      else launch((k_attn_dec<8, false, true>), gs, block, dl, st, a);
+      if (opt) launch((k_attn_dec<8, true, 1>), gs, block, dl, st, a);
+      else launch((k_attn_dec<8, false, 2>), gs, block, dl, st, a);
     } else if (opt) {
       switch (a.hd / 16) {
         case 1: launch((k_attn_dec<1, true>), grid, block, dl, st, a); break;
@@ -336,7 +344,7 @@ long long carve(Model* m, char* base, int M) {
   m->status = c.take<int32_t>(1);
   m->pos_rows = c.take<int32_t>(M);
   m->sp_s = c.take<float>((long long)d.heads * d.seq_len);
-  m->sp_o = c.take<int32_t>((long long)d.heads * kMaxHd);
+  m->sp_o = c.take<int32_t>(4LL * d.heads * kMaxHd);
   m->sp_sync = c.take<uint32_t>(2LL * d.heads);
   if (d.n_experts > 0) {
     const long long routes = (long long)M * k;
@@ -555,7 +563,7 @@ AttnArgs layer_attn_args(Model* m, int l, const int32_t* pos, int mode) {
   at.qsum = d.attn_qsum;
   // batch-1 decode at head dim 128 over caches of more than 512 rows: each head's keys over 4
   // workgroups (k_attn_dec's SPLIT form); at most 256 workgroups, so all of them are resident at once
-  if (mode == RUN_DECODE && d.head_dim == 128 && d.seq_len > 512 && d.heads * 4 <= 256) {
+  if (mode == RUN_DECODE && d.head_dim == 128 && d.seq_len > 512 && d.heads * 4 <= 256) {   // (4 splits: sp_o)
     at.nsplit = 4;
     at.sp_s = m->sp_s; at.sp_o = m->sp_o; at.sp_sync = m->sp_sync; at.sp_status = m->status;
   }
@@ -620,7 +628,12 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
   a.s_w = d.s_wo + L_dim;
   a.x = m->att; a.x_stride = m->q_dim;
   a.N = d.dim; a.K = m->q_dim; a.y = m->x; a.y_stride = d.dim; a.res = m->x; a.res_stride = d.dim;
-  if (decode) {
+  if (decode && attn_split_to_linear(at, rows)) {
+    // the split attention left its four per-split int32 P.V sums: x = F(f32(sum) a_v), then quant_act
+    a.xs = m->sp_o; a.xs_stride = m->q_dim; a.xs_scale = at.a_v;
+    ProfScope p(m, T2R_PROF_WO, st);
+    if ((rc = gemv_launch<PRO_SPLITQ, EPI_RESID>(a, rows, st))) return rc;
+  } else if (decode) {
     ProfScope p(m, T2R_PROF_WO, st);
     if ((rc = gemv_launch<PRO_QUANT, EPI_RESID>(a, rows, st))) return rc;
   } else {
@@ -789,7 +802,7 @@ int model_init(Model* m, const t2r_model_desc& dv) {
   carve(m, (char*)desc->workspace, desc->max_rows);
   // the status word, the split attention's sums and counters start clear
   if (hipMemset(m->status, 0, sizeof(int32_t)) != hipSuccess ||
-      hipMemset(m->sp_o, 0, sizeof(int32_t) * (size_t)desc->heads * kMaxHd) != hipSuccess ||
+      hipMemset(m->sp_o, 0, sizeof(int32_t) * 4 * (size_t)desc->heads * kMaxHd) != hipSuccess ||
       hipMemset(m->sp_sync, 0, sizeof(uint32_t) * 2 * (size_t)desc->heads) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess)
     return T2R_EHIP;

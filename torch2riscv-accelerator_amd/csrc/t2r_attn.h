@@ -68,10 +68,12 @@ struct AttnArgs {
   const float* ch_isk;       //   and 1 / s_k for the cache row
   const float* ch_isv;       // V per channel [kv_dim]: 1 / s_v for the cache row
   const float* ch_av;        //   and a_v per output channel
-  // batch-1 decode with a head's keys split over nsplit workgroups (grid y; k_attn_dec's SPLIT form,
-  // nsplit > 1): the scores published [H, S], the P.V sums [H, kMaxHd] (int32) and arrival counters
-  // [H, 2] (both zero between launches: the last workgroup of a head clears them), the status word
-  // (bit 1: a bounded wait ran out)
+  // batch-1 decode with a head's keys split over nsplit workgroups (grid y; k_attn_dec's SPLIT forms,
+  // nsplit > 1): the scores published [H, S]; the P.V sums, int32 (SPLIT 1: met as [H, kMaxHd], zero
+  // between launches; SPLIT 2: each split's own [nsplit, H HD] for the next linear's prologue); per
+  // head two counters [H, 2]: the arrivals (every launch adds nsplit, so a launch's target is the
+  // next multiple of nsplit: never cleared) and SPLIT 1's finish count (zero between launches); the
+  // status word (bit 1: a bounded wait ran out)
   float* sp_s;
   int32_t* sp_o;
   uint32_t* sp_sync;
@@ -79,11 +81,11 @@ struct AttnArgs {
   int nsplit;
 };
 
-// A bounded wait for *p >= want at device scope (one lane polls); on running out it sets bit 1 of
-// *status and returns, so every workgroup reaches its end whatever happens.
+// A bounded wait for *p to reach want (modulo 2^32) at device scope (one lane polls); on running out
+// it sets bit 1 of *status and returns, so every workgroup reaches its end whatever happens.
 T2R_DEV void split_wait(uint32_t* p, uint32_t want, int32_t* status) {
   for (int it = 0; it < (1 << 20); ++it) {
-    if (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= want) {
+    if ((int32_t)(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - want) >= 0) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       return;
     }
@@ -389,10 +391,13 @@ T2R_DEV int slot_group_sum(int v) {
 // at most ~95 GB/s (522 KB at head dim 128 and T = 2048), so more CUs per head shorten that part.
 // Each split publishes its scores with device-coherent stores and arrives once; after one bounded
 // wait every split reads all T scores and forms the max, the EXPs, the ordered sum and RECIP itself
-// (the same bits in each), then the probabilities and P.V of its own passes; the P.V sums meet as
-// exact int32 device atomics, and the head's last split to arrive writes the output and clears the
-// sums and counters for the next launch.
-template <int NCH, bool OPT = false, bool SPLIT = false>   // 16-byte chunks per head row: hd = 16 NCH; OPT: the HF options
+// (the same bits in each), then the probabilities and P.V of its own passes. The splits past the
+// passes arrive too, so each launch adds exactly nsplit arrivals and waits for the next multiple.
+// SPLIT 1: the P.V sums meet as exact int32 device atomics, and the head's last split to finish
+// writes the output and clears the sums and its counter for the next launch. SPLIT 2 (no HF
+// options): each split stores its own int32 sums (splits past the passes store zeros) and the next
+// linear's prologue adds the four and scales them (F(f32(sum) a_v), the output's own formula).
+template <int NCH, bool OPT = false, int SPLIT = 0>   // 16-byte chunks per head row: hd = 16 NCH; OPT: the HF options
 __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   constexpr int HD = 16 * NCH;
   constexpr int NCHP = NCH <= 1 ? 1 : (NCH <= 2 ? 2 : (NCH <= 4 ? 4 : 8));
@@ -422,9 +427,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   const int pos = a.pos[row];
   if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
   const int T = pos + 1;
-  // SPLIT: splits past the number of passes end here (all of a launch's workgroups agree on it)
+  // SPLIT: splits past the number of passes end here (all of a launch's workgroups agree on it);
+  // SPLIT 2: with zero sums
   const int nsp = SPLIT ? min(a.nsplit, (T + TS * R - 1) / (TS * R)) : 1;
-  if (SPLIT && sj >= nsp) return;
+  if (SPLIT && sj >= nsp) {
+    if (SPLIT == 2)
+      for (int j = tid; j < HD; j += kAttnThreads) a.sp_o[(long long)sj * q_dim + (long long)h * HD + j] = 0;
+    if (tid == 0) __hip_atomic_fetch_add(a.sp_sync + 2 * h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   const float* qkv = a.qkv + row * a.qkv_stride;
   const int c = tid & (NCHP - 1), ts = tid / NCHP;
   const bool cok = c < NCH;
@@ -621,8 +632,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     __syncthreads();
     uint32_t* arrive = a.sp_sync + 2 * h;
     if (tid == 0) {
-      __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-      split_wait(arrive, (uint32_t)nsp, a.sp_status);
+      const uint32_t old = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t ns = (uint32_t)a.nsplit;
+      split_wait(arrive, old - old % ns + ns, a.sp_status);
     }
     __syncthreads();
     mloc = -__builtin_inff();
@@ -771,7 +783,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     for (int w = 0; w < kAttnWaves; ++w) tot += s_qs[w];
     rq = qsum_scale(tot, tab);
   }
-  if constexpr (SPLIT) {
+  if constexpr (SPLIT == 2) {
+    // this split's sums for the next linear's prologue; the counters cleared by the last split
+    for (int j = tid; j < HD; j += kAttnThreads) {
+      int ssum = 0;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
+      a.sp_o[(long long)sj * q_dim + (long long)h * HD + j] = ssum;
+    }
+    return;
+  }
+  if constexpr (SPLIT == 1) {
     // this split's sums into the head's (exact int32 device atomics); the last split to arrive
     // finishes the output from them and clears them and the counters for the next launch
     for (int j = tid; j < HD; j += kAttnThreads) {
@@ -805,10 +827,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
       out[(long long)h * HD + j] = (float)ssum * a.a_v;
     }
   }
-  if (SPLIT && tid == 0) {
-    __hip_atomic_store(a.sp_sync + 2 * h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(a.sp_sync + 2 * h + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (SPLIT && tid == 0) __hip_atomic_store(a.sp_sync + 2 * h + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- prefill prep (ATTN_PREP): one wave per head vector of a row (the H query heads, then the Hk

@@ -80,6 +80,7 @@ template <int PRO, int EPI>
 inline bool gemv_operands_ok(const GemvArgs& a) {
   if ((PRO != PRO_XQ || EPI == EPI_SWIGLU) && (a.tab == nullptr || ((uintptr_t)a.tab & 15))) return false;
   if (PRO == PRO_XQ) return ((uintptr_t)a.xq & 15) == 0 && a.xq_stride % 16 == 0;
+  if (PRO == PRO_SPLITQ) return a.xs != nullptr && ((uintptr_t)a.xs & 15) == 0 && a.xs_stride % 4 == 0 && a.K % 4 == 0;
   if (((uintptr_t)a.x & 15) || a.x_stride % 4) return false;
   return PRO != PRO_NORM_QUANT || ((uintptr_t)a.g & 15) == 0;
 }

@@ -6,6 +6,8 @@
 //  prologue  PRO_XQ          the int8 activations and their scale are given
 //            PRO_QUANT       quant_act of an fp32 vector (llm/ref_model.py:191-196)
 //            PRO_NORM_QUANT  RMSNorm then quant_act (llm/ref_model.py:204-207)
+//            PRO_SPLITQ      quant_act of x = F(f32(p0 + p1 + p2 + p3) * xs_scale) from four int32
+//                            partial vectors (the split decode attention's P.V sums)
 //  epilogue  EPI_STORE       y[n]
 //            EPI_RESID       y[n] = F(res[n] + y)           (the residual add)
 //            EPI_SWIGLU      two weight matrices W1, W3 with the same input:
@@ -22,7 +24,7 @@
 
 namespace t2r {
 
-enum { PRO_XQ = 0, PRO_QUANT = 1, PRO_NORM_QUANT = 2 };
+enum { PRO_XQ = 0, PRO_QUANT = 1, PRO_NORM_QUANT = 2, PRO_SPLITQ = 3 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 constexpr int kMaxK = 8192;
 constexpr int kOsumLds = kMaxK + 16 * 8;   // D * osum_stride(kMaxK, D) floats, D <= 16
@@ -51,6 +53,9 @@ struct GemvArgs {
   int rows_per_id;           //   ids[row * ids_stride + r / rows_per_id] * rows_per_id + r % rows_per_id
   int ids_stride;
   const float* tab;          // the SFU tables (kSfuWords floats, 16-byte aligned) in device memory
+  const int32_t* xs;         // PRO_SPLITQ: four int32 partial vectors [4][xs_stride] (16-byte aligned)
+  long long xs_stride;
+  float xs_scale;
   int act;                   // EPI_SWIGLU gate: 0 SiLU, 1 GELU-tanh (gate_mul)
 };
 
@@ -164,7 +169,8 @@ struct XStage {
   static constexpr int NX = (256 * NCB) / NT > 0 ? (256 * NCB) / NT : 1;   // float4 per thread
   static constexpr int NQ = (64 * NCB) / NT > 0 ? (64 * NCB) / NT : 1;     // int4 per thread
   static constexpr bool SFU = PRO != PRO_XQ || EPI == EPI_SWIGLU;
-  float4 x[PRO == PRO_XQ ? 1 : NX];
+  float4 x[PRO == PRO_XQ || PRO == PRO_SPLITQ ? 1 : NX];
+  v4i_t xs[PRO == PRO_SPLITQ ? 4 * NX : 1];
   float4 g[PRO == PRO_NORM_QUANT ? NX : 1];
   v4i_t q[PRO == PRO_XQ ? NQ : 1];
   v4f_t tab;
@@ -180,6 +186,13 @@ T2R_DEV void stage_load(XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& a, int ro
     const int8_t* src = a.xq + row * a.xq_stride;
 #pragma unroll
     for (int j = 0; j < S::NQ; ++j) st.q[j] = *(const v4i_t*)(src + min((tid + j * NT) * 16, K - 16));
+  } else if (PRO == PRO_SPLITQ) {
+#pragma unroll
+    for (int j = 0; j < S::NX; ++j) {
+      const int i = min((tid + j * NT) * 4, K - 4);
+#pragma unroll
+      for (int z = 0; z < 4; ++z) st.xs[4 * j + z] = *(const v4i_t*)(a.xs + z * a.xs_stride + i);
+    }
   } else {
     const float* x = a.x + row * a.x_stride;
 #pragma unroll
@@ -210,9 +223,19 @@ T2R_DEV float stage_finish(const XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& 
   }
   constexpr int NV = 4 * S::NX;
   float xv[NV];
+  if constexpr (PRO == PRO_SPLITQ) {
+    // the four partial sums (exact int32), then x = F(f32(sum) * xs_scale)
 #pragma unroll
-  for (int j = 0; j < S::NX; ++j) {
-    xv[4 * j] = st.x[j].x; xv[4 * j + 1] = st.x[j].y; xv[4 * j + 2] = st.x[j].z; xv[4 * j + 3] = st.x[j].w;
+    for (int j = 0; j < S::NX; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xv[4 * j + e] = (float)(((st.xs[4 * j][e] + st.xs[4 * j + 1][e]) + st.xs[4 * j + 2][e]) + st.xs[4 * j + 3][e]) *
+                        a.xs_scale;
+  } else {
+#pragma unroll
+    for (int j = 0; j < S::NX; ++j) {
+      xv[4 * j] = st.x[j].x; xv[4 * j + 1] = st.x[j].y; xv[4 * j + 2] = st.x[j].z; xv[4 * j + 3] = st.x[j].w;
+    }
   }
   float r = 1.0f;
   if (PRO == PRO_NORM_QUANT) {
