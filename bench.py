@@ -371,7 +371,7 @@ def main():
         "batch_decode": batch,
         "prefill_gemm": prefill_gemm,
         "eager_tok_s": round(steps / eager_dt, 2),
-        "roofline": {"kernel": "k_gemv<PRO_NORM_QUANT, EPI_SWIGLU> (fused SwiGLU decode GEMV)", "bound": "hbm",
+        "roofline": {"kernel": "k_gemv_pw<EPI_SWIGLU> (fused RMSNorm + SwiGLU decode GEMV, prologue wave)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
                      "bytes_per_launch": nbytes["ffn_up"], "avg_us": dom.get("avg_us"),

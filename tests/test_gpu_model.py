@@ -79,6 +79,34 @@ def test_generalised_decode_vs_oracle(name):
     assert np.array_equal(kc, om.kc[:, :n]) and np.array_equal(vc, om.vc[:, :n])
 
 
+@pytest.mark.parametrize("dim,hidden,D", [(2048, 8176, 16), (1024, 8192, 8)])
+def test_wide_ffn_decode_vs_oracle(dim, hidden, D):
+    """FFNs of about 8192 rows (the largest a model takes: W2's K) fill a grid of one block per CU or
+    more, so their SwiGLU GEMV is the form with a prologue wave. 8176 rows need 2044 waves of
+    four-row tiles: the last of the 256 blocks has rows for four of its eight streaming waves. dim
+    1024 takes the one-chunk register slice, D = 8 the eight-lane ordered sum; the norm gains are not
+    all ones. Logits and KV bit-exact with the oracle."""
+    import t2r_amd.config as C
+    from oracle import OracleModel
+    cfg = C.ModelConfig(f"wide-{dim}-{hidden}", dim=dim, hidden=hidden, layers=1, heads=8, kv_heads=4, head_dim=64,
+                        vocab=1024, seq_len=64, gain_std=0.1, D=D, seed_w=77, seed_p=78, prompt_len=2,
+                        decode_steps=2).validate()
+    qm, rm = resident(cfg, D=D)
+    om = OracleModel(qm)
+    seq = list(cfg.prompt())
+    print(f"{cfg.name} D={D}", flush=True)
+    for pos in range(cfg.prompt_len + cfg.decode_steps):
+        want = om.forward(seq[pos], pos)
+        got = rm.decode(seq[pos], pos).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{cfg.name} pos {pos}"
+        if pos + 1 >= len(seq):
+            seq.append(int(np.argmax(want)))
+    n = len(seq) - 1
+    kc, vc = kv_host(rm, n)
+    assert np.array_equal(kc, om.kc[:, :n]) and np.array_equal(vc, om.vc[:, :n])
+    rm.close()
+
+
 @pytest.mark.parametrize("name", ["tiny", "tiny-qwen", "tiny-moe", "c1-stories15m"])
 def test_prefill_equals_decode(name):
     """A prompt through t2r_prefill (all rows at once, and the reference's 16-row chunk schedule with

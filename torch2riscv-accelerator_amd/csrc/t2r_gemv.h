@@ -283,34 +283,13 @@ T2R_DEV float stage_finish(const XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& 
   return s_x;
 }
 
-// NCB: 1024-byte column chunks per row covered by the register slice (K <= NCB * 1024);
-// RU: rows per wave tile; NT: threads per block. A wave's first tile is requested right after the
-// prologue's inputs and before the prologue runs, and each next tile right after the current one's
-// dot products, so HBM stays busy while the prologue, the reductions and the epilogues run.
-template <int PRO, int EPI, int NCB, int RU, int NT, bool IDX>
-__global__ __launch_bounds__(NT) void k_gemv(GemvArgs a) {
-  __shared__ __align__(16) int8_t xq_lds[kMaxK];
-  __shared__ __align__(16) float xf_lds[PRO == PRO_NORM_QUANT ? kOsumLds : 1];
-  __shared__ __align__(16) float tab_lds[XStage<PRO, EPI, NCB, NT>::SFU ? kSfuWords : 1];
-  __shared__ float red[64];
-  const int row_in = blockIdx.y;                  // activation row (MoE prefill runs rows on grid y)
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// The tile walk of one wave: dot products of the wave's tile with the int8 activations in xq_lds,
+// the next tile requested right after them, the tile's row sums in one multi-value reduction, and
+// the dequant epilogue. Returns the wave's largest argmax key (0: none).
+template <int EPI, int NCB, int RU, bool IDX>
+T2R_DEV unsigned long long gemv_tiles(const GemvArgs& a, WTile<EPI, NCB, RU>& t, const float* res, int row_in, int r0,
+                                      int nwaves, float s_x, const int8_t* xq_lds, const float* tab_lds, int lane) {
   const int N = a.N, K = a.K;
-  const int nwaves = gridDim.x * (NT / 64);
-  const float* res = a.res ? a.res + row_in * a.res_stride : nullptr;
-  int r0 = (blockIdx.x * (NT / 64) + wave) * RU;
-  XStage<PRO, EPI, NCB, NT> st;
-  stage_load(st, a, row_in);
-  // keep the issue order: the prologue's loads strictly before the tile's (waits count in order)
-  __builtin_amdgcn_sched_barrier(0);
-  WTile<EPI, NCB, RU> t;
-  load_tile<EPI, NCB, RU, IDX>(t, a, res, row_in, r0, lane);
-  __builtin_amdgcn_sched_barrier(0);
-  const float s_x = stage_finish(st, a, row_in, xq_lds, xf_lds, tab_lds, red);
-  if (a.xq_out != nullptr && blockIdx.x == 0) {
-    for (int i = threadIdx.x; i < K; i += NT) a.xq_out[row_in * a.xq_stride + i] = xq_lds[i];
-    if (threadIdx.x == 0) a.sx_out[row_in] = s_x;
-  }
   int4 xr[NCB];
 #pragma unroll
   for (int c = 0; c < NCB; ++c) {
@@ -382,22 +361,159 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs a) {
       }
     }
   }
-  // greedy argmax: one atomic per block at most, skipped when the key already holds a larger one
-  if (a.argmax_key != nullptr) {
-    __shared__ unsigned long long bk[NT / 64];
-    for (int o = 1; o < 64; o <<= 1) {
-      const unsigned long long other = __shfl_xor(best, o);
-      best = other > best ? other : best;
-    }
-    if (lane == 0) bk[wave] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      unsigned long long b = bk[0];
-      for (int w = 1; w < NT / 64; ++w) b = bk[w] > b ? bk[w] : b;
-      unsigned long long* key = a.argmax_key + row_in;
-      if (b != 0 && b > __atomic_load_n(key, __ATOMIC_RELAXED)) atomicMax(key, b);
-    }
+  return best;
+}
+
+// greedy argmax over the block's NW waves: one atomic per block at most, skipped when the key
+// already holds a larger one. Every wave of the block calls it (it has a barrier).
+template <int NW>
+T2R_DEV void gemv_argmax(const GemvArgs& a, unsigned long long best, int row_in, int lane, int wave) {
+  __shared__ unsigned long long bk[NW];
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned long long other = __shfl_xor(best, o);
+    best = other > best ? other : best;
   }
+  if (lane == 0) bk[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long b = bk[0];
+    for (int w = 1; w < NW; ++w) b = bk[w] > b ? bk[w] : b;
+    unsigned long long* key = a.argmax_key + row_in;
+    if (b != 0 && b > __atomic_load_n(key, __ATOMIC_RELAXED)) atomicMax(key, b);
+  }
+}
+
+// NCB: 1024-byte column chunks per row covered by the register slice (K <= NCB * 1024);
+// RU: rows per wave tile; NT: threads per block. A wave's first tile is requested right after the
+// prologue's inputs and before the prologue runs, and each next tile right after the current one's
+// dot products, so HBM stays busy while the prologue, the reductions and the epilogues run.
+template <int PRO, int EPI, int NCB, int RU, int NT, bool IDX>
+__global__ __launch_bounds__(NT) void k_gemv(GemvArgs a) {
+  __shared__ __align__(16) int8_t xq_lds[kMaxK];
+  __shared__ __align__(16) float xf_lds[PRO == PRO_NORM_QUANT ? kOsumLds : 1];
+  __shared__ __align__(16) float tab_lds[XStage<PRO, EPI, NCB, NT>::SFU ? kSfuWords : 1];
+  __shared__ float red[64];
+  const int row_in = blockIdx.y;                  // activation row (MoE prefill runs rows on grid y)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int K = a.K;
+  const int nwaves = gridDim.x * (NT / 64);
+  const float* res = a.res ? a.res + row_in * a.res_stride : nullptr;
+  const int r0 = (blockIdx.x * (NT / 64) + wave) * RU;
+  XStage<PRO, EPI, NCB, NT> st;
+  stage_load(st, a, row_in);
+  // keep the issue order: the prologue's loads strictly before the tile's (waits count in order)
+  __builtin_amdgcn_sched_barrier(0);
+  WTile<EPI, NCB, RU> t;
+  load_tile<EPI, NCB, RU, IDX>(t, a, res, row_in, r0, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const float s_x = stage_finish(st, a, row_in, xq_lds, xf_lds, tab_lds, red);
+  if (a.xq_out != nullptr && blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < K; i += NT) a.xq_out[row_in * a.xq_stride + i] = xq_lds[i];
+    if (threadIdx.x == 0) a.sx_out[row_in] = s_x;
+  }
+  const unsigned long long best = gemv_tiles<EPI, NCB, RU, IDX>(a, t, res, row_in, r0, nwaves, s_x, xq_lds, tab_lds, lane);
+  if (a.argmax_key != nullptr) gemv_argmax<NT / 64>(a, best, row_in, lane, wave);
+}
+
+// RMSNorm + quant_act of row `row` by one wave (the block's wave 0), with the numerics of
+// stage_finish<PRO_NORM_QUANT>: squares F(x * x) in the lane-major layout, the ordered sum by
+// lanes [0, D), RSQRT, x F(x r) g, max |x| over the row, RECIP of s_x, to_i8. Writes the SFU
+// tables to tab_lds, the int8 row to xq_lds and s_x to *sx_lds. Only this wave's own LDS writes are
+// read back before the block's barrier: a wave's LDS accesses complete in program order.
+template <int NCB>
+T2R_DEV void pw_prologue(const GemvArgs& a, int row, int8_t* xq_lds, float* xf_lds, float* tab_lds, float* sx_lds,
+                         int lane) {
+  constexpr int NX = 4 * NCB;                     // float4 per lane: K <= 1024 NCB
+  constexpr int NTB = kSfuWords / 256;            // table float4 per lane
+  const int K = a.K;
+  const float* x = a.x + row * a.x_stride;
+  v4f_t tb[NTB];
+  float4 xv4[NX], g4[NX];
+#pragma unroll
+  for (int s = 0; s < NTB; ++s) tb[s] = ((const v4f_t*)a.tab)[lane + 64 * s];
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    const int i = min((lane + 64 * j) * 4, K - 4);  // clamped: elements past K are never used
+    xv4[j] = *(const float4*)(x + i);
+    g4[j] = *(const float4*)(a.g + i);
+  }
+#pragma unroll
+  for (int s = 0; s < NTB; ++s) ((v4f_t*)tab_lds)[lane + 64 * s] = tb[s];
+  float xv[4 * NX];
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    xv[4 * j] = xv4[j].x; xv[4 * j + 1] = xv4[j].y; xv[4 * j + 2] = xv4[j].z; xv[4 * j + 3] = xv4[j].w;
+  }
+  const int P = osum_stride(K, a.D);
+#pragma unroll
+  for (int j = 0; j < NX; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = (lane + 64 * j) * 4 + e;
+      if (i < K) xf_lds[osum_index(i, a.D, P)] = xv[4 * j + e] * xv[4 * j + e];
+    }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  float rr = 0.0f;
+  if (lane < a.D) {
+    const float ss = ordered_sum_t<false>(xf_lds, K, a.D, P, lane);
+    rr = sfu_rsqrt(ss * a.inv_n + a.eps, tab_lds);
+  }
+  const float r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rr), 0));
+  uint32_t am = 0;
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    xv[4 * j] = (xv[4 * j] * r) * g4[j].x;
+    xv[4 * j + 1] = (xv[4 * j + 1] * r) * g4[j].y;
+    xv[4 * j + 2] = (xv[4 * j + 2] * r) * g4[j].z;
+    xv[4 * j + 3] = (xv[4 * j + 3] * r) * g4[j].w;
+    if ((lane + 64 * j) * 4 < K)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) am = max(am, abs_bits(xv[4 * j + e]));
+  }
+  const float s_x = fv(wave_max_u32(am)) * kInv127;
+  const float inv = sfu_recip(s_x, tab_lds);
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    const int i = (lane + 64 * j) * 4;
+    if (i < K)
+      *(int*)(xq_lds + i) = pack_i8x4(to_i8(xv[4 * j] * inv), to_i8(xv[4 * j + 1] * inv), to_i8(xv[4 * j + 2] * inv),
+                                      to_i8(xv[4 * j + 3] * inv));
+  }
+  if (lane == 0) *sx_lds = s_x;
+}
+
+// The RMSNorm GEMV with a prologue wave: wave 0 of each block loads the row, the gain and the SFU
+// tables and runs the whole prologue (pw_prologue); waves 1..WS issue their weight tiles at once and
+// wait at the block's barrier. The prologue's instructions then never sit behind a tile's load
+// issue (a wave issues in order, and a CU accepts new loads only as its outstanding ones drain), and
+// the chain of the ordered sum runs while the weights stream. Same results as k_gemv<PRO_NORM_QUANT>.
+// Bounded to three waves per SIMD (<= 168 VGPRs), so that a 9-wave block fits on one CU beside
+// another kernel's tail.
+template <int EPI, int NCB, int RU, int WS>
+__global__ __launch_bounds__(64 * (WS + 1), 3) void k_gemv_pw(GemvArgs a) {
+  static_assert(EPI != EPI_RESID, "the prologue-wave GEMV has no residual operand");
+  __shared__ __align__(16) int8_t xq_lds[kMaxK];
+  __shared__ __align__(16) float xf_lds[kOsumLds];
+  __shared__ __align__(16) float tab_lds[kSfuWords];
+  __shared__ float sx_lds;
+  const int row_in = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int K = a.K;
+  const int nwaves = gridDim.x * WS;
+  const int r0 = (blockIdx.x * WS + wave - 1) * RU;
+  WTile<EPI, NCB, RU> t;
+  if (wave == 0) pw_prologue<NCB>(a, row_in, xq_lds, xf_lds, tab_lds, &sx_lds, lane);
+  else load_tile<EPI, NCB, RU, false>(t, a, nullptr, row_in, r0, lane);
+  __syncthreads();
+  const float s_x = sx_lds;
+  if (a.xq_out != nullptr && blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < K; i += 64 * (WS + 1)) a.xq_out[row_in * a.xq_stride + i] = xq_lds[i];
+    if (threadIdx.x == 0) a.sx_out[row_in] = s_x;
+  }
+  unsigned long long best = 0;
+  if (wave > 0) best = gemv_tiles<EPI, NCB, RU, false>(a, t, nullptr, row_in, r0, nwaves, s_x, xq_lds, tab_lds, lane);
+  if (a.argmax_key != nullptr) gemv_argmax<WS + 1>(a, best, row_in, lane, wave);
 }
 
 }  // namespace t2r
