@@ -92,13 +92,13 @@ inline bool gemv_operands_ok(const GemvArgs& a) {
 // the longer path (Qwen3-0.6B's 3072 rows: decode 1,217 -> 1,187 tok/s in that form).
 constexpr int kPwWaves = 8;
 constexpr int kPwMinBlocks = 256;
+constexpr int kPwMaxBlocks = 512;
 
 template <int EPI, int NCB>
 bool gemv_pw_try(const GemvArgs& a, int rows, hipStream_t st, int& rc) {
   const GemvShape g = gemv_shape<NCB>(a.N);
-  int blocks = cdiv_i(cdiv_i(a.N, g.ru), kPwWaves);
-  if (a.ids != nullptr || blocks < kPwMinBlocks) return false;
-  if (blocks > 2048 / kPwWaves) blocks = 2048 / kPwWaves;   // the waves then walk several tiles
+  const int blocks = cdiv_i(cdiv_i(a.N, g.ru), kPwWaves);   // one tile per streaming wave
+  if (a.ids != nullptr || blocks < kPwMinBlocks || blocks > kPwMaxBlocks) return false;
   dim3 grid(blocks, rows), block(64 * (kPwWaves + 1));
   constexpr int RUMAX = gemv_rumax<NCB>();
   if (g.ru == 1) launch((k_gemv_pw<EPI, NCB, 1, kPwWaves>), grid, block, 0, st, a);

@@ -285,8 +285,9 @@ T2R_DEV float stage_finish(const XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& 
 
 // The tile walk of one wave: dot products of the wave's tile with the int8 activations in xq_lds,
 // the next tile requested right after them, the tile's row sums in one multi-value reduction, and
-// the dequant epilogue. Returns the wave's largest argmax key (0: none).
-template <int EPI, int NCB, int RU, bool IDX>
+// the dequant epilogue. Returns the wave's largest argmax key (0: none). WALK false: the grid covers
+// every row in one tile per wave, so no next tile is ever requested (nor held in registers).
+template <int EPI, int NCB, int RU, bool IDX, bool WALK = true>
 T2R_DEV unsigned long long gemv_tiles(const GemvArgs& a, WTile<EPI, NCB, RU>& t, const float* res, int row_in, int r0,
                                       int nwaves, float s_x, const int8_t* xq_lds, const float* tab_lds, int lane) {
   const int N = a.N, K = a.K;
@@ -314,7 +315,7 @@ T2R_DEV unsigned long long gemv_tiles(const GemvArgs& a, WTile<EPI, NCB, RU>& t,
       sw3[u] = EPI == EPI_SWIGLU ? t.sw3[u] : 0.0f;
       rs[u] = EPI == EPI_RESID ? t.res[u] : 0.0f;
     }
-    if (r0 + nwaves * RU < N) load_tile<EPI, NCB, RU, IDX>(t, a, res, row_in, r0 + nwaves * RU, lane);
+    if (WALK && r0 + nwaves * RU < N) load_tile<EPI, NCB, RU, IDX>(t, a, res, row_in, r0 + nwaves * RU, lane);
     // the tile's RU row sums (and W3's) in one multi-value reduction: lane L ends with sum
     // (L >> SH) & (NV - 1) of vv; the lanes holding W1's sum of row u (and, beside them, W3's)
     // finish row r0 + u
@@ -360,6 +361,7 @@ T2R_DEV unsigned long long gemv_tiles(const GemvArgs& a, WTile<EPI, NCB, RU>& t,
         }
       }
     }
+    if (!WALK) break;
   }
   return best;
 }
@@ -420,9 +422,15 @@ __global__ __launch_bounds__(NT) void k_gemv(GemvArgs a) {
 // lanes [0, D), RSQRT, x F(x r) g, max |x| over the row, RECIP of s_x, to_i8. Writes the SFU
 // tables to tab_lds, the int8 row to xq_lds and s_x to *sx_lds. Only this wave's own LDS writes are
 // read back before the block's barrier: a wave's LDS accesses complete in program order.
+// where pw_prologue parks x in its LDS scratch: past the lane-major squares (at most D * P = 2080
+// floats for K <= 2048), with room for K <= 2048 values of its own
+constexpr int kPwXNat = 4096;
+static_assert(kPwXNat + 2048 <= kOsumLds, "pw_prologue's LDS scratch");
+
 template <int NCB>
 T2R_DEV void pw_prologue(const GemvArgs& a, int row, int8_t* xq_lds, float* xf_lds, float* tab_lds, float* sx_lds,
                          int lane) {
+  static_assert(NCB <= 2, "pw_prologue holds K <= 2048");
   constexpr int NX = 4 * NCB;                     // float4 per lane: K <= 1024 NCB
   constexpr int NTB = kSfuWords / 256;            // table float4 per lane
   const int K = a.K;
@@ -439,19 +447,20 @@ T2R_DEV void pw_prologue(const GemvArgs& a, int row, int8_t* xq_lds, float* xf_l
   }
 #pragma unroll
   for (int s = 0; s < NTB; ++s) ((v4f_t*)tab_lds)[lane + 64 * s] = tb[s];
-  float xv[4 * NX];
+  // the squares in the lane-major layout of the ordered sum, and x itself parked in LDS (at
+  // kPwXNat, past the squares) so that its registers are free during the chain
+  const int P = osum_stride(K, a.D);
+  float* xnat = xf_lds + kPwXNat;
 #pragma unroll
   for (int j = 0; j < NX; ++j) {
-    xv[4 * j] = xv4[j].x; xv[4 * j + 1] = xv4[j].y; xv[4 * j + 2] = xv4[j].z; xv[4 * j + 3] = xv4[j].w;
-  }
-  const int P = osum_stride(K, a.D);
-#pragma unroll
-  for (int j = 0; j < NX; ++j)
+    const float e4[4] = {xv4[j].x, xv4[j].y, xv4[j].z, xv4[j].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = (lane + 64 * j) * 4 + e;
-      if (i < K) xf_lds[osum_index(i, a.D, P)] = xv[4 * j + e] * xv[4 * j + e];
+      if (i < K) xf_lds[osum_index(i, a.D, P)] = e4[e] * e4[e];
     }
+    *(float4*)(xnat + (lane + 64 * j) * 4) = xv4[j];
+  }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
   float rr = 0.0f;
@@ -460,6 +469,12 @@ T2R_DEV void pw_prologue(const GemvArgs& a, int row, int8_t* xq_lds, float* xf_l
     rr = sfu_rsqrt(ss * a.inv_n + a.eps, tab_lds);
   }
   const float r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rr), 0));
+  float xv[4 * NX];
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    const float4 v = *(const float4*)(xnat + (lane + 64 * j) * 4);
+    xv[4 * j] = v.x; xv[4 * j + 1] = v.y; xv[4 * j + 2] = v.z; xv[4 * j + 3] = v.w;
+  }
   uint32_t am = 0;
 #pragma unroll
   for (int j = 0; j < NX; ++j) {
@@ -489,7 +504,7 @@ T2R_DEV void pw_prologue(const GemvArgs& a, int row, int8_t* xq_lds, float* xf_l
 // issue (a wave issues in order, and a CU accepts new loads only as its outstanding ones drain), and
 // the chain of the ordered sum runs while the weights stream. Same results as k_gemv<PRO_NORM_QUANT>.
 // Bounded to three waves per SIMD (<= 168 VGPRs), so that a 9-wave block fits on one CU beside
-// another kernel's tail.
+// another kernel's tail. The grid covers the N rows in one tile per streaming wave.
 template <int EPI, int NCB, int RU, int WS>
 __global__ __launch_bounds__(64 * (WS + 1), 3) void k_gemv_pw(GemvArgs a) {
   static_assert(EPI != EPI_RESID, "the prologue-wave GEMV has no residual operand");
@@ -512,7 +527,7 @@ __global__ __launch_bounds__(64 * (WS + 1), 3) void k_gemv_pw(GemvArgs a) {
     if (threadIdx.x == 0) a.sx_out[row_in] = s_x;
   }
   unsigned long long best = 0;
-  if (wave > 0) best = gemv_tiles<EPI, NCB, RU, false>(a, t, nullptr, row_in, r0, nwaves, s_x, xq_lds, tab_lds, lane);
+  if (wave > 0) best = gemv_tiles<EPI, NCB, RU, false, false>(a, t, nullptr, row_in, r0, nwaves, s_x, xq_lds, tab_lds, lane);
   if (a.argmax_key != nullptr) gemv_argmax<WS + 1>(a, best, row_in, lane, wave);
 }
 
