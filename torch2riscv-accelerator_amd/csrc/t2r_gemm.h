@@ -40,7 +40,10 @@ inline GemvShape gemv_shape(int N) {
   const int waves = cdiv_i(N, g.ru);
   g.nt = NCB >= 4 ? 512 : 256;
   g.blocks = cdiv_i(waves, g.nt / 64);
-  const int cap = 2048 * 256 / g.nt;
+  // at most 3072 waves (three per SIMD); a longer N walks more tiles per wave. Measured on the
+  // Llama-3.2-1B classifier (128256 rows): 42.6 us at 3072 waves against 46.6 at 8192, 45.2 at 4096
+  // and 43.7 at 2048.
+  const int cap = 3072 * 64 / g.nt;
   if (g.blocks > cap) g.blocks = cap;
   return g;
 }
