@@ -201,16 +201,21 @@ typedef struct t2r_model_desc {
 int64_t t2r_model_workspace_bytes(const t2r_model_desc* desc, int max_rows);
 /* Validates desc (shapes, pointers, workspace; layers <= 256) and returns a handle; copies desc. */
 int t2r_model_create(const t2r_model_desc* desc, void** model);
-/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph
- * capture, serving loops that forbid hipMalloc). t2r_model_create with desc->workspace = NULL and
- * desc->workspace_bytes = 0: the model's workspace is the library's static device array of
- * T2R_STATIC_WORKSPACE_BYTES on the current device, and the handle comes from a fixed pool of 8, so the
- * call allocates nothing. Models made this way on one device share that array: their calls (decode,
- * prefill, batched decode) must not overlap; calls in sequence are fine, each starts from scratch.
- * Returns T2R_ENOMEM when max_rows needs more than the array (t2r_model_workspace_bytes tells),
- * T2R_EINVAL when a workspace is given, T2R_ESTATE when the 8 handles are taken. t2r_model_destroy
- * returns the handle to the pool. */
+/* No counterpart in the reference: for callers that cannot allocate device memory (serving loops that
+ * forbid hipMalloc, code that later replays the model's calls from a captured HIP graph).
+ * t2r_model_create with desc->workspace = NULL and desc->workspace_bytes = 0: the model's workspace is
+ * the library's static device array of T2R_STATIC_WORKSPACE_BYTES on the current device, and the handle
+ * comes from a fixed pool of 8, so the call allocates nothing. Creation itself clears the model's state
+ * and synchronises the device: make the model before a capture starts; its decode, prefill and batched
+ * calls are then capturable. Each handle keeps the state it carries from call to call (the status word,
+ * the split attention's counters and sums) in its own part of the array (T2R_STATIC_STATE_BYTES in
+ * all); the rest is one call's scratch, shared by all such models on the device: their calls must not
+ * overlap, calls in sequence are fine. Returns T2R_ENOMEM when max_rows needs more than the array's
+ * scratch part (T2R_STATIC_WORKSPACE_BYTES - T2R_STATIC_STATE_BYTES; t2r_model_workspace_bytes tells,
+ * within the state's few KB), T2R_EINVAL when a workspace is given, T2R_ESTATE when the 8 handles are
+ * taken. t2r_model_destroy returns the handle to the pool. */
 #define T2R_STATIC_WORKSPACE_BYTES (16 * 1024 * 1024)
+#define T2R_STATIC_STATE_BYTES (512 * 1024)
 int t2r_model_create_static(const t2r_model_desc* desc, void** model);
 void t2r_model_destroy(void* model);
 /* One decode step (the reference's static token list: llm/compile_model.py:351-374, run per token
@@ -248,8 +253,10 @@ int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* position
 
 /* The model's status word (the reference's per-list status, llm/runtime.py:116-119): bit 0 a token
  * outside [0, vocab) was embedded (row 0 read instead); bit 1 a bounded wait between the workgroups of
- * a head's decode attention ran out (its output is then not to be trusted). Waits for the device;
- * clear != 0 then zeroes the word. */
+ * a head's decode attention ran out (its output is then not to be trusted); bit 2 a row's position
+ * (device memory: a replayed graph's advancing position, say) was outside the cache, and its attention
+ * neither read nor wrote the cache. The bits stay set until cleared. Waits for the device; clear != 0
+ * then zeroes the word. */
 int t2r_model_status(void* model, int32_t* out, int clear);
 
 /* Kernel timing of a resident model with HIP events on the launch stream (the GPU counterpart of

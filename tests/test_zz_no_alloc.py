@@ -85,3 +85,74 @@ def test_static_workspace_batched_and_rejections():
     assert lib.t2r_model_create_static(ctypes.byref(d2), ctypes.byref(h)) == abi.T2R_ENOMEM
     st.close()
     ref.close()
+
+
+def c3_small():
+    """C3's attention shape (head dim 128, QK-norm) with a 640-row cache, so that batch-1 decode splits
+    each head's keys over workgroups and carries counters from call to call; small elsewhere."""
+    import t2r_amd.config as C
+    return C.C3.with_(name="c3-small", dim=256, hidden=256, layers=2, heads=4, kv_heads=2, vocab=512, seq_len=640,
+                      seed_w=911, seed_p=912, prompt_len=530, weight_std=None, gain_std=0.1, emb_scale=4.0)
+
+
+def test_two_static_models_interleaved():
+    """Two static models of different max_rows alive at once (each handle keeps its carried state, the
+    status word and the split attention's counters, in its own part of the array; the rest is shared
+    scratch), their calls interleaved: prefills in their own chunk sizes, then decode steps in turn, each
+    equal bit for bit to an allocated model doing the same; no status bit set."""
+    from t2r_amd import weights as W
+    from t2r_amd.model import ResidentModel
+    cfg = c3_small()
+    qm = W.QuantModel(cfg)
+    rng = np.random.default_rng(5)
+    prompts = [cfg.prompt(), rng.integers(0, cfg.vocab, 522).tolist()]
+    rows = (64, 16)
+    st = [ResidentModel(qm, max_rows=r, static_workspace=True) for r in rows]
+    ref = [ResidentModel(qm, max_rows=r) for r in rows]
+    outs = {0: [], 1: []}
+    for k in (0, 1):
+        print(f"static model {k} (max_rows {rows[k]}): prefill {len(prompts[k])} rows", flush=True)
+        a = st[k].prefill(prompts[k]).cpu().numpy().copy()
+        b = ref[k].prefill(prompts[k]).cpu().numpy().copy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        outs[k].append(int(np.argmax(b)))
+    for i in range(3):
+        for k in (0, 1):
+            p = len(prompts[k]) + i
+            print(f"static model {k}: decode pos {p}", flush=True)
+            a = st[k].decode(outs[k][-1], p).cpu().numpy().copy()
+            b = ref[k].decode(outs[k][-1], p).cpu().numpy().copy()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"model {k} pos {p}"
+            outs[k].append(int(np.argmax(b)))
+    for k in (0, 1):
+        n = len(prompts[k]) + 3
+        assert np.array_equal(st[k].kc[:, :n].cpu().numpy(), ref[k].kc[:, :n].cpu().numpy())
+        assert st[k].status() == 0 and ref[k].status() == 0
+    for m in st + ref:
+        m.close()
+
+
+def test_static_create_allocates_nothing():
+    """t2r_model_create_static leaves the device's free memory unchanged (after one warm-up creation, which
+    may set up the runtime's own state)."""
+    import torch
+    import t2r_amd.config as C
+    from t2r_amd import abi
+    from t2r_amd import weights as W
+    from t2r_amd.model import ResidentModel
+    qm = W.QuantModel(C.get("tiny-qwen"))
+    ref = ResidentModel(qm, max_rows=8)
+    lib = abi.load()
+    d = abi.ModelDesc.from_buffer_copy(bytes(ref.desc))
+    d.workspace, d.workspace_bytes = None, 0
+    for i in range(2):
+        h = ctypes.c_void_p()
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        abi.check("t2r_model_create_static", lib.t2r_model_create_static(ctypes.byref(d), ctypes.byref(h)))
+        torch.cuda.synchronize()
+        free1 = torch.cuda.mem_get_info()[0]
+        lib.t2r_model_destroy(h)
+        if i == 1:
+            assert free1 == free0, f"creation took {free0 - free1} bytes of device memory"
+    ref.close()

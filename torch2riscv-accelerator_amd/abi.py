@@ -16,6 +16,7 @@ T2R_OK, T2R_EINVAL, T2R_ESHAPE, T2R_ERANGE, T2R_EHIP, T2R_ENOMEM, T2R_ESTATE = 0
 T2R_ADVANCE_POS = 1
 T2R_ATTN_QSUM = 1
 T2R_STATIC_WORKSPACE_BYTES = 16 * 1024 * 1024
+T2R_STATIC_STATE_BYTES = 512 * 1024
 
 c_int, c_int64, c_uint64, c_float, c_void_p = ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_void_p
 P = c_void_p    # every tensor argument is a raw device pointer

@@ -22,7 +22,9 @@ __constant__ float c_sfu[kSfuWords];
 }
 
 // The workspace of every model made by t2r_model_create_static on a device: one array per device,
-// held until the process ends and shared by all such models there (their calls must not overlap).
+// held until the process ends. Its first T2R_STATIC_STATE_BYTES hold each pool slot's carried state
+// (kStateSlotBytes a slot: the status word, the split attention's counters and SPLIT 1's sums), the
+// rest is the scratch of one call, shared by all such models there (their calls must not overlap).
 // Host code uses its per-device address from hipGetSymbolAddress (g_scratch_addr), never the name.
 static __device__ __align__(256) char scratch[T2R_STATIC_WORKSPACE_BYTES];
 
@@ -137,9 +139,15 @@ bool pre_ok(const AttnArgs& a) {
   return a.hd % 16 == 0 && a.hd <= 128 && attn_pre_lds_bytes(pre_cap(a), (a.hd + 31) & ~31) <= kPreMaxLds;
 }
 
-// batch-1 decode attention split over workgroups per head (k_attn_dec's SPLIT forms)
+// batch-1 decode attention split over workgroups per head (k_attn_dec's SPLIT forms): the heads of a
+// model whose shape takes it (head dim 128, caches over 512 rows, 4 splits a head in at most 256
+// workgroups), else 0
+constexpr int kSplits = 4;
+inline int split_heads(const t2r_model_desc& d) {
+  return d.head_dim == 128 && d.seq_len > 512 && d.heads * kSplits <= 256 ? d.heads : 0;
+}
 inline bool attn_split(const AttnArgs& a, int rows) {
-  return a.nsplit > 1 && rows == 1 && a.hd == 128 && a.sp_s && a.sp_o && a.sp_sync;
+  return a.nsplit > 1 && rows == 1 && a.hd == 128 && a.sp_s && a.sp_o && a.sp_acc && a.sp_sync;
 }
 // ... and whether it leaves its int32 P.V sums per split for the next linear (SPLIT 2) instead of att
 inline bool attn_split_to_linear(const AttnArgs& a, int rows) { return attn_split(a, rows) && !attn_opt(a); }
@@ -259,10 +267,14 @@ struct Model {
   int8_t* mxq;
   float* msx;
   int32_t* status;
-  // batch-1 decode attention split over workgroups per head: published scores [H, S], P.V sums
-  // [H, kMaxHd] and arrival counters [H, 2] (the last two zero between launches)
+  // batch-1 decode attention split over workgroups per head (nsplit > 1; 0 when the shape does not take
+  // it or the device cannot hold a launch's workgroups at once): published scores [H, S] and SPLIT 2's
+  // per-split P.V sums [4, H, kMaxHd] (both within one step); SPLIT 1's met sums [H, kMaxHd] and the
+  // arrival counters [H, 2], carried from launch to launch (zeroed at creation)
+  int nsplit = 0;
   float* sp_s;
   int32_t* sp_o;
+  int32_t* sp_acc;
   uint32_t* sp_sync;
   // MoE over many rows, grouped by expert: route lists, the routes' int8 expert outputs and scales,
   // and their weighted down projections (MoE models only)
@@ -325,9 +337,20 @@ struct Carve {
   }
 };
 
-long long carve(Model* m, char* base, int M) {
+// The state a model carries from one call to the next (the status word, the split attention's counters
+// and SPLIT 1's sums) comes first, from `state` when ext_state (a static model's own pool slot), else
+// from the workspace; the rest is the scratch of one call. Returns the workspace bytes; *state_bytes
+// (when given) the state's.
+long long carve(Model* m, char* base, int M, char* state = nullptr, bool ext_state = false,
+                long long* state_bytes = nullptr) {
   const t2r_model_desc& d = m->d;
-  Carve c{base, 0};
+  Carve c{base, 0}, cs{state, 0};
+  Carve& st = ext_state ? cs : c;
+  const int hs = split_heads(d);
+  m->status = st.take<int32_t>(1);
+  m->sp_sync = st.take<uint32_t>(2LL * hs);
+  m->sp_acc = st.take<int32_t>((long long)hs * kMaxHd);
+  if (state_bytes) *state_bytes = st.off;
   m->x = c.take<float>((long long)M * d.dim);
   m->qkv = c.take<float>((long long)M * m->qkv_dim);
   m->att = c.take<float>((long long)M * m->q_dim);
@@ -341,11 +364,9 @@ long long carve(Model* m, char* base, int M) {
   m->wts = c.take<float>((long long)M * k);
   m->mxq = c.take<int8_t>((long long)M * d.dim);
   m->msx = c.take<float>(M);
-  m->status = c.take<int32_t>(1);
   m->pos_rows = c.take<int32_t>(M);
-  m->sp_s = c.take<float>((long long)d.heads * d.seq_len);
-  m->sp_o = c.take<int32_t>(4LL * d.heads * kMaxHd);
-  m->sp_sync = c.take<uint32_t>(2LL * d.heads);
+  m->sp_s = c.take<float>((long long)hs * d.seq_len);
+  m->sp_o = c.take<int32_t>((long long)kSplits * hs * kMaxHd);
   if (d.n_experts > 0) {
     const long long routes = (long long)M * k;
     m->moe_off = c.take<int32_t>(d.n_experts + 1);
@@ -561,11 +582,12 @@ AttnArgs layer_attn_args(Model* m, int l, const int32_t* pos, int mode) {
   at.att = m->att; at.att_stride = m->q_dim;
   at.tab = sfu_table_ptr();
   at.qsum = d.attn_qsum;
+  at.status = m->status;
   // batch-1 decode at head dim 128 over caches of more than 512 rows: each head's keys over 4
-  // workgroups (k_attn_dec's SPLIT form); at most 256 workgroups, so all of them are resident at once
-  if (mode == RUN_DECODE && d.head_dim == 128 && d.seq_len > 512 && d.heads * 4 <= 256) {   // (4 splits: sp_o)
-    at.nsplit = 4;
-    at.sp_s = m->sp_s; at.sp_o = m->sp_o; at.sp_sync = m->sp_sync; at.sp_status = m->status;
+  // workgroups (k_attn_dec's SPLIT form), all of them resident at once (checked at creation)
+  if (mode == RUN_DECODE && m->nsplit > 1) {
+    at.nsplit = m->nsplit;
+    at.sp_s = m->sp_s; at.sp_o = m->sp_o; at.sp_acc = m->sp_acc; at.sp_sync = m->sp_sync;
   }
   if (m->kv_flags[l]) {
     const float* ch = d.kv_channel + (long long)l * 4 * m->kv_dim;   // s_k, 1/s_k, 1/s_v, a_v
@@ -793,17 +815,41 @@ int run_final(Model* m, int row, float* logits, int32_t* next_token, int32_t* po
   return T2R_OK;
 }
 
-// the model's state from a validated descriptor whose workspace is in dv (the caller's or the static one)
-int model_init(Model* m, const t2r_model_desc& dv) {
+// whether every workgroup of one split decode attention launch (kSplits per head) can be resident at
+// once on this device: the splits of a head wait for each other
+bool split_fits(const t2r_model_desc& d, int heads) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return false;
+  const void* ks[] = {(const void*)k_attn_dec<8, false, 2>, (const void*)k_attn_dec<8, true, 1>};
+  for (const void* k : ks) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kAttnThreads, attn_dec_lds_bytes(d.seq_len, d.D)) !=
+        hipSuccess)
+      return false;
+    if ((long long)per_cu * cus < (long long)heads * kSplits) return false;
+  }
+  return true;
+}
+
+// The model's state from a validated descriptor whose workspace is in dv (the caller's or the static
+// one's scratch part); state: a static model's slot for its carried state (else in the workspace).
+// Synchronises the device: creation is set-up, not a capturable call.
+int model_init(Model* m, const t2r_model_desc& dv, char* state = nullptr, long long state_cap = 0) {
   m->d = dv;
   const t2r_model_desc* desc = &m->d;
   model_dims(m);
-  if (carve(m, nullptr, desc->max_rows) > desc->workspace_bytes) return T2R_ENOMEM;
-  carve(m, (char*)desc->workspace, desc->max_rows);
-  // the status word, the split attention's sums and counters start clear
+  long long sb = 0;
+  if (carve(m, nullptr, desc->max_rows, nullptr, state != nullptr, &sb) > desc->workspace_bytes || sb > (state ? state_cap : sb))
+    return T2R_ENOMEM;
+  carve(m, (char*)desc->workspace, desc->max_rows, state, state != nullptr);
+  const int hs = split_heads(m->d);
+  m->nsplit = hs > 0 && split_fits(m->d, hs) ? kSplits : 0;
+  // the carried state starts clear: the status word, the split counters and SPLIT 1's sums
   if (hipMemset(m->status, 0, sizeof(int32_t)) != hipSuccess ||
-      hipMemset(m->sp_o, 0, sizeof(int32_t) * 4 * (size_t)desc->heads * kMaxHd) != hipSuccess ||
-      hipMemset(m->sp_sync, 0, sizeof(uint32_t) * 2 * (size_t)desc->heads) != hipSuccess ||
+      (hs > 0 && hipMemset(m->sp_acc, 0, sizeof(int32_t) * (size_t)hs * kMaxHd) != hipSuccess) ||
+      (hs > 0 && hipMemset(m->sp_sync, 0, sizeof(uint32_t) * 2 * (size_t)hs) != hipSuccess) ||
       hipDeviceSynchronize() != hipSuccess)
     return T2R_EHIP;
   std::memcpy(m->kvc, desc->kv_consts, sizeof(float) * 4 * desc->layers);
@@ -813,8 +859,11 @@ int model_init(Model* m, const t2r_model_desc& dv) {
   return T2R_OK;
 }
 
-// the handles of t2r_model_create_static: a fixed pool, so that creating one allocates nothing
+// the handles of t2r_model_create_static: a fixed pool, so that creating one allocates nothing; slot i's
+// carried state at i * kStateSlotBytes of the static array
 constexpr int kStaticModels = 8;
+constexpr long long kStateSlotBytes = T2R_STATIC_STATE_BYTES / kStaticModels;
+static_assert(kStateSlotBytes >= 256 + 2 * 4 * 64 + 256 + 64 * kMaxHd * 4, "a slot holds the state of 64 split heads");
 std::mutex g_pool_mu;
 Model g_pool[kStaticModels];
 bool g_pool_used[kStaticModels];
@@ -1088,8 +1137,8 @@ int t2r_model_create_static(const t2r_model_desc* desc, void** model) {
   T2R_INIT();
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices || !g_scratch_addr[dev]) return T2R_EHIP;
-  dv.workspace = g_scratch_addr[dev];
-  dv.workspace_bytes = T2R_STATIC_WORKSPACE_BYTES;
+  dv.workspace = g_scratch_addr[dev] + T2R_STATIC_STATE_BYTES;
+  dv.workspace_bytes = T2R_STATIC_WORKSPACE_BYTES - T2R_STATIC_STATE_BYTES;
   int rc = validate(&dv);
   if (rc) return rc;
   Model* m = nullptr;
@@ -1104,7 +1153,7 @@ int t2r_model_create_static(const t2r_model_desc* desc, void** model) {
       }
   }
   if (!m) return T2R_ESTATE;                     // every static model slot is taken
-  if ((rc = model_init(m, dv))) {
+  if ((rc = model_init(m, dv, g_scratch_addr[dev] + (long long)m->pool_slot * kStateSlotBytes, kStateSlotBytes))) {
     t2r_model_destroy(m);
     return rc;                                   // T2R_ENOMEM: max_rows needs more than the static array
   }

@@ -69,17 +69,34 @@ struct AttnArgs {
   const float* ch_isv;       // V per channel [kv_dim]: 1 / s_v for the cache row
   const float* ch_av;        //   and a_v per output channel
   // batch-1 decode with a head's keys split over nsplit workgroups (grid y; k_attn_dec's SPLIT forms,
-  // nsplit > 1): the scores published [H, S]; the P.V sums, int32 (SPLIT 1: met as [H, kMaxHd], zero
-  // between launches; SPLIT 2: each split's own [nsplit, H HD] for the next linear's prologue); per
-  // head two counters [H, 2]: the arrivals (every launch adds nsplit, so a launch's target is the
-  // next multiple of nsplit: never cleared) and SPLIT 1's finish count (zero between launches); the
-  // status word (bit 1: a bounded wait ran out)
+  // nsplit > 1): the scores published [H, S]; SPLIT 2's per-split int32 P.V sums [nsplit, H HD] for
+  // the next linear's prologue (written and read within one step); SPLIT 1's P.V sums met as
+  // [H, kMaxHd] (zero between launches); per head two counters [H, 2]: the arrivals (every launch
+  // adds nsplit, so a launch's target is the next multiple of nsplit: never cleared) and SPLIT 1's
+  // finish count (zero between launches)
   float* sp_s;
   int32_t* sp_o;
+  int32_t* sp_acc;
   uint32_t* sp_sync;
-  int32_t* sp_status;
   int nsplit;
+  // the model's status word (nullptr: none): bit 1 a split's bounded wait ran out, bit 2 a row's
+  // position was outside the cache (the row is then neither read nor written)
+  int32_t* status;
 };
+
+// a row whose position is outside the cache: its kernels end at once and flag it (bit 2)
+T2R_DEV void flag_bad_pos(int32_t* status) {
+  if (status) atomicOr(status, 4);
+}
+
+// Every vector memory operation of this wave (the stores and atomics that a release by another wave
+// of the workgroup is about to publish) completed before the wave passes on: a release at agent
+// scope waits only for its own wave's operations. The fence keeps the compiler from moving this
+// wave's accesses past the wait.
+T2R_DEV void wave_mem_done() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0x0F70);           // vmcnt(0): gfx9 encoding, expcnt / lgkmcnt untouched
+}
 
 // A bounded wait for *p to reach want (modulo 2^32) at device scope (one lane polls); on running out
 // it sets bit 1 of *status and returns, so every workgroup reaches its end whatever happens.
@@ -172,7 +189,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
   a.kc += row * a.kv_row_stride;                 // this row's sequence cache
   a.vc += row * a.kv_row_stride;
   const int pos = a.pos[row];
-  if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
+  if (pos < 0 || pos >= S) {                     // a position outside the cache: nothing is read or written
+    if (tid == 0) flag_bad_pos(a.status);
+    return;
+  }
   const int T = pos + 1;
   float* qkv = a.qkv + row * a.qkv_stride;
   constexpr int CW = CB / 4;                     // int32 words per chunk
@@ -425,7 +445,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   const long long q_dim = (long long)a.H * HD;
   const int kv_dim = a.Hk * HD;
   const int pos = a.pos[row];
-  if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
+  if (pos < 0 || pos >= S) {                     // a position outside the cache: nothing is read or written
+    if (tid == 0) flag_bad_pos(a.status);
+    return;
+  }
   const int T = pos + 1;
   // SPLIT: splits past the number of passes end here (all of a launch's workgroups agree on it);
   // SPLIT 2: with zero sums
@@ -627,14 +650,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     }
   }
   if constexpr (SPLIT) {
-    // every split's scores published (this workgroup's stores done at the barrier), then all T of
-    // them into sc from the published copy (the own ones read back unchanged); the max over them
+    // every split's scores published (every wave's stores complete before the barrier, so thread 0's
+    // release covers all of them), then all T of them into sc from the published copy (the own ones
+    // read back unchanged); the max over them
+    wave_mem_done();
     __syncthreads();
     uint32_t* arrive = a.sp_sync + 2 * h;
     if (tid == 0) {
       const uint32_t old = __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
       const uint32_t ns = (uint32_t)a.nsplit;
-      split_wait(arrive, old - old % ns + ns, a.sp_status);
+      split_wait(arrive, old - old % ns + ns, a.status);
     }
     __syncthreads();
     mloc = -__builtin_inff();
@@ -794,14 +819,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     return;
   }
   if constexpr (SPLIT == 1) {
-    // this split's sums into the head's (exact int32 device atomics); the last split to arrive
-    // finishes the output from them and clears them and the counters for the next launch
+    // this split's sums into the head's (exact int32 device atomics, every wave's complete before the
+    // barrier); the last split to arrive finishes the output from them and clears them and the
+    // counters for the next launch
     for (int j = tid; j < HD; j += kAttnThreads) {
       int ssum = 0;
 #pragma unroll
       for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
-      __hip_atomic_fetch_add(a.sp_o + (long long)h * kMaxHd + j, ssum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(a.sp_acc + (long long)h * kMaxHd + j, ssum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    wave_mem_done();
     __syncthreads();
     if (tid == 0)
       s_last = __hip_atomic_fetch_add(a.sp_sync + 2 * h + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -812,7 +839,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   for (int j = tid; j < HD; j += kAttnThreads) {
     int ssum = 0;
     if constexpr (SPLIT) {
-      int* o = a.sp_o + (long long)h * kMaxHd + j;
+      int* o = a.sp_acc + (long long)h * kMaxHd + j;
       ssum = __hip_atomic_load(o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(o, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
@@ -843,7 +870,10 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
   const int hd = a.hd;
   if (vi >= a.H + a.Hk) return;                  // (wave-uniform; the kernel has no block barrier)
   const int pos = a.pos[row];
-  if (pos < 0 || pos >= a.S) return;             // a position outside the cache: nothing is written
+  if (pos < 0 || pos >= a.S) {                   // a position outside the cache: nothing is written
+    if (lane == 0) flag_bad_pos(a.status);
+    return;
+  }
   const int q_dim = a.H * hd, kv_dim = a.Hk * hd;
   float* qkv = a.qkv + row * a.qkv_stride;
   const int32_t* pr = a.part + row * a.qkv_stride;
@@ -1314,7 +1344,10 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   const long long q_dim = (long long)a.H * HD;
   const int kv_dim = a.Hk * HD;
   const int pos = a.pos[row];
-  if (pos < 0 || pos >= S) return;               // a position outside the cache: nothing is read or written
+  if (pos < 0 || pos >= S) {                     // a position outside the cache: nothing is read or written
+    if (tid == 0) flag_bad_pos(a.status);
+    return;
+  }
   const int T = pos + 1;
   const float* qkv = a.qkv + row * a.qkv_stride;
   // cache rows [0, pos) of this KV head's columns: rows past pos - 1 read as zero

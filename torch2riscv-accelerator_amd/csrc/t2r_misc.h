@@ -15,7 +15,7 @@ __global__ __launch_bounds__(256) void k_embed(const int8_t* emb_q, const float*
   const int r = blockIdx.x;
   int t = tokens[r];
   if (t < 0 || t >= vocab) {
-    if (threadIdx.x == 0 && status) *status = 1;      // out-of-range token: row 0 of the table instead
+    if (threadIdx.x == 0 && status) atomicOr(status, 1);   // out-of-range token: row 0 of the table instead
     t = 0;
   }
   const float s = emb_s[t];

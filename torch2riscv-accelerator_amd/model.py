@@ -149,10 +149,20 @@ class ResidentModel:
 
     def status(self, clear=True):
         """The device status word (bit 0: a token outside the vocabulary was embedded; bit 1: a bounded
-        wait between the workgroups of a head's split decode attention ran out); waits for the device."""
+        wait between the workgroups of a head's split decode attention ran out; bit 2: a row's position
+        was outside the cache); waits for the device."""
         out = np.zeros(1, np.int32)
         abi.check("t2r_model_status", self.lib.t2r_model_status(self.handle, out.ctypes.data, int(clear)))
         return int(out[0])
+
+    def check_status(self, where):
+        """The reference's check after every list (llm/runtime.py:118-119, 202-203): a non-zero status
+        word raises RuntimeError(f"{where} failed, status {s:#x}") and is cleared, so the next call starts
+        clean. Waits for the device (the caller is about to read results anyway)."""
+        s = self.status(clear=False)
+        if s:
+            self.status(clear=True)
+            raise RuntimeError(f"{where} failed, status {s:#x}")
 
     def prefill(self, tokens, start=0, logits=True):
         """Rows tokens at positions start.. as one call per max_rows chunk; logits of the last row."""
@@ -263,5 +273,37 @@ class ResidentModel:
                 self.step(logits=False, advance=True)
         self.tok.copy_(tok)
         self.pos.copy_(pos)
+        torch.cuda.synchronize(self.device)
+        return g
+
+    def capture_prefill(self, tokens, start=0):
+        """A HIP graph of one prefill call (t2r_prefill_at) of `tokens` (at most max_rows) at positions
+        start..: the token ids are copied to the device first, so each replay runs the prompt's layers
+        with no host work (the prefill's ~8 launches a layer replayed at once); the last row's logits go
+        to self.logits and its greedy token to self.next. The KV rows are rewritten by every replay.
+        Kernel timing is switched off, as for capture_decode."""
+        torch = self.torch
+        toks = [int(t) for t in tokens]
+        M = len(toks)
+        if not 1 <= M <= self.max_rows or start < 0 or start + M > self.cfg.seq_len:
+            raise ValueError(f"{M} rows at {start}: 1..max_rows = {self.max_rows} rows inside the cache")
+        self._check_tokens(toks)
+        if getattr(self, "_prof_max", 0):
+            self.profile(kinds=())
+        self.rows_tok[:M].copy_(torch.tensor(toks, dtype=torch.int32))
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+
+        def call(st):
+            abi.check("t2r_prefill_at", self.lib.t2r_prefill_at(
+                self.handle, abi.ptr(self.rows_tok), int(start), M, abi.ptr(self.logits), abi.ptr(self.next),
+                abi.stream_ptr(st)))
+        with torch.cuda.stream(side):
+            call(side)                                  # one eager call on the capture stream first
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        with torch.cuda.graph(g, stream=side):
+            call(side)
         torch.cuda.synchronize(self.device)
         return g

@@ -142,6 +142,7 @@ class LlamaDevice:
             logits = lg.cpu().numpy().copy()
         except RuntimeError as e:
             raise RuntimeError(f"pos {self.pos}: step failed: {e}") from e
+        self.m.check_status(f"pos {self.pos}: list")       # RuntimeError("pos N: list failed, status 0x..")
         wall = time.perf_counter() - t0
         dev_ns = int(ev0.elapsed_time(ev1) * 1e6) if perf else None
         self.stats.append((self.pos, dev_ns, wall))
@@ -155,8 +156,10 @@ class LlamaDevice:
         if self.pos + len(tokens) > c.seq_len:
             raise ValueError(f"sequence full ({c.seq_len} positions)")
         lg = self.m.prefill(tokens, start=self.pos)
+        out = lg.cpu().numpy().copy()
+        self.m.check_status(f"pos {self.pos}: list")
         self.pos += len(tokens)
-        return lg.cpu().numpy().copy()
+        return out
 
     def generate(self, prompt, steps=256, temperature=0.0, topp=0.9, seed=1, stop_at_bos=True, forced=None):
         """Yield (token, text piece) per generated token, run.c style: the prompt tokens are fed first,
@@ -219,6 +222,7 @@ class LlamaDevice:
             gen[i + 1:i + 2].copy_(self.m.tok)
         self.pos = steps
         g = gen.cpu().numpy().tolist()
+        self.m.check_status(f"pos {done}..{steps - 1}: list")
         if done < P:
             return out
         return out + g[:steps - done + 1]
@@ -271,6 +275,7 @@ class BatchLlamaDevice:
             out = lg.cpu().numpy().copy()
         except RuntimeError as e:
             raise RuntimeError(f"step failed: {e}") from e
+        self.m.check_status("step")                        # RuntimeError("step failed, status 0x..")
         self.stats.append((int(ev0.elapsed_time(ev1) * 1e6) if perf else None, time.perf_counter() - t0))
         return out
 
