@@ -329,7 +329,14 @@ def gate_mul(h1, h3, act):
     return gelu_mul(h1, h3) if act == "gelu_tanh" else silu_mul(h1, h3)
 
 
-def attention(q, K, V, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None):
+# Mistakes the tests plant in attention() to show that the reference fixtures catch them (test use only):
+# "rq_av_first" F(att * F(rq * a_v)); "qsum_e" qsum's total over the exps instead of the int8
+# probabilities; "fold_head0" the K fold with KV head 0's scales for every head; "fold_after_quant" q
+# quantised, dequantised, folded and quantised again.
+PLANTS = ("rq_av_first", "qsum_e", "fold_head0", "fold_after_quant")
+
+
+def attention(q, K, V, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None, plant=None):
     """One query row q [H * hd] against the int8 cache rows K, V [T, Hk * hd] (llm/ref_model.py:230-243,
     GQA as compiler/frontend/qhf.py:304-319): per head quant_act(q), exact int32 scores
     F(F(f32(dot) * s_q) * a_k), e = EXP(F(s - max)), then
@@ -337,7 +344,8 @@ def attention(q, K, V, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None):
     - qsum (compiler/frontend/hf_generic.py:265-292): pq = to_i8(F(e * 127)),
       out = F(F(f32(pq . V) * F(RECIP(f32(sum pq)) * 127)) * a_v).
     ch_sk [Hk * hd]: K's per-channel scales, q = F(q * s_k) before its quant_act (hf_generic.py:252-254);
-    ch_av [Hk * hd]: a_v per output channel (hf_generic.py:183-186, 292)."""
+    ch_av [Hk * hd]: a_v per output channel (hf_generic.py:183-186, 292). plant: one of PLANTS (tests)."""
+    assert plant in (None,) + PLANTS
     T = K.shape[0]
     hd = q.shape[-1] // H
     G = H // Hk
@@ -346,8 +354,12 @@ def attention(q, K, V, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None):
     Kg = np.asarray(K).reshape(T, Hk, hd).transpose(1, 0, 2).astype(np.float64)      # (Hk, T, hd)
     Vg = np.asarray(V).reshape(T, Hk, hd).transpose(1, 0, 2).astype(np.float64)
     qh = np.asarray(q, F).reshape(H, hd)
-    if ch_sk is not None:
-        qh = (qh * per_head(ch_sk)).astype(F)
+    if ch_sk is not None and plant == "fold_after_quant":
+        qq, s_q = quant_act(qh)
+        qh = ((qq.astype(F) * s_q[:, None]).astype(F) * per_head(ch_sk)).astype(F)
+    elif ch_sk is not None:
+        sk = np.tile(np.asarray(ch_sk, F).reshape(Hk, hd)[:1], (H, 1)) if plant == "fold_head0" else per_head(ch_sk)
+        qh = (qh * sk).astype(F)
     qq, s_q = quant_act(qh)                                                          # (H, hd), (H,)
     qg = qq.astype(np.float64).reshape(Hk, G, hd)
     dots = np.matmul(qg, Kg.transpose(0, 2, 1)).reshape(H, T)                        # (H, T) exact
@@ -356,14 +368,17 @@ def attention(q, K, V, H, Hk, a_k, a_v, D, qsum=False, ch_sk=None, ch_av=None):
     e = sfu_exp((sc - np.max(sc, axis=-1, keepdims=True)).astype(F))
     if qsum:
         pq = to_i8((e * F(127)).astype(F)).astype(np.int64)
-        rq = (sfu_recip(pq.sum(-1).astype(F)) * F(127)).astype(F)                   # (H,), the sum exact
+        tot = red_sum(e, D) if plant == "qsum_e" else pq.sum(-1).astype(F)
+        rq = (sfu_recip(tot) * F(127)).astype(F)                                    # (H,), the sum exact
     else:
         r = sfu_recip(red_sum(e, D))
         pq = to_i8(((e * r[:, None]).astype(F) * F(127)).astype(F)).astype(np.int64)
     att = np.matmul(pq.astype(np.float64).reshape(Hk, G, T), Vg).reshape(H, hd).astype(F)   # exact sums
+    av = per_head(ch_av) if ch_av is not None else F(a_v)
+    if qsum and plant == "rq_av_first":
+        return (att * (rq[:, None] * av).astype(F)).astype(F).reshape(H * hd)
     if qsum:
         att = (att * rq[:, None]).astype(F)
-    av = per_head(ch_av) if ch_av is not None else F(a_v)
     return (att * av).astype(F).reshape(H * hd)
 
 

@@ -30,8 +30,21 @@ inputs and the reference's outputs, committed so the tests never need the refere
                        byte pieces, multi-byte UTF-8) and llm/tokenizer.Tokenizer's ids and text for it.
   sampler_golden.json  llm/runtime.Sampler (llm/runtime.py:37-72) draws on seeded logits at several
                        temperatures, top-p values and seeds.
+  hfopt_golden.npz     the HF path's numerics options as hf_generic computes them, in the device's numerics
+                       (torch.exp / torch.reciprocal as SfuExact's EXP / RECIP, as write_moe does; the only
+                       sum, qsum's total of the int8 probabilities, is exact in any order):
+                       - SaCache (compiler/frontend/hf_generic.py:136-229) built from per-layer or per-channel
+                         KV scales: its constants (1/s_k, s_k, a_k, 1/s_v, a_v) and the int8 cache rows its
+                         update() writes from seeded fp32 K / V rows (V_PACKED off: the row layout);
+                       - sa_attention (:231-293) of seeded query rows at several positions over that cache
+                         (qsum normalisation; K per channel folded into q; V per channel);
+                       - SaGELUTanh (:840-852) on a sweep through EXP overflow and the specials;
+                       - the logits_scaling fold (:909-917) of seeded classifier scales.
+  hf_tokenizer_golden.json  hf_tokenizer.BpeTokenizer (compiler/frontend/hf_tokenizer.py:11-205) on a
+                       synthetic byte-level tokenizer.json: ids and decoded text of sample texts.
 
-    python3 tests/golden/make_golden_hf.py [--reference /root/reference] [--only rope qmodel moe w8a8 tok sampler]
+    python3 tests/golden/make_golden_hf.py [--reference /root/reference]
+        [--only rope qmodel moe w8a8 tok sampler hfopt hftok]
 """
 import argparse
 import contextlib
@@ -283,6 +296,97 @@ def write_moe(hfg, out_path, D=16):
     np.savez_compressed(out_path, meta=np.frombuffer(json.dumps(meta).encode(), np.uint8), **arrays)
 
 
+# ------------------------------------------------------------------ the HF path's numerics options
+# (name, heads, kv heads, head dim, cache rows T, query positions, per-channel parts, KV spread, seed)
+HFOPT_PLAN = [
+    ("g2-hd16-layer", 4, 2, 16, 40, [0, 1, 15, 16, 17, 39], "", 1.0, 1),
+    ("g2-hd16-k", 4, 2, 16, 40, [0, 1, 15, 16, 17, 39], "k", 1.0, 2),
+    ("g1-hd32-v", 2, 2, 32, 33, [0, 7, 31, 32], "v", 1.0, 3),
+    ("g4-hd64-kv", 8, 2, 64, 70, [0, 5, 63, 64, 69], "kv", 1.0, 4),
+    ("g2-hd128-kv", 4, 2, 128, 300, [0, 100, 255, 256, 299], "kv", 1.0, 5),
+    ("g3-hd64-k-wide", 6, 2, 64, 90, [3, 50, 89], "k", 40.0, 6),        # scores spread past EXP's underflow
+]
+
+
+def write_hfopt(hfg, out_path):
+    """SaCache constants and cache rows, sa_attention outputs, SaGELUTanh and the logits fold (see the module
+    docstring), with torch.exp / torch.reciprocal as the device SFU."""
+    import torch
+    from types import SimpleNamespace
+    from transformers import LlamaConfig
+    from ref_model import SfuExact
+    assert not hfg.V_PACKED, "run with SA_V_PACKED=0: the row layout of the V cache"
+    sfu_exp = lambda t: torch.from_numpy(SfuExact.exp(t.detach().numpy().astype(F)))
+    sfu_rec = lambda t: torch.from_numpy(SfuExact.recip(t.detach().numpy().astype(F)))
+    arrays, meta = {}, []
+    for name, H, Hk, hd, T, positions, parts, spread, seed in HFOPT_PLAN:
+        rng = np.random.default_rng(3100 + seed)
+        kv_dim = Hk * hd
+        kf = (rng.standard_normal((T, kv_dim)) * rng.uniform(0.2, 3.0, kv_dim) * spread).astype(F)
+        vf = (rng.standard_normal((T, kv_dim)) * rng.uniform(0.2, 3.0, kv_dim)).astype(F)
+        q = (rng.standard_normal((len(positions), H * hd)) * 2.0).astype(F)
+        amax = np.stack([np.abs(kf).max(0), np.abs(vf).max(0)])                    # (2, kv_dim)
+        kv = (np.maximum(amax, 1e-8) / 127.0).astype(F)
+        for j, part in enumerate("kv"):
+            if part not in parts:
+                kv[j] = kv[j].max()                                                # one value: per layer
+        kv = kv[None]                                                              # (L = 1, 2, kv_dim)
+        cfg = LlamaConfig(hidden_size=H * hd, intermediate_size=16, num_hidden_layers=1, num_attention_heads=H,
+                          num_key_value_heads=Hk, head_dim=hd, vocab_size=32, max_position_embeddings=T)
+        owner = SimpleNamespace(kc=torch.zeros((T, kv_dim), dtype=torch.int8),
+                                vc=torch.zeros((T, kv_dim), dtype=torch.int8))
+        cache = hfg.SaCache(cfg, T, owner, kv)
+        assert (cache.k_ch[0], cache.v_ch[0]) == ("k" in parts, "v" in parts)
+        with torch.no_grad(), patched(torch, "exp", sfu_exp), patched(torch, "reciprocal", sfu_rec):
+            # the cache rows through the reference's update (key_states [1, Hk, M, hd])
+            cache.positions = torch.arange(T)
+            ks = torch.from_numpy(kf).reshape(T, Hk, hd).transpose(0, 1)[None]
+            vs = torch.from_numpy(vf).reshape(T, Hk, hd).transpose(0, 1)[None]
+            cache.layers[0].update(ks, vs)
+            key, value = owner.kc[0:T], owner.vc[0:T]
+            module = SimpleNamespace(sa_cache=cache, layer_idx=0)
+            outs = []
+            for m, p in enumerate(positions):
+                cache.positions = torch.tensor([p])
+                query = torch.from_numpy(q[m]).reshape(H, hd)[None, :, None, :]
+                o, _ = hfg.sa_attention(module, query, key, value, None)
+                outs.append(o.reshape(-1).numpy().astype(F))
+        f32 = lambda v: np.asarray(v.numpy() if torch.is_tensor(v) else v, F).reshape(-1)
+        key_ = f"a{len(meta)}"
+        arrays.update({key_ + "_kf": kf, key_ + "_vf": vf, key_ + "_q": q, key_ + "_kv": kv,
+                       key_ + "_kc": owner.kc.numpy().copy(), key_ + "_vc": owner.vc.numpy().copy(),
+                       key_ + "_out": np.asarray(outs, F),
+                       key_ + "_inv_sk": f32(cache.inv_sk[0]), key_ + "_inv_sv": f32(cache.inv_sv[0]),
+                       key_ + "_a_k": f32(cache.a_k[0]),
+                       key_ + "_a_v": f32(cache.a_v[0]),           # per channel: [Hk, G, hd], per query head
+                       key_ + "_sk": f32(cache.sk[0]) if cache.sk[0] is not None else np.zeros(0, F)})
+        meta.append({"key": key_, "name": name, "H": H, "Hk": Hk, "hd": hd, "T": T, "positions": positions,
+                     "parts": parts})
+        print(f"sa_attention {name}: {len(positions)} rows over {T} cache rows (K per channel {cache.k_ch[0]}, "
+              f"V per channel {cache.v_ch[0]})", flush=True)
+    # SaGELUTanh: a dense sweep through EXP's overflow (x < about -10.1) plus specials and extremes
+    rng = np.random.default_rng(3200)
+    xs = [np.linspace(-14.0, 14.0, 56001, dtype=np.float64).astype(F), (rng.standard_normal(20000) * 6).astype(F),
+          np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 1e-30, -1e-30, 1e19, -1e19, 1e20, -1e20,
+                    3e38, -3e38, -10.5, -10.0, -10.1, -10.2, 10.5, 89.0, -89.0], F)]
+    x = np.concatenate(xs).astype(F)
+    with torch.no_grad(), patched(torch, "exp", sfu_exp), patched(torch, "reciprocal", sfu_rec), \
+            np.errstate(over="ignore", invalid="ignore"):
+        g = hfg.SaGELUTanh()(torch.from_numpy(x)).numpy().astype(F)
+    arrays["gelu_x"], arrays["gelu_y"] = x, g
+    arrays["gelu_AB"] = np.array([hfg.SaGELUTanh.A, hfg.SaGELUTanh.B], F)
+    # the logits_scaling fold: head.s_w / float(ls) on a float32 tensor
+    s_w = (np.abs(rng.standard_normal(4096)) * 0.01 + 1e-4).astype(F)
+    folds = {}
+    for ls in (8.0, 3.0, 0.7, 1.0 / 3.0, 16.0, 10.0):
+        folds[repr(ls)] = (torch.from_numpy(s_w) / float(ls)).numpy().astype(F)
+    arrays["fold_s_w"] = s_w
+    arrays["fold_ls"] = np.array(list(map(float, folds)), np.float64)
+    arrays["fold_out"] = np.stack(list(folds.values()))
+    print(f"SaGELUTanh: {len(x)} inputs; logits fold: {len(folds)} scalings", flush=True)
+    np.savez_compressed(out_path, meta=np.frombuffer(json.dumps(meta).encode(), np.uint8), **arrays)
+
+
 # ------------------------------------------------------------------ .w8a8, tokenizer, sampler
 def write_w8a8(path):
     import checkpoint
@@ -357,6 +461,58 @@ def write_sampler(json_path):
     print(f"sampler: {len(runs)} runs", flush=True)
 
 
+HFTOK_CORPUS = ["hello world, hello there! The quick brown fox jumps over the lazy dog 12345 times.",
+                "Tokenizers split text into pieces; byte-level BPE keeps every byte: caf\u00e9, na\u00efve, \u4e16\u754c.",
+                "   leading spaces, trailing spaces   \n\nnew lines\ttabs and 2024-12-02 dates 3.14159",
+                "It's we're they've I'm you'll he'd -- punctuation!!! ??? ... $100 #tag @user"] * 4
+HFTOK_TEXTS = ["", "hello world", " hello  world ", "The quick brown fox.", "It's 2024: caf\u00e9 \u4e16\u754c!",
+               "\n\n  tabs\tand\nnewlines  ", "12345678901234567890", "unseen words zyxwv qqq",
+               "<|begin|>hello<|end|> world<|begin|>", "e\u0301 composed (NFC)", "\U0001F600 emoji!!",
+               "they've we'll I'd ... $$$"]
+
+
+def hftok_files():
+    """Two synthetic byte-level tokenizer.json files, trained here with the `tokenizers` library on a small
+    corpus: GPT-2 style (ByteLevel's own split) and Llama-3 style (NFC, a Split regex then ByteLevel
+    without its regex, ignore_merges), each with two added special tokens."""
+    from tokenizers import Regex, Tokenizer, decoders, models, normalizers, pre_tokenizers, trainers
+    out = []
+    for style in ("gpt2", "llama3"):
+        tk = Tokenizer(models.BPE(ignore_merges=style == "llama3"))
+        if style == "gpt2":
+            tk.pre_tokenizer = pre_tokenizers.ByteLevel(add_prefix_space=False)
+        else:
+            tk.normalizer = normalizers.NFC()
+            split = r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}{1,3}| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+"
+            tk.pre_tokenizer = pre_tokenizers.Sequence([
+                pre_tokenizers.Split(Regex(split), behavior="isolated"),
+                pre_tokenizers.ByteLevel(add_prefix_space=False, use_regex=False)])
+        tk.decoder = decoders.ByteLevel()
+        trainer = trainers.BpeTrainer(vocab_size=420, special_tokens=["<|begin|>", "<|end|>"],
+                                      initial_alphabet=pre_tokenizers.ByteLevel.alphabet(), show_progress=False)
+        tk.train_from_iterator(HFTOK_CORPUS, trainer)
+        out.append((style, tk.to_str()))
+    return out
+
+
+def write_hftok(json_path):
+    import hf_tokenizer
+    recs = []
+    for style, text in hftok_files():
+        with tempfile.TemporaryDirectory() as tmp:
+            with open(os.path.join(tmp, "tokenizer.json"), "w") as f:
+                f.write(text)
+            ref = hf_tokenizer.BpeTokenizer(tmp)
+            assert ref.exact, "the regex module is needed for the exact Unicode classes"
+            cases = []
+            for t in HFTOK_TEXTS:
+                ids = ref.encode(t)
+                cases.append({"text": t, "ids": ids, "decoded": ref.decode(ids)})
+        recs.append({"style": style, "tokenizer_json": text, "cases": cases})
+        print(f"hf_tokenizer {style}: {len(cases)} texts", flush=True)
+    json.dump({"generator": "tests/golden/make_golden_hf.py", "tokenizers": recs}, open(json_path, "w"), indent=0)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--reference", default="/root/reference")
@@ -365,7 +521,8 @@ def main():
     ref = args.reference
     for p in (os.path.join(ref, "llm"), os.path.join(ref, "driver"), os.path.join(ref, "compiler", "frontend")):
         sys.path.insert(0, p)
-    only = set(args.only or ["rope", "qmodel", "moe", "w8a8", "tok", "sampler"])
+    only = set(args.only or ["rope", "qmodel", "moe", "w8a8", "tok", "sampler", "hfopt", "hftok"])
+    os.environ["SA_V_PACKED"] = "0"      # hf_generic's V cache in the row layout (its flag is read at import)
     path = os.path.join(HERE, "qhf_golden.json")
     out = json.load(open(path)) if os.path.exists(path) else {}
     out["generator"] = "tests/golden/make_golden_hf.py"
@@ -379,8 +536,13 @@ def main():
     if "moe" in only:
         import hf_generic
         write_moe(hf_generic, os.path.join(HERE, "moe_golden.npz"))
+    if "hfopt" in only:
+        import hf_generic
+        write_hfopt(hf_generic, os.path.join(HERE, "hfopt_golden.npz"))
     if "w8a8" in only:
         write_w8a8(os.path.join(HERE, "w8a8_tiny.w8a8"))
+    if "hftok" in only:
+        write_hftok(os.path.join(HERE, "hf_tokenizer_golden.json"))
     if "tok" in only:
         write_tokenizer(os.path.join(HERE, "tokenizer_golden.bin"), os.path.join(HERE, "tokenizer_golden.json"))
     if "sampler" in only:

@@ -32,6 +32,32 @@ def quant_model(cfg, calib=64):
 
 
 # ------------------------------------------------------------------ op level
+def test_attention_options_equal_sa_attention(env):
+    """t2r_attn_decode_opt and t2r_attn_prefill (qsum; K / V per channel as each case has them) on the cache
+    rows the reference's SaCache wrote, against sa_attention's outputs in the device numerics
+    (tests/golden/hfopt_golden.npz, compiler/frontend/hf_generic.py:231-293): every bit."""
+    import json
+    import os
+    from types import SimpleNamespace
+    from t2r_amd import weights as W
+    torch, N, ops, T, H = env
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hfopt_golden.npz"))
+    for rec in json.loads(bytes(z["meta"]).decode()):
+        k, Hh, Hk, hd = rec["key"], rec["H"], rec["Hk"], rec["hd"]
+        kv = z[k + "_kv"]
+        cfg = SimpleNamespace(layers=1, head_dim=hd, kv_dim=Hk * hd)
+        fl, kvc, ch = int(W.kv_channel_flags(cfg, kv)[0]), W.kv_constants(cfg, kv)[0], W.kv_channel_constants(cfg, kv)[0]
+        args = dict(qsum=True, ch_sk=T(ch[0]) if fl & 1 else None, ch_av=T(ch[3]) if fl & 2 else None)
+        kc, vc, q = T(z[k + "_kc"]), T(z[k + "_vc"]), T(z[k + "_q"])
+        pos = T(np.asarray(rec["positions"], np.int32))
+        want = z[k + "_out"].view(np.uint32)
+        print(f"sa_attention case {rec['name']}", flush=True)
+        got = H(ops.attention_opt(q, kc, vc, pos, Hh, Hk, kvc[2], kvc[3], 16, **args))
+        assert np.array_equal(got.view(np.uint32), want), rec["name"]
+        got = H(ops.attention_prefill(q, kc, vc, pos, Hh, Hk, kvc[2], kvc[3], 16, **args))
+        assert np.array_equal(got.view(np.uint32), want), rec["name"] + " (prefill kernel)"
+
+
 def test_gated_ffn_gelu(env):
     """t2r_gated_ffn_w8a8 with the GELU-tanh gate over h1 out to about +-100 (EXP overflow to +inf, RECIP
     of +inf, signed zeros past +-10.5) against numerics.gelu_mul, and act 0 against the SiLU gate."""

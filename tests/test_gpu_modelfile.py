@@ -1,12 +1,14 @@
 """LlamaDevice on model files: a .w8a8 (version 1 and 2) with a tokenizer.bin next to it runs the
 same numbers as the in-memory model, and generate() takes text and yields text pieces
 (llm/runtime.py:75-146)."""
+import os
 import struct
 
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 LETTERS = [chr(c).encode() for c in range(ord("a"), ord("z") + 1)]
 
@@ -120,4 +122,31 @@ def test_compressed_tensors_on_device(tmp_path, kind):
     dev.m.reset()
     pre = dev.m.prefill(toks).cpu().numpy()
     assert np.array_equal(pre.view(np.uint32), want.view(np.uint32))
+    dev.close()
+
+
+def test_reference_w8a8_file_equals_device_model_run():
+    """The reference exporter's own file (tests/golden/w8a8_tiny.w8a8: llm/export_w8a8.export of the tiny
+    model at D = 8) through LlamaDevice, the reference's consumer path (llm/runtime.py:76-99, the file read
+    as llm/export_w8a8.py:133-167 lays it out), against the reference's DeviceModel(SfuExact) run of the
+    same model in model_golden.json: every position's logits (sha256 of the bytes), the argmax, and the
+    int8 KV cache."""
+    import hashlib
+    import json
+    from t2r_amd.runtime import LlamaDevice
+    gold = json.load(open(os.path.join(GOLD, "model_golden.json")))
+    run = next(r for r in gold["device_model"] if r["config"] == "tiny" and r["D"] == 8)
+    dev = LlamaDevice(os.path.join(GOLD, "w8a8_tiny.w8a8"), tokenizer_path=None)
+    assert dev.cfg.D == 8 and dev.cfg.layers == 2
+    assert np.array_equal(np.asarray(dev.qm.kv_scales, np.float32).reshape(-1).view(np.uint32),
+                          np.array(run["kv_bits"], np.uint32))
+    sha = lambda *a: hashlib.sha256(b"".join(np.ascontiguousarray(x).tobytes() for x in a)).hexdigest()
+    print(f"reference w8a8 file: {run['steps']} positions", flush=True)
+    for rec in run["positions"]:
+        assert dev.pos == rec["pos"]
+        lg = dev.forward(rec["token"])
+        assert sha(lg) == rec["logits_sha"], f"pos {rec['pos']}: logits differ from the reference's run"
+        assert int(np.argmax(lg)) == rec["argmax"]
+    n = run["steps"]
+    assert sha(dev.m.kc[:, :n].cpu().numpy(), dev.m.vc[:, :n].cpu().numpy()) == run["kv_sha"]
     dev.close()

@@ -258,3 +258,23 @@ def test_w8a8_hf_options_round_trip(tmp_path, name):
     if cfg.tied:
         assert back.cls_q is back.emb_q
         assert (cfg.logits_scaling == 1.0) == (back.cls_s is back.emb_s)
+
+
+def test_reference_w8a8_file_through_oracle_equals_device_model_run():
+    """The reference exporter's file (tests/golden/w8a8_tiny.w8a8) read by W8A8File / read_w8a8 and run by the
+    oracle reproduces the reference's DeviceModel(SfuExact) run of the same model (model_golden.json, tiny at
+    D = 8): every position's logits bytes and the KV cache. The GPU test runs the same file through LlamaDevice."""
+    import hashlib
+    import json
+    from oracle import OracleModel
+    gold_dir = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    gold = json.load(open(os.path.join(gold_dir, "model_golden.json")))
+    run = next(r for r in gold["device_model"] if r["config"] == "tiny" and r["D"] == 8)
+    qm = MF.read_w8a8(os.path.join(gold_dir, "w8a8_tiny.w8a8"))
+    assert qm.cfg.D == 8
+    sha = lambda *a: hashlib.sha256(b"".join(np.ascontiguousarray(x).tobytes() for x in a)).hexdigest()
+    om = OracleModel(qm)
+    for rec in run["positions"]:
+        assert sha(om.forward(rec["token"], rec["pos"])) == rec["logits_sha"], rec["pos"]
+    n = run["steps"]
+    assert sha(om.kc[:, :n], om.vc[:, :n]) == run["kv_sha"]

@@ -10,8 +10,15 @@ itself (tests/golden/make_golden_hf.py):
 - the .w8a8 bytes of llm/export_w8a8.export, llm/tokenizer.Tokenizer's ids and text, and
   llm/runtime.Sampler's draws.
 
+- the HF path's numerics options as hf_generic computes them in the device's numerics: SaCache's per-layer
+  and per-channel KV constants and the int8 rows its update() writes, sa_attention's outputs (qsum
+  normalisation, K per channel folded into q, V per channel), SaGELUTanh through EXP overflow and the logits
+  scaling fold, bit for bit; hf_tokenizer.BpeTokenizer's ids and text on two synthetic byte-level
+  tokenizer.json files against modelfile.HFTokenizer.
+
 Each QModel run also checks planted mistakes in the oracle (eps, theta, QK-norm after RoPE, the KV head of a
-query head) against the same fixture: each must fail it."""
+query head) against the same fixture: each must fail it; so do the attention mistakes of
+numerics.PLANTS and an expanded GELU-tanh exponent against the HF-option fixtures."""
 import hashlib
 import json
 import os
@@ -259,3 +266,124 @@ def test_sampler_equals_reference():
         s = Sampler(temperature=r["temperature"], topp=r["topp"], seed=r["seed"])
         assert [s(x) for x in lg] == r["draws"], (r["temperature"], r["topp"], r["seed"])
         assert str(s.state) == r["state"]
+
+
+# ------------------------------------------------------------------ the HF path's numerics options
+@pytest.fixture(scope="module")
+def hfopt():
+    z = np.load(os.path.join(GOLD, "hfopt_golden.npz"))
+    return json.loads(bytes(z["meta"]).decode()), z
+
+
+def _hf_case(z, rec):
+    """The oracle's constants and cache rows for one sa_attention case, from the case's KV scales."""
+    from types import SimpleNamespace
+    from t2r_amd import weights as W
+    k = rec["key"]
+    kv = z[k + "_kv"]
+    cfg = SimpleNamespace(layers=1, head_dim=rec["hd"], kv_dim=rec["Hk"] * rec["hd"])
+    flags = W.kv_channel_flags(cfg, kv)
+    kvc = W.kv_constants(cfg, kv)[0]                       # 1/s_k, 1/s_v, a_k, a_v per layer
+    ch = W.kv_channel_constants(cfg, kv)[0]                # s_k, 1/s_k, 1/s_v, a_v per channel
+    return int(flags[0]), kvc, ch
+
+
+def test_hf_kv_constants_and_cache_equal_sacache(hfopt):
+    """SaCache's constants (hf_generic.py:153-187) and the int8 rows its update() writes (:203-218) equal
+    weights.kv_constants / kv_channel_constants and the oracle's append to_i8(F(k * inv_s))."""
+    from oracle import numerics as N
+    meta, z = hfopt
+    u = lambda a: np.asarray(a, F).view(np.uint32)
+    for rec in meta:
+        k, fl, (kvc, ch) = rec["key"], *(lambda t: (t[0], t[1:]))(_hf_case(z, rec))
+        G = rec["H"] // rec["Hk"]
+        want_isk = ch[1] if fl & 1 else kvc[0:1]
+        want_isv = ch[2] if fl & 2 else kvc[1:2]
+        assert np.array_equal(u(z[k + "_inv_sk"]), u(want_isk)), rec["name"]
+        assert np.array_equal(u(z[k + "_inv_sv"]), u(want_isv)), rec["name"]
+        assert np.array_equal(u(z[k + "_a_k"]), u(kvc[2:3])), rec["name"]
+        if fl & 1:
+            want_sk = np.repeat(ch[0].reshape(rec["Hk"], 1, rec["hd"]), G, 1).reshape(-1)    # per query head
+            assert np.array_equal(u(z[k + "_sk"]), u(want_sk)), rec["name"]
+        want_av = np.repeat(ch[3].reshape(rec["Hk"], 1, rec["hd"]), G, 1).reshape(-1) if fl & 2 else kvc[3:4]
+        assert np.array_equal(u(z[k + "_a_v"]), u(want_av)), rec["name"]
+        kc = N.to_i8((z[k + "_kf"] * want_isk).astype(F))
+        vc = N.to_i8((z[k + "_vf"] * want_isv).astype(F))
+        assert np.array_equal(kc, z[k + "_kc"]) and np.array_equal(vc, z[k + "_vc"]), rec["name"]
+
+
+def _hf_attention(z, rec, plant=None):
+    """numerics.attention (qsum, the case's per-channel options) of every query row of a case: [rows, H hd]."""
+    from oracle import numerics as N
+    k = rec["key"]
+    fl, kvc, ch = _hf_case(z, rec)
+    out = []
+    for m, p in enumerate(rec["positions"]):
+        out.append(N.attention(z[k + "_q"][m], z[k + "_kc"][:p + 1], z[k + "_vc"][:p + 1], rec["H"], rec["Hk"],
+                               kvc[2], kvc[3], 16, qsum=True, ch_sk=ch[0] if fl & 1 else None,
+                               ch_av=ch[3] if fl & 2 else None, plant=plant))
+    return np.asarray(out, F)
+
+
+def test_hf_attention_equals_sa_attention(hfopt):
+    """sa_attention (hf_generic.py:231-293) with the device SFU: every output bit, on GQA groups of 1-4, head
+    dims 16-128, per-layer, K, V and K+V per-channel scales, positions at and past D-lane boundaries, and a
+    case whose scores spread past EXP's underflow."""
+    meta, z = hfopt
+    for rec in meta:
+        got = _hf_attention(z, rec)
+        want = z[rec["key"] + "_out"]
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rec["name"]
+
+
+@pytest.mark.parametrize("plant", ["rq_av_first", "qsum_e", "fold_head0", "fold_after_quant"])
+def test_hf_attention_planted_mistakes_fail(hfopt, plant):
+    from oracle import numerics as N
+    assert plant in N.PLANTS
+    meta, z = hfopt
+    caught = [rec["name"] for rec in meta
+              if not np.array_equal(_hf_attention(z, rec, plant).view(np.uint32), z[rec["key"] + "_out"].view(np.uint32))]
+    assert caught, f"{plant}: no sa_attention case tells it from the reference"
+
+
+def test_gelu_tanh_equals_sagelutanh(hfopt):
+    """SaGELUTanh (hf_generic.py:840-852) with the device SFU on 76k inputs (a dense sweep over [-14, 14]
+    through EXP's overflow, random values, specials): every bit (NaN as NaN); its constants A and B; and an
+    expanded exponent F(F(x A) + F(F(F(x x) x) B)) misses the fixture."""
+    from oracle import numerics as N
+    _, z = hfopt
+    x, want = z["gelu_x"], z["gelu_y"]
+    assert np.array_equal(z["gelu_AB"].view(np.uint32), np.array([N.GELU_A, N.GELU_B], F).view(np.uint32))
+    got = N.gelu_tanh(x)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    with np.errstate(over="ignore", invalid="ignore"):
+        zexp = ((x * N.GELU_A).astype(F) + ((((x * x).astype(F) * x).astype(F)) * N.GELU_B).astype(F)).astype(F)
+        bad = (x * N.sfu_recip((N.sfu_exp(zexp) + F(1)).astype(F))).astype(F)
+    assert not np.array_equal(bad[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_logits_fold_equals_reference(hfopt):
+    """head.s_w / float(ls) (hf_generic.py:909-917) equals weights.fold_logits_scaling bit for bit."""
+    from t2r_amd import weights as W
+    _, z = hfopt
+    for ls, want in zip(z["fold_ls"], z["fold_out"]):
+        got = W.fold_logits_scaling(z["fold_s_w"], float(ls))
+        assert np.array_equal(np.asarray(got, F).view(np.uint32), want.view(np.uint32)), ls
+
+
+def test_hf_tokenizer_equals_reference_port(tmp_path):
+    """modelfile.HFTokenizer (the tokenizers library) equals the reference's own byte-level BPE port
+    (compiler/frontend/hf_tokenizer.py:11-205) on a GPT-2-style and a Llama-3-style tokenizer.json: ids and
+    decoded text of every sample (added tokens, NFC, digits, whitespace runs, multi-byte characters)."""
+    from t2r_amd.modelfile import HFTokenizer
+    gold = json.load(open(os.path.join(GOLD, "hf_tokenizer_golden.json")))
+    for rec in gold["tokenizers"]:
+        d = tmp_path / rec["style"]
+        d.mkdir()
+        (d / "tokenizer.json").write_text(rec["tokenizer_json"])
+        tk = HFTokenizer(str(d))
+        for case in rec["cases"]:
+            assert tk.encode(case["text"], bos=False) == case["ids"], (rec["style"], case["text"])
+            assert tk.decode(case["ids"]) == case["decoded"], (rec["style"], case["text"])
