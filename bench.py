@@ -72,6 +72,21 @@ def measured_traffic(kind, cfg_name):
     return None
 
 
+def profiled_avg_us(kind, cfg_name):
+    """The dominant kernel's average duration in the committed rocprofv3 --kernel-trace --stats summary of
+    this bench (profiles/gemv_swiglu_c4_decode.md, line `rocprof_avg_us: <class> <config> <us>`), so that the
+    line's roofline fraction follows from profiles/; None when not recorded for this configuration."""
+    path = os.path.join(ROOT, "profiles", "gemv_swiglu_c4_decode.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("rocprof_avg_us:"):
+            _, k, c, v = line.split()
+            if k == kind and c == cfg_name:
+                return float(v)
+    return None
+
+
 def host_cpu():
     """This host's CPU model, logical cores, and the BLAS threads the oracle's matrix products use."""
     model = "unknown"
@@ -208,6 +223,21 @@ def main():
         times.append(time.perf_counter() - t)
     prefill_s = float(np.median(times[1:])) if len(times) > 1 else times[0]
     log(f"prefill {P} rows: {prefill_s * 1e3:.2f} ms ({P / prefill_s:.0f} tok/s)")
+    # the same prefill replayed from a HIP graph (no host launch work)
+    prefill_graph_s = None
+    if not args.no_graph and P <= rm.max_rows:
+        gp = rm.capture_prefill(prompt)
+        gts = []
+        for r in range(args.prefill_reps + 1):
+            rm.reset()
+            sync()
+            t = time.perf_counter()
+            gp.replay()
+            sync()
+            gts.append(time.perf_counter() - t)
+        prefill_graph_s = float(np.median(gts[1:])) if len(gts) > 1 else gts[0]
+        del gp
+        log(f"prefill {P} rows from a HIP graph: {prefill_graph_s * 1e3:.2f} ms")
     # the prefill GEMMs' int8 MFMA rate: one more prefill with HIP events around each GEMM launch
     prefill_gemm, g_ms, g_tops = prefill_gemm_rates(rm, cfg, prompt)
     if g_tops:
@@ -345,7 +375,15 @@ def main():
     if dom_ms:                                              # from the timed region itself
         dom = {"launches": len(dom_ms), "avg_us": round(sum(dom_ms) / len(dom_ms) * 1e3, 3),
                "GBps": round(nbytes["ffn_up"] / (sum(dom_ms) / len(dom_ms) * 1e-3) / 1e9, 1)}
-    achieved = dom.get("GBps")
+    achieved_event = dom.get("GBps")
+    # the line's fraction from the committed rocprofv3 summary's average (reproducible from profiles/); the
+    # live HIP-event timing of the same kernel beside it
+    prof_us = profiled_avg_us("ffn_up", cfg.name)
+    if prof_us:
+        achieved, avg_us, src = round(nbytes["ffn_up"] / (prof_us * 1e-6) / 1e9, 1), prof_us, \
+            "rocprofv3 --kernel-trace --stats average, profiles/gemv_swiglu_c4_decode.md"
+    else:
+        achieved, avg_us, src = achieved_event, dom.get("avg_us"), "HIP events in this run"
     out = {
         "metric": "decode & prefill tok/s at batch 1; W8A8 GEMV % of HBM peak",
         "value": round(tok_s, 2),
@@ -364,6 +402,7 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "prefill_tok_s": round(P / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 3),
+        "prefill_graph_ms": round(prefill_graph_s * 1e3, 3) if prefill_graph_s else None,
         "kernels": classes,
         "gemv_all_GBps": round(gemv_b / gemv_t / 1e9, 1) if gemv_t else None,
         "gemv_all_frac": round(gemv_b / gemv_t / 1e9 / HBM_PEAK_GBS, 4) if gemv_t else None,
@@ -374,8 +413,11 @@ def main():
         "roofline": {"kernel": "k_gemv_pw<EPI_SWIGLU> (fused RMSNorm + SwiGLU decode GEMV, prologue wave)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-                     "bytes_per_launch": nbytes["ffn_up"], "avg_us": dom.get("avg_us"),
-                     "launches": dom.get("launches"), "traffic": measured_traffic("ffn_up", cfg.name)},
+                     "bytes_per_launch": nbytes["ffn_up"], "avg_us": avg_us, "duration_source": src,
+                     "traffic": measured_traffic("ffn_up", cfg.name),
+                     "avg_us_event": dom.get("avg_us"), "achieved_event": achieved_event,
+                     "frac_event": round(achieved_event / HBM_PEAK_GBS, 4) if achieved_event else None,
+                     "launches_event": dom.get("launches")},
     }
 
     # ---- CPU baseline at the GPU run's positions (+ a bit-exactness spot check of those positions)
@@ -421,6 +463,7 @@ def per_config(args, c4_out):
         cfg = C.get(key)
         if c4_out is not None and cfg.name == args.config:
             table[cfg.name] = {"gpu_decode_tok_s": c4_out["value"], "gpu_prefill_tok_s": c4_out["prefill_tok_s"],
+                               "gpu_prefill_ms": c4_out["prefill_ms"], "gpu_prefill_graph_ms": c4_out["prefill_graph_ms"],
                                "prefill_gemm_TOPS": c4_out["prefill_gemm"].get("all", {}).get("TOPS"),
                                "prefill_gemm_frac": c4_out["prefill_gemm"].get("all", {}).get("frac"),
                                "cpu_decode_tok_s": c4_out["cpu_baseline"]["value"],
@@ -442,6 +485,21 @@ def per_config(args, c4_out):
             ts.append(time.perf_counter() - t)
         pre = float(np.median(ts[1:]))
         tok0 = int(rm.next.item())
+        # the same prefill replayed from a HIP graph (prompts of at most 512 rows: one t2r_prefill_at call)
+        pre_g = None
+        if P <= 512:
+            gp = rm.capture_prefill(prompt)
+            gts = []
+            for _ in range(4):
+                rm.reset()
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                gp.replay()
+                torch.cuda.synchronize()
+                gts.append(time.perf_counter() - t)
+            pre_g = float(np.median(gts[1:]))
+            assert int(rm.next.item()) == tok0, "the prefill graph's greedy token differs from the eager prefill's"
+            del gp
         gemm, _, g_tops = prefill_gemm_rates(rm, cfg, prompt)
         # GPU decode: a HIP graph of the config's decode steps (at most 64) from the prompt's end
         K = max(1, min(cfg.decode_steps, 64, cfg.seq_len - P))
@@ -459,7 +517,10 @@ def per_config(args, c4_out):
         torch.cuda.synchronize()
         gdt = time.perf_counter() - t
         del g
-        rec = {"prompt": P, "gpu_prefill_tok_s": round(P / pre, 1), "gpu_decode_tok_s": round(K / gdt, 1),
+        rec = {"prompt": P, "gpu_prefill_tok_s": round(P / pre, 1), "gpu_prefill_ms": round(pre * 1e3, 3),
+               "gpu_prefill_graph_ms": round(pre_g * 1e3, 3) if pre_g else None,
+               "gpu_prefill_graph_tok_s": round(P / pre_g, 1) if pre_g else None,
+               "gpu_decode_tok_s": round(K / gdt, 1),
                "gpu_decode_steps": K, "decode_positions": f"{P}..{P + K - 1}",
                "prefill_gemm_TOPS": gemm.get("all", {}).get("TOPS"), "prefill_gemm_frac": gemm.get("all", {}).get("frac")}
         if c4_out is not None:

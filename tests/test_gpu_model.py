@@ -245,3 +245,34 @@ def test_status_word_and_token_range():
     assert rm.status() == 1
     assert rm.status() == 0
     rm.close()
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen", "c2-smollm2-135m"])
+def test_prefill_graph_replays_equal_eager(name):
+    """ResidentModel.capture_prefill: a HIP graph of one t2r_prefill_at call, replayed three times with eager
+    work between the replays (the cache cleared, an eager decode step), each replay's last logits, greedy
+    token and KV rows equal to the eager prefill's."""
+    import torch
+    import t2r_amd.config as C
+    cfg = C.get(name)
+    toks = cfg.prompt()[:40]
+    qm, rm = resident(cfg, max_rows=len(toks))
+    rm.reset()
+    want = rm.prefill(toks).cpu().numpy().copy()
+    nxt = int(rm.next.item())
+    kv = kv_host(rm, len(toks))
+    g = rm.capture_prefill(toks)
+    for i in range(3):
+        rm.reset()
+        rm.logits.zero_()
+        print(f"{name}: prefill graph replay {i}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        got = rm.logits.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {i}"
+        assert int(rm.next.item()) == nxt
+        a, b = kv_host(rm, len(toks))
+        assert np.array_equal(a, kv[0]) and np.array_equal(b, kv[1])
+        rm.decode(nxt, len(toks))                          # eager work between the replays
+    assert rm.status() == 0
+    rm.close()
