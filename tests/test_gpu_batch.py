@@ -11,7 +11,8 @@ pytestmark = pytest.mark.gpu
 # head dims 64 and 128, groups of 2, 3 and 4 query heads, QK-norm and MoE.
 @pytest.mark.parametrize("name,B", [("tiny", 4), ("tiny-gqa", 3), ("tiny-qwen", 4), ("tiny-moe", 4),
                                     ("c1-stories15m", 8), ("c2-smollm2-135m", 4), ("c3-qwen3-0.6b", 3),
-                                    ("c4-llama3.2-1b", 4), ("c5-granite-1b-a400m", 4)])
+                                    ("c4-llama3.2-1b", 4), ("c5-granite-1b-a400m", 4),
+                                    ("tiny-gqa", 40), ("c2-smollm2-135m", 36)])   # (33..64 rows: two row groups)
 def test_decode_batch_equals_single(name, B):
     import torch
     import t2r_amd.config as C

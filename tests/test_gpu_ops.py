@@ -126,7 +126,8 @@ def test_ieee_vector_steps_keep_subnormals(env):
 
 @pytest.mark.parametrize("N_,K,M", [(1, 16, 1), (37, 288, 1), (300, 2048, 1), (129, 8192, 1), (64, 1040, 3),
                                      (257, 3072, 5), (3072, 2048, 512), (40, 48, 77), (130, 288, 33),
-                                     (2048, 8192, 130), (16, 16, 1000), (200, 576, 70), (1536, 1600, 260)])
+                                     (2048, 8192, 130), (16, 16, 1000), (200, 576, 70), (1536, 1600, 260),
+                                     (960, 576, 40), (576, 1536, 64), (96, 8192, 63), (3072, 2048, 48)])
 def test_linear_exact(env, N_, K, M):
     torch, N, ops, T, H = env
     rng = np.random.default_rng(N_ * 7 + K)

@@ -92,6 +92,13 @@ int ensure_init() {
   for (const void* f : gqa)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGqaMaxLds) != hipSuccess)
       return T2R_EHIP;
+  // the two-row-group batched GEMV at eight waves: 8 x 8448 bytes of LDS (the int32 tile of 64 rows)
+  const void* bg2[] = {(const void*)k_bgemv<EPI_STORE, 8, false, 2>, (const void*)k_bgemv<EPI_STORE, 8, true, 2>,
+                       (const void*)k_bgemv<EPI_RESID, 8, false, 2>, (const void*)k_bgemv<EPI_RESID, 8, true, 2>,
+                       (const void*)k_bgemv<EPI_SWIGLU, 8, false, 2>};
+  for (const void* f : bg2)
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 8 * bg_wave_lds(2)) != hipSuccess)
+      return T2R_EHIP;
   if (hipFuncSetAttribute((const void*)k_gemm_d<EPI_SWIGLU, false, 128, 3, 2 * kGT>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmDTallLds) != hipSuccess)
     return T2R_EHIP;
@@ -531,7 +538,7 @@ int rows_linear(Model* m, const int8_t* w, const float* s_w, const int8_t* w3, c
   a.act = m->d.ffn_act;
   if (m->pend_z > 1) return T2R_ESTATE;          // the partials buffer still holds an unfinished linear
   if (argmax_done) *argmax_done = false;
-  if (argmax && EPI == EPI_STORE && rows <= kBgMaxRows) {
+  if (argmax && EPI == EPI_STORE && rows <= kBgMaxRows * kBgMaxGroups) {
     a.argmax_key = argmax;
     const int r = bgemv_launch<EPI>(a, st, nullptr);
     if (r == 0) {

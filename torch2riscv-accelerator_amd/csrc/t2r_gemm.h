@@ -614,7 +614,7 @@ int gemm_d_launch(const GemmArgs& a, hipStream_t st, int z, int* defer_z) {
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-// ---- batched decode linears (M <= 32 activation rows): y[m][n] on int8 MFMA with every weight
+// ---- batched decode linears (M <= 64 activation rows): y[m][n] on int8 MFMA with every weight
 // byte read once, in whole 128-byte lines. A workgroup takes a tile of 32 weight rows (SwiGLU: 16
 // rows of W1 and the same 16 of W3) and kBgWin-byte k-windows of it, one window per wave at a time:
 // the wave copies its 32 x 256-byte window into its own 8 KB of LDS with global_load_lds (four rows
@@ -623,15 +623,21 @@ int gemm_d_launch(const GemmArgs& a, hipStream_t st, int z, int* defer_z) {
 // row lane % 32, B: weight row lane % 32, the same 16 k-bytes in both: exact int32 sums). No
 // workgroup barrier until the waves' tiles are added in LDS. With nz > 1 the windows are split over
 // nz workgroups per tile, which write int32 partials [nz, M, N] for k_gemm_fin. Activation rows past
-// M read row M - 1 and are never stored.
+// M read row M - 1 and are never stored. MG row groups of 32 (M <= 32 MG): each weight fragment read
+// from LDS feeds MG MFMAs, one per group's activation rows (a prompt of 33..64 rows streams the
+// weights once instead of filling one mostly empty 128-row tile of the prefill GEMM).
 constexpr int kBgMaxRows = 32;
+constexpr int kBgMaxGroups = 2;                   // M <= kBgMaxRows * kBgMaxGroups
 constexpr int kBgWin = 256;                       // k-bytes of a wave window
 constexpr int kBgWaveLds = 32 * kBgWin;           // one wave's window of 32 weight rows
+// LDS per wave: the window, or the wave's int32 tile [32 MG][33] when that is larger
+__host__ __device__ constexpr int bg_wave_lds(int MG) { return 32 * MG * 33 * 4 > kBgWaveLds ? 32 * MG * 33 * 4 : kBgWaveLds; }
 
 
-template <int EPI, int KW, bool SPLIT>
+template <int EPI, int KW, bool SPLIT, int MG = 1>
 __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
-  extern __shared__ __align__(16) int8_t lds[];    // KW x kBgWaveLds
+  constexpr int WS = bg_wave_lds(MG);
+  extern __shared__ __align__(16) int8_t lds[];    // KW x WS
   __shared__ __align__(16) float tab_lds[EPI == EPI_SWIGLU ? kSfuWords : 4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, kh = lane >> 5;
@@ -640,7 +646,7 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
   const int n0 = tile * NT, K = a.K;
   const int nwin = cdiv_i(K, kBgWin), wpz = cdiv_i(nwin, nz);
   const int w_end = min(nwin, (z + 1) * wpz);
-  int8_t* wl = lds + wave * kBgWaveLds;
+  int8_t* wl = lds + wave * WS;
   if (EPI == EPI_SWIGLU && tid < kSfuWords / 4) ((v4f_t*)tab_lds)[tid] = ((const v4f_t*)a.tab)[tid];
   // chunk q of window row r sits at 256 r + 16 (q ^ (r & 15)): the 16 rows a 16-lane LDS pass reads
   // (rows {0-3, 8-11, 20-23, 28-31} or the other 16 of a half-wave, one chunk) hit 16 bank groups
@@ -653,10 +659,12 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
     if (EPI == EPI_SWIGLU) rowp[i] = (r < 16 ? a.w : a.w3) + (long long)min(n0 + (r & 15), a.N - 1) * K;
     else rowp[i] = a.w + (long long)min(n0 + r, a.N - 1) * K;
   }
-  const int8_t* xrow = a.xq + (long long)min(lr, a.M - 1) * K + 16 * kh;
+  const int8_t* xrow[MG];
+#pragma unroll
+  for (int g = 0; g < MG; ++g) xrow[g] = a.xq + (long long)min(32 * g + lr, a.M - 1) * K + 16 * kh;
   // the epilogue's scales and residuals, loaded now (their latency hides under the weight stream):
   // output i of this thread is o = tid + i 64 KW, (m, j) = (o / NT, o % NT)
-  constexpr int OPT = (32 * NT + 64 * KW - 1) / (64 * KW);
+  constexpr int OPT = (32 * MG * NT + 64 * KW - 1) / (64 * KW);
   float e_sx[OPT], e_sw[OPT], e_sw3[OPT], e_res[OPT];
   if constexpr (!SPLIT) {
 #pragma unroll
@@ -668,33 +676,40 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
       if (EPI == EPI_RESID) e_res[i] = a.res[(long long)m * a.y_stride + n];
     }
   }
-  v16i_t acc;
+  v16i_t acc[MG];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0;
+  for (int g = 0; g < MG; ++g)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[g][r] = 0;
   for (int w = z * wpz + wave; w < w_end; w += KW) {
     const int k0 = w * kBgWin, nst = min(kBgWin, K - k0) >> 5;   // k-steps of this window (uniform)
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < 8; ++i)                                 // (chunks past K: clamped, unused)
       __builtin_amdgcn_global_load_lds((const void*)(rowp[i] + min(k0 + qo[i], K - 16)), (void*)(wl + 1024 * i), 16, 0, 0);
-    v4i_t xv[8];
+    v4i_t xv[MG][8];
 #pragma unroll
-    for (int st = 0; st < 8; ++st) xv[st] = *(const v4i_t*)(xrow + min(k0 + 32 * st, K - 32));
+    for (int g = 0; g < MG; ++g)
+#pragma unroll
+      for (int st = 0; st < 8; ++st) xv[g][st] = *(const v4i_t*)(xrow[g] + min(k0 + 32 * st, K - 32));
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       if (st < nst) {
         const v4i_t wv = *(const v4i_t*)(wl + 256 * lr + 16 * ((2 * st + kh) ^ (lr & 15)));
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[st], wv, acc, 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < MG; ++g) acc[g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[g][st], wv, acc[g], 0, 0, 0);
       }
     }
   }
-  // the wave's 32 x 32 tile into its own LDS (its DMA has landed and its reads are done)
+  // the wave's 32 MG x 32 tile into its own LDS (its DMA has landed and its reads are done)
   asm volatile("" ::: "memory");
   int* red = (int*)wl;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) red[((r >> 2) * 8 + kh * 4 + (r & 3)) * 33 + lr] = acc[r];
+  for (int g = 0; g < MG; ++g)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(32 * g + (r >> 2) * 8 + kh * 4 + (r & 3)) * 33 + lr] = acc[g][r];
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < OPT; ++i) {
@@ -705,7 +720,7 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
       if (m < a.M && n < a.N) {
         int s = 0;
 #pragma unroll
-        for (int v = 0; v < KW; ++v) s += ((const int*)(lds + v * kBgWaveLds))[m * 33 + j];
+        for (int v = 0; v < KW; ++v) s += ((const int*)(lds + v * WS))[m * 33 + j];
         key = argmax_key(dequant(s, e_sw[i], e_sx[i]), n);
       }
 #pragma unroll
@@ -721,7 +736,7 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
     int s1 = 0, s3 = 0;
 #pragma unroll
     for (int v = 0; v < KW; ++v) {
-      const int* rv = (const int*)(lds + v * kBgWaveLds);
+      const int* rv = (const int*)(lds + v * WS);
       s1 += rv[m * 33 + j];
       if (EPI == EPI_SWIGLU) s3 += rv[m * 33 + 16 + j];
     }
@@ -743,12 +758,32 @@ __global__ __launch_bounds__(64 * KW) void k_bgemv(GemmArgs a, int nz) {
   }
 }
 
-// the batched-decode linear when it applies (1 <= M <= 32, K % 32 == 0, 16-byte aligned rows), else -1.
+// the batched-decode linear when it applies (1 <= M <= 64, K % 32 == 0, 16-byte aligned rows), else -1.
 // Waves per workgroup: one per window up to 8; the windows split over up to 4 workgroups per tile when
 // the caller finishes the partials (defer_z) and its buffer (a.part, a.part_cap int32) holds them.
+template <int EPI, int MG>
+void bgemv_go(const GemmArgs& a, hipStream_t st, int kw, int nz, dim3 grid, bool split) {
+  const size_t lb = (size_t)kw * bg_wave_lds(MG);
+  auto go = [&](auto kern) { launch(kern, grid, dim3(64 * kw), lb, st, a, nz); };
+  if (split) {
+    if constexpr (EPI != EPI_SWIGLU) {
+      if (kw == 8) go(k_bgemv<EPI, 8, true, MG>);
+      else if (kw == 4) go(k_bgemv<EPI, 4, true, MG>);
+      else if (kw == 2) go(k_bgemv<EPI, 2, true, MG>);
+      else go(k_bgemv<EPI, 1, true, MG>);
+    }
+  } else {
+    if (kw == 8) go(k_bgemv<EPI, 8, false, MG>);
+    else if (kw == 4) go(k_bgemv<EPI, 4, false, MG>);
+    else if (kw == 2) go(k_bgemv<EPI, 2, false, MG>);
+    else go(k_bgemv<EPI, 1, false, MG>);
+  }
+}
+
 template <int EPI>
 int bgemv_launch(const GemmArgs& a, hipStream_t st, int* defer_z) {
-  if (a.M < 1 || a.M > kBgMaxRows || a.K % 32 || ((uintptr_t)a.w & 15) || ((uintptr_t)a.xq & 15)) return -1;
+  if (a.M < 1 || a.M > kBgMaxRows * kBgMaxGroups || a.K % 32 || ((uintptr_t)a.w & 15) || ((uintptr_t)a.xq & 15))
+    return -1;
   if (EPI == EPI_SWIGLU && (!a.tab || !a.w3 || ((uintptr_t)a.tab & 15) || ((uintptr_t)a.w3 & 15))) return -1;
   const int nwin = cdiv_i(a.K, kBgWin);
   const int kw = nwin >= 8 ? 8 : nwin >= 4 ? 4 : nwin >= 2 ? 2 : 1;
@@ -758,23 +793,13 @@ int bgemv_launch(const GemmArgs& a, hipStream_t st, int* defer_z) {
   const long long blocks = (long long)cdiv_i(a.N, EPI == EPI_SWIGLU ? 16 : 32) * nz;
   if (blocks > 0x7FFFFFFF) return -2;
   if (defer_z) *defer_z = nz;
-  const dim3 grid((unsigned)blocks), block(64 * kw);
-  const size_t lb = (size_t)kw * kBgWaveLds;
-  auto go = [&](auto kern) { launch(kern, grid, block, lb, st, a, nz); };
-  if (nz > 1) {
-    if constexpr (EPI != EPI_SWIGLU) {
-      if (kw == 8) go(k_bgemv<EPI, 8, true>);
-      else if (kw == 4) go(k_bgemv<EPI, 4, true>);
-      else if (kw == 2) go(k_bgemv<EPI, 2, true>);
-      else go(k_bgemv<EPI, 1, true>);
-      const long long total = (long long)a.M * a.N;
-      if (!defer_z) launch((k_gemm_fin<EPI>), dim3((unsigned)min(4096LL, (total + 255) / 256)), dim3(256), 0, st, a, nz);
-    }
-  } else {
-    if (kw == 8) go(k_bgemv<EPI, 8, false>);
-    else if (kw == 4) go(k_bgemv<EPI, 4, false>);
-    else if (kw == 2) go(k_bgemv<EPI, 2, false>);
-    else go(k_bgemv<EPI, 1, false>);
+  const dim3 grid((unsigned)blocks);
+  if (a.M > kBgMaxRows) bgemv_go<EPI, 2>(a, st, kw, nz, grid, nz > 1);
+  else bgemv_go<EPI, 1>(a, st, kw, nz, grid, nz > 1);
+  if constexpr (EPI != EPI_SWIGLU) {
+    const long long total = (long long)a.M * a.N;
+    if (nz > 1 && !defer_z)
+      launch((k_gemm_fin<EPI>), dim3((unsigned)min(4096LL, (total + 255) / 256)), dim3(256), 0, st, a, nz);
   }
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
@@ -786,7 +811,7 @@ template <int EPI>
 int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0, int* defer_z = nullptr) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 16) return -2;
   if (EPI == EPI_SWIGLU && (a.tab == nullptr || ((uintptr_t)a.tab & 15))) return -1;
-  if (a.M <= kBgMaxRows) {                                 // few rows: stream the weights once
+  if (a.M <= kBgMaxRows * kBgMaxGroups) {                 // few rows: stream the weights once
     const int r = bgemv_launch<EPI>(a, st, EPI == EPI_SWIGLU ? nullptr : defer_z);
     if (r != -1) return r;
   }
