@@ -292,6 +292,7 @@ def main():
         dt, mode = eager_dt, "eager"
     tok_s = steps / dt
     log(f"decode {mode}: {steps} steps, {dt / steps * 1e3:.3f} ms/token ({tok_s:.1f} tok/s)")
+    rm.check_status("decode")                               # a replay's device status (RuntimeError if set)
 
     # (3) batched decode: B sequences per step, each continuing the prompt from its own copy of the
     # prompt's KV rows; greedy tokens and positions stay on the device
@@ -353,6 +354,7 @@ def main():
                 del g
             except Exception as e:                          # capture not available: eager timing only
                 log(f"batched HIP graph capture failed ({e}); eager timing")
+        rm.check_status(f"batched decode B={B}")
         batch[str(B)] = {"tok_s": round(B * K / bdt, 1), "ms_per_step": round(bdt / K * 1e3, 4), "steps": K,
                          "mode": bmode, "eager_tok_s": round(B * K / edt, 1)}
         log(f"batched decode B={B} ({bmode}): {bdt / K * 1e3:.3f} ms/step ({B * K / bdt:.0f} tok/s aggregate); "
@@ -517,6 +519,7 @@ def per_config(args, c4_out):
         torch.cuda.synchronize()
         gdt = time.perf_counter() - t
         del g
+        rm.check_status(f"{cfg.name} decode")
         rec = {"prompt": P, "gpu_prefill_tok_s": round(P / pre, 1), "gpu_prefill_ms": round(pre * 1e3, 3),
                "gpu_prefill_graph_ms": round(pre_g * 1e3, 3) if pre_g else None,
                "gpu_prefill_graph_tok_s": round(P / pre_g, 1) if pre_g else None,
