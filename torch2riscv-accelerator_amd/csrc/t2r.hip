@@ -1184,6 +1184,8 @@ void t2r_model_destroy(void* model) {
 int t2r_model_status(void* model, int32_t* out, int clear) {
   Model* m = (Model*)model;
   if (!m || !out) return T2R_EINVAL;
+  // every stream's work first (a non-blocking stream is not ordered with the copy's default stream)
+  if (hipDeviceSynchronize() != hipSuccess) return T2R_EHIP;
   if (hipMemcpy(out, m->status, sizeof(int32_t), hipMemcpyDeviceToHost) != hipSuccess) return T2R_EHIP;
   if (clear && hipMemset(m->status, 0, sizeof(int32_t)) != hipSuccess) return T2R_EHIP;
   return T2R_OK;
