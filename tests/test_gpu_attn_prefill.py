@@ -31,7 +31,7 @@ def caches(rng, S, kvd):
 
 @pytest.mark.parametrize("H_,Hk,hd,S,D", [(6, 6, 48, 256, 16), (9, 3, 64, 2048, 16), (16, 8, 128, 2048, 16),
                                          (32, 8, 64, 2048, 16), (4, 2, 32, 512, 8), (4, 2, 8, 16, 8),
-                                         (6, 2, 24, 96, 16)])
+                                         (6, 2, 24, 96, 16), (8, 2, 128, 2048, 8), (4, 4, 128, 1000, 16)])
 @pytest.mark.parametrize("layout", ["chunk", "scattered"])
 def test_attn_prefill_vs_oracle(env, H_, Hk, hd, S, D, layout):
     torch, N, ops, T, H = env
@@ -165,3 +165,27 @@ def test_model_exp_underflow(name):
     assert np.array_equal(got[0].view(np.uint32), w0.view(np.uint32))
     assert np.array_equal(got[1].view(np.uint32), w1.view(np.uint32))
     assert torch.equal(kc[1, :, 30].cpu(), torch.from_numpy(om.kc[:, 30]))
+
+
+@pytest.mark.parametrize("D", [16, 8])
+def test_attn_prefill_c3_prompt(env, D):
+    """C3's attention shape over its whole 2032-row prompt at once (16 query heads, 8 KV heads, head dim
+    128, every row attending to all earlier positions: 64 blocks of 32 rows, the longest 2032 keys):
+    every row against the decode op, and rows spread over the blocks (both ends of each of several
+    blocks) against the oracle."""
+    torch, N, ops, T, H = env
+    H_, Hk, hd, S, M = 16, 8, 128, 2048, 2032
+    rng = np.random.default_rng(2032 + D)
+    kc, vc = caches(rng, S, Hk * hd)
+    pos = np.arange(M, dtype=np.int32)
+    q = (rng.standard_normal((M, H_ * hd)) * 2).astype(F)
+    a_k, a_v = F(0.05 / np.sqrt(hd)), F(0.03 / 127)
+    print(f"C3 prompt shape, D {D}: {M} rows", flush=True)
+    Tq, Tk, Tv, Tp = T(q), T(kc), T(vc), T(pos)
+    got = H(ops.attention_prefill(Tq, Tk, Tv, Tp, H_, Hk, a_k, a_v, D))
+    dec = H(ops.attention(Tq, Tk, Tv, Tp, H_, Hk, a_k, a_v, D))
+    bad = np.flatnonzero((got.view(np.uint32) != dec.view(np.uint32)).any(axis=1))
+    assert bad.size == 0, f"rows {bad[:8]} differ from the decode op"
+    for i in (0, 1, 31, 32, 63, 500, 1023, 1024, 1535, 2000, 2015, 2016, 2031):
+        want = N.attention(q[i], kc[:i + 1], vc[:i + 1], H_, Hk, a_k, a_v, D)
+        assert np.array_equal(got[i].view(np.uint32), want.view(np.uint32)), f"row {i}"

@@ -68,12 +68,13 @@ def test_sfu_sweep_vs_oracle(env, name):
     assert bad.size == 0, [(hex(x[i]), hex(got[i]), hex(want[i])) for i in bad[:6]]
 
 
-@pytest.mark.parametrize("name", ["exp", "recip", "rsqrt", "exp_np", "recip_ge1"])
+@pytest.mark.parametrize("name", ["exp", "recip", "rsqrt", "exp_np", "recip_ge1", "exp_sm"])
 def test_sfu_exhaustive_vs_literal_sequence(env, name):
     """All 2^32 inputs: the datapath SFU (plain IEEE steps where the FTZ rule cannot change a result)
     equals the per-operation FTZ sequence of llm/sfu.py, which the sweep above pins to the oracle.
     'exp_np', the attention softmax's EXP, over its whole domain (x <= 0 and NaN: 2^31 + 2^23 inputs);
-    'recip_ge1', the SwiGLU / GeGLU gates' RECIP, over its (x >= 1 and NaN)."""
+    'recip_ge1', the SwiGLU / GeGLU gates' RECIP, over its (x >= 1 and NaN); 'exp_sm', the prefill
+    softmax's EXP under a finite row maximum, over its (x <= 0: 2^31 + 1 inputs)."""
     torch, N, ops, T, H = env
     bad, first = ops.sfu_check(name)
     assert bad == 0, (name, bad, None if first is None else hex(first))

@@ -67,6 +67,8 @@ int ensure_init() {
   if (g_inited[dev]) return T2R_OK;
   float t[kSfuWords];
   sfu_host_tables(t);
+  // sfu_exp_sm's table identities: F(T[63] + S[63]) = 2 and T[0] = 1
+  if (t[kSfuExpT + 63] + t[kSfuExpS + 63] != 2.0f || t[kSfuExpT] != 1.0f) return T2R_EHIP;
   if (hipMemcpyToSymbol(HIP_SYMBOL(c_sfu), t, sizeof(t), 0, hipMemcpyHostToDevice) != hipSuccess) return T2R_EHIP;
   void* addr = nullptr;
   if (hipGetSymbolAddress(&addr, HIP_SYMBOL(c_sfu)) != hipSuccess || addr == nullptr) return T2R_EHIP;
@@ -77,6 +79,8 @@ int ensure_init() {
   for (const void* f : pre)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPreMaxLds) != hipSuccess)
       return T2R_EHIP;
+  if (hipFuncSetAttribute((const void*)k_attn_pw, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kApLds) != hipSuccess)
+    return T2R_EHIP;
   // the GEMM's deep-ring configuration: 128 KB of LDS, one workgroup per CU
   const void* deep[] = {(const void*)k_gemm_d<EPI_STORE, false, 128, 4>, (const void*)k_gemm_d<EPI_STORE, true, 128, 4>,
                         (const void*)k_gemm_d<EPI_RESID, false, 128, 4>, (const void*)k_gemm_d<EPI_RESID, true, 128, 4>,
@@ -144,6 +148,11 @@ int pre_cap(const AttnArgs& a) { return a.t_cap > 0 && a.t_cap < a.S ? a.t_cap :
 // score rows fit the LDS the kernels are set up for (kPreMaxLds)
 bool pre_ok(const AttnArgs& a) {
   return a.hd % 16 == 0 && a.hd <= 128 && attn_pre_lds_bytes(pre_cap(a), (a.hd + 31) & ~31) <= kPreMaxLds;
+}
+// ... and its 32-row form (k_attn_pw): head dim 128 without the HF options, rows attending to at most
+// kApKeys positions
+bool pw_ok(const AttnArgs& a) {
+  return a.hd == 128 && !attn_opt(a) && pre_cap(a) <= kApKeys && (a.D == 8 || a.D == 16);
 }
 
 // batch-1 decode attention split over workgroups per head (k_attn_dec's SPLIT forms): the heads of a
@@ -225,6 +234,8 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
     else launch((k_attn<ATTN_FUSED, 8>), grid, block, lds, st, a);
   } else if (mode == ATTN_PREP) {
     launch(k_attn_prep, dim3(cdiv(a.H + a.Hk, kPrepWaves), rows), dim3(64 * kPrepWaves), 0, st, a);
+  } else if (a.tab != nullptr && a.kv_row_stride == 0 && pw_ok(a)) {
+    launch(k_attn_pw, dim3(a.H, cdiv(rows, kApRows)), dim3(kApThreads), kApLds, st, a, rows);
   } else if (a.tab != nullptr && a.kv_row_stride == 0 && pre_ok(a)) {
     const int hdp = (a.hd + 31) & ~31;
     dim3 pg(a.H, cdiv(rows, kPreRows));
@@ -916,7 +927,7 @@ int t2r_sfu(int fn, const uint32_t* x, uint32_t* y, int64_t n, void* stream) {
 }
 
 int t2r_sfu_check(int fn, uint64_t first, uint64_t count, uint32_t* out, void* stream) {
-  if (fn < 0 || fn > 4 || !out || first > 0xFFFFFFFFull || count > 0x100000000ull - first) return T2R_EINVAL;
+  if (fn < 0 || fn > 5 || !out || first > 0xFFFFFFFFull || count > 0x100000000ull - first) return T2R_EINVAL;
   T2R_INIT();
   launch(k_sfu_check_init, dim3(1), dim3(64), 0, S(stream), out);
   if (count > 0) launch(k_sfu_check, dim3(8192), dim3(256), 0, S(stream), fn, (unsigned long long)first,

@@ -1275,6 +1275,277 @@ inline size_t attn_pre_lds_bytes(int S, int HDP) {
   return e > p ? e : p;
 }
 
+// ------------------------------------------------------------------ prefill attention, 32-row blocks
+// k_attn_pre's numerics for head dim 128 without the HF options over up to kApKeys positions, one
+// 512-thread workgroup per (query head, 32 rows): every K and V byte read serves 32 rows, and the
+// score MFMA's 32 output columns are all rows of the block. The scores stay in registers:
+//  - scores as S^T = K Q^T (v_mfma_i32_32x32x32_i8, A = 32 keys of a tile, B = the block's int8 q):
+//    lane (n, half) holds row n's scores of keys 8 (r / 4) + 4 half + r % 4 of each tile, r < 16.
+//    Wave w takes tiles w, w + 8, ...: 8 tiles of 16 values a lane at 2048 keys;
+//  - the row maximum (order-free) from each lane's, the two halves' and the waves' (LDS);
+//  - e = EXP(s - max) in place (sfu_exp_sm where every row's maximum is finite, else sfu_exp_np and
+//    the t < T select, k_attn_pre's form);
+//  - the D-lane ordered sum: the waves' tiles of 256 keys at a time go to LDS (double-buffered) and
+//    each chain lane (row, l < D) adds keys l, l + D, ... of the chunk in order; chunks in key order,
+//    so every chain adds its keys in the reference's order (keys past T are +0, which leave a sum
+//    of non-negative terms unchanged); then the pairwise tree over the D lanes and RECIP;
+//  - p = to_i8(F(F(e r) 127)) packed in the lane's own key order, which is the P.V MFMA's A operand
+//    (its k order within a tile is that permutation of the keys; the V operand is gathered to match),
+//    through LDS ([32 rows][keys]) to the P.V waves;
+//  - P.V: wave (column quarter c, tile group z) multiplies the group's tiles (z, z + 2, ...) against
+//    V's 32 columns of c transposed in registers (k_attn_pre's quad exchange) into its own LDS tile;
+//    the two groups' int32 sums are added (exact) and scaled.
+constexpr int kApRows = 32, kApThreads = 512, kApWaves = kApThreads / 64;
+constexpr int kApKeys = 2048;                            // positions a row may attend to
+constexpr int kApTW = kApKeys / 32 / kApWaves;          // score tiles a wave holds (16 registers each)
+constexpr int kApStage = 256 + 16;                       // float stride of a row of a 256-key chunk
+constexpr int kApPStride = kApKeys + 16;                 // byte stride of a row of int8 p
+// dynamic LDS: the two chunk buffers of exps, then (reused) the rows of p, then the int32 sums
+constexpr size_t kApLds = (size_t)2 * kApRows * kApStage * 4;
+static_assert((size_t)kApRows * kApPStride <= kApLds && (size_t)kApRows * 128 * 4 <= kApLds, "LDS reuse");
+
+__global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
+  constexpr int HD = 128, KS = HD / 32, NW = kApWaves, TW = kApTW;
+  extern __shared__ __align__(16) float big[];
+  __shared__ __align__(16) float tab[kSfuWords];
+  __shared__ __align__(16) float2 et[kSfuExpPairs];
+  __shared__ __align__(16) int8_t Q8[kApRows][HD];
+  __shared__ __align__(16) int8_t VT[NW][32 * 32];
+  __shared__ __align__(16) float s_mx[kApRows][NW];
+  __shared__ float s_sq[kApRows], s_r[kApRows];
+  __shared__ int s_T[kApRows];
+  // row blocks longest first (a causal prompt's later rows attend to more positions)
+  const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kApRows, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, n = lane & 31, half = lane >> 5;
+  const int G = a.H / a.Hk, g = h / G, S = a.S, D = a.D;
+  const int cap = a.t_cap > 0 && a.t_cap < S ? a.t_cap : S;
+  const int kv_dim = a.Hk * HD;
+
+  // ---- q of the block's rows to int8, a wave per row (rows wave, wave + 8, ...); invalid rows T = 0
+  float qx[kApRows / NW][2];
+  int qpos[kApRows / NW];
+#pragma unroll
+  for (int k = 0; k < kApRows / NW; ++k) {
+    const int r = min(r0 + wave + NW * k, M - 1);
+    qpos[k] = a.pos[r];
+    const float* q = a.qkv + (long long)r * a.qkv_stride + (long long)h * HD;
+    qx[k][0] = q[lane];
+    qx[k][1] = q[lane + 64];
+  }
+  if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = ((const v4f_t*)a.tab)[tid];
+  if (tid < kSfuExpPairs) et[tid] = sfu_exp_pair(tid, a.tab);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kApRows / NW; ++k) {
+    const int i = wave + NW * k, pos = qpos[k];
+    const bool ok = r0 + i < M && pos >= 0 && pos < S;
+    const float sq = fv(wave_max_u32(max(abs_bits(qx[k][0]), abs_bits(qx[k][1])))) * kInv127;
+    const float inv = sfu_recip(sq, tab);
+    Q8[i][lane] = (int8_t)(ok ? to_i8(qx[k][0] * inv) : 0);
+    Q8[i][lane + 64] = (int8_t)(ok ? to_i8(qx[k][1] * inv) : 0);
+    if (lane == 0) {
+      s_sq[i] = sq;
+      s_T[i] = ok ? min(pos + 1, cap) : 0;
+    }
+  }
+  __syncthreads();
+  const int Tn = s_T[n];
+  const int ntile = ((int)wave_max_u32((uint32_t)Tn) + 31) / 32;   // lanes n cover the 32 rows
+  const float sqn = s_sq[n];
+
+  // ---- scores of the wave's tiles (ti = wave + 8 j), PTS tiles' K rows in flight at a time. A tile
+  // past the block's last gets an offset outside the buffer: zeros, with no memory access.
+  constexpr uint32_t kNoRow = 0x80000000u;      // beyond every cache (S kv_dim < 2^31)
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.kc, (uint32_t)S * kv_dim);
+  v4i_t qb[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qb[ks] = *(const v4i_t*)&Q8[n][32 * ks + 16 * half];
+  constexpr int PTS = 2;
+  float sc[TW][16];
+  float rmx = -__builtin_inff();
+#pragma unroll
+  for (int j0 = 0; j0 < TW; j0 += PTS) {
+    if (wave + NW * j0 >= ntile) break;
+    v4i_t kb[PTS][KS];
+#pragma unroll
+    for (int u = 0; u < PTS; ++u) {
+      const int ti = wave + NW * (j0 + u);
+      const uint32_t off = ti < ntile ? (uint32_t)(32 * ti + n) * kv_dim + g * HD + 16 * half : kNoRow;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kb[u][ks] = buffer_load16(krs, off + 32 * ks);
+    }
+#pragma unroll
+    for (int u = 0; u < PTS; ++u) {
+      const int j = j0 + u, ti = wave + NW * j;
+      if (ti >= ntile) break;
+      v16i_t acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kb[u][ks], qb[ks], acc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = 32 * ti + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float sv = ((float)acc[r] * sqn) * a.a_k;
+        sc[j][r] = t < Tn ? sv : -__builtin_inff();
+        rmx = smax(rmx, sc[j][r]);
+      }
+    }
+  }
+  rmx = smax(rmx, __shfl_xor(rmx, 32));
+  if (half == 0) s_mx[n][wave] = rmx;
+  __syncthreads();
+  float mx;
+  {
+    const v4f_t m0 = *(const v4f_t*)&s_mx[n][0], m1 = *(const v4f_t*)&s_mx[n][4];
+    mx = smax(smax(smax(m0.x, m0.y), smax(m0.z, m0.w)), smax(smax(m1.x, m1.y), smax(m1.z, m1.w)));
+  }
+  // every valid row's maximum finite: its e sum is >= 1 (EXP(0) = 1 at the maximum), so
+  // y = F(F(e r) 127) lies in [0, 127] and to_i8(y) is y's RNE integer
+  const bool fast = __all(Tn == 0 || __builtin_isfinite(mx));
+
+  // ---- e = EXP(s - max) in place, keys past T included (their s is -inf), and the D-lane ordered
+  // sums, a 256-key chunk at a time: chunk k is tile 8 k + w of wave w (its slot k), whose exps the
+  // wave forms and stores; then chain lane (row cr, l < D) adds keys l, l + D, ... of the chunk.
+  // With a finite maximum e is k_attn_pre's (sfu_exp_sm = EXP on x <= 0, EXP(-inf) = 0). A row
+  // whose maximum is not finite (NaN, +inf, or -inf over its keys) ends with every p = 0 in the
+  // reference (its e sum is NaN, p = to_i8(NaN)); here s - max is NaN or -inf for all its keys,
+  // sfu_exp_sm gives 0, the sum is 0 and p = to_i8(F(0 RECIP(0))) = 0 as well (the full to_i8 below).
+  const int cpr = 64 / D, cr = wave * cpr + lane / D, cl = lane % D;
+  const bool chain = cr < kApRows;
+  const int nchunk = (ntile + NW - 1) / NW;
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < TW; ++k) {
+    if (k >= nchunk) break;
+    float* sb = big + (k & 1) * (kApRows * kApStage);
+    float* wp = sb + n * kApStage + 32 * wave + 4 * half;
+    if (wave + NW * k < ntile) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[k][r] = sfu_exp_sm(sc[k][r] - mx, et);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        *(v4f_t*)(wp + 8 * rr) = v4f_t{sc[k][4 * rr], sc[k][4 * rr + 1], sc[k][4 * rr + 2], sc[k][4 * rr + 3]};
+    } else {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) *(v4f_t*)(wp + 8 * rr) = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    __syncthreads();
+    if (chain) {
+      const float* cb = sb + cr * kApStage + cl;
+      for (int q0 = 0; q0 < 256; q0 += 8 * D) {
+        float e[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) e[u] = cb[q0 + u * D];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = acc + e[u];
+      }
+    }
+  }
+  // pairwise tree over the row's D lanes (within a 16-lane DPP row), RECIP on the row's first lane
+  {
+    float o = dpp_f<0x101>(acc);                  // row_shl:1
+    if (D > 1 && (cl & 1) == 0) acc = acc + o;
+    o = dpp_f<0x102>(acc);
+    if (D > 2 && (cl & 3) == 0) acc = acc + o;
+    o = dpp_f<0x104>(acc);
+    if (D > 4 && (cl & 7) == 0) acc = acc + o;
+    o = dpp_f<0x108>(acc);
+    if (D > 8 && (cl & 15) == 0) acc = acc + o;
+    if (chain && cl == 0) s_r[cr] = sfu_recip(acc, tab);
+  }
+  __syncthreads();
+
+  // ---- p = to_i8(F(F(e r) 127)) of every (row, key), 16 bytes a lane and tile, into rows of LDS
+  int8_t* P = (int8_t*)big;
+  {
+    const float rn = s_r[n];
+#pragma unroll
+    for (int j = 0; j < TW; ++j) {
+      const int ti = wave + NW * j;
+      if (ti >= ntile) break;
+      uint32_t w4[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        uint32_t b[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float y = (sc[j][4 * rr + c] * rn) * 127.0f;
+          // fast: y in [0, 127], whose RNE integer is the low byte of F(y + 1.5 2^23)
+          b[c] = fast ? fb(y + 12582912.0f) : (uint32_t)to_i8(y);
+        }
+        const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0C0C0400u);   // bytes b0[0], b1[0]
+        const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x0C0C0400u);
+        w4[rr] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+      }
+      *(v4i_t*)&P[n * kApPStride + 32 * ti + 16 * half] = v4i_t{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
+    }
+  }
+  __syncthreads();
+
+  // ---- P.V: wave (quarter c of V's columns, tile group z): tiles z, z + 2, ...
+  const int vq = wave & 3, vz = wave >> 2;
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc, (uint32_t)S * kv_dim);
+  int8_t* vt = &VT[wave][0];
+  // V rows 32 ti + n, the quarter's columns 16 half.. +15: the quad's four rows exchanged so that
+  // lane 4k + c holds column 16 half + 4 d + c of rows 4 (n / 4) .. + 3 (one word), stored at key
+  // group position (g4 % 2) 4 + g4 / 2 of the column (g4 = n / 4): lane (column j, kg) then reads its
+  // 16 bytes for keys 8 q + 4 kg + 0..3, q = 0..3, the A operand's k order.
+  const int g4 = n >> 2, gpos = 4 * (((g4 & 1) << 2) | (g4 >> 1));
+  v16i_t pv;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) pv[r] = 0;
+  constexpr int PTV = 8;
+  for (int c0 = vz; c0 < ntile; c0 += 2 * PTV) {
+    v4i_t vb[PTV];
+#pragma unroll
+    for (int u = 0; u < PTV; ++u) {
+      const int ti = c0 + 2 * u;
+      vb[u] = buffer_load16(vrs, ti < ntile ? (uint32_t)(32 * ti + n) * kv_dim + g * HD + 32 * vq + 16 * half : kNoRow);
+    }
+#pragma unroll
+    for (int u = 0; u < PTV; ++u) {
+      const int ti = c0 + 2 * u;
+      if (ti >= ntile) break;
+      const v4i_t pa = *(const v4i_t*)&P[n * kApPStride + 32 * ti + 16 * half];
+      __builtin_amdgcn_wave_barrier();
+      const int w4[4] = {vb[u].x, vb[u].y, vb[u].z, vb[u].w};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t x = (uint32_t)w4[d];
+        const uint32_t y = (uint32_t)dpp_i<kDppXor1>((int)x);
+        const uint32_t s1 = __builtin_amdgcn_perm(y, x, (lane & 1) ? 0x03070105u : 0x06020400u);
+        const uint32_t y2 = (uint32_t)dpp_i<kDppXor2>((int)s1);
+        const uint32_t col = __builtin_amdgcn_perm(y2, s1, (lane & 2) ? 0x03020706u : 0x05040100u);
+        *(uint32_t*)&vt[(16 * half + 4 * d + (lane & 3)) * 32 + gpos] = col;
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);           // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
+      const v4i_t vbop = *(const v4i_t*)&vt[n * 32 + 16 * half];
+      pv = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, vbop, pv, 0, 0, 0);
+    }
+  }
+
+  // ---- the two tile groups' sums (exact int32), then att = F(f32(sum) a_v) of the valid rows
+  __syncthreads();                                  // every wave's reads of P done
+  int* O = (int*)big;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = 8 * (r >> 2) + 4 * half + (r & 3);
+    if (vz == 0) O[m * HD + 32 * vq + n] = pv[r];
+  }
+  __syncthreads();
+  if (vz == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = 8 * (r >> 2) + 4 * half + (r & 3);
+      if (s_T[m] == 0) continue;
+      const int sum = pv[r] + O[m * HD + 32 * vq + n];
+      a.att[(long long)(r0 + m) * a.att_stride + (long long)h * HD + 32 * vq + n] = (float)sum * a.a_v;
+    }
+  }
+}
+
 // dynamic LDS bytes of k_attn: the scores (lane-major, D * osum_stride(S, D) floats) and the int8
 // probabilities of S cache rows
 inline size_t attn_lds_bytes(int S, int D) { return (size_t)D * osum_stride(S, D) * 4 + (size_t)S; }

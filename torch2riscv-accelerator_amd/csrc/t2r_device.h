@@ -190,6 +190,38 @@ T2R_DEV float sfu_exp_np(float xin, const float* tab = c_sfu) {
   return x != x ? fv(kQNaN) : out;
 }
 
+// The EXP table as 65 {T, S} pairs: entries 0..63 the table's, entry 64 {F(T[63] + S[63]), 0}.
+constexpr int kSfuExpPairs = 65;
+T2R_DEV float2 sfu_exp_pair(int i, const float* tab) {
+  return i < 64 ? make_float2(tab[kSfuExpT + i], tab[kSfuExpS + i])
+                : make_float2(tab[kSfuExpT + 63] + tab[kSfuExpS + 63], 0.0f);
+}
+
+// EXP of a softmax argument x = s - max under a finite maximum: x <= 0 or -inf, never NaN. Equal to
+// sfu_exp_np there (the GPU self-check compares it with the literal sequence over that whole domain)
+// with fewer steps, given the table's F(T[63] + S[63]) = 2 and T[0] = 1 (checked by the library's
+// init):
+//  - i = trunc(u) and r = fract(u), both exact for u in [0, 64]: below 64 they are the reference's
+//    index and remainder; at u = 64 the reference takes i = 63, r = 1, whose F(T[63] + 1 S[63]) is
+//    pair 64's T (and 0 S[64] = 0);
+//  - no entry flush: x in (-2^-126, 0) gives t in (-2^-125, 0), floor -1, F(t + 1) = 1, u = 64, y = 2,
+//    and 2 2^-1 = 1 = T[0], the EXP of the flushed zero;
+//  - no NaN select (x is never NaN).
+T2R_DEV float sfu_exp_sm(float x, const float2* et) {
+  const float tc = fmaxf(x * (float)1.4426950408889634, -160.0f);
+  const float tf = floorf(tc);
+  const float u = (tc - tf) * 64.0f;
+  const float2 ts = et[(int)u];
+  const uint32_t b = fb(ts.x + __builtin_amdgcn_fractf(u) * ts.y);
+  const int e = (int)(b + ((uint32_t)(int)tf << 23));
+  // e < 2^23 -> +0 as integer steps (e - 2^23 > -2^31 here; the shift in asm, so that the compiler
+  // does not turn it back into a compare and select, whose lane masks it would keep in scalar
+  // registers across the unrolled callers)
+  uint32_t m;
+  asm("v_ashrrev_i32 %0, 31, %1" : "=v"(m) : "v"(e - 0x00800000));
+  return fv((uint32_t)e & ~m);
+}
+
 // RECIP (llm/sfu.py:12-15, 85-96)
 T2R_DEV float sfu_recip(float xin, const float* tab = c_sfu) {
   const uint32_t b = fb(ftz(vreg(xin)));
