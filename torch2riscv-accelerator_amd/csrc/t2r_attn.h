@@ -1278,31 +1278,34 @@ inline size_t attn_pre_lds_bytes(int S, int HDP) {
 // ------------------------------------------------------------------ prefill attention, 32-row blocks
 // k_attn_pre's numerics for head dim 128 without the HF options over up to kApKeys positions, one
 // 512-thread workgroup per (query head, 32 rows): every K and V byte read serves 32 rows, and the
-// score MFMA's 32 output columns are all rows of the block. The scores stay in registers:
-//  - scores as S^T = K Q^T (v_mfma_i32_32x32x32_i8, A = 32 keys of a tile, B = the block's int8 q):
-//    lane (n, half) holds row n's scores of keys 8 (r / 4) + 4 half + r % 4 of each tile, r < 16.
-//    Wave w takes tiles w, w + 8, ...: 8 tiles of 16 values a lane at 2048 keys;
+// MFMAs' 32 query columns / rows are all rows of the block. Wave w owns the key tiles (32 keys)
+// w, w + 8, ... (8 tiles at 2048 keys) from the scores to P.V, and keeps them in registers:
+//  - K tiles go global -> LDS by global_load_lds (whole 128-byte rows per instruction; chunk kc of row
+//    r at 16-byte position 8 r + (kc ^ swz(r)), the GEMM operand swizzle) into a two-tile ring of the
+//    wave's own; scores as S^T = K Q^T (v_mfma_i32_32x32x32_i8, A = the tile's 32 keys, B = the
+//    block's int8 q): lane (n, half) holds row n's scores of keys 8 (r / 4) + 4 half + r % 4, r < 16;
 //  - the row maximum (order-free) from each lane's, the two halves' and the waves' (LDS);
-//  - e = EXP(s - max) in place (sfu_exp_sm where every row's maximum is finite, else sfu_exp_np and
-//    the t < T select, k_attn_pre's form);
-//  - the D-lane ordered sum: the waves' tiles of 256 keys at a time go to LDS (double-buffered) and
-//    each chain lane (row, l < D) adds keys l, l + D, ... of the chunk in order; chunks in key order,
-//    so every chain adds its keys in the reference's order (keys past T are +0, which leave a sum
-//    of non-negative terms unchanged); then the pairwise tree over the D lanes and RECIP;
-//  - p = to_i8(F(F(e r) 127)) packed in the lane's own key order, which is the P.V MFMA's A operand
-//    (its k order within a tile is that permutation of the keys; the V operand is gathered to match),
-//    through LDS ([32 rows][keys]) to the P.V waves;
-//  - P.V: wave (column quarter c, tile group z) multiplies the group's tiles (z, z + 2, ...) against
-//    V's 32 columns of c transposed in registers (k_attn_pre's quad exchange) into its own LDS tile;
-//    the two groups' int32 sums are added (exact) and scaled.
+//  - e = EXP(s - max) in place (sfu_exp_sm) and the D-lane ordered sums: the waves' tiles of 256
+//    keys at a time go to LDS (double-buffered) and each chain lane (row, l < D) adds keys l, l + D,
+//    ... of the chunk in order; chunks in key order, so every chain adds its keys in the reference's
+//    order (keys past T are +0, which leave a sum of non-negative terms unchanged); then the pairwise
+//    tree over the D lanes and RECIP;
+//  - p = to_i8(F(F(e r) 127)) packed in the lane's own key order: the P.V MFMA's A operand (its k
+//    order within a tile is that permutation of the keys; the V operand is gathered to match);
+//  - P.V: the tile's V rows loaded whole (lane: row 8 i + 4 (lane / 32) + lane % 4, 16-byte chunk
+//    (lane / 4) % 8, instruction i), a quad's four rows exchanged into words of four keys of one
+//    column (k_attn_pre's quad exchange); the four instructions' words of a column are the 16 bytes
+//    of that column's B operand, one LDS store each; four MFMAs (128 columns) a tile;
+//  - the waves' int32 sums added by LDS integer atomics (exact in any order) and scaled.
 constexpr int kApRows = 32, kApThreads = 512, kApWaves = kApThreads / 64;
 constexpr int kApKeys = 2048;                            // positions a row may attend to
-constexpr int kApTW = kApKeys / 32 / kApWaves;          // score tiles a wave holds (16 registers each)
+constexpr int kApTW = kApKeys / 32 / kApWaves;          // key tiles a wave owns (16 score registers each)
 constexpr int kApStage = 256 + 16;                       // float stride of a row of a 256-key chunk
-constexpr int kApPStride = kApKeys + 16;                 // byte stride of a row of int8 p
-// dynamic LDS: the two chunk buffers of exps, then (reused) the rows of p, then the int32 sums
+constexpr int kApOStride = 128 + 8;                      // int32 stride of a row of the P.V sums
+// dynamic LDS: the waves' K rings (2 x 4 KB each), then (reused) the two chunk buffers of exps, then
+// (reused) the waves' transposed V tiles (4 KB each)
 constexpr size_t kApLds = (size_t)2 * kApRows * kApStage * 4;
-static_assert((size_t)kApRows * kApPStride <= kApLds && (size_t)kApRows * 128 * 4 <= kApLds, "LDS reuse");
+static_assert((size_t)kApWaves * 8192 <= kApLds && (size_t)kApWaves * 4096 <= kApLds, "LDS reuse");
 
 __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   constexpr int HD = 128, KS = HD / 32, NW = kApWaves, TW = kApTW;
@@ -1310,7 +1313,7 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   __shared__ __align__(16) float tab[kSfuWords];
   __shared__ __align__(16) float2 et[kSfuExpPairs];
   __shared__ __align__(16) int8_t Q8[kApRows][HD];
-  __shared__ __align__(16) int8_t VT[NW][32 * 32];
+  __shared__ __align__(16) int O[kApRows * kApOStride];
   __shared__ __align__(16) float s_mx[kApRows][NW];
   __shared__ float s_sq[kApRows], s_r[kApRows];
   __shared__ int s_T[kApRows];
@@ -1321,13 +1324,44 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   const int cap = a.t_cap > 0 && a.t_cap < S ? a.t_cap : S;
   const int kv_dim = a.Hk * HD;
 
-  // ---- q of the block's rows to int8, a wave per row (rows wave, wave + 8, ...); invalid rows T = 0
+  // ---- lane n's row: its position bounds T (rows past M or outside the cache: 0), the block's tiles
+  int Tn;
+  {
+    const int pn = a.pos[min(r0 + n, M - 1)];
+    Tn = r0 + n < M && pn >= 0 && pn < S ? min(pn + 1, cap) : 0;
+  }
+  const int ntile = ((int)wave_max_u32((uint32_t)Tn) + 31) / 32;   // lanes n cover the 32 rows
+  const int nown = ntile > wave ? (ntile - wave + NW - 1) / NW : 0;  // tiles this wave owns
+
+  // ---- the first two owned K tiles requested (DMA into the wave's ring) before q's quantisation.
+  // Rows past the cache are clamped to its last (their keys are past every T).
+  auto swz = [](int r) { return (r ^ (r >> 3)) & 7; };
+  int8_t* ring = (int8_t*)big + wave * 8192;
+  const int8_t* kcol[4];                             // this lane's 16-byte chunk of instruction i
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pos = 64 * i + lane, r = pos >> 3;
+    kcol[i] = a.kc + (long long)g * HD + 16 * ((pos & 7) ^ swz(r));
+  }
+  auto k_issue = [&](int j) {                        // owned tile j into ring slot j % 2
+    const int ti = wave + NW * j;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = min(32 * ti + ((64 * i + lane) >> 3), S - 1);
+      __builtin_amdgcn_global_load_lds((const void*)(kcol[i] + (long long)row * kv_dim),
+                                       (void*)(ring + 4096 * (j & 1) + 1024 * i), 16, 0, 0);
+    }
+  };
+  if (nown > 0) k_issue(0);
+  if (nown > 1) k_issue(1);
+  for (int k = tid; k < kApRows * kApOStride; k += kApThreads) O[k] = 0;
+  if (wave == 0 && half == 0) s_T[n] = Tn;
+
+  // ---- q of the block's rows to int8, a wave per row (rows wave, wave + 8, ...); invalid rows 0
   float qx[kApRows / NW][2];
-  int qpos[kApRows / NW];
 #pragma unroll
   for (int k = 0; k < kApRows / NW; ++k) {
     const int r = min(r0 + wave + NW * k, M - 1);
-    qpos[k] = a.pos[r];
     const float* q = a.qkv + (long long)r * a.qkv_stride + (long long)h * HD;
     qx[k][0] = q[lane];
     qx[k][1] = q[lane + 64];
@@ -1337,59 +1371,51 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < kApRows / NW; ++k) {
-    const int i = wave + NW * k, pos = qpos[k];
-    const bool ok = r0 + i < M && pos >= 0 && pos < S;
+    const int i = wave + NW * k;
+    const bool ok = __shfl(Tn, i) > 0;              // lane i holds row i
     const float sq = fv(wave_max_u32(max(abs_bits(qx[k][0]), abs_bits(qx[k][1])))) * kInv127;
     const float inv = sfu_recip(sq, tab);
     Q8[i][lane] = (int8_t)(ok ? to_i8(qx[k][0] * inv) : 0);
     Q8[i][lane + 64] = (int8_t)(ok ? to_i8(qx[k][1] * inv) : 0);
-    if (lane == 0) {
-      s_sq[i] = sq;
-      s_T[i] = ok ? min(pos + 1, cap) : 0;
-    }
+    if (lane == 0) s_sq[i] = sq;
   }
   __syncthreads();
-  const int Tn = s_T[n];
-  const int ntile = ((int)wave_max_u32((uint32_t)Tn) + 31) / 32;   // lanes n cover the 32 rows
   const float sqn = s_sq[n];
 
-  // ---- scores of the wave's tiles (ti = wave + 8 j), PTS tiles' K rows in flight at a time. A tile
-  // past the block's last gets an offset outside the buffer: zeros, with no memory access.
-  constexpr uint32_t kNoRow = 0x80000000u;      // beyond every cache (S kv_dim < 2^31)
-  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.kc, (uint32_t)S * kv_dim);
+  // ---- scores of the owned tiles: wait for the tile's DMA (the next one's may be in flight), its
+  // A fragments from the ring, four MFMAs, then the ring slot refilled with tile j + 2
   v4i_t qb[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) qb[ks] = *(const v4i_t*)&Q8[n][32 * ks + 16 * half];
-  constexpr int PTS = 2;
   float sc[TW][16];
   float rmx = -__builtin_inff();
 #pragma unroll
-  for (int j0 = 0; j0 < TW; j0 += PTS) {
-    if (wave + NW * j0 >= ntile) break;
-    v4i_t kb[PTS][KS];
+  for (int j = 0; j < TW; ++j) {
+    if (j >= nown) break;
+    if (j + 1 < nown) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    asm volatile("" ::: "memory");
+    const int8_t* kt = ring + 4096 * (j & 1);
+    v4i_t ka[KS];
 #pragma unroll
-    for (int u = 0; u < PTS; ++u) {
-      const int ti = wave + NW * (j0 + u);
-      const uint32_t off = ti < ntile ? (uint32_t)(32 * ti + n) * kv_dim + g * HD + 16 * half : kNoRow;
+    for (int ks = 0; ks < KS; ++ks) ka[ks] = *(const v4i_t*)(kt + 16 * (8 * n + ((2 * ks + half) ^ swz(n))));
+    v16i_t acc;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kb[u][ks] = buffer_load16(krs, off + 32 * ks);
+    for (int r = 0; r < 16; ++r) acc[r] = 0;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks], qb[ks], acc, 0, 0, 0);
+    if (j + 2 < nown) {
+      __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0): the slot's fragments are read
+      asm volatile("" ::: "memory");
+      k_issue(j + 2);
     }
+    const int ti = wave + NW * j;
 #pragma unroll
-    for (int u = 0; u < PTS; ++u) {
-      const int j = j0 + u, ti = wave + NW * j;
-      if (ti >= ntile) break;
-      v16i_t acc;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kb[u][ks], qb[ks], acc, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int t = 32 * ti + 8 * (r >> 2) + 4 * half + (r & 3);
-        const float sv = ((float)acc[r] * sqn) * a.a_k;
-        sc[j][r] = t < Tn ? sv : -__builtin_inff();
-        rmx = smax(rmx, sc[j][r]);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int t = 32 * ti + 8 * (r >> 2) + 4 * half + (r & 3);
+      const float sv = ((float)acc[r] * sqn) * a.a_k;
+      sc[j][r] = t < Tn ? sv : -__builtin_inff();
+      rmx = smax(rmx, sc[j][r]);
     }
   }
   rmx = smax(rmx, __shfl_xor(rmx, 32));
@@ -1420,7 +1446,7 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
     if (k >= nchunk) break;
     float* sb = big + (k & 1) * (kApRows * kApStage);
     float* wp = sb + n * kApStage + 32 * wave + 4 * half;
-    if (wave + NW * k < ntile) {
+    if (k < nown) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[k][r] = sfu_exp_sm(sc[k][r] - mx, et);
 #pragma unroll
@@ -1456,14 +1482,13 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   }
   __syncthreads();
 
-  // ---- p = to_i8(F(F(e r) 127)) of every (row, key), 16 bytes a lane and tile, into rows of LDS
-  int8_t* P = (int8_t*)big;
+  // ---- p = to_i8(F(F(e r) 127)) of the owned tiles, 16 bytes a lane and tile (the A operand)
+  v4i_t pa[TW];
   {
     const float rn = s_r[n];
 #pragma unroll
     for (int j = 0; j < TW; ++j) {
-      const int ti = wave + NW * j;
-      if (ti >= ntile) break;
+      if (j >= nown) break;
       uint32_t w4[4];
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
@@ -1478,70 +1503,82 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
         const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x0C0C0400u);
         w4[rr] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
       }
-      *(v4i_t*)&P[n * kApPStride + 32 * ti + 16 * half] = v4i_t{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
+      pa[j] = v4i_t{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
     }
   }
-  __syncthreads();
 
-  // ---- P.V: wave (quarter c of V's columns, tile group z): tiles z, z + 2, ...
-  const int vq = wave & 3, vz = wave >> 2;
+  // ---- P.V of the owned tiles: V rows whole (lane: row 8 i + 4 half + lane % 4 of the tile, chunk
+  // cq = (lane / 4) % 8); the quad (four consecutive rows of one chunk) exchanged so that lane
+  // 4 k + cc holds, for dword d, the word of column 16 cq + 4 d + cc over the quad's rows = keys of
+  // key group 2 i + half; the four instructions' words are then keys 8 i' + 4 half + 0..3, i' = 0..3:
+  // that column's B operand half `half`, stored whole. Lane (column j, kg) reads its 16 bytes back.
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc, (uint32_t)S * kv_dim);
-  int8_t* vt = &VT[wave][0];
-  // V rows 32 ti + n, the quarter's columns 16 half.. +15: the quad's four rows exchanged so that
-  // lane 4k + c holds column 16 half + 4 d + c of rows 4 (n / 4) .. + 3 (one word), stored at key
-  // group position (g4 % 2) 4 + g4 / 2 of the column (g4 = n / 4): lane (column j, kg) then reads its
-  // 16 bytes for keys 8 q + 4 kg + 0..3, q = 0..3, the A operand's k order.
-  const int g4 = n >> 2, gpos = 4 * (((g4 & 1) << 2) | (g4 >> 1));
-  v16i_t pv;
+  int8_t* vt = (int8_t*)big + wave * 4096;          // [128 columns][32 bytes]
+  const int cq = (lane >> 2) & 7, vr = 4 * half + (lane & 3);
+  v16i_t pv[4];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) pv[r] = 0;
-  constexpr int PTV = 8;
-  for (int c0 = vz; c0 < ntile; c0 += 2 * PTV) {
-    v4i_t vb[PTV];
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int u = 0; u < PTV; ++u) {
-      const int ti = c0 + 2 * u;
-      vb[u] = buffer_load16(vrs, ti < ntile ? (uint32_t)(32 * ti + n) * kv_dim + g * HD + 32 * vq + 16 * half : kNoRow);
-    }
+    for (int r = 0; r < 16; ++r) pv[c][r] = 0;
+  auto v_load = [&](v4i_t (&dst)[4], int j) {
+    const int ti = wave + NW * j;
 #pragma unroll
-    for (int u = 0; u < PTV; ++u) {
-      const int ti = c0 + 2 * u;
-      if (ti >= ntile) break;
-      const v4i_t pa = *(const v4i_t*)&P[n * kApPStride + 32 * ti + 16 * half];
-      __builtin_amdgcn_wave_barrier();
-      const int w4[4] = {vb[u].x, vb[u].y, vb[u].z, vb[u].w};
+    for (int i = 0; i < 4; ++i)
+      dst[i] = buffer_load16(vrs, (uint32_t)(32 * ti + 8 * i + vr) * kv_dim + g * HD + 16 * cq);
+  };
+  v4i_t vb[4], vn[4];
+  if (nown > 0) v_load(vb, 0);
+#pragma unroll
+  for (int j = 0; j < TW; ++j) {
+    if (j >= nown) break;
+    if (j + 1 < nown) v_load(vn, j + 1);
+    uint32_t wd[4][4];                               // [dword d][instruction i]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w4[4] = {vb[i].x, vb[i].y, vb[i].z, vb[i].w};
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         const uint32_t x = (uint32_t)w4[d];
         const uint32_t y = (uint32_t)dpp_i<kDppXor1>((int)x);
         const uint32_t s1 = __builtin_amdgcn_perm(y, x, (lane & 1) ? 0x03070105u : 0x06020400u);
         const uint32_t y2 = (uint32_t)dpp_i<kDppXor2>((int)s1);
-        const uint32_t col = __builtin_amdgcn_perm(y2, s1, (lane & 2) ? 0x03020706u : 0x05040100u);
-        *(uint32_t*)&vt[(16 * half + 4 * d + (lane & 3)) * 32 + gpos] = col;
+        wd[d][i] = __builtin_amdgcn_perm(y2, s1, (lane & 2) ? 0x03020706u : 0x05040100u);
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);           // lgkmcnt(0)
-      __builtin_amdgcn_wave_barrier();
-      const v4i_t vbop = *(const v4i_t*)&vt[n * 32 + 16 * half];
-      pv = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, vbop, pv, 0, 0, 0);
     }
+    __builtin_amdgcn_wave_barrier();                // the previous tile's operand reads come first
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      *(v4i_t*)&vt[(16 * cq + 4 * d + (lane & 3)) * 32 + 16 * half] =
+          v4i_t{(int)wd[d][0], (int)wd[d][1], (int)wd[d][2], (int)wd[d][3]};
+    __builtin_amdgcn_s_waitcnt(0xc07f);              // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const v4i_t vbop = *(const v4i_t*)&vt[(32 * c + n) * 32 + 16 * half];
+      pv[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa[j], vbop, pv[c], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vb[i] = vn[i];
   }
 
-  // ---- the two tile groups' sums (exact int32), then att = F(f32(sum) a_v) of the valid rows
-  __syncthreads();                                  // every wave's reads of P done
-  int* O = (int*)big;
+  // ---- the waves' sums (exact int32 atomics), then att = F(f32(sum) a_v) of the valid rows
+  if (nown > 0) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int m = 8 * (r >> 2) + 4 * half + (r & 3);
-    if (vz == 0) O[m * HD + 32 * vq + n] = pv[r];
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = 8 * (r >> 2) + 4 * half + (r & 3);
+        atomicAdd(&O[m * kApOStride + 32 * c + n], pv[c][r]);
+      }
   }
   __syncthreads();
-  if (vz == 1) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = 8 * (r >> 2) + 4 * half + (r & 3);
-      if (s_T[m] == 0) continue;
-      const int sum = pv[r] + O[m * HD + 32 * vq + n];
-      a.att[(long long)(r0 + m) * a.att_stride + (long long)h * HD + 32 * vq + n] = (float)sum * a.a_v;
+  {
+    const int m = tid >> 4, c0 = 8 * (tid & 15);
+    if (s_T[m] > 0) {
+      const v4i_t s0 = *(const v4i_t*)&O[m * kApOStride + c0], s1 = *(const v4i_t*)&O[m * kApOStride + c0 + 4];
+      float* out = a.att + (long long)(r0 + m) * a.att_stride + (long long)h * HD + c0;
+      *(v4f_t*)out = v4f_t{(float)s0.x * a.a_v, (float)s0.y * a.a_v, (float)s0.z * a.a_v, (float)s0.w * a.a_v};
+      *(v4f_t*)(out + 4) = v4f_t{(float)s1.x * a.a_v, (float)s1.y * a.a_v, (float)s1.z * a.a_v, (float)s1.w * a.a_v};
     }
   }
 }

@@ -45,6 +45,9 @@ void launch(K kernel, dim3 grid, dim3 block, size_t shmem, hipStream_t st, A... 
   }
 }
 
+// s_waitcnt with vmcnt(v) only (expcnt / lgkmcnt at their maxima): gfx9 encoding
+constexpr int waitcnt_vm(int v) { return (v & 15) | ((v >> 4) << 14) | 0x0F70; }
+
 constexpr uint32_t kQNaN = 0x7FC00000u;
 constexpr uint32_t kPInf = 0x7F800000u;
 constexpr float kInv127 = (float)(1.0 / 127.0);      // F(1/127): double quotient rounded once

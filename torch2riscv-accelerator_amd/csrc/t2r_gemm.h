@@ -282,9 +282,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(GemmArgs a) {
 constexpr int kGT = 128;                // tile edge of the direct-to-LDS GEMM below
 
 
-// s_waitcnt with vmcnt(v) only (expcnt / lgkmcnt at their maxima): gfx9 encoding
-constexpr int waitcnt_vm(int v) { return (v & 15) | ((v >> 4) << 14) | 0x0F70; }
-
 // Workgroup b runs on XCD b % 8 (round-robin dispatch). Give each XCD a contiguous range of the
 // n work items, so that the consecutive ones (the M tiles of one weight slab) share that XCD's L2.
 T2R_DEV int xcd_order(int b, int n) {
