@@ -1324,7 +1324,18 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   const int cap = a.t_cap > 0 && a.t_cap < S ? a.t_cap : S;
   const int kv_dim = a.Hk * HD;
 
-  // ---- lane n's row: its position bounds T (rows past M or outside the cache: 0), the block's tiles
+  // ---- the loads that depend on nothing first: q of the wave's rows (rows wave, wave + 8, ...),
+  // the SFU tables; then lane n's row: its position bounds T (rows past M or outside the cache: 0)
+  float qx[kApRows / NW][2];
+#pragma unroll
+  for (int k = 0; k < kApRows / NW; ++k) {
+    const int r = min(r0 + wave + NW * k, M - 1);
+    const float* q = a.qkv + (long long)r * a.qkv_stride + (long long)h * HD;
+    qx[k][0] = q[lane];
+    qx[k][1] = q[lane + 64];
+  }
+  const v4f_t tv = tid < kSfuWords / 4 ? ((const v4f_t*)a.tab)[tid] : v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const float2 ev = tid < kSfuExpPairs ? sfu_exp_pair(tid, a.tab) : make_float2(0.0f, 0.0f);
   int Tn;
   {
     const int pn = a.pos[min(r0 + n, M - 1)];
@@ -1357,17 +1368,9 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   for (int k = tid; k < kApRows * kApOStride; k += kApThreads) O[k] = 0;
   if (wave == 0 && half == 0) s_T[n] = Tn;
 
-  // ---- q of the block's rows to int8, a wave per row (rows wave, wave + 8, ...); invalid rows 0
-  float qx[kApRows / NW][2];
-#pragma unroll
-  for (int k = 0; k < kApRows / NW; ++k) {
-    const int r = min(r0 + wave + NW * k, M - 1);
-    const float* q = a.qkv + (long long)r * a.qkv_stride + (long long)h * HD;
-    qx[k][0] = q[lane];
-    qx[k][1] = q[lane + 64];
-  }
-  if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = ((const v4f_t*)a.tab)[tid];
-  if (tid < kSfuExpPairs) et[tid] = sfu_exp_pair(tid, a.tab);
+  // ---- q of the block's rows to int8, a wave per row; invalid rows 0
+  if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = tv;
+  if (tid < kSfuExpPairs) et[tid] = ev;
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < kApRows / NW; ++k) {
@@ -1429,6 +1432,18 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   // every valid row's maximum finite: its e sum is >= 1 (EXP(0) = 1 at the maximum), so
   // y = F(F(e r) 127) lies in [0, 127] and to_i8(y) is y's RNE integer
   const bool fast = __all(Tn == 0 || __builtin_isfinite(mx));
+
+  // the first owned tile's V rows requested now, in flight through the softmax (P.V below)
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc, (uint32_t)S * kv_dim);
+  const int cq = (lane >> 2) & 7, vr = 4 * half + (lane & 3);
+  auto v_load = [&](v4i_t (&dst)[4], int j) {
+    const int ti = wave + NW * j;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dst[i] = buffer_load16(vrs, (uint32_t)(32 * ti + 8 * i + vr) * kv_dim + g * HD + 16 * cq);
+  };
+  v4i_t vb[4], vn[4];
+  if (nown > 0) v_load(vb, 0);
 
   // ---- e = EXP(s - max) in place, keys past T included (their s is -inf), and the D-lane ordered
   // sums, a 256-key chunk at a time: chunk k is tile 8 k + w of wave w (its slot k), whose exps the
@@ -1512,22 +1527,12 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   // 4 k + cc holds, for dword d, the word of column 16 cq + 4 d + cc over the quad's rows = keys of
   // key group 2 i + half; the four instructions' words are then keys 8 i' + 4 half + 0..3, i' = 0..3:
   // that column's B operand half `half`, stored whole. Lane (column j, kg) reads its 16 bytes back.
-  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc, (uint32_t)S * kv_dim);
   int8_t* vt = (int8_t*)big + wave * 4096;          // [128 columns][32 bytes]
-  const int cq = (lane >> 2) & 7, vr = 4 * half + (lane & 3);
   v16i_t pv[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
 #pragma unroll
     for (int r = 0; r < 16; ++r) pv[c][r] = 0;
-  auto v_load = [&](v4i_t (&dst)[4], int j) {
-    const int ti = wave + NW * j;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dst[i] = buffer_load16(vrs, (uint32_t)(32 * ti + 8 * i + vr) * kv_dim + g * HD + 16 * cq);
-  };
-  v4i_t vb[4], vn[4];
-  if (nown > 0) v_load(vb, 0);
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
     if (j >= nown) break;
