@@ -1302,10 +1302,11 @@ constexpr int kApKeys = 2048;                            // positions a row may 
 constexpr int kApTW = kApKeys / 32 / kApWaves;          // key tiles a wave owns (16 score registers each)
 constexpr int kApStage = 256 + 16;                       // float stride of a row of a 256-key chunk
 constexpr int kApOStride = 128 + 8;                      // int32 stride of a row of the P.V sums
-// dynamic LDS: the waves' K rings (2 x 4 KB each), then (reused) the two chunk buffers of exps, then
-// (reused) the waves' transposed V tiles (4 KB each)
-constexpr size_t kApLds = (size_t)2 * kApRows * kApStage * 4;
-static_assert((size_t)kApWaves * 8192 <= kApLds && (size_t)kApWaves * 4096 <= kApLds, "LDS reuse");
+constexpr int kApRing = 4;                               // K tiles (4 KB) in a wave's ring
+// dynamic LDS: the waves' K rings, then (reused) the two chunk buffers of exps, then (reused) the
+// waves' transposed V tiles (4 KB each)
+constexpr size_t kApLds = (size_t)kApWaves * kApRing * 4096;
+static_assert((size_t)2 * kApRows * kApStage * 4 <= kApLds && (size_t)kApWaves * 4096 <= kApLds, "LDS reuse");
 
 __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   constexpr int HD = 128, KS = HD / 32, NW = kApWaves, TW = kApTW;
@@ -1347,24 +1348,25 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   // ---- the first two owned K tiles requested (DMA into the wave's ring) before q's quantisation.
   // Rows past the cache are clamped to its last (their keys are past every T).
   auto swz = [](int r) { return (r ^ (r >> 3)) & 7; };
-  int8_t* ring = (int8_t*)big + wave * 8192;
+  int8_t* ring = (int8_t*)big + wave * (kApRing * 4096);
   const int8_t* kcol[4];                             // this lane's 16-byte chunk of instruction i
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int pos = 64 * i + lane, r = pos >> 3;
     kcol[i] = a.kc + (long long)g * HD + 16 * ((pos & 7) ^ swz(r));
   }
-  auto k_issue = [&](int j) {                        // owned tile j into ring slot j % 2
+  auto k_issue = [&](int j) {                        // owned tile j into ring slot j % kApRing
     const int ti = wave + NW * j;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = min(32 * ti + ((64 * i + lane) >> 3), S - 1);
       __builtin_amdgcn_global_load_lds((const void*)(kcol[i] + (long long)row * kv_dim),
-                                       (void*)(ring + 4096 * (j & 1) + 1024 * i), 16, 0, 0);
+                                       (void*)(ring + 4096 * (j % kApRing) + 1024 * i), 16, 0, 0);
     }
   };
-  if (nown > 0) k_issue(0);
-  if (nown > 1) k_issue(1);
+#pragma unroll
+  for (int j = 0; j < kApRing - 1; ++j)
+    if (j < nown) k_issue(j);
   for (int k = tid; k < kApRows * kApOStride; k += kApThreads) O[k] = 0;
   if (wave == 0 && half == 0) s_T[n] = Tn;
 
@@ -1385,8 +1387,10 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   __syncthreads();
   const float sqn = s_sq[n];
 
-  // ---- scores of the owned tiles: wait for the tile's DMA (the next one's may be in flight), its
-  // A fragments from the ring, four MFMAs, then the ring slot refilled with tile j + 2
+  // ---- scores of the owned tiles: tile j + 3 requested into the slot tile j - 1 left (its fragments
+  // were read before its MFMAs), then wait for tile j's DMA (the newer ones may be in flight), its A
+  // fragments from the ring and four MFMAs. Tiles wholly below every valid row's T need no mask.
+  const int Tmin = (int)~wave_max_u32(~(Tn > 0 ? (uint32_t)Tn : 0xFFFFFFFFu));
   v4i_t qb[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) qb[ks] = *(const v4i_t*)&Q8[n][32 * ks + 16 * half];
@@ -1395,10 +1399,14 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
     if (j >= nown) break;
-    if (j + 1 < nown) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
+    if (j + kApRing - 1 < nown) k_issue(j + kApRing - 1);
+    const int newer = min(nown - 1, j + kApRing - 1) - j;   // tiles requested after tile j
+    if (newer >= 3) __builtin_amdgcn_s_waitcnt(waitcnt_vm(12));
+    else if (newer == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+    else if (newer == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
     else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     asm volatile("" ::: "memory");
-    const int8_t* kt = ring + 4096 * (j & 1);
+    const int8_t* kt = ring + 4096 * (j % kApRing);
     v4i_t ka[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) ka[ks] = *(const v4i_t*)(kt + 16 * (8 * n + ((2 * ks + half) ^ swz(n))));
@@ -1407,18 +1415,21 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
     for (int r = 0; r < 16; ++r) acc[r] = 0;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks], qb[ks], acc, 0, 0, 0);
-    if (j + 2 < nown) {
-      __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0): the slot's fragments are read
-      asm volatile("" ::: "memory");
-      k_issue(j + 2);
-    }
     const int ti = wave + NW * j;
+    if (32 * ti + 32 <= Tmin) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int t = 32 * ti + 8 * (r >> 2) + 4 * half + (r & 3);
-      const float sv = ((float)acc[r] * sqn) * a.a_k;
-      sc[j][r] = t < Tn ? sv : -__builtin_inff();
-      rmx = smax(rmx, sc[j][r]);
+      for (int r = 0; r < 16; ++r) {
+        sc[j][r] = ((float)acc[r] * sqn) * a.a_k;
+        rmx = smax(rmx, sc[j][r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = 32 * ti + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float sv = ((float)acc[r] * sqn) * a.a_k;
+        sc[j][r] = t < Tn ? sv : -__builtin_inff();
+        rmx = smax(rmx, sc[j][r]);
+      }
     }
   }
   rmx = smax(rmx, __shfl_xor(rmx, 32));
@@ -1442,8 +1453,9 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
     for (int i = 0; i < 4; ++i)
       dst[i] = buffer_load16(vrs, (uint32_t)(32 * ti + 8 * i + vr) * kv_dim + g * HD + 16 * cq);
   };
-  v4i_t vb[4], vn[4];
+  v4i_t vb[4], vn[4], vn2[4];
   if (nown > 0) v_load(vb, 0);
+  if (nown > 1) v_load(vn, 1);
 
   // ---- e = EXP(s - max) in place, keys past T included (their s is -inf), and the D-lane ordered
   // sums, a 256-key chunk at a time: chunk k is tile 8 k + w of wave w (its slot k), whose exps the
@@ -1460,24 +1472,29 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   for (int k = 0; k < TW; ++k) {
     if (k >= nchunk) break;
     float* sb = big + (k & 1) * (kApRows * kApStage);
-    float* wp = sb + n * kApStage + 32 * wave + 4 * half;
+    // key k of row n at float n kApStage + 4 ((k / 4) ^ ((n / 4) % 4)) + k % 4: the 16-byte stores of
+    // 16 rows land in distinct bank groups, a chain lane's 4-byte reads stay in one row's 16 banks
+    float* wp = sb + n * kApStage;
+    const int sx = (n >> 2) & 3;
     if (k < nown) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[k][r] = sfu_exp_sm(sc[k][r] - mx, et);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
-        *(v4f_t*)(wp + 8 * rr) = v4f_t{sc[k][4 * rr], sc[k][4 * rr + 1], sc[k][4 * rr + 2], sc[k][4 * rr + 3]};
+        *(v4f_t*)(wp + 4 * ((8 * wave + 2 * rr + half) ^ sx)) =
+            v4f_t{sc[k][4 * rr], sc[k][4 * rr + 1], sc[k][4 * rr + 2], sc[k][4 * rr + 3]};
     } else {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) *(v4f_t*)(wp + 8 * rr) = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int rr = 0; rr < 4; ++rr) *(v4f_t*)(wp + 4 * ((8 * wave + 2 * rr + half) ^ sx)) = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
     __syncthreads();
     if (chain) {
-      const float* cb = sb + cr * kApStage + cl;
+      const float* cb = sb + cr * kApStage + (cl & 3);
+      const int cx = (cr >> 2) & 3;
       for (int q0 = 0; q0 < 256; q0 += 8 * D) {
         float e[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) e[u] = cb[q0 + u * D];
+        for (int u = 0; u < 8; ++u) e[u] = cb[4 * (((q0 + u * D + cl) >> 2) ^ cx)];
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc = acc + e[u];
       }
@@ -1501,24 +1518,28 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   v4i_t pa[TW];
   {
     const float rn = s_r[n];
-#pragma unroll
-    for (int j = 0; j < TW; ++j) {
-      if (j >= nown) break;
+    auto pack = [&](int j, auto to_byte) {
       uint32_t w4[4];
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         uint32_t b[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float y = (sc[j][4 * rr + c] * rn) * 127.0f;
-          // fast: y in [0, 127], whose RNE integer is the low byte of F(y + 1.5 2^23)
-          b[c] = fast ? fb(y + 12582912.0f) : (uint32_t)to_i8(y);
-        }
+        for (int c = 0; c < 4; ++c) b[c] = to_byte((sc[j][4 * rr + c] * rn) * 127.0f);
         const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0C0C0400u);   // bytes b0[0], b1[0]
         const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x0C0C0400u);
         w4[rr] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
       }
       pa[j] = v4i_t{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
+    };
+    if (fast) {
+      // y in [0, 127]: its RNE integer is the low byte of F(y + 1.5 2^23)
+#pragma unroll
+      for (int j = 0; j < TW; ++j)
+        if (j < nown) pack(j, [](float y) { return fb(y + 12582912.0f); });
+    } else {
+#pragma unroll
+      for (int j = 0; j < TW; ++j)
+        if (j < nown) pack(j, [](float y) { return (uint32_t)to_i8(y); });
     }
   }
 
@@ -1527,7 +1548,11 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   // 4 k + cc holds, for dword d, the word of column 16 cq + 4 d + cc over the quad's rows = keys of
   // key group 2 i + half; the four instructions' words are then keys 8 i' + 4 half + 0..3, i' = 0..3:
   // that column's B operand half `half`, stored whole. Lane (column j, kg) reads its 16 bytes back.
-  int8_t* vt = (int8_t*)big + wave * 4096;          // [128 columns][32 bytes]
+  // (column col, half kg) at 16-byte slot 16 (col / 16 + 8 kg) + ((col % 16) ^ 4 ((col / 16) % 4)): the
+  // stores of a 16-lane pass (four columns of four chunks) and the reads (16 consecutive columns) each
+  // meet 16 distinct bank groups
+  auto vslot = [](int col, int kg) { return 16 * ((col >> 4) + 8 * kg) + ((col & 15) ^ (((col >> 4) & 3) << 2)); };
+  int8_t* vt = (int8_t*)big + wave * 4096;          // 128 columns x 32 bytes
   v16i_t pv[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
@@ -1536,7 +1561,7 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
     if (j >= nown) break;
-    if (j + 1 < nown) v_load(vn, j + 1);
+    if (j + 2 < nown) v_load(vn2, j + 2);
     uint32_t wd[4][4];                               // [dword d][instruction i]
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1544,26 +1569,29 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         const uint32_t x = (uint32_t)w4[d];
-        const uint32_t y = (uint32_t)dpp_i<kDppXor1>((int)x);
+        const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)x, kDppXor1, 0xF, 0xF, false);
         const uint32_t s1 = __builtin_amdgcn_perm(y, x, (lane & 1) ? 0x03070105u : 0x06020400u);
-        const uint32_t y2 = (uint32_t)dpp_i<kDppXor2>((int)s1);
+        const uint32_t y2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s1, kDppXor2, 0xF, 0xF, false);
         wd[d][i] = __builtin_amdgcn_perm(y2, s1, (lane & 2) ? 0x03020706u : 0x05040100u);
       }
     }
     __builtin_amdgcn_wave_barrier();                // the previous tile's operand reads come first
 #pragma unroll
     for (int d = 0; d < 4; ++d)
-      *(v4i_t*)&vt[(16 * cq + 4 * d + (lane & 3)) * 32 + 16 * half] =
+      *(v4i_t*)&vt[16 * vslot(16 * cq + 4 * d + (lane & 3), half)] =
           v4i_t{(int)wd[d][0], (int)wd[d][1], (int)wd[d][2], (int)wd[d][3]};
     __builtin_amdgcn_s_waitcnt(0xc07f);              // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const v4i_t vbop = *(const v4i_t*)&vt[(32 * c + n) * 32 + 16 * half];
+      const v4i_t vbop = *(const v4i_t*)&vt[16 * vslot(32 * c + n, half)];
       pv[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa[j], vbop, pv[c], 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vb[i] = vn[i];
+    for (int i = 0; i < 4; ++i) {
+      vb[i] = vn[i];
+      vn[i] = vn2[i];
+    }
   }
 
   // ---- the waves' sums (exact int32 atomics), then att = F(f32(sum) a_v) of the valid rows
