@@ -1374,15 +1374,25 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = tv;
   if (tid < kSfuExpPairs) et[tid] = ev;
   __syncthreads();
+  {
+    // the four rows' |q| maxima, then s_q = F(max (1/127)) and RECIP once for all four (lane k: row
+    // wave + 8 k); an invalid row's multiplier 0 gives q8 = to_i8(0 or NaN) = 0
+    uint32_t am[kApRows / NW];
 #pragma unroll
-  for (int k = 0; k < kApRows / NW; ++k) {
-    const int i = wave + NW * k;
-    const bool ok = __shfl(Tn, i) > 0;              // lane i holds row i
-    const float sq = fv(wave_max_u32(max(abs_bits(qx[k][0]), abs_bits(qx[k][1])))) * kInv127;
-    const float inv = sfu_recip(sq, tab);
-    Q8[i][lane] = (int8_t)(ok ? to_i8(qx[k][0] * inv) : 0);
-    Q8[i][lane + 64] = (int8_t)(ok ? to_i8(qx[k][1] * inv) : 0);
-    if (lane == 0) s_sq[i] = sq;
+    for (int k = 0; k < kApRows / NW; ++k) am[k] = wave_max_u32(max(abs_bits(qx[k][0]), abs_bits(qx[k][1])));
+    static_assert(kApRows / NW == 4, "four rows a wave");
+    const uint32_t mine = lane == 0 ? am[0] : lane == 1 ? am[1] : lane == 2 ? am[2] : am[3];
+    const float sq_l = fv(mine) * kInv127;
+    const float inv_l = sfu_recip(sq_l, tab);
+#pragma unroll
+    for (int k = 0; k < kApRows / NW; ++k) {
+      const int i = wave + NW * k;
+      const bool ok = __shfl(Tn, i) > 0;            // lane i holds row i
+      const float inv = ok ? fv((uint32_t)__builtin_amdgcn_readlane((int)fb(inv_l), k)) : 0.0f;
+      Q8[i][lane] = (int8_t)to_i8(qx[k][0] * inv);
+      Q8[i][lane + 64] = (int8_t)to_i8(qx[k][1] * inv);
+      if (lane == k) s_sq[i] = sq_l;
+    }
   }
   __syncthreads();
   const float sqn = s_sq[n];

@@ -404,6 +404,10 @@ T2R_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0
 template <int CTRL>
 T2R_DEV float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+// the same move for controls whose source lane is always inside the 16-lane row (quad permutes,
+// mirrors): no old value to keep, so no copy of the source first
+template <int CTRL>
+T2R_DEV int dpp_mov_i(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
 
 // every lane returns the sum over the wave (all 64 lanes active)
 T2R_DEV int wave_sum_i32(int v) {
@@ -514,10 +518,10 @@ T2R_DEV float lane_tree_sum(float acc, int D, int l) {
 // maximum of abs_bits values over the wave / the block (order-free, so any tree works); every
 // thread gets the result. `red` holds >= 16 words.
 T2R_DEV uint32_t wave_max_u32(uint32_t v) {
-  v = max(v, (uint32_t)dpp_i<kDppXor1>((int)v));
-  v = max(v, (uint32_t)dpp_i<kDppXor2>((int)v));
-  v = max(v, (uint32_t)dpp_i<kDppHalfMirror>((int)v));
-  v = max(v, (uint32_t)dpp_i<kDppMirror>((int)v));
+  v = max(v, (uint32_t)dpp_mov_i<kDppXor1>((int)v));
+  v = max(v, (uint32_t)dpp_mov_i<kDppXor2>((int)v));
+  v = max(v, (uint32_t)dpp_mov_i<kDppHalfMirror>((int)v));
+  v = max(v, (uint32_t)dpp_mov_i<kDppMirror>((int)v));
   const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
   const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
   return max(max(a, b), max(c, d));
