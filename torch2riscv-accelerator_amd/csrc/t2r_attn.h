@@ -116,17 +116,38 @@ inline bool attn_opt(const AttnArgs& a) { return a.qsum || a.ch_sk || a.ch_isk |
 // qsum's output scale rq = F(RECIP(f32(sum of the int8 probabilities)) * 127)
 T2R_DEV float qsum_scale(int sum, const float* tab) { return sfu_recip((float)sum, tab) * 127.0f; }
 
-// RMSNorm (optional) and RoPE of one head vector v[0..hd) in LDS, by one wave.
-T2R_DEV void head_norm_rope(float* v, const float* gain, const AttnArgs& a, int pos, int lane) {
+// The per-lane operands of head_norm_rope, loadable before the head vector is: the norm gains of
+// elements lane + 64 k and the RoPE cos / sin of pairs lane + 64 k at the row's position (0 past
+// the vector).
+struct NormRopeOps {
+  float g[2], c[2], s[2];
+};
+T2R_DEV NormRopeOps norm_rope_ops(const float* gain, const AttnArgs& a, int pos, int lane) {
+  NormRopeOps o;
   const int hd = a.hd;
-  if (gain != nullptr) {
+  const float* cs = a.cos_t + (long long)pos * (hd / 2);
+  const float* sn = a.sin_t + (long long)pos * (hd / 2);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int j = lane + 64 * k;
+    o.g[k] = gain != nullptr && j < hd ? gain[j] : 0.0f;
+    o.c[k] = j < hd / 2 ? cs[j] : 0.0f;
+    o.s[k] = j < hd / 2 ? sn[j] : 0.0f;
+  }
+  return o;
+}
+
+// RMSNorm (optional) and RoPE of one head vector v[0..hd) in LDS, by one wave.
+T2R_DEV void head_norm_rope(float* v, bool norm, const NormRopeOps& p, const AttnArgs& a, int lane) {
+  const int hd = a.hd;
+  if (norm) {
     float ss = 0.0f;
     if (lane < a.D) ss = ordered_sum<true>(v, hd, a.D, lane);
     const float r = sfu_rsqrt(__shfl(ss, 0) * a.inv_hd + a.eps);
     float nv[2];
     for (int k = 0; k < 2; ++k) {
       const int j = lane + 64 * k;
-      if (j < hd) nv[k] = (v[j] * r) * gain[j];
+      if (j < hd) nv[k] = (v[j] * r) * p.g[k];
     }
     __builtin_amdgcn_wave_barrier();
     for (int k = 0; k < 2; ++k) {
@@ -135,13 +156,11 @@ T2R_DEV void head_norm_rope(float* v, const float* gain, const AttnArgs& a, int 
     }
     __builtin_amdgcn_wave_barrier();
   }
-  const float* cs = a.cos_t + (long long)pos * (hd / 2);
-  const float* sn = a.sin_t + (long long)pos * (hd / 2);
   float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int k = 0; k < 2; ++k) {
     const int i = lane + 64 * k;
     if (i < hd / 2) {
-      const float v0 = v[2 * i], v1 = v[2 * i + 1], c = cs[i], s = sn[i];
+      const float v0 = v[2 * i], v1 = v[2 * i + 1], c = p.c[k], s = p.s[k];
       o[2 * k] = (v0 * c) + ((-v1) * s);
       o[2 * k + 1] = (v1 * c) + (v0 * s);
     }
@@ -155,6 +174,9 @@ T2R_DEV void head_norm_rope(float* v, const float* gain, const AttnArgs& a, int 
     }
   }
   __builtin_amdgcn_wave_barrier();
+}
+T2R_DEV void head_norm_rope(float* v, const float* gain, const AttnArgs& a, int pos, int lane) {
+  head_norm_rope(v, gain != nullptr, norm_rope_ops(gain, a, pos, lane), a, lane);
 }
 
 // 8 or 16 int8 of a cache row as int32 words (hd % 16 == 0: one 16-byte load)
@@ -885,10 +907,12 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
     return dequant(acc, a.part_sw[c], sx);
   };
   float* v0 = sv[wave][0];
+  const float* gain = vi < a.H ? a.qn : a.kn;
+  const NormRopeOps ops = norm_rope_ops(gain, a, pos, lane);   // requested with the head vector
   if (vi < a.H) {
     for (int j = lane; j < hd; j += 64) v0[j] = col(vi * hd + j);
     __builtin_amdgcn_wave_barrier();
-    head_norm_rope(v0, a.qn, a, pos, lane);
+    head_norm_rope(v0, gain != nullptr, ops, a, lane);
     for (int j = lane; j < hd; j += 64) qkv[vi * hd + j] = v0[j];
     return;
   }
@@ -899,7 +923,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
     v1[j] = col(q_dim + kv_dim + g * hd + j);
   }
   __builtin_amdgcn_wave_barrier();
-  head_norm_rope(v0, a.kn, a, pos, lane);
+  head_norm_rope(v0, gain != nullptr, ops, a, lane);
   int8_t* kc = a.kc + row * a.kv_row_stride + (long long)pos * kv_dim + g * hd;
   int8_t* vc = a.vc + row * a.kv_row_stride + (long long)pos * kv_dim + g * hd;
   for (int j = lane; j < hd / 4; j += 64) {
