@@ -233,7 +233,10 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
     if (c16) launch((k_attn<ATTN_FUSED, 16>), grid, block, lds, st, a);
     else launch((k_attn<ATTN_FUSED, 8>), grid, block, lds, st, a);
   } else if (mode == ATTN_PREP) {
-    launch(k_attn_prep, dim3(cdiv(a.H + a.Hk, kPrepWaves), rows), dim3(64 * kPrepWaves), 0, st, a);
+    const dim3 pg(cdiv(a.H + a.Hk, kPrepWaves), rows), pb(64 * kPrepWaves);
+    if (a.hd == 128) launch(k_attn_prep_h<128>, pg, pb, 0, st, a);
+    else if (a.hd == 64) launch(k_attn_prep_h<64>, pg, pb, 0, st, a);
+    else launch(k_attn_prep, pg, pb, 0, st, a);
   } else if (a.tab != nullptr && a.kv_row_stride == 0 && pw_ok(a)) {
     launch(k_attn_pw, dim3(a.H, cdiv(rows, kApRows)), dim3(kApThreads), kApLds, st, a, rows);
   } else if (a.tab != nullptr && a.kv_row_stride == 0 && pre_ok(a)) {

@@ -938,6 +938,94 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep(AttnArgs a) {
   }
 }
 
+// k_attn_prep at head dims 64 and 128 (NV = HD / 64 elements a lane: element lane + 64 k), without
+// branches on the elements: the head vector, the norm gains and the RoPE tables are requested
+// together; lanes [0, D) run the RMSNorm chain over an LDS copy; the RoPE partner of element j (j ^ 1,
+// the lane next door) comes by one DPP exchange; q goes back as fp32, k and v to int8 cache rows (a
+// byte a lane, consecutive lanes consecutive bytes). The numerics are head_norm_rope's.
+template <int HD>
+__global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h(AttnArgs a) {
+  constexpr int NV = HD / 64;
+  __shared__ float sv[kPrepWaves][HD];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = blockIdx.y, vi = blockIdx.x * kPrepWaves + wave;
+  if (vi >= a.H + a.Hk) return;                  // (wave-uniform; the kernel has no block barrier)
+  const int pos = a.pos[row];
+  if (pos < 0 || pos >= a.S) {                   // a position outside the cache: nothing is written
+    if (lane == 0) flag_bad_pos(a.status);
+    return;
+  }
+  const int q_dim = a.H * HD, kv_dim = a.Hk * HD;
+  float* qkv = a.qkv + row * a.qkv_stride;
+  const int32_t* pr = a.part + row * a.qkv_stride;
+  const float sx = a.part_nz > 1 ? a.part_sx[row] : 0.0f;
+  auto col = [&](int c) {                        // column c of the row's [q | k | v]
+    if (a.part_nz <= 1) return qkv[c];
+    int acc = 0;
+    for (int z = 0; z < a.part_nz; ++z) acc += pr[z * a.part_zstride + c];
+    return dequant(acc, a.part_sw[c], sx);
+  };
+  const bool isq = vi < a.H;
+  const int g = vi - a.H;
+  const int c0 = isq ? vi * HD : q_dim + g * HD;    // the vector (k for a KV head's wave)
+  const float* gain = isq ? a.qn : a.kn;
+  const float* cs = a.cos_t + (long long)pos * (HD / 2);
+  const float* sn = a.sin_t + (long long)pos * (HD / 2);
+  float x[NV], y[NV], gv[NV], c[NV], s[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int j = lane + 64 * k;
+    x[k] = col(c0 + j);
+    gv[k] = gain != nullptr ? gain[j] : 0.0f;
+    c[k] = cs[j >> 1];
+    s[k] = sn[j >> 1];
+  }
+  if (!isq) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) y[k] = col(q_dim + kv_dim + g * HD + lane + 64 * k);
+  }
+  if (gain != nullptr) {
+    float* v = sv[wave];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[lane + 64 * k] = x[k];
+    __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    float acc = 0.0f;
+    if (lane < a.D) {
+      const int n = HD / a.D;                    // the chain's length (HD a multiple of D)
+      acc = v[lane] * v[lane];
+#pragma unroll
+      for (int m = 1; m < HD / 8; ++m)
+        if (m < n) {
+          const float e = v[lane + m * a.D];
+          acc = acc + e * e;
+        }
+    }
+    const float r = sfu_rsqrt(lane_tree_sum(acc, a.D, lane) * a.inv_hd + a.eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) x[k] = (x[k] * r) * gv[k];
+  }
+  // RoPE: even element 2i -> (x c) + ((-x[2i+1]) s), odd 2i+1 -> (x c) + (x[2i] s)
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const float p = __int_as_float(dpp_mov_i<kDppXor1>(__float_as_int(x[k])));
+    x[k] = (lane & 1) ? (x[k] * c[k]) + (p * s[k]) : (x[k] * c[k]) + ((-p) * s[k]);
+  }
+  if (isq) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) qkv[c0 + lane + 64 * k] = x[k];
+    return;
+  }
+  int8_t* kc = a.kc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD;
+  int8_t* vc = a.vc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int j = lane + 64 * k, ch = g * HD + j;
+    kc[j] = (int8_t)to_i8(x[k] * (a.ch_isk ? a.ch_isk[ch] : a.inv_sk));
+    vc[j] = (int8_t)to_i8(y[k] * (a.ch_isv ? a.ch_isv[ch] : a.inv_sv));
+  }
+}
+
 // ------------------------------------------------------------------ prefill attention
 // ATTN_ONLY for many rows at once (rows whose q is rotated and whose KV rows are in the cache), one
 // workgroup of 8 or 16 waves per (query head, 16 consecutive rows). Scores and P.V run on the int8
