@@ -31,7 +31,8 @@ def caches(rng, S, kvd):
 
 @pytest.mark.parametrize("H_,Hk,hd,S,D", [(6, 6, 48, 256, 16), (9, 3, 64, 2048, 16), (16, 8, 128, 2048, 16),
                                          (32, 8, 64, 2048, 16), (4, 2, 32, 512, 8), (4, 2, 8, 16, 8),
-                                         (6, 2, 24, 96, 16), (8, 2, 128, 2048, 8), (4, 4, 128, 1000, 16)])
+                                         (6, 2, 24, 96, 16), (8, 2, 128, 2048, 8), (4, 4, 128, 1000, 16),
+                                         (32, 8, 64, 512, 16), (8, 2, 64, 500, 8), (9, 3, 64, 96, 16)])
 @pytest.mark.parametrize("layout", ["chunk", "scattered"])
 def test_attn_prefill_vs_oracle(env, H_, Hk, hd, S, D, layout):
     torch, N, ops, T, H = env
@@ -165,6 +166,29 @@ def test_model_exp_underflow(name):
     assert np.array_equal(got[0].view(np.uint32), w0.view(np.uint32))
     assert np.array_equal(got[1].view(np.uint32), w1.view(np.uint32))
     assert torch.equal(kc[1, :, 30].cpu(), torch.from_numpy(om.kc[:, 30]))
+
+
+@pytest.mark.parametrize("D", [16, 8])
+def test_attn_prefill_c4_prompt(env, D):
+    """C4's attention shape over its whole 512-row prompt at once (32 query heads, 8 KV heads, head dim
+    64, a 512-position cache: the 32-row kernel's head-dim-64 form, 16 blocks of 32 rows): every row
+    against the decode op, and rows at both ends of several blocks against the oracle."""
+    torch, N, ops, T, H = env
+    H_, Hk, hd, S, M = 32, 8, 64, 512, 512
+    rng = np.random.default_rng(512 + D)
+    kc, vc = caches(rng, S, Hk * hd)
+    pos = np.arange(M, dtype=np.int32)
+    q = (rng.standard_normal((M, H_ * hd)) * 2).astype(F)
+    a_k, a_v = F(0.05 / np.sqrt(hd)), F(0.03 / 127)
+    print(f"C4 prompt shape, D {D}: {M} rows", flush=True)
+    Tq, Tk, Tv, Tp = T(q), T(kc), T(vc), T(pos)
+    got = H(ops.attention_prefill(Tq, Tk, Tv, Tp, H_, Hk, a_k, a_v, D))
+    dec = H(ops.attention(Tq, Tk, Tv, Tp, H_, Hk, a_k, a_v, D))
+    bad = np.flatnonzero((got.view(np.uint32) != dec.view(np.uint32)).any(axis=1))
+    assert bad.size == 0, f"rows {bad[:8]} differ from the decode op"
+    for i in (0, 1, 31, 32, 255, 256, 479, 480, 511):
+        want = N.attention(q[i], kc[:i + 1], vc[:i + 1], H_, Hk, a_k, a_v, D)
+        assert np.array_equal(got[i].view(np.uint32), want.view(np.uint32)), f"row {i}"
 
 
 @pytest.mark.parametrize("D", [16, 8])

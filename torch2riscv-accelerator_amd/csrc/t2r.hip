@@ -79,7 +79,8 @@ int ensure_init() {
   for (const void* f : pre)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPreMaxLds) != hipSuccess)
       return T2R_EHIP;
-  if (hipFuncSetAttribute((const void*)k_attn_pw, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kApLds) != hipSuccess)
+  if (hipFuncSetAttribute((const void*)k_attn_pw<128>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ap_lds<128>()) != hipSuccess ||
+      hipFuncSetAttribute((const void*)k_attn_pw<64>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ap_lds<64>()) != hipSuccess)
     return T2R_EHIP;
   // the GEMM's deep-ring configuration: 128 KB of LDS, one workgroup per CU
   const void* deep[] = {(const void*)k_gemm_d<EPI_STORE, false, 128, 4>, (const void*)k_gemm_d<EPI_STORE, true, 128, 4>,
@@ -149,10 +150,11 @@ int pre_cap(const AttnArgs& a) { return a.t_cap > 0 && a.t_cap < a.S ? a.t_cap :
 bool pre_ok(const AttnArgs& a) {
   return a.hd % 16 == 0 && a.hd <= 128 && attn_pre_lds_bytes(pre_cap(a), (a.hd + 31) & ~31) <= kPreMaxLds;
 }
-// ... and its 32-row form (k_attn_pw): head dim 128 without the HF options, rows attending to at most
-// kApKeys positions
+// ... and its 32-row form (k_attn_pw): head dims 128 and 64 without the HF options, rows attending to at
+// most ap_keys positions
 bool pw_ok(const AttnArgs& a) {
-  return a.hd == 128 && !attn_opt(a) && pre_cap(a) <= kApKeys && (a.D == 8 || a.D == 16);
+  if (attn_opt(a) || !(a.D == 8 || a.D == 16)) return false;
+  return (a.hd == 128 && pre_cap(a) <= ap_keys<128>()) || (a.hd == 64 && pre_cap(a) <= ap_keys<64>());
 }
 
 // batch-1 decode attention split over workgroups per head (k_attn_dec's SPLIT forms): the heads of a
@@ -238,7 +240,9 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
     else if (a.hd == 64) launch(k_attn_prep_h<64>, pg, pb, 0, st, a);
     else launch(k_attn_prep, pg, pb, 0, st, a);
   } else if (a.tab != nullptr && a.kv_row_stride == 0 && pw_ok(a)) {
-    launch(k_attn_pw, dim3(a.H, cdiv(rows, kApRows)), dim3(kApThreads), kApLds, st, a, rows);
+    const dim3 grid_pw(a.H, cdiv(rows, kApRows));
+    if (a.hd == 128) launch(k_attn_pw<128>, grid_pw, dim3(kApThreads), ap_lds<128>(), st, a, rows);
+    else launch(k_attn_pw<64>, grid_pw, dim3(kApThreads), ap_lds<64>(), st, a, rows);
   } else if (a.tab != nullptr && a.kv_row_stride == 0 && pre_ok(a)) {
     const int hdp = (a.hd + 31) & ~31;
     dim3 pg(a.H, cdiv(rows, kPreRows));

@@ -1388,45 +1388,66 @@ inline size_t attn_pre_lds_bytes(int S, int HDP) {
 }
 
 // ------------------------------------------------------------------ prefill attention, 32-row blocks
-// k_attn_pre's numerics for head dim 128 without the HF options over up to kApKeys positions, one
-// 512-thread workgroup per (query head, 32 rows): every K and V byte read serves 32 rows, and the
-// MFMAs' 32 query columns / rows are all rows of the block. Wave w owns the key tiles (32 keys)
-// w, w + 8, ... (8 tiles at 2048 keys) from the scores to P.V, and keeps them in registers:
-//  - K tiles go global -> LDS by global_load_lds (whole 128-byte rows per instruction; chunk kc of row
-//    r at 16-byte position 8 r + (kc ^ swz(r)), the GEMM operand swizzle) into a two-tile ring of the
-//    wave's own; scores as S^T = K Q^T (v_mfma_i32_32x32x32_i8, A = the tile's 32 keys, B = the
-//    block's int8 q): lane (n, half) holds row n's scores of keys 8 (r / 4) + 4 half + r % 4, r < 16;
+// k_attn_pre's numerics without the HF options at head dims 128 (up to 2048 positions) and 64 (up to
+// 512), one 512-thread workgroup per (query head, 32 rows): every K and V byte read serves 32 rows,
+// and the MFMAs' 32 query columns / rows are all rows of the block. Wave w owns the key tiles (32
+// keys) w, w + 8, ... (TW of them at the largest T) from the scores to P.V, and keeps them in
+// registers:
+//  - K tiles go global -> LDS by global_load_lds (whole rows, 16 rows of 64 bytes or 8 of 128 per
+//    instruction; chunk kc of row r at 16-byte position CPR r + (kc ^ swz(r)), the GEMM operand
+//    swizzle) into a ring of the wave's own; scores as S^T = K Q^T (v_mfma_i32_32x32x32_i8, A = the
+//    tile's 32 keys, B = the block's int8 q): lane (n, half) holds row n's scores of keys
+//    8 (r / 4) + 4 half + r % 4, r < 16;
 //  - the row maximum (order-free) from each lane's, the two halves' and the waves' (LDS);
 //  - e = EXP(s - max) in place (sfu_exp_sm) and the D-lane ordered sums: the waves' tiles of 256
-//    keys at a time go to LDS (double-buffered) and each chain lane (row, l < D) adds keys l, l + D,
-//    ... of the chunk in order; chunks in key order, so every chain adds its keys in the reference's
-//    order (keys past T are +0, which leave a sum of non-negative terms unchanged); then the pairwise
-//    tree over the D lanes and RECIP;
+//    keys at a time go to LDS and each chain lane (row, l < D) adds keys l, l + D, ... of the chunk in
+//    order; chunks in key order, so every chain adds its keys in the reference's order (keys past T
+//    are +0, which leave a sum of non-negative terms unchanged); then the pairwise tree over the D
+//    lanes and RECIP;
 //  - p = to_i8(F(F(e r) 127)) packed in the lane's own key order: the P.V MFMA's A operand (its k
 //    order within a tile is that permutation of the keys; the V operand is gathered to match);
-//  - P.V: the tile's V rows loaded whole (lane: row 8 i + 4 (lane / 32) + lane % 4, 16-byte chunk
-//    (lane / 4) % 8, instruction i), a quad's four rows exchanged into words of four keys of one
-//    column (k_attn_pre's quad exchange); the four instructions' words of a column are the 16 bytes
-//    of that column's B operand, one LDS store each; four MFMAs (128 columns) a tile;
+//  - P.V: the tile's V rows loaded whole (lane: row 8 i + 4 (lane / 32) + lane % 4, chunk
+//    (lane / 4) % 8 of HD / 8 bytes, instruction i), a quad's four rows exchanged into words of four
+//    keys of one column (k_attn_pre's quad exchange); the four instructions' words of a column are
+//    the 16 bytes of that column's B operand, one LDS store each; HD / 32 MFMAs a tile;
 //  - the waves' int32 sums added by LDS integer atomics (exact in any order) and scaled.
+// HD 128 keeps 8 tiles a wave (128 score registers, one workgroup per CU, a four-tile K ring, two
+// exp-chunk buffers); HD 64 keeps 2 (512 positions), so that two workgroups share a CU.
 constexpr int kApRows = 32, kApThreads = 512, kApWaves = kApThreads / 64;
-constexpr int kApKeys = 2048;                            // positions a row may attend to
-constexpr int kApTW = kApKeys / 32 / kApWaves;          // key tiles a wave owns (16 score registers each)
 constexpr int kApStage = 256 + 16;                       // float stride of a row of a 256-key chunk
-constexpr int kApOStride = 128 + 8;                      // int32 stride of a row of the P.V sums
-constexpr int kApRing = 4;                               // K tiles (4 KB) in a wave's ring
-// dynamic LDS: the waves' K rings, then (reused) the two chunk buffers of exps, then (reused) the
-// waves' transposed V tiles (4 KB each)
-constexpr size_t kApLds = (size_t)kApWaves * kApRing * 4096;
-static_assert((size_t)2 * kApRows * kApStage * 4 <= kApLds && (size_t)kApWaves * 4096 <= kApLds, "LDS reuse");
+template <int HD> struct ApCfg;
+template <> struct ApCfg<128> { static constexpr int TW = 8, RING = 4, NSB = 2, MINB = 1; };
+template <> struct ApCfg<64> { static constexpr int TW = 2, RING = 2, NSB = 1, MINB = 2; };
+template <int HD> constexpr int ap_keys() { return 32 * kApWaves * ApCfg<HD>::TW; }   // positions a row may attend to
+// dynamic LDS: the waves' K rings, then (reused) the exp-chunk buffers, then (reused) the waves'
+// transposed V tiles
+template <int HD> constexpr size_t ap_lds() {
+  constexpr size_t ring = (size_t)kApWaves * ApCfg<HD>::RING * 32 * HD;
+  constexpr size_t stage = (size_t)ApCfg<HD>::NSB * kApRows * kApStage * 4;
+  constexpr size_t vt = (size_t)kApWaves * HD * 32;
+  return ring > stage ? (ring > vt ? ring : vt) : (stage > vt ? stage : vt);
+}
 
-__global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
-  constexpr int HD = 128, KS = HD / 32, NW = kApWaves, TW = kApTW;
+T2R_DEV v4i_t buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const v2i_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return v4i_t{v.x, v.y, 0, 0};
+}
+
+template <int HD>
+__global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArgs a, int M) {
+  constexpr int KS = HD / 32, NW = kApWaves, TW = ApCfg<HD>::TW, RING = ApCfg<HD>::RING, NSB = ApCfg<HD>::NSB;
+  constexpr int CPR = HD / 16;                    // 16-byte chunks of a K row
+  constexpr int NDMA = HD / 32;                   // DMA instructions (1 KB) a K tile
+  constexpr int TB = 32 * HD;                     // bytes of a K tile
+  constexpr int NQ = HD / 64;                     // q elements a lane and row
+  constexpr int VDW = HD / 32;                    // dwords a lane per V load (HD / 8 bytes)
+  constexpr int NCT = HD / 32;                    // P.V column tiles
+  constexpr int OST = HD + 8;                     // int32 stride of a row of the P.V sums
   extern __shared__ __align__(16) float big[];
   __shared__ __align__(16) float tab[kSfuWords];
   __shared__ __align__(16) float2 et[kSfuExpPairs];
   __shared__ __align__(16) int8_t Q8[kApRows][HD];
-  __shared__ __align__(16) int O[kApRows * kApOStride];
+  __shared__ __align__(16) int O[kApRows * OST];
   __shared__ __align__(16) float s_mx[kApRows][NW];
   __shared__ float s_sq[kApRows], s_r[kApRows];
   __shared__ int s_T[kApRows];
@@ -1439,13 +1460,13 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
 
   // ---- the loads that depend on nothing first: q of the wave's rows (rows wave, wave + 8, ...),
   // the SFU tables; then lane n's row: its position bounds T (rows past M or outside the cache: 0)
-  float qx[kApRows / NW][2];
+  float qx[kApRows / NW][NQ];
 #pragma unroll
   for (int k = 0; k < kApRows / NW; ++k) {
     const int r = min(r0 + wave + NW * k, M - 1);
     const float* q = a.qkv + (long long)r * a.qkv_stride + (long long)h * HD;
-    qx[k][0] = q[lane];
-    qx[k][1] = q[lane + 64];
+#pragma unroll
+    for (int e = 0; e < NQ; ++e) qx[k][e] = q[lane + 64 * e];
   }
   const v4f_t tv = tid < kSfuWords / 4 ? ((const v4f_t*)a.tab)[tid] : v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
   const float2 ev = tid < kSfuExpPairs ? sfu_exp_pair(tid, a.tab) : make_float2(0.0f, 0.0f);
@@ -1457,29 +1478,29 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   const int ntile = ((int)wave_max_u32((uint32_t)Tn) + 31) / 32;   // lanes n cover the 32 rows
   const int nown = ntile > wave ? (ntile - wave + NW - 1) / NW : 0;  // tiles this wave owns
 
-  // ---- the first two owned K tiles requested (DMA into the wave's ring) before q's quantisation.
-  // Rows past the cache are clamped to its last (their keys are past every T).
-  auto swz = [](int r) { return (r ^ (r >> 3)) & 7; };
-  int8_t* ring = (int8_t*)big + wave * (kApRing * 4096);
-  const int8_t* kcol[4];                             // this lane's 16-byte chunk of instruction i
+  // ---- the first RING - 1 owned K tiles requested (DMA into the wave's ring) before q's
+  // quantisation. Rows past the cache are clamped to its last (their keys are past every T).
+  auto swz = [](int r) { return CPR == 8 ? ((r ^ (r >> 3)) & 7) : ((r >> 2) & 3); };
+  int8_t* ring = (int8_t*)big + wave * (RING * TB);
+  const int8_t* kcol[NDMA];                          // this lane's 16-byte chunk of instruction i
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int pos = 64 * i + lane, r = pos >> 3;
-    kcol[i] = a.kc + (long long)g * HD + 16 * ((pos & 7) ^ swz(r));
+  for (int i = 0; i < NDMA; ++i) {
+    const int pos = 64 * i + lane, r = pos / CPR;
+    kcol[i] = a.kc + (long long)g * HD + 16 * ((pos % CPR) ^ swz(r));
   }
-  auto k_issue = [&](int j) {                        // owned tile j into ring slot j % kApRing
+  auto k_issue = [&](int j) {                        // owned tile j into ring slot j % RING
     const int ti = wave + NW * j;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = min(32 * ti + ((64 * i + lane) >> 3), S - 1);
+    for (int i = 0; i < NDMA; ++i) {
+      const int row = min(32 * ti + (64 * i + lane) / CPR, S - 1);
       __builtin_amdgcn_global_load_lds((const void*)(kcol[i] + (long long)row * kv_dim),
-                                       (void*)(ring + 4096 * (j % kApRing) + 1024 * i), 16, 0, 0);
+                                       (void*)(ring + TB * (j % RING) + 1024 * i), 16, 0, 0);
     }
   };
 #pragma unroll
-  for (int j = 0; j < kApRing - 1; ++j)
+  for (int j = 0; j < RING - 1; ++j)
     if (j < nown) k_issue(j);
-  for (int k = tid; k < kApRows * kApOStride; k += kApThreads) O[k] = 0;
+  for (int k = tid; k < kApRows * OST; k += kApThreads) O[k] = 0;
   if (wave == 0 && half == 0) s_T[n] = Tn;
 
   // ---- q of the block's rows to int8, a wave per row; invalid rows 0
@@ -1491,7 +1512,12 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
     // wave + 8 k); an invalid row's multiplier 0 gives q8 = to_i8(0 or NaN) = 0
     uint32_t am[kApRows / NW];
 #pragma unroll
-    for (int k = 0; k < kApRows / NW; ++k) am[k] = wave_max_u32(max(abs_bits(qx[k][0]), abs_bits(qx[k][1])));
+    for (int k = 0; k < kApRows / NW; ++k) {
+      uint32_t m = abs_bits(qx[k][0]);
+#pragma unroll
+      for (int e = 1; e < NQ; ++e) m = max(m, abs_bits(qx[k][e]));
+      am[k] = wave_max_u32(m);
+    }
     static_assert(kApRows / NW == 4, "four rows a wave");
     const uint32_t mine = lane == 0 ? am[0] : lane == 1 ? am[1] : lane == 2 ? am[2] : am[3];
     const float sq_l = fv(mine) * kInv127;
@@ -1501,17 +1527,18 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
       const int i = wave + NW * k;
       const bool ok = __shfl(Tn, i) > 0;            // lane i holds row i
       const float inv = ok ? fv((uint32_t)__builtin_amdgcn_readlane((int)fb(inv_l), k)) : 0.0f;
-      Q8[i][lane] = (int8_t)to_i8(qx[k][0] * inv);
-      Q8[i][lane + 64] = (int8_t)to_i8(qx[k][1] * inv);
+#pragma unroll
+      for (int e = 0; e < NQ; ++e) Q8[i][lane + 64 * e] = (int8_t)to_i8(qx[k][e] * inv);
       if (lane == k) s_sq[i] = sq_l;
     }
   }
   __syncthreads();
   const float sqn = s_sq[n];
 
-  // ---- scores of the owned tiles: tile j + 3 requested into the slot tile j - 1 left (its fragments
-  // were read before its MFMAs), then wait for tile j's DMA (the newer ones may be in flight), its A
-  // fragments from the ring and four MFMAs. Tiles wholly below every valid row's T need no mask.
+  // ---- scores of the owned tiles: tile j + RING - 1 requested into the slot tile j - 1 left (its
+  // fragments were read before its MFMAs), then wait for tile j's DMA (the newer ones may be in
+  // flight), its A fragments from the ring and KS MFMAs. Tiles wholly below every valid row's T need
+  // no mask.
   const int Tmin = (int)~wave_max_u32(~(Tn > 0 ? (uint32_t)Tn : 0xFFFFFFFFu));
   v4i_t qb[KS];
 #pragma unroll
@@ -1521,17 +1548,17 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
     if (j >= nown) break;
-    if (j + kApRing - 1 < nown) k_issue(j + kApRing - 1);
-    const int newer = min(nown - 1, j + kApRing - 1) - j;   // tiles requested after tile j
-    if (newer >= 3) __builtin_amdgcn_s_waitcnt(waitcnt_vm(12));
-    else if (newer == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
-    else if (newer == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4));
+    if (j + RING - 1 < nown) k_issue(j + RING - 1);
+    const int newer = min(nown - 1, j + RING - 1) - j;      // tiles requested after tile j
+    if (newer >= 3) __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * NDMA));
+    else if (newer == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NDMA));
+    else if (newer == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(NDMA));
     else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     asm volatile("" ::: "memory");
-    const int8_t* kt = ring + 4096 * (j % kApRing);
+    const int8_t* kt = ring + TB * (j % RING);
     v4i_t ka[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) ka[ks] = *(const v4i_t*)(kt + 16 * (8 * n + ((2 * ks + half) ^ swz(n))));
+    for (int ks = 0; ks < KS; ++ks) ka[ks] = *(const v4i_t*)(kt + 16 * (CPR * n + ((2 * ks + half) ^ swz(n))));
     v16i_t acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0;
@@ -1566,14 +1593,16 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   // y = F(F(e r) 127) lies in [0, 127] and to_i8(y) is y's RNE integer
   const bool fast = __all(Tn == 0 || __builtin_isfinite(mx));
 
-  // the first owned tile's V rows requested now, in flight through the softmax (P.V below)
+  // the first owned tiles' V rows requested now, in flight through the softmax (P.V below)
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc, (uint32_t)S * kv_dim);
   const int cq = (lane >> 2) & 7, vr = 4 * half + (lane & 3);
   auto v_load = [&](v4i_t (&dst)[4], int j) {
     const int ti = wave + NW * j;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dst[i] = buffer_load16(vrs, (uint32_t)(32 * ti + 8 * i + vr) * kv_dim + g * HD + 16 * cq);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t off = (uint32_t)(32 * ti + 8 * i + vr) * kv_dim + g * HD + (HD / 8) * cq;
+      dst[i] = HD == 128 ? buffer_load16(vrs, off) : buffer_load8(vrs, off);
+    }
   };
   v4i_t vb[4], vn[4], vn2[4];
   if (nown > 0) v_load(vb, 0);
@@ -1593,7 +1622,7 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
 #pragma unroll
   for (int k = 0; k < TW; ++k) {
     if (k >= nchunk) break;
-    float* sb = big + (k & 1) * (kApRows * kApStage);
+    float* sb = big + (k % NSB) * (kApRows * kApStage);
     // key k of row n at float n kApStage + 4 ((k / 4) ^ ((n / 4) % 4)) + k % 4: the 16-byte stores of
     // 16 rows land in distinct bank groups, a chain lane's 4-byte reads stay in one row's 16 banks
     float* wp = sb + n * kApStage;
@@ -1621,6 +1650,7 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
         for (int u = 0; u < 8; ++u) acc = acc + e[u];
       }
     }
+    if (NSB == 1 && k + 1 < nchunk) __syncthreads();   // one buffer: its reads before the next stores
   }
   // pairwise tree over the row's D lanes (within a 16-lane DPP row), RECIP on the row's first lane
   {
@@ -1666,30 +1696,30 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   }
 
   // ---- P.V of the owned tiles: V rows whole (lane: row 8 i + 4 half + lane % 4 of the tile, chunk
-  // cq = (lane / 4) % 8); the quad (four consecutive rows of one chunk) exchanged so that lane
-  // 4 k + cc holds, for dword d, the word of column 16 cq + 4 d + cc over the quad's rows = keys of
-  // key group 2 i + half; the four instructions' words are then keys 8 i' + 4 half + 0..3, i' = 0..3:
-  // that column's B operand half `half`, stored whole. Lane (column j, kg) reads its 16 bytes back.
-  // (column col, half kg) at 16-byte slot 16 (col / 16 + 8 kg) + ((col % 16) ^ 4 ((col / 16) % 4)): the
-  // stores of a 16-lane pass (four columns of four chunks) and the reads (16 consecutive columns) each
-  // meet 16 distinct bank groups
-  auto vslot = [](int col, int kg) { return 16 * ((col >> 4) + 8 * kg) + ((col & 15) ^ (((col >> 4) & 3) << 2)); };
-  int8_t* vt = (int8_t*)big + wave * 4096;          // 128 columns x 32 bytes
-  v16i_t pv[4];
+  // cq = (lane / 4) % 8 of HD / 8 bytes); the quad (four consecutive rows of one chunk) exchanged so
+  // that lane 4 k + cc holds, for dword d, the word of column (HD / 8) cq + 4 d + cc over the quad's
+  // rows = keys of key group 2 i + half; the four instructions' words are then keys 8 i' + 4 half +
+  // 0..3, i' = 0..3: that column's B operand half `half`, stored whole. Lane (column j, kg) reads its
+  // 16 bytes back. (column col, half kg) at 16-byte slot 16 (col / 16 + (HD / 16) kg) + ((col % 16) ^
+  // 4 ((col / 16) % 4)): the stores of a 16-lane pass and the reads (16 consecutive columns) each meet
+  // 16 distinct bank groups
+  auto vslot = [](int col, int kg) { return 16 * ((col >> 4) + (HD / 16) * kg) + ((col & 15) ^ (((col >> 4) & 3) << 2)); };
+  int8_t* vt = (int8_t*)big + wave * (HD * 32);   // HD columns x 32 bytes
+  v16i_t pv[NCT];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < NCT; ++c)
 #pragma unroll
     for (int r = 0; r < 16; ++r) pv[c][r] = 0;
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
     if (j >= nown) break;
     if (j + 2 < nown) v_load(vn2, j + 2);
-    uint32_t wd[4][4];                               // [dword d][instruction i]
+    uint32_t wd[VDW][4];                             // [dword d][instruction i]
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int w4[4] = {vb[i].x, vb[i].y, vb[i].z, vb[i].w};
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
+      for (int d = 0; d < VDW; ++d) {
         const uint32_t x = (uint32_t)w4[d];
         const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)x, kDppXor1, 0xF, 0xF, false);
         const uint32_t s1 = __builtin_amdgcn_perm(y, x, (lane & 1) ? 0x03070105u : 0x06020400u);
@@ -1699,13 +1729,13 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
     }
     __builtin_amdgcn_wave_barrier();                // the previous tile's operand reads come first
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
-      *(v4i_t*)&vt[16 * vslot(16 * cq + 4 * d + (lane & 3), half)] =
+    for (int d = 0; d < VDW; ++d)
+      *(v4i_t*)&vt[16 * vslot((HD / 8) * cq + 4 * d + (lane & 3), half)] =
           v4i_t{(int)wd[d][0], (int)wd[d][1], (int)wd[d][2], (int)wd[d][3]};
     __builtin_amdgcn_s_waitcnt(0xc07f);              // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < NCT; ++c) {
       const v4i_t vbop = *(const v4i_t*)&vt[16 * vslot(32 * c + n, half)];
       pv[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa[j], vbop, pv[c], 0, 0, 0);
     }
@@ -1719,21 +1749,24 @@ __global__ __launch_bounds__(kApThreads) void k_attn_pw(AttnArgs a, int M) {
   // ---- the waves' sums (exact int32 atomics), then att = F(f32(sum) a_v) of the valid rows
   if (nown > 0) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < NCT; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = 8 * (r >> 2) + 4 * half + (r & 3);
-        atomicAdd(&O[m * kApOStride + 32 * c + n], pv[c][r]);
+        atomicAdd(&O[m * OST + 32 * c + n], pv[c][r]);
       }
   }
   __syncthreads();
   {
-    const int m = tid >> 4, c0 = 8 * (tid & 15);
+    constexpr int CPT = HD / 16;                   // output columns a thread
+    const int m = tid >> 4, c0 = CPT * (tid & 15);
     if (s_T[m] > 0) {
-      const v4i_t s0 = *(const v4i_t*)&O[m * kApOStride + c0], s1 = *(const v4i_t*)&O[m * kApOStride + c0 + 4];
       float* out = a.att + (long long)(r0 + m) * a.att_stride + (long long)h * HD + c0;
-      *(v4f_t*)out = v4f_t{(float)s0.x * a.a_v, (float)s0.y * a.a_v, (float)s0.z * a.a_v, (float)s0.w * a.a_v};
-      *(v4f_t*)(out + 4) = v4f_t{(float)s1.x * a.a_v, (float)s1.y * a.a_v, (float)s1.z * a.a_v, (float)s1.w * a.a_v};
+#pragma unroll
+      for (int u = 0; u < CPT / 4; ++u) {
+        const v4i_t sv = *(const v4i_t*)&O[m * OST + c0 + 4 * u];
+        *(v4f_t*)(out + 4 * u) = v4f_t{(float)sv.x * a.a_v, (float)sv.y * a.a_v, (float)sv.z * a.a_v, (float)sv.w * a.a_v};
+      }
     }
   }
 }

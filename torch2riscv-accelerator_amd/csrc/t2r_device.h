@@ -22,6 +22,7 @@ namespace t2r {
 
 // Native vector types for values that are loaded and stored whole (HIP's int4 / float4 are
 // structs; arrays of them copied as aggregates can end up in scratch memory).
+typedef int v2i_t __attribute__((ext_vector_type(2)));
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 typedef int v16i_t __attribute__((ext_vector_type(16)));   // int8 MFMA 32 x 32 accumulators
