@@ -1618,36 +1618,54 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
   const int cpr = 64 / D, cr = wave * cpr + lane / D, cl = lane % D;
   const bool chain = cr < kApRows;
   const int nchunk = (ntile + NW - 1) / NW;
+  // Key k of row n sits at float n kApStage + 4 ((k / 4) ^ ((n / 4) % 4)) + k % 4: the 16-byte stores
+  // of 16 rows land in distinct bank groups, and a chain lane's 4-byte reads stay in one row's 16
+  // banks. The XOR touches the low two bits of the 16-byte slot, so each lane's addresses are a lane
+  // constant plus a fixed offset: the writer's slot 8 w + 2 rr + half -> wb[rr % 2] + 16 (rr / 2)
+  // floats; a chain lane's keys l + 16 u (D 16) -> cb0 + 16 u, l + 8 u (D 8) -> cb[u % 2] + 16 (u / 2).
+  const int sx = (n >> 2) & 3, cx = (cr >> 2) & 3;
+  const int wb0 = n * kApStage + 4 * ((8 * wave + half) ^ sx), wb1 = n * kApStage + 4 * ((8 * wave + 2 + half) ^ sx);
+  const int cb0 = cr * kApStage + 4 * ((cl >> 2) ^ cx) + (cl & 3);
+  const int cb1 = cr * kApStage + 4 * ((2 + (cl >> 2)) ^ cx) + (cl & 3);      // D 8: odd u
   float acc = 0.0f;
 #pragma unroll
   for (int k = 0; k < TW; ++k) {
     if (k >= nchunk) break;
     float* sb = big + (k % NSB) * (kApRows * kApStage);
-    // key k of row n at float n kApStage + 4 ((k / 4) ^ ((n / 4) % 4)) + k % 4: the 16-byte stores of
-    // 16 rows land in distinct bank groups, a chain lane's 4-byte reads stay in one row's 16 banks
-    float* wp = sb + n * kApStage;
-    const int sx = (n >> 2) & 3;
     if (k < nown) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[k][r] = sfu_exp_sm(sc[k][r] - mx, et);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
-        *(v4f_t*)(wp + 4 * ((8 * wave + 2 * rr + half) ^ sx)) =
+        *(v4f_t*)(sb + ((rr & 1) ? wb1 : wb0) + 16 * (rr >> 1)) =
             v4f_t{sc[k][4 * rr], sc[k][4 * rr + 1], sc[k][4 * rr + 2], sc[k][4 * rr + 3]};
     } else {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) *(v4f_t*)(wp + 4 * ((8 * wave + 2 * rr + half) ^ sx)) = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int rr = 0; rr < 4; ++rr) *(v4f_t*)(sb + ((rr & 1) ? wb1 : wb0) + 16 * (rr >> 1)) = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
     __syncthreads();
     if (chain) {
-      const float* cb = sb + cr * kApStage + (cl & 3);
-      const int cx = (cr >> 2) & 3;
-      for (int q0 = 0; q0 < 256; q0 += 8 * D) {
-        float e[8];
+      if (D == 16) {
+        const float* c0 = sb + cb0;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) e[u] = cb[4 * (((q0 + u * D + cl) >> 2) ^ cx)];
+        for (int h8 = 0; h8 < 2; ++h8) {
+          float e[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc = acc + e[u];
+          for (int u = 0; u < 8; ++u) e[u] = c0[16 * (8 * h8 + u)];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc = acc + e[u];
+        }
+      } else {
+        const float* c0 = sb + cb0;
+        const float* c1 = sb + cb1;
+#pragma unroll
+        for (int h8 = 0; h8 < 4; ++h8) {
+          float e[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) e[u] = (u & 1) ? c1[16 * ((8 * h8 + u) >> 1)] : c0[16 * ((8 * h8 + u) >> 1)];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc = acc + e[u];
+        }
       }
     }
     if (NSB == 1 && k + 1 < nchunk) __syncthreads();   // one buffer: its reads before the next stores
