@@ -59,9 +59,10 @@ int t2r_sfu(int fn, const uint32_t* x, uint32_t* y, int64_t n, void* stream);
 /* Self-check of the datapath SFU (no counterpart in the reference; for tests): every fp32 input
  * x in [first, first + count) (as bit patterns, count <= 2^32 - first) through fn (0 EXP,
  * 1 RECIP, 2 RSQRT, 3 the softmax's EXP on its domain x <= 0 and NaN, 4 the gates' RECIP on its
- * domain x >= 1 and NaN, 5 the softmax's EXP under a finite maximum on its domain x <= 0; other
- * inputs of fn 3, 4 and 5 skipped) as the kernels compute it and as the literal per-operation FTZ
- * sequence of llm/sfu.py:69-118 (EXP for fn 3 and 5, RECIP for fn 4). Device
+ * domain x >= 1 and NaN, 5 the softmax's EXP under a finite maximum on its domain x <= 0, 6 the
+ * gates' pair-table EXP on every non-NaN x, 7 the gates' pair-table RECIP on x >= 1 (not NaN);
+ * other inputs of fn 3 .. 7 skipped) as the kernels compute it and as the literal per-operation FTZ
+ * sequence of llm/sfu.py:69-118 (EXP for fn 3, 5 and 6, RECIP for fn 4 and 7). Device
  * out[0] = number of inputs whose results differ, out[1] = the smallest such input (0xFFFFFFFF if
  * none). */
 int t2r_sfu_check(int fn, uint64_t first, uint64_t count, uint32_t* out, void* stream);

@@ -68,13 +68,14 @@ def test_sfu_sweep_vs_oracle(env, name):
     assert bad.size == 0, [(hex(x[i]), hex(got[i]), hex(want[i])) for i in bad[:6]]
 
 
-@pytest.mark.parametrize("name", ["exp", "recip", "rsqrt", "exp_np", "recip_ge1", "exp_sm"])
+@pytest.mark.parametrize("name", ["exp", "recip", "rsqrt", "exp_np", "recip_ge1", "exp_sm", "exp_g", "recip_g1"])
 def test_sfu_exhaustive_vs_literal_sequence(env, name):
     """All 2^32 inputs: the datapath SFU (plain IEEE steps where the FTZ rule cannot change a result)
     equals the per-operation FTZ sequence of llm/sfu.py, which the sweep above pins to the oracle.
     'exp_np', the attention softmax's EXP, over its whole domain (x <= 0 and NaN: 2^31 + 2^23 inputs);
     'recip_ge1', the SwiGLU / GeGLU gates' RECIP, over its (x >= 1 and NaN); 'exp_sm', the prefill
-    softmax's EXP under a finite row maximum, over its (x <= 0: 2^31 + 1 inputs)."""
+    softmax's EXP under a finite row maximum, over its (x <= 0: 2^31 + 1 inputs); 'exp_g' and
+    'recip_g1', the prefill gate epilogues' pair-table forms, over every non-NaN input and x >= 1."""
     torch, N, ops, T, H = env
     bad, first = ops.sfu_check(name)
     assert bad == 0, (name, bad, None if first is None else hex(first))
@@ -128,7 +129,8 @@ def test_ieee_vector_steps_keep_subnormals(env):
 @pytest.mark.parametrize("N_,K,M", [(1, 16, 1), (37, 288, 1), (300, 2048, 1), (129, 8192, 1), (64, 1040, 3),
                                      (257, 3072, 5), (3072, 2048, 512), (40, 48, 77), (130, 288, 33),
                                      (2048, 8192, 130), (16, 16, 1000), (200, 576, 70), (1536, 1600, 260),
-                                     (960, 576, 40), (576, 1536, 64), (96, 8192, 63), (3072, 2048, 48)])
+                                     (960, 576, 40), (576, 1536, 64), (96, 8192, 63), (3072, 2048, 48),
+                                     (200, 1024, 100), (3500, 512, 300)])
 def test_linear_exact(env, N_, K, M):
     torch, N, ops, T, H = env
     rng = np.random.default_rng(N_ * 7 + K)

@@ -89,6 +89,12 @@ int ensure_init() {
   for (const void* f : deep)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmDDeepLds) != hipSuccess)
       return T2R_EHIP;
+  // the wave-split-K linears: four wave rings of 2 x (64 + TN) x 128 bytes (128 / 160 KB)
+  if (hipFuncSetAttribute((const void*)k_gemm_w<EPI_STORE, 64, 64>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_w_lds<64, 64>()) != hipSuccess ||
+      hipFuncSetAttribute((const void*)k_gemm_w<EPI_RESID, 64, 64>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_w_lds<64, 64>()) != hipSuccess ||
+      hipFuncSetAttribute((const void*)k_gemm_w<EPI_STORE, 64, 96>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_w_lds<64, 96>()) != hipSuccess ||
+      hipFuncSetAttribute((const void*)k_gemm_w<EPI_RESID, 64, 96>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_w_lds<64, 96>()) != hipSuccess)
+    return T2R_EHIP;
   // the grouped decode attention: score rows of caches up to kMaxS positions
   const void* gqa[] = {(const void*)k_attn_gqa<4, false, 1>, (const void*)k_attn_gqa<4, true, 1>,
                        (const void*)k_attn_gqa<4, false, 2>, (const void*)k_attn_gqa<4, true, 2>,
@@ -934,7 +940,7 @@ int t2r_sfu(int fn, const uint32_t* x, uint32_t* y, int64_t n, void* stream) {
 }
 
 int t2r_sfu_check(int fn, uint64_t first, uint64_t count, uint32_t* out, void* stream) {
-  if (fn < 0 || fn > 5 || !out || first > 0xFFFFFFFFull || count > 0x100000000ull - first) return T2R_EINVAL;
+  if (fn < 0 || fn > 7 || !out || first > 0xFFFFFFFFull || count > 0x100000000ull - first) return T2R_EINVAL;
   T2R_INIT();
   launch(k_sfu_check_init, dim3(1), dim3(64), 0, S(stream), out);
   if (count > 0) launch(k_sfu_check, dim3(8192), dim3(256), 0, S(stream), fn, (unsigned long long)first,

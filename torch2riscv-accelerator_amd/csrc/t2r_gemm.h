@@ -13,6 +13,7 @@
 // of W1 and the same 32 rows of W3, so a lane holds h1 and h3 of the same (m, n).
 #pragma once
 #include "t2r_gemv.h"
+#include <type_traits>
 
 namespace t2r {
 
@@ -296,8 +297,9 @@ T2R_DEV int xcd_order(int b, int n) {
 // so each 16-lane pass of a 128-bit fragment read hits all 64 banks once.
 // Wave w issues the slab's DMA instructions NI w .. NI w + NI - 1 (1 KB each, NI = BKD/16: the first
 // half fill A, the second B); lane l of instruction i fills position 64 (i mod 2NI) + l of its operand.
-// Every wave issues every slab's loads (a slab index past the range re-reads the last slab), so
-// `vmcnt((NST - 2) NI)` is always "this slab landed, NST - 2 newer in flight".
+// Every wave issues its share of every slab, slabs 0 .. nk - 1 only: before the MFMAs of slab s the
+// wave waits until at most min(NST - 2, nk - 1 - s) newer slabs of its own are in flight (its own
+// in-order vmcnt), then the barrier makes every wave's share of slab s visible.
 // BKD: K bytes per slab (64 or 128: a 128-byte row segment is one cache line per request);
 // NST: LDS stages (NST - 1 slabs in flight). Stage bytes 2 * 128 * BKD.
 template <int BKD, int NST, int BM = kGT>
@@ -311,27 +313,19 @@ constexpr size_t kGemmDDeepLds = gemm_d_lds<128, 4>();
 // and the 256-row tiles' ring (3 x 48 KB)
 constexpr size_t kGemmDTallLds = gemm_d_lds<128, 3, 2 * kGT>();
 
-// The LDS epilogue of k_gemm_d. C (int32) of the 64-row band b is staged as ct[64][kEpiCS] (SwiGLU:
-// the W1 and the W3 sums, 64 output columns each, then the SFU tables); then row mr, columns
-// 4 c .. 4 c + 3 are finished by one thread.
+// The LDS epilogue of k_gemm_d (store / residual). C (int32) of the 64-row band b is staged as
+// ct[64][kEpiCS]; then row mr, columns 4 c .. 4 c + 3 are finished by one thread.
 constexpr int kEpiCS = kGT + 4;                   // staged row stride (ints): 16-byte aligned rows
 template <int EPI, bool SPLIT, int BM>
 T2R_DEV void gemm_d_epilogue_vec(const GemmArgs& a, const v16i_t (&acc)[2][2], int8_t* lds, int m0, int n0, int z,
                                  int wm, int wn, int lane, int tid) {
+  static_assert(EPI != EPI_SWIGLU, "the gate epilogue runs in registers");
   constexpr int NT = 2 * BM, NB = BM / 64;
-  constexpr int OC = EPI == EPI_SWIGLU ? kGT / 2 : kGT;          // output columns of the tile
-  constexpr int CS = EPI == EPI_SWIGLU ? OC + 4 : kEpiCS;
+  constexpr int OC = kGT, CS = kEpiCS;                            // output columns of the tile, stride
   int* c1 = (int*)lds;                                            // [64][CS]
-  int* c3 = c1 + 64 * CS;                                         // SwiGLU: W3 sums [64][CS]
-  float* tab_lds = (float*)(c3 + (EPI == EPI_SWIGLU ? 64 * CS : 0));
   const int lr = lane & 31, kh = lane >> 5;
   __syncthreads();                                                // every wave is done with the ring
-  if constexpr (EPI == EPI_SWIGLU) {
-    v4f_t t4 = {0.f, 0.f, 0.f, 0.f};
-    if (tid < kSfuWords / 4) t4 = ((const v4f_t*)a.tab)[tid];
-    sfu_store(tab_lds, t4);
-  }
-  const int nbase = EPI == EPI_SWIGLU ? (n0 >> 1) : n0;           // first output column of the tile
+  const int nbase = n0;                                           // first output column of the tile
   for (int b = 0; b < NB; ++b) {
     if (wm == b) {
 #pragma unroll
@@ -339,13 +333,8 @@ T2R_DEV void gemm_d_epilogue_vec(const GemmArgs& a, const v16i_t (&acc)[2][2], i
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int mr = 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
-          if constexpr (EPI == EPI_SWIGLU) {
-            c1[mr * CS + wn * 32 + lr] = acc[i][0][r];
-            c3[mr * CS + wn * 32 + lr] = acc[i][1][r];
-          } else {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) c1[mr * CS + wn * 64 + j * 32 + lr] = acc[i][j][r];
-          }
+          for (int j = 0; j < 2; ++j) c1[mr * CS + wn * 64 + j * 32 + lr] = acc[i][j][r];
         }
     }
     __syncthreads();
@@ -360,19 +349,12 @@ T2R_DEV void gemm_d_epilogue_vec(const GemmArgs& a, const v16i_t (&acc)[2][2], i
           const float sx = a.s_x[m];
           const v4f_t sw = *(const v4f_t*)&a.s_w[n];
           v4f_t y;
-          if constexpr (EPI == EPI_SWIGLU) {
-            const v4i_t v3 = *(const v4i_t*)&c3[mr * CS + nc];
-            const v4f_t sw3 = *(const v4f_t*)&a.s_w3[n];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) y[q] = gate_mul(dequant(v[q], sw[q], sx), dequant(v3[q], sw3[q], sx), a.act, tab_lds);
-          } else {
+          for (int q = 0; q < 4; ++q) y[q] = dequant(v[q], sw[q], sx);
+          if constexpr (EPI == EPI_RESID) {
+            const v4f_t rv = *(const v4f_t*)&a.res[(long long)m * a.y_stride + n];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) y[q] = dequant(v[q], sw[q], sx);
-            if constexpr (EPI == EPI_RESID) {
-              const v4f_t rv = *(const v4f_t*)&a.res[(long long)m * a.y_stride + n];
-#pragma unroll
-              for (int q = 0; q < 4; ++q) y[q] = rv[q] + y[q];
-            }
+            for (int q = 0; q < 4; ++q) y[q] = rv[q] + y[q];
           }
           *(v4f_t*)&a.y[(long long)m * a.y_stride + n] = y;
         }
@@ -426,15 +408,14 @@ __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz
   // Each workgroup walks its K range from a different slab (the int32 sums are exact in any order):
   // the workgroups that share an A or B tile then do not request the same lines at the same time.
   const int rot = nk > 0 ? (mt + 3 * nt) % nk : 0;
-  auto issue = [&](int s, int stage) {
-    const long long k0 = (long long)(nk > 0 ? s0 + (min(s, nk - 1) + rot) % nk : min(s0, nslab - 1)) * BKD;
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const int i = NI * wave + j;
-      int8_t* dst = lds + stage * STB + (i >= NA ? OPA + 1024 * (i - NA) : 1024 * i);
-      __builtin_amdgcn_global_load_lds((const void*)(src[j] + k0), (void*)dst, 16, 0, 0);
-    }
+  // instruction j of this wave's share of slab s (s < nk) into stage s % NST
+  auto issue1 = [&](int s, int j) {
+    const long long k0 = (long long)(s0 + (s + rot) % nk) * BKD;
+    const int i = NI * wave + j;
+    int8_t* dst = lds + (s % NST) * STB + (i >= NA ? OPA + 1024 * (i - NA) : 1024 * i);
+    __builtin_amdgcn_global_load_lds((const void*)(src[j] + k0), (void*)dst, 16, 0, 0);
   };
+  constexpr int KKS = BKD / 32;                   // MFMA k-steps per slab
   v16i_t acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -447,20 +428,36 @@ __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz
     return *(const v4i_t*)(base + (row * CPR + (kc ^ swz(row))) * 16);
   };
 #pragma unroll
-  for (int p = 0; p < NST - 1; ++p) issue(p, p);
-  for (int s = 0; s < nk; ++s) {
-    // this wave's DMA of slab s landed (NST - 2 newer slabs in flight); then a bare s_barrier:
-    // every wave's part of slab s is in LDS, and every wave's reads of stage (s + NST - 1) % NST
-    // (slab s - 1, consumed by its MFMAs) are done. (__syncthreads would also wait for the newer DMAs.)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm((NST - 2) * NI));
+  for (int p = 0; p < NST - 1; ++p)
+    if (p < nk) {
+#pragma unroll
+      for (int j = 0; j < NI; ++j) issue1(p, j);
+    }
+  // slab s: MORE = slab s + NST - 1 exists (it goes into the stage slab s - 1 used)
+  auto step = [&](int s, auto more) {
+    constexpr bool MORE = decltype(more)::value;
+    // this wave's share of slab s landed; then a bare s_barrier: every wave's share of slab s is in
+    // LDS, and every wave's reads of stage (s + NST - 1) % NST (slab s - 1) are done. (__syncthreads
+    // would also wait for the newer DMAs.)
+    if constexpr (MORE) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm((NST - 2) * NI));
+    } else {
+      const int newer = nk - 1 - s;                 // < NST - 1
+      if (newer >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NI));
+      else if (newer == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(NI));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    issue(s + NST - 1, (s + NST - 1) % NST);
+    if constexpr (MORE) {
+#pragma unroll
+      for (int j = 0; j < NI; ++j) issue1(s + NST - 1, j);
+    }
     const int8_t* As = lds + (s % NST) * STB;
     const int8_t* Bs = As + OPA;
 #pragma unroll
-    for (int kk = 0; kk < BKD / 32; ++kk) {
+    for (int kk = 0; kk < KKS; ++kk) {
       v4i_t fa[2], fb[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) fa[i] = frag(As, wm * 64 + i * 32 + lr, 2 * kk + kh);
@@ -471,21 +468,28 @@ __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
-  }
+  };
+  int s = 0;
+  for (; s + NST - 1 < nk; ++s) step(s, std::true_type{});
+  for (; s < nk; ++s) step(s, std::false_type{});
   __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): no DMA into LDS outlives the workgroup
 
-  // Epilogue through LDS (16-byte aligned operands, no int32 copy requested): the tile's int32 sums go
-  // to LDS a 64-row band at a time (written by the band's two waves, read back by every thread), and
-  // each thread then finishes four consecutive columns of a row with one 16-byte load per operand
-  // (scales, residual) and one 16-byte store, instead of the MFMA layout's 4-byte accesses.
+  // Store / residual epilogue through LDS (16-byte aligned operands, no int32 copy requested): the
+  // tile's int32 sums go to LDS a 64-row band at a time (written by the band's two waves, read back by
+  // every thread), and each thread then finishes four consecutive columns of a row with one 16-byte
+  // load per operand (scales, residual) and one 16-byte store, instead of the MFMA layout's 4-byte
+  // accesses. The SwiGLU gate runs on the accumulators in registers (below): it is VALU-bound, its
+  // W1 and W3 sums of an output sit in one lane, and a wave's 4-byte stores cover two 128-byte rows.
   {
     const bool vec = a.acc_out == nullptr && a.N % 4 == 0 && a.y_stride % 4 == 0 &&
-                     ((uintptr_t)a.s_w & 15) == 0 && (EPI != EPI_SWIGLU || ((uintptr_t)a.s_w3 & 15) == 0) &&
+                     ((uintptr_t)a.s_w & 15) == 0 &&
                      (SPLIT ? ((uintptr_t)a.part & 15) == 0 : ((uintptr_t)a.y & 15) == 0) &&
                      (EPI != EPI_RESID || SPLIT || ((uintptr_t)a.res & 15) == 0);
-    if (vec) {
-      gemm_d_epilogue_vec<EPI, SPLIT, BM>(a, acc, lds, m0, n0, z, wm, wn, lane, tid);
-      return;
+    if constexpr (EPI != EPI_SWIGLU) {
+      if (vec) {
+        gemm_d_epilogue_vec<EPI, SPLIT, BM>(a, acc, lds, m0, n0, z, wm, wn, lane, tid);
+        return;
+      }
     }
   }
 
@@ -515,11 +519,11 @@ __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz
   if constexpr (EPI == EPI_SWIGLU) {
     const int n = (n0 >> 1) + wn * 32 + lr, nc = min(n, a.N - 1);
     const float sw1 = a.s_w[nc], sw3 = a.s_w3[nc];
-    v4f_t t4 = {0.f, 0.f, 0.f, 0.f};
-    if (tid < kSfuWords / 4) t4 = ((const v4f_t*)a.tab)[tid];
-    float* tab_lds = (float*)lds;
+    float2* ep = (float2*)lds;                    // the gates' pair tables
+    float2* rp = ep + kSfuExpPairs;
     __syncthreads();                              // every wave is done with the stage ring
-    sfu_store(tab_lds, t4);
+    if (tid < kSfuExpPairs) ep[tid] = sfu_exp_pair(tid, a.tab);
+    if (tid < 64) rp[tid] = sfu_recip_pair(tid, a.tab);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -528,7 +532,7 @@ __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz
         const int m = mrow(i, r);
         if (m >= a.M || n >= a.N) continue;
         const int ac1 = acc[i][0][r], ac3 = acc[i][1][r];
-        a.y[(long long)m * a.y_stride + n] = gate_mul(dequant(ac1, sw1, sx[i][r]), dequant(ac3, sw3, sx[i][r]), a.act, tab_lds);
+        a.y[(long long)m * a.y_stride + n] = gate_mul_p(dequant(ac1, sw1, sx[i][r]), dequant(ac3, sw3, sx[i][r]), a.act, ep, rp);
         if (a.acc_out) {
           a.acc_out[(long long)m * 2 * a.N + n] = ac1;
           a.acc_out[(long long)m * 2 * a.N + a.N + n] = ac3;
@@ -565,6 +569,124 @@ __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz
   }
 }
 
+// ---- narrow store / residual linears (Wqkv, Wo, W2 at a few hundred rows): small tiles, K split over
+// the four waves of the workgroup instead of over workgroups. Tile TM x TN (TM = 64, TN = 64 or 96); wave
+// w takes the K range [w K/4, (w + 1) K/4) in 128-byte slabs through a ring of its own (kGwStages
+// stages of (TM + TN) x 128 bytes, the k_gemm_d layout and swizzle), so the K loop has no workgroup
+// barrier: each wave waits on its own in-order vmcnt only, with kGwStages - 1 of its slabs in flight
+// behind the one it multiplies (a stage is refilled as soon as its fragments are in registers). The
+// four int32 partial tiles meet in LDS (exact in any order) and the epilogue finishes four columns per
+// thread with 16-byte accesses. No int32 partials leave the workgroup, so no finishing pass follows.
+// Requires K % 512 == 0, N % 4 == 0 and 16-byte aligned s_w / y / res (the launcher checks).
+constexpr int kGwStages = 2;
+template <int TM, int TN>
+constexpr size_t gemm_w_lds() { return (size_t)4 * kGwStages * (TM + TN) * 128; }
+template <int EPI, int TM, int TN>
+__global__ __launch_bounds__(256) void k_gemm_w(GemmArgs a, int ntile) {
+  static_assert(EPI != EPI_SWIGLU, "store / residual only");
+  constexpr int CPR = 8, FM = TM / 32, FN = TN / 32;
+  constexpr int NA = TM * CPR / 64, NI = (TM + TN) * CPR / 64;     // DMA instructions per slab (A, all)
+  constexpr int STB = (TM + TN) * 128, WRB = kGwStages * STB;      // stage / wave ring bytes
+  constexpr int PS = TN + 4;                                       // partial tile row stride (ints)
+  static_assert(NI * (kGwStages - 1) <= 63, "vmcnt range");
+  static_assert(4 * TM * PS * 4 <= 4 * WRB, "partial tiles fit in the rings");
+  extern __shared__ __align__(16) int8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int mtiles = cdiv_i(a.M, TM);
+  const int w = xcd_order((int)blockIdx.x, ntile);                // M tiles fastest: weight tiles shared in L2
+  const int mt = w % mtiles, nt = w / mtiles, m0 = mt * TM, n0 = nt * TN;
+  const int K = a.K, nk = K / 512, s0 = wave * nk;                 // this wave's slabs s0 .. s0 + nk - 1
+  int8_t* ring = lds + wave * WRB;
+  auto swz = [](int r) { return (r ^ (r >> 3)) & 7; };
+  // lane's source row and chunk for DMA instruction i (A rows 0 .. TM - 1, then B rows)
+  const int8_t* src[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int ii = i < NA ? i : i - NA, pos = 64 * ii + lane, r = pos / CPR, kc = (pos % CPR) ^ swz(r);
+    if (i < NA) {
+      src[i] = a.xq + (long long)min(m0 + r, a.M - 1) * K + 16 * kc;
+    } else {
+      int n;
+      bool ok;
+      src[i] = b_row<EPI>(a, n0, r, n, ok) + 16 * kc;
+    }
+  }
+  auto issue = [&](int s) {
+    const long long k0 = (long long)(s0 + s) * 128;
+    int8_t* st = ring + (s % kGwStages) * STB;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0), (void*)(st + 1024 * i), 16, 0, 0);
+  };
+  v16i_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  const int lr = lane & 31, kh = lane >> 5;
+  auto frag = [&](const int8_t* base, int row, int kc) { return *(const v4i_t*)(base + (row * CPR + (kc ^ swz(row))) * 16); };
+#pragma unroll
+  for (int p = 0; p < kGwStages; ++p)
+    if (p < nk) issue(p);
+  for (int s = 0; s < nk; ++s) {
+    // slab s landed: kGwStages - 1 newer ones in flight, fewer at the end of the range
+    if (s + kGwStages - 1 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm((kGwStages - 1) * NI));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    asm volatile("" ::: "memory");
+    const int8_t* As = ring + (s % kGwStages) * STB;
+    const int8_t* Bs = As + TM * 128;
+    v4i_t fa[4][FM], fb[4][FN];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) fa[kk][i] = frag(As, i * 32 + lr, 2 * kk + kh);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) fb[kk][j] = frag(Bs, j * 32 + lr, 2 * kk + kh);
+    }
+    // the stage's fragments are in registers: refill it with slab s + kGwStages
+    __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    if (s + kGwStages < nk) issue(s + kGwStages);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): no DMA into LDS outlives the K loop
+  __syncthreads();                                // every wave is done with every ring
+  int* pt = (int*)lds + wave * TM * PS;           // this wave's partial tile [TM][PS]
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pt[(32 * i + 8 * (r >> 2) + 4 * kh + (r & 3)) * PS + 32 * j + lr] = acc[i][j][r];
+  __syncthreads();
+  const int* p0 = (const int*)lds;
+  for (int e = tid; e < TM * (TN / 4); e += 256) {
+    const int mr = e / (TN / 4), nc = 4 * (e % (TN / 4));
+    const int m = m0 + mr, n = n0 + nc;
+    if (m >= a.M || n >= a.N) continue;                           // (N % 4 == 0: all four columns)
+    v4i_t v = *(const v4i_t*)(p0 + mr * PS + nc);
+#pragma unroll
+    for (int q = 1; q < 4; ++q) v += *(const v4i_t*)(p0 + q * TM * PS + mr * PS + nc);
+    const float sx = a.s_x[m];
+    const v4f_t sw = *(const v4f_t*)&a.s_w[n];
+    v4f_t y;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y[q] = dequant(v[q], sw[q], sx);
+    if constexpr (EPI == EPI_RESID) {
+      const v4f_t rv = *(const v4f_t*)&a.res[(long long)m * a.y_stride + n];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) y[q] = rv[q] + y[q];
+    }
+    *(v4f_t*)&a.y[(long long)m * a.y_stride + n] = y;
+  }
+}
+
 // split-K finish: acc = sum of the nz partials (exact), then the STORE / RESID epilogue
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_fin(GemmArgs a, int nz) {
@@ -590,6 +712,26 @@ inline int gemm_splits(int M, int ncols, int K, int part_rows, int epi, bool def
   int z = 1;
   while (z < 4 && tiles * z * 2 <= 256 && K / kBK >= 16 * z && (long long)M * z * 2 <= 4LL * part_rows) z *= 2;
   return z;
+}
+
+// The wave-split-K kernel where its tiles fill the chip in one round (at most 256 workgroups of 64 x 64,
+// else of 64 x 96) and its operand rules hold; -1: not taken (the caller uses k_gemm_d). Two rounds
+// (C3's 2032-row Wo and W2: 512 tiles) measured slower than k_gemm_d's split-K: 20.1 / 24.9 against
+// 14.8 / 17.5 us.
+template <int EPI>
+int gemm_w_launch(const GemmArgs& a, hipStream_t st) {
+  if (a.K % 512 || a.N % 4 || a.y_stride % 4 || a.acc_out != nullptr || ((uintptr_t)a.s_w & 15) ||
+      ((uintptr_t)a.y & 15) || (EPI == EPI_RESID && ((uintptr_t)a.res & 15)))
+    return -1;
+  const long long mt = cdiv_i(a.M, 64), t64 = mt * cdiv_i(a.N, 64), t96 = mt * cdiv_i(a.N, 96);
+  if (t64 <= 256) {
+    launch((k_gemm_w<EPI, 64, 64>), dim3((unsigned)t64), dim3(256), gemm_w_lds<64, 64>(), st, a, (int)t64);
+  } else if (t96 <= 256) {
+    launch((k_gemm_w<EPI, 64, 96>), dim3((unsigned)t96), dim3(256), gemm_w_lds<64, 96>(), st, a, (int)t96);
+  } else {
+    return -1;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 // defer_z (STORE / RESID): when the launch splits K, the int32 partials [z, M, N] are left in a.part
@@ -816,6 +958,10 @@ int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0, int* defer
   // the direct-to-LDS kernel (split-K for the narrow STORE / RESID layers)
   if (EPI == EPI_SWIGLU) defer_z = nullptr;
   if (defer_z) *defer_z = 1;
+  if constexpr (EPI != EPI_SWIGLU) {                     // narrow linears: K split over waves
+    const int r = gemm_w_launch<EPI>(a, st);
+    if (r != -1) return r;
+  }
   if (a.K % 64 == 0) {
     const int z = gemm_splits(a.M, ncols, a.K, a.part != nullptr ? part_rows : 0, EPI, defer_z != nullptr);
     // a grid of at most one workgroup per CU takes the deep ring (4 x 32 KB: three 128-byte slabs in

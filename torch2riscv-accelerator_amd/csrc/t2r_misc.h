@@ -704,8 +704,9 @@ __global__ void k_sfu_check_init(uint32_t* out) {
   }
 }
 __global__ void k_sfu_check(int fn, unsigned long long first, unsigned long long count, uint32_t* out) {
-  __shared__ float2 et[kSfuExpPairs];
+  __shared__ float2 et[kSfuExpPairs], rt[64];
   if (threadIdx.x < kSfuExpPairs) et[threadIdx.x] = sfu_exp_pair(threadIdx.x, c_sfu);
+  if (threadIdx.x < 64) rt[threadIdx.x] = sfu_recip_pair(threadIdx.x, c_sfu);
   __syncthreads();
   uint32_t bad = 0, lowest = 0xFFFFFFFFu;
   for (unsigned long long k = blockIdx.x * (unsigned long long)blockDim.x + threadIdx.x; k < count;
@@ -721,6 +722,12 @@ __global__ void k_sfu_check(int fn, unsigned long long first, unsigned long long
     } else if (fn == 5) {                       // the finite-maximum softmax form (x <= 0, not NaN)
       if (!(v <= 0.0f)) continue;
       a = fb(sfu_exp_sm(v, et)); b = fb(seq::sfu_exp(v, c_sfu));
+    } else if (fn == 6) {                       // the gates' pair-table EXP (x not NaN)
+      if (v != v) continue;
+      a = fb(sfu_exp_g(v, et)); b = fb(seq::sfu_exp(v, c_sfu));
+    } else if (fn == 7) {                       // the gates' pair-table RECIP (x >= 1 or +inf)
+      if (!(v >= 1.0f)) continue;
+      a = fb(sfu_recip_g1(v, rt)); b = fb(seq::sfu_recip(v, c_sfu));
     } else if (fn == 4) {                       // the gate form, on its domain (x >= 1, NaN)
       if (v < 1.0f) continue;
       a = fb(sfu_recip_ge1(v)); b = fb(seq::sfu_recip(v, c_sfu));

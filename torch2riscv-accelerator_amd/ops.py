@@ -37,8 +37,9 @@ def sfu_check(fn, first=0, count=1 << 32):
     (number of differing results, smallest differing input or None). 'exp_np': the softmax's EXP,
     checked against EXP on its domain (x <= 0 and NaN); 'recip_ge1': the gates' RECIP, against RECIP
     on its domain (x >= 1 and NaN); 'exp_sm': the softmax's EXP under a finite maximum, against EXP
-    on its domain (x <= 0); other inputs skipped."""
-    code = {"exp": 0, "recip": 1, "rsqrt": 2, "exp_np": 3, "recip_ge1": 4, "exp_sm": 5}[fn]
+    on its domain (x <= 0); 'exp_g' / 'recip_g1': the gates' pair-table EXP (x not NaN) and RECIP
+    (x >= 1, not NaN), against EXP and RECIP; other inputs skipped."""
+    code = {"exp": 0, "recip": 1, "rsqrt": 2, "exp_np": 3, "recip_ge1": 4, "exp_sm": 5, "exp_g": 6, "recip_g1": 7}[fn]
     out = torch.empty(2, dtype=torch.int32, device="cuda")
     abi.call("t2r_sfu_check", code, first, count, abi.ptr(out), _s())
     n, lo = (int(v) & 0xFFFFFFFF for v in out.cpu().tolist())
