@@ -525,6 +525,26 @@ __global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz
     if (tid < kSfuExpPairs) ep[tid] = sfu_exp_pair(tid, a.tab);
     if (tid < 64) rp[tid] = sfu_recip_pair(tid, a.tab);
     __syncthreads();
+    // A whole tile without an int32 copy: no bounds checks, one gate branch for the tile, and each
+    // store at the tile's (uniform) origin plus a 32-bit byte offset: one add per output.
+    if (a.acc_out == nullptr && m0 + BM <= a.M && (n0 >> 1) + kGT / 2 <= a.N) {
+      char* yb = (char*)(a.y + (long long)m0 * a.y_stride + (n0 >> 1));
+      const uint32_t ys4 = 4u * (uint32_t)a.y_stride;
+      const uint32_t lo4 = (uint32_t)(wm * 64 + kh * 4) * ys4 + 4u * (uint32_t)(wn * 32 + lr);
+      auto run = [&](auto gelu) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float h1 = dequant(acc[i][0][r], sw1, sx[i][r]), h3 = dequant(acc[i][1][r], sw3, sx[i][r]);
+            const float g = decltype(gelu)::value ? gelu_mul_p(h1, h3, ep, rp) : silu_mul_p(h1, h3, ep, rp);
+            *(float*)(yb + (lo4 + (uint32_t)(32 * i + 8 * (r >> 2) + (r & 3)) * ys4)) = g;
+          }
+      };
+      if (a.act) run(std::true_type{});
+      else run(std::false_type{});
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
