@@ -366,7 +366,7 @@ T2R_DEV void gemm_d_epilogue_vec(const GemmArgs& a, const v16i_t (&acc)[2][2], i
 
 // BM: tile rows (128: four waves, 2 x 2; 256: eight waves, 4 x 2), always 128 columns.
 template <int EPI, bool SPLIT, int BKD, int NST, int BM = kGT>
-__global__ __launch_bounds__(2 * BM) void k_gemm_d(GemmArgs a, int ntile, int nz) {
+__global__ __launch_bounds__(2 * BM, (BKD == 64 && NST == 3) ? 3 : 1) void k_gemm_d(GemmArgs a, int ntile, int nz) {
   constexpr int CPR = BKD / 16;                   // 16-byte chunks per row per slab
   constexpr int NWAVE = 2 * BM / 64;
   constexpr int NA = BM * CPR / 64;               // DMA instructions (1 KB each) of A per slab; B: 2 CPR
@@ -992,6 +992,12 @@ int gemm_launch(const GemmArgs& a, hipStream_t st, int part_rows = 0, int* defer
     if constexpr (EPI == EPI_SWIGLU) {
       // 256-row tiles (eight waves) with a 3 x 48 KB ring: two slabs in flight, one workgroup per CU
       if (a.M >= 2 * kGT && a.M <= 1024) return gemm_d_launch<EPI, 128, 3, 2 * kGT>(a, st, z, defer_z);
+      // three 128 x 128 workgroups a CU (3 x 16 KB stages of 64-byte slabs each, 160 VGPRs) where two a
+      // CU would leave a partial second round (C3's 768 tiles: 36.9 -> 31.3 us)
+      if (a.M > 1024) {
+        const long long t = (long long)cdiv_i(a.M, kGT) * cdiv_i(2 * a.N, kGT);
+        if (t > 512 && t <= 768) return gemm_d_launch<EPI, 64, 3>(a, st, z, defer_z);
+      }
     }
     return nwg <= 256 ? gemm_d_launch<EPI, 128, 4>(a, st, z, defer_z) : gemm_d_launch<EPI, 128, 2>(a, st, z, defer_z);
   }
