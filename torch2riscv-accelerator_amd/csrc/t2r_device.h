@@ -688,4 +688,41 @@ T2R_DEV float ordered_sum_t(const float* buf, int n, int D, int P, int l) {
   return lane_tree_sum(acc, D, l);
 }
 
+// ordered_sum_t for a lane whose chain is the only work of its wave: all 16-value batches of the
+// chain requested at once (G <= 16 * NB, NB x 16 registers), then the adds in order.
+template <bool SQ, int NB>
+T2R_DEV float ordered_sum_t_all(const float* buf, int n, int D, int P, int l) {
+  const int G = n > 0 ? (n + D - 1) / D : 1;
+  if (G < 16 || G > 16 * NB) return ordered_sum_t<SQ>(buf, n, D, P, l);
+  const float* row = buf + l * P;
+  const int nb = G / 16;
+  float4 c[NB][4];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+    if (b < nb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) c[b][q] = *(const float4*)(row + 16 * b + 4 * q);
+  float acc = 0.0f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b < nb) {
+      float v[16] = {c[b][0].x, c[b][0].y, c[b][0].z, c[b][0].w, c[b][1].x, c[b][1].y, c[b][1].z, c[b][1].w,
+                     c[b][2].x, c[b][2].y, c[b][2].z, c[b][2].w, c[b][3].x, c[b][3].y, c[b][3].z, c[b][3].w};
+      if (SQ) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = v[j] * v[j];
+      }
+      acc = b == 0 ? v[0] : acc + v[0];
+#pragma unroll
+      for (int j = 1; j < 16; ++j) acc = acc + v[j];
+    }
+  }
+  for (int g = 16 * nb; g < G; ++g) {
+    float v = row[g];
+    if (SQ) v = v * v;
+    acc = acc + v;
+  }
+  return lane_tree_sum(acc, D, l);
+}
+
 }  // namespace t2r

@@ -465,7 +465,8 @@ T2R_DEV void pw_prologue(const GemvArgs& a, int row, int8_t* xq_lds, float* xf_l
   __builtin_amdgcn_wave_barrier();
   float rr = 0.0f;
   if (lane < a.D) {
-    const float ss = ordered_sum_t<false>(xf_lds, K, a.D, P, lane);
+    // the chain's values requested at once (K / D <= 128; C4 decode 1,903 -> 1,909 tok/s)
+    const float ss = ordered_sum_t_all<false, 8>(xf_lds, K, a.D, P, lane);
     rr = sfu_rsqrt(ss * a.inv_n + a.eps, tab_lds);
   }
   const float r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rr), 0));
