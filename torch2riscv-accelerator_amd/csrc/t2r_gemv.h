@@ -206,7 +206,7 @@ T2R_DEV void stage_load(XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& a, int ro
 
 // RMSNorm / quant_act from the staged registers (same numerics as gemv_prologue); leaves the int8
 // activations in xq_lds and the SFU tables in tab_lds, returns s_x
-template <int PRO, int EPI, int NCB, int NT>
+template <int PRO, int EPI, int NCB, int NT, bool DEEP = false>
 T2R_DEV float stage_finish(const XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& a, int row, int8_t* xq_lds,
                            float* xf_lds, float* tab_lds, float* red) {
   typedef XStage<PRO, EPI, NCB, NT> S;
@@ -250,7 +250,8 @@ T2R_DEV float stage_finish(const XStage<PRO, EPI, NCB, NT>& st, const GemvArgs& 
       }
     __syncthreads();
     if (tid < a.D) {
-      const float ss = ordered_sum_t<false>(xf_lds, K, a.D, P, tid);
+      // DEEP: the chain's values requested at once (K / D <= 128)
+      const float ss = DEEP ? ordered_sum_t_all<false, 8>(xf_lds, K, a.D, P, tid) : ordered_sum_t<false>(xf_lds, K, a.D, P, tid);
       if (tid == 0) red[32] = sfu_rsqrt(ss * a.inv_n + a.eps, tab_lds);
     }
     __syncthreads();

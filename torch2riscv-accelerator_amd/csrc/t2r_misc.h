@@ -24,6 +24,11 @@ __global__ __launch_bounds__(256) void k_embed(const int8_t* emb_q, const float*
     for (int i = threadIdx.x; i < nkeys; i += blockDim.x) keys[i] = 0;
 }
 
+// The prefill row kernels over rows of more than 1024 values request their norm chain's values at once
+// (C4's 512 rows: prefill 1.86 -> 1.83 ms); over shorter rows, with thousands of rows, the registers
+// that takes cost more occupancy than it saves (C3 measured slower).
+template <int NCB>
+constexpr bool rows_deep() { return NCB == 2; }
 // RMSNorm and / or quant_act of rows (prefill inputs of the MFMA GEMM; the op-level ABI).
 // out_f: normalised rows (optional), xq / s_x: quantised rows (optional).
 __global__ __launch_bounds__(kGemvThreads) void k_rows_norm_quant(GemvArgs a, int norm, float* out_f, long long out_stride) {
@@ -53,7 +58,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_rows_quant(GemvArgs a) {
   const int row = blockIdx.x;
   XStage<PRO, EPI_STORE, NCB, kGemvThreads> st;
   stage_load(st, a, row);
-  const float s_x = stage_finish(st, a, row, xq_lds, xf_lds, tab_lds, red);
+  const float s_x = stage_finish<PRO, EPI_STORE, NCB, kGemvThreads, rows_deep<NCB>()>(st, a, row, xq_lds, xf_lds, tab_lds, red);
   int8_t* out = a.xq_out + row * a.xq_stride;
   for (int i = threadIdx.x * 16; i < a.K; i += kGemvThreads * 16) *(v4i_t*)(out + i) = *(const v4i_t*)(xq_lds + i);
   if (threadIdx.x == 0) a.sx_out[row] = s_x;
@@ -111,7 +116,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_rows_fin_quant(GemvArgs a, Fin
     const int i = (tid + j * kGemvThreads) * 4;
     if (i < K) *(float4*)(xr + i) = v;
   }
-  const float s_x = stage_finish(st, a, row, xq_lds, xf_lds, tab_lds, red);
+  const float s_x = stage_finish<PRO_NORM_QUANT, EPI_STORE, NCB, kGemvThreads, rows_deep<NCB>()>(st, a, row, xq_lds, xf_lds, tab_lds, red);
   int8_t* out = a.xq_out + row * a.xq_stride;
   for (int i = tid * 16; i < K; i += kGemvThreads * 16) *(v4i_t*)(out + i) = *(const v4i_t*)(xq_lds + i);
   if (tid == 0) a.sx_out[row] = s_x;
