@@ -1026,6 +1026,98 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h(AttnArgs a) {
   }
 }
 
+// k_attn_prep_h with half a wave per head vector (two vectors a wave, HD / 32 elements a lane): the
+// same steps per vector, with the two vectors' chains, pairwise trees and RSQRTs in the same
+// instructions (lanes [0, D) and [32, 32 + D)). A wave's halves may hold a q and a k vector (odd H):
+// each half stores what its vector writes.
+template <int HD>
+__global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h2(AttnArgs a) {
+  constexpr int NV = HD / 32;
+  __shared__ float sv[kPrepWaves][2][HD];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, hl = lane & 31;
+  const int row = blockIdx.y, w2 = 2 * (blockIdx.x * kPrepWaves + wave);
+  const int nvec = a.H + a.Hk;
+  if (w2 >= nvec) return;                        // (wave-uniform; the kernel has no block barrier)
+  const int pos = a.pos[row];
+  if (pos < 0 || pos >= a.S) {                   // a position outside the cache: nothing is written
+    if (lane == 0) flag_bad_pos(a.status);
+    return;
+  }
+  const bool live = w2 + half < nvec;            // the second half of the last wave when nvec is odd
+  const int vi = min(w2 + half, nvec - 1);
+  const int q_dim = a.H * HD, kv_dim = a.Hk * HD;
+  float* qkv = a.qkv + row * a.qkv_stride;
+  const int32_t* pr = a.part + row * a.qkv_stride;
+  const float sx = a.part_nz > 1 ? a.part_sx[row] : 0.0f;
+  auto col = [&](int c) {                        // column c of the row's [q | k | v]
+    if (a.part_nz <= 1) return qkv[c];
+    int acc = 0;
+    for (int z = 0; z < a.part_nz; ++z) acc += pr[z * a.part_zstride + c];
+    return dequant(acc, a.part_sw[c], sx);
+  };
+  const bool isq = vi < a.H;
+  const int g = isq ? 0 : vi - a.H;
+  const int c0 = isq ? vi * HD : q_dim + g * HD;  // the vector (k for a KV head's half)
+  const float* gain = isq ? a.qn : a.kn;
+  const float* cs = a.cos_t + (long long)pos * (HD / 2);
+  const float* sn = a.sin_t + (long long)pos * (HD / 2);
+  float x[NV], y[NV], gv[NV], c[NV], s[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int j = hl + 32 * k;
+    x[k] = col(c0 + j);
+    gv[k] = gain != nullptr ? gain[j] : 0.0f;
+    c[k] = cs[j >> 1];
+    s[k] = sn[j >> 1];
+    y[k] = isq ? 0.0f : col(q_dim + kv_dim + g * HD + j);
+  }
+  if (a.qn != nullptr || a.kn != nullptr) {      // QK-norm of the halves whose vector has a gain
+    float* v = sv[wave][half];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[hl + 32 * k] = x[k];
+    __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    float acc = 0.0f;
+    if (hl < a.D) {
+      const int n = HD / a.D;                    // the chain's length (HD a multiple of D)
+      acc = v[hl] * v[hl];
+#pragma unroll
+      for (int m = 1; m < HD / 8; ++m)
+        if (m < n) {
+          const float e = v[hl + m * a.D];
+          acc = acc + e * e;
+        }
+    }
+    acc = lane_tree_rows(acc, a.D, lane);
+    const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+    const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 32));
+    const float r = sfu_rsqrt((half ? s1 : s0) * a.inv_hd + a.eps);
+    if (gain != nullptr)
+#pragma unroll
+      for (int k = 0; k < NV; ++k) x[k] = (x[k] * r) * gv[k];
+  }
+  // RoPE: even element 2i -> (x c) + ((-x[2i+1]) s), odd 2i+1 -> (x c) + (x[2i] s)
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const float p = __int_as_float(dpp_mov_i<kDppXor1>(__float_as_int(x[k])));
+    x[k] = (lane & 1) ? (x[k] * c[k]) + (p * s[k]) : (x[k] * c[k]) + ((-p) * s[k]);
+  }
+  if (!live) return;
+  if (isq) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) qkv[c0 + hl + 32 * k] = x[k];
+  } else {
+    int8_t* kc = a.kc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD;
+    int8_t* vc = a.vc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int j = hl + 32 * k, ch = g * HD + j;
+      kc[j] = (int8_t)to_i8(x[k] * (a.ch_isk ? a.ch_isk[ch] : a.inv_sk));
+      vc[j] = (int8_t)to_i8(y[k] * (a.ch_isv ? a.ch_isv[ch] : a.inv_sv));
+    }
+  }
+}
+
 // ------------------------------------------------------------------ prefill attention
 // ATTN_ONLY for many rows at once (rows whose q is rotated and whose KV rows are in the cache), one
 // workgroup of 8 or 16 waves per (query head, 16 consecutive rows). Scores and P.V run on the int8

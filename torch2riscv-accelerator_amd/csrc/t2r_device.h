@@ -556,6 +556,19 @@ T2R_DEV float wave_max(float v) {
 
 // The pairwise tree of the ordered sum over lanes [0, D) of a row (D <= 16 a power of two):
 // lane l, l % 2s == 0, adds lane l + s; returns lane 0's total to every lane that calls it.
+// lane_tree_sum's pairwise steps without the broadcast: the sum of lanes [r, r + D) ends in lane r of
+// every 16-lane row r (D <= 16), so two half waves can sum two vectors at once (lanes 0 and 32)
+T2R_DEV float lane_tree_rows(float acc, int D, int l) {
+  float o = dpp_f<0x101>(acc);                                  // row_shl:1
+  if (D > 1 && (l & 1) == 0) acc = acc + o;
+  o = dpp_f<0x102>(acc);
+  if (D > 2 && (l & 3) == 0) acc = acc + o;
+  o = dpp_f<0x104>(acc);
+  if (D > 4 && (l & 7) == 0) acc = acc + o;
+  o = dpp_f<0x108>(acc);
+  if (D > 8 && (l & 15) == 0) acc = acc + o;
+  return acc;
+}
 T2R_DEV float lane_tree_sum(float acc, int D, int l) {
   float o = dpp_f<0x101>(acc);                                  // row_shl:1
   if (D > 1 && (l & 1) == 0) acc = acc + o;
