@@ -1498,10 +1498,10 @@ inline size_t attn_pre_lds_bytes(int S, int HDP) {
 //    lanes and RECIP;
 //  - p = to_i8(F(F(e r) 127)) packed in the lane's own key order: the P.V MFMA's A operand (its k
 //    order within a tile is that permutation of the keys; the V operand is gathered to match);
-//  - P.V: the tile's V rows loaded whole (lane: row 8 i + 4 (lane / 32) + lane % 4, chunk
-//    (lane / 4) % 8 of HD / 8 bytes, instruction i), a quad's four rows exchanged into words of four
-//    keys of one column (k_attn_pre's quad exchange); the four instructions' words of a column are
-//    the 16 bytes of that column's B operand, one LDS store each; HD / 32 MFMAs a tile;
+//  - P.V: the tile's V rows loaded whole (16-byte chunks, HD / 32 loads a lane), stored in the K
+//    ring's layout to an LDS tile of the wave's own and read back transposed by the LDS transpose
+//    read (ds_read_b64_tr_b8), two reads a B operand gathering column n's bytes of the A operand's
+//    keys; HD / 32 MFMAs a tile;
 //  - the waves' int32 sums added by LDS integer atomics (exact in any order) and scaled.
 // HD 128 keeps 8 tiles a wave (128 score registers, one workgroup per CU, a four-tile K ring, two
 // exp-chunk buffers); HD 64 keeps 2 (512 positions), so that two workgroups share a CU.
@@ -1520,9 +1520,11 @@ template <int HD> constexpr size_t ap_lds() {
   return ring > stage ? (ring > vt ? ring : vt) : (stage > vt ? stage : vt);
 }
 
-T2R_DEV v4i_t buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const v2i_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-  return v4i_t{v.x, v.y, 0, 0};
+// ds_read_b64_tr_b8 (gfx950 LDS transpose read): in each 16-lane group, lane 8 h + j receives as
+// byte b (b < 8) the byte at the address supplied by the group's lane 2 b + h, plus j
+T2R_DEV v2i_t lds_read_tr8(int8_t* p) {
+  typedef __attribute__((address_space(3))) v2i_t lds_v2i_t;
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)p);
 }
 
 template <int HD>
@@ -1532,7 +1534,7 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
   constexpr int NDMA = HD / 32;                   // DMA instructions (1 KB) a K tile
   constexpr int TB = 32 * HD;                     // bytes of a K tile
   constexpr int NQ = HD / 64;                     // q elements a lane and row
-  constexpr int VDW = HD / 32;                    // dwords a lane per V load (HD / 8 bytes)
+  constexpr int NV = HD / 32;                     // 16-byte V loads a lane and tile
   constexpr int NCT = HD / 32;                    // P.V column tiles
   constexpr int OST = HD + 8;                     // int32 stride of a row of the P.V sums
   extern __shared__ __align__(16) float big[];
@@ -1685,18 +1687,19 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
   // y = F(F(e r) 127) lies in [0, 127] and to_i8(y) is y's RNE integer
   const bool fast = __all(Tn == 0 || __builtin_isfinite(mx));
 
-  // the first owned tiles' V rows requested now, in flight through the softmax (P.V below)
+  // the first owned tiles' V rows requested now, in flight through the softmax (P.V below): load i
+  // of a tile gives the lane chunk (64 i + lane) % CPR of row (64 i + lane) / CPR (rows past the
+  // cache read 0 through the buffer's range; their p is 0)
   const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc, (uint32_t)S * kv_dim);
-  const int cq = (lane >> 2) & 7, vr = 4 * half + (lane & 3);
-  auto v_load = [&](v4i_t (&dst)[4], int j) {
+  auto v_load = [&](v4i_t (&dst)[NV], int j) {
     const int ti = wave + NW * j;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t off = (uint32_t)(32 * ti + 8 * i + vr) * kv_dim + g * HD + (HD / 8) * cq;
-      dst[i] = HD == 128 ? buffer_load16(vrs, off) : buffer_load8(vrs, off);
+    for (int i = 0; i < NV; ++i) {
+      const int pos = 64 * i + lane;
+      dst[i] = buffer_load16(vrs, (uint32_t)(32 * ti + pos / CPR) * kv_dim + g * HD + 16 * (pos % CPR));
     }
   };
-  v4i_t vb[4], vn[4], vn2[4];
+  v4i_t vb[NV], vn[NV], vn2[NV];
   if (nown > 0) v_load(vb, 0);
   if (nown > 1) v_load(vn, 1);
 
@@ -1805,16 +1808,25 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
     }
   }
 
-  // ---- P.V of the owned tiles: V rows whole (lane: row 8 i + 4 half + lane % 4 of the tile, chunk
-  // cq = (lane / 4) % 8 of HD / 8 bytes); the quad (four consecutive rows of one chunk) exchanged so
-  // that lane 4 k + cc holds, for dword d, the word of column (HD / 8) cq + 4 d + cc over the quad's
-  // rows = keys of key group 2 i + half; the four instructions' words are then keys 8 i' + 4 half +
-  // 0..3, i' = 0..3: that column's B operand half `half`, stored whole. Lane (column j, kg) reads its
-  // 16 bytes back. (column col, half kg) at 16-byte slot 16 (col / 16 + (HD / 16) kg) + ((col % 16) ^
-  // 4 ((col / 16) % 4)): the stores of a 16-lane pass and the reads (16 consecutive columns) each meet
-  // 16 distinct bank groups
-  auto vslot = [](int col, int kg) { return 16 * ((col >> 4) + (HD / 16) * kg) + ((col & 15) ^ (((col >> 4) & 3) << 2)); };
-  int8_t* vt = (int8_t*)big + wave * (HD * 32);   // HD columns x 32 bytes
+  // ---- P.V of the owned tiles: a tile's V rows stored as loaded, row r's chunk kc at 16-byte slot
+  // CPR r + (kc ^ swz(r)) of the wave's LDS tile (the K ring's layout), and read back transposed
+  // (lds_read_tr8). The B operand of lane (column n, half) is column 32 c + n over keys
+  // 8 (q / 4) + 4 half + q % 4, q < 16 (the A operand's key order): its read t (bytes q = 8 t ..)
+  // takes, from group lane k, row 16 t + 8 (k / 8) + 4 half + (k / 2) % 4 at column
+  // 32 c + 16 (group % 2) + 8 (k % 2). The stores of a 16-lane pass and each group's reads meet
+  // distinct 16-byte bank groups.
+  int8_t* vt = (int8_t*)big + wave * TB;
+  uint32_t tra[NCT][2];                            // the lane's read addresses in the tile
+  {
+    const int gq = lane >> 4, b = (lane & 15) >> 1;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = 16 * t + 8 * (b >> 2) + 4 * (gq >> 1) + (b & 3);
+#pragma unroll
+      for (int c = 0; c < NCT; ++c)
+        tra[c][t] = (uint32_t)(row * HD + 16 * ((2 * c + (gq & 1)) ^ swz(row)) + 8 * (lane & 1));
+    }
+  }
   v16i_t pv[NCT];
 #pragma unroll
   for (int c = 0; c < NCT; ++c)
@@ -1824,33 +1836,21 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
   for (int j = 0; j < TW; ++j) {
     if (j >= nown) break;
     if (j + 2 < nown) v_load(vn2, j + 2);
-    uint32_t wd[VDW][4];                             // [dword d][instruction i]
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int w4[4] = {vb[i].x, vb[i].y, vb[i].z, vb[i].w};
-#pragma unroll
-      for (int d = 0; d < VDW; ++d) {
-        const uint32_t x = (uint32_t)w4[d];
-        const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)x, kDppXor1, 0xF, 0xF, false);
-        const uint32_t s1 = __builtin_amdgcn_perm(y, x, (lane & 1) ? 0x03070105u : 0x06020400u);
-        const uint32_t y2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s1, kDppXor2, 0xF, 0xF, false);
-        wd[d][i] = __builtin_amdgcn_perm(y2, s1, (lane & 2) ? 0x03020706u : 0x05040100u);
-      }
-    }
     __builtin_amdgcn_wave_barrier();                // the previous tile's operand reads come first
 #pragma unroll
-    for (int d = 0; d < VDW; ++d)
-      *(v4i_t*)&vt[16 * vslot((HD / 8) * cq + 4 * d + (lane & 3), half)] =
-          v4i_t{(int)wd[d][0], (int)wd[d][1], (int)wd[d][2], (int)wd[d][3]};
+    for (int i = 0; i < NV; ++i) {
+      const int pos = 64 * i + lane, r = pos / CPR;
+      *(v4i_t*)(vt + 16 * (CPR * r + ((pos % CPR) ^ swz(r)))) = vb[i];
+    }
     __builtin_amdgcn_s_waitcnt(0xc07f);              // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {
-      const v4i_t vbop = *(const v4i_t*)&vt[16 * vslot(32 * c + n, half)];
-      pv[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa[j], vbop, pv[c], 0, 0, 0);
+      const v2i_t lo = lds_read_tr8(vt + tra[c][0]), hi = lds_read_tr8(vt + tra[c][1]);
+      pv[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa[j], v4i_t{lo.x, lo.y, hi.x, hi.y}, pv[c], 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NV; ++i) {
       vb[i] = vn[i];
       vn[i] = vn2[i];
     }

@@ -210,20 +210,19 @@ T2R_DEV float2 sfu_exp_pair(int i, const float* tab) {
 //    pair 64's T (and 0 S[64] = 0);
 //  - no entry flush: x in (-2^-126, 0) gives t in (-2^-125, 0), floor -1, F(t + 1) = 1, u = 64, y = 2,
 //    and 2 2^-1 = 1 = T[0], the EXP of the flushed zero;
-//  - no NaN select (x is never NaN).
+//  - no NaN select (x is never NaN);
+//  - t clamped at -127 (not -160) and the power of two applied as a product, y F(2^n): with n >= -126
+//    F(2^n) is normal and y 2^n (y in [1, 2]) exact and normal, the reference's result; n = -127 (t in
+//    [-127, -126), and every t below, clamped to -127) gives F(2^n)'s bits 0, so y 0 = +0, the
+//    reference's underflow there (its y < 2: u = 64 (t + 127) is exact, at most 64 - 2^-11, and
+//    F(T[63] + F(r S[63])) stays below 2 for r <= 1 - 2^-11).
 T2R_DEV float sfu_exp_sm(float x, const float2* et) {
-  const float tc = fmaxf(x * (float)1.4426950408889634, -160.0f);
+  const float tc = fmaxf(x * (float)1.4426950408889634, -127.0f);
   const float tf = floorf(tc);
   const float u = (tc - tf) * 64.0f;
   const float2 ts = et[(int)u];
-  const uint32_t b = fb(ts.x + __builtin_amdgcn_fractf(u) * ts.y);
-  const int e = (int)(b + ((uint32_t)(int)tf << 23));
-  // e < 2^23 -> +0 as integer steps (e - 2^23 > -2^31 here; the shift in asm, so that the compiler
-  // does not turn it back into a compare and select, whose lane masks it would keep in scalar
-  // registers across the unrolled callers)
-  uint32_t m;
-  asm("v_ashrrev_i32 %0, 31, %1" : "=v"(m) : "v"(e - 0x00800000));
-  return fv((uint32_t)e & ~m);
+  const float y = ts.x + __builtin_amdgcn_fractf(u) * ts.y;
+  return y * fv(((uint32_t)(int)tf << 23) + 0x3F800000u);
 }
 
 // RECIP (llm/sfu.py:12-15, 85-96)
