@@ -79,8 +79,10 @@ int ensure_init() {
   for (const void* f : pre)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPreMaxLds) != hipSuccess)
       return T2R_EHIP;
-  if (hipFuncSetAttribute((const void*)k_attn_pw<128>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ap_lds<128>()) != hipSuccess ||
-      hipFuncSetAttribute((const void*)k_attn_pw<64>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ap_lds<64>()) != hipSuccess)
+  if (hipFuncSetAttribute((const void*)k_attn_pw<128, false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ap_lds<128>()) != hipSuccess ||
+      hipFuncSetAttribute((const void*)k_attn_pw<64, false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ap_lds<64>()) != hipSuccess ||
+      hipFuncSetAttribute((const void*)k_attn_pw<128, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ap_lds<128>()) != hipSuccess ||
+      hipFuncSetAttribute((const void*)k_attn_pw<64, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)ap_lds<64>()) != hipSuccess)
     return T2R_EHIP;
   // the GEMM's deep-ring configuration: 128 KB of LDS, one workgroup per CU
   const void* deep[] = {(const void*)k_gemm_d<EPI_STORE, false, 128, 4>, (const void*)k_gemm_d<EPI_STORE, true, 128, 4>,
@@ -162,6 +164,8 @@ bool pw_ok(const AttnArgs& a) {
   if (attn_opt(a) || !(a.D == 8 || a.D == 16)) return false;
   return (a.hd == 128 && pre_cap(a) <= ap_keys<128>()) || (a.hd == 64 && pre_cap(a) <= ap_keys<64>());
 }
+// the multi-row ATTN_ONLY launch runs k_attn_pw (only then may q come as int8 rows: AttnArgs::q8)
+inline bool pw_takes(const AttnArgs& a) { return a.tab != nullptr && a.kv_row_stride == 0 && pw_ok(a); }
 
 // batch-1 decode attention split over workgroups per head (k_attn_dec's SPLIT forms): the heads of a
 // model whose shape takes it (head dim 128, caches over 512 rows, 4 splits a head in at most 256
@@ -179,6 +183,10 @@ inline bool attn_split_to_linear(const AttnArgs& a, int rows) { return attn_spli
 int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
   if (a.H <= 0 || a.Hk <= 0 || a.H % a.Hk || a.hd <= 0 || a.hd > kMaxHd || a.hd % 8 || a.S <= 0 || a.S > kMaxS ||
       (a.D != 8 && a.D != 16))
+    return T2R_ESHAPE;
+  // int8 q rows (AttnArgs::q8) pass from the prep kernels at head dims 64 / 128 to k_attn_pw only
+  if (a.q8 != nullptr && (mode == ATTN_FUSED || (mode == ATTN_PREP && a.hd != 64 && a.hd != 128) ||
+                          (mode == ATTN_ONLY && !pw_takes(a))))
     return T2R_ESHAPE;
   const size_t lds = mode == ATTN_PREP ? 0 : attn_lds_bytes(a.S, a.D);
   dim3 grid(a.H, rows), block(kAttnThreads);
@@ -250,10 +258,17 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
     else if (a.hd == 128) launch(k_attn_prep_h<128>, pg, pb, 0, st, a);
     else if (a.hd == 64) launch(k_attn_prep_h<64>, pg, pb, 0, st, a);
     else launch(k_attn_prep, pg, pb, 0, st, a);
-  } else if (a.tab != nullptr && a.kv_row_stride == 0 && pw_ok(a)) {
+  } else if (pw_takes(a)) {
     const dim3 grid_pw(a.H, cdiv(rows, kApRows));
-    if (a.hd == 128) launch(k_attn_pw<128>, grid_pw, dim3(kApThreads), ap_lds<128>(), st, a, rows);
-    else launch(k_attn_pw<64>, grid_pw, dim3(kApThreads), ap_lds<64>(), st, a, rows);
+    // (q quantized by the prep kernel when the caller set q8: the Q8I form)
+    if (a.q8 != nullptr) {
+      if (a.hd == 128) launch((k_attn_pw<128, true>), grid_pw, dim3(kApThreads), ap_lds<128>(), st, a, rows);
+      else launch((k_attn_pw<64, true>), grid_pw, dim3(kApThreads), ap_lds<64>(), st, a, rows);
+    } else if (a.hd == 128) {
+      launch((k_attn_pw<128, false>), grid_pw, dim3(kApThreads), ap_lds<128>(), st, a, rows);
+    } else {
+      launch((k_attn_pw<64, false>), grid_pw, dim3(kApThreads), ap_lds<64>(), st, a, rows);
+    }
   } else if (a.tab != nullptr && a.kv_row_stride == 0 && pre_ok(a)) {
     const int hdp = (a.hd + 31) & ~31;
     dim3 pg(a.H, cdiv(rows, kPreRows));
@@ -676,6 +691,13 @@ int run_layer(Model* m, int l, int rows, const int32_t* pos, int mode, hipStream
     if (decode || batch) {
       if ((rc = attn_launch(ATTN_FUSED, at, rows, st))) return rc;
     } else {
+      // k_attn_pw at head dim 128 takes q as the prep kernel's int8 rows: in xq (free from the Wqkv
+      // linear to the Wo row quant) with their scales in u (free until the FFN): C3's attention 62.5
+      // against 65.6 us from fp32 q. (At head dim 64 the prep kernel's quant_act costs
+      // what the attention saves: C4's prep 6.3 against 5.3 us, its attention 10.3 against 11.3.)
+      if (pw_takes(at) && d.head_dim == 128 && m->ffn_rows >= d.heads) {
+        at.q8 = m->xq; at.q8_stride = m->q_dim; at.q8s = m->u;
+      }
       if ((rc = attn_launch(ATTN_PREP, at, rows, st))) return rc;
       if ((rc = attn_launch(ATTN_ONLY, at, rows, st))) return rc;
     }

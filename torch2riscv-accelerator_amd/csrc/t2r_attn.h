@@ -82,6 +82,12 @@ struct AttnArgs {
   // the model's status word (nullptr: none): bit 1 a split's bounded wait ran out, bit 2 a row's
   // position was outside the cache (the row is then neither read nor written)
   int32_t* status;
+  // prefill at head dims 64 / 128: the prep kernels' quant_act of each q head vector, the int8 rows
+  // [rows, q8_stride] and the scales [rows, H], written instead of the fp32 q and read by the
+  // 32-row attention (k_attn_pw's Q8I form); nullptr: q stays fp32 in qkv
+  int8_t* q8;
+  long long q8_stride;
+  float* q8s;
 };
 
 // a row whose position is outside the cache: its kernels end at once and flag it (bit 2)
@@ -984,6 +990,8 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h(AttnArgs a) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) y[k] = col(q_dim + kv_dim + g * HD + lane + 64 * k);
   }
+  // int8 q (a.q8): RECIP's 64 table pairs, lane i holding pair i, read by lane exchange
+  const float2 rt = isq && a.q8 != nullptr ? sfu_recip_pair(lane, c_sfu) : make_float2(0.0f, 0.0f);
   if (gain != nullptr) {
     float* v = sv[wave];
 #pragma unroll
@@ -1011,6 +1019,19 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h(AttnArgs a) {
     const float p = __int_as_float(dpp_mov_i<kDppXor1>(__float_as_int(x[k])));
     x[k] = (lane & 1) ? (x[k] * c[k]) + (p * s[k]) : (x[k] * c[k]) + ((-p) * s[k]);
   }
+  if (isq && a.q8 != nullptr) {
+    // quant_act of the q vector for k_attn_pw: s = F(max |q| F(1/127)), q8 = to_i8(F(q RECIP(s)))
+    uint32_t am = abs_bits(x[0]);
+#pragma unroll
+    for (int k = 1; k < NV; ++k) am = max(am, abs_bits(x[k]));
+    const float sq = fv(wave_max_u32(am)) * kInv127;
+    const float inv = sfu_recip_by(sq, [&](int i) { return make_float2(__shfl(rt.x, i), __shfl(rt.y, i)); });
+    int8_t* q8 = a.q8 + row * a.q8_stride + vi * HD;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) q8[lane + 64 * k] = (int8_t)to_i8(x[k] * inv);
+    if (lane == 0) a.q8s[row * a.H + vi] = sq;
+    return;
+  }
   if (isq) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) qkv[c0 + lane + 64 * k] = x[k];
@@ -1026,14 +1047,21 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h(AttnArgs a) {
   }
 }
 
-// k_attn_prep_h with half a wave per head vector (two vectors a wave, HD / 32 elements a lane): the
-// same steps per vector, with the two vectors' chains, pairwise trees and RSQRTs in the same
-// instructions (lanes [0, D) and [32, 32 + D)). A wave's halves may hold a q and a k vector (odd H):
-// each half stores what its vector writes.
+// k_attn_prep_h with half a wave per head vector (two vectors a wave): the same steps per vector, with
+// the two vectors' chains, pairwise trees and RSQRTs in the same instructions (lanes [0, D) and
+// [32, 32 + D)). At head dim 128 lane hl of a half holds the 4 consecutive elements 4 hl .. 4 hl + 3:
+// the row's columns and gains come as one vector load each, an element's RoPE partner (j ^ 1) is in
+// the same lane, and q, the int8 q and the int8 cache rows go out as one store a lane (C3's prep
+// kernel, writing the int8 q, 15.5 us against 15.9 writing fp32 q from the strided layout). At head
+// dim 64 lane hl holds elements hl and hl + 32 (the partner one DPP exchange away, byte stores): two
+// consecutive elements a lane, with 16-bit cache stores, took 5.6 us against 5.3 at C4. A wave's
+// halves may hold a q and a k vector (odd H): each half stores what its vector writes.
 template <int HD>
 __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h2(AttnArgs a) {
   constexpr int NV = HD / 32;
-  __shared__ float sv[kPrepWaves][2][HD];
+  constexpr bool CONTIG = HD == 128;
+  static_assert(NV == 2 || NV == 4, "head dims 64 and 128");
+  __shared__ __align__(16) float sv[kPrepWaves][2][HD];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, hl = lane & 31;
   const int row = blockIdx.y, w2 = 2 * (blockIdx.x * kPrepWaves + wave);
   const int nvec = a.H + a.Hk;
@@ -1049,11 +1077,24 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h2(AttnArgs a) {
   float* qkv = a.qkv + row * a.qkv_stride;
   const int32_t* pr = a.part + row * a.qkv_stride;
   const float sx = a.part_nz > 1 ? a.part_sx[row] : 0.0f;
-  auto col = [&](int c) {                        // column c of the row's [q | k | v]
-    if (a.part_nz <= 1) return qkv[c];
-    int acc = 0;
-    for (int z = 0; z < a.part_nz; ++z) acc += pr[z * a.part_zstride + c];
-    return dequant(acc, a.part_sw[c], sx);
+  auto el = [&](int k) { return CONTIG ? NV * hl + k : hl + 32 * k; };   // the lane's element k
+  auto cols = [&](int c, float (&o)[NV]) {       // the lane's elements of the vector at column c
+    if (a.part_nz <= 1) {
+      if constexpr (CONTIG) {
+        const v4f_t v = *(const v4f_t*)(qkv + c + el(0));
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+      } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) o[k] = qkv[c + el(k)];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        int acc = 0;
+        for (int z = 0; z < a.part_nz; ++z) acc += pr[z * a.part_zstride + c + el(k)];
+        o[k] = dequant(acc, a.part_sw[c + el(k)], sx);
+      }
+    }
   };
   const bool isq = vi < a.H;
   const int g = isq ? 0 : vi - a.H;
@@ -1062,19 +1103,38 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h2(AttnArgs a) {
   const float* cs = a.cos_t + (long long)pos * (HD / 2);
   const float* sn = a.sin_t + (long long)pos * (HD / 2);
   float x[NV], y[NV], gv[NV], c[NV], s[NV];
+  cols(c0, x);
+  if (isq) {
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int j = hl + 32 * k;
-    x[k] = col(c0 + j);
-    gv[k] = gain != nullptr ? gain[j] : 0.0f;
-    c[k] = cs[j >> 1];
-    s[k] = sn[j >> 1];
-    y[k] = isq ? 0.0f : col(q_dim + kv_dim + g * HD + j);
+    for (int k = 0; k < NV; ++k) y[k] = 0.0f;
+  } else {
+    cols(q_dim + kv_dim + g * HD, y);
   }
+  if (gain == nullptr) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) gv[k] = 0.0f;
+  } else if constexpr (CONTIG) {
+    const v4f_t v = *(const v4f_t*)(gain + el(0));
+    gv[0] = v.x; gv[1] = v.y; gv[2] = v.z; gv[3] = v.w;
+  } else {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) gv[k] = gain[el(k)];
+  }
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {                 // element j's RoPE entry j / 2
+    c[k] = cs[el(k) >> 1];
+    s[k] = sn[el(k) >> 1];
+  }
+  // int8 q (a.q8): RECIP's 64 table pairs, lane i holding pair i, read by lane exchange
+  const float2 rt = a.q8 != nullptr ? sfu_recip_pair(lane, c_sfu) : make_float2(0.0f, 0.0f);
   if (a.qn != nullptr || a.kn != nullptr) {      // QK-norm of the halves whose vector has a gain
     float* v = sv[wave][half];
+    if constexpr (CONTIG) {
+      *(v4f_t*)(v + el(0)) = v4f_t{x[0], x[1], x[2], x[3]};
+    } else {
 #pragma unroll
-    for (int k = 0; k < NV; ++k) v[hl + 32 * k] = x[k];
+      for (int k = 0; k < NV; ++k) v[el(k)] = x[k];
+    }
     __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
     float acc = 0.0f;
@@ -1097,24 +1157,62 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h2(AttnArgs a) {
       for (int k = 0; k < NV; ++k) x[k] = (x[k] * r) * gv[k];
   }
   // RoPE: even element 2i -> (x c) + ((-x[2i+1]) s), odd 2i+1 -> (x c) + (x[2i] s)
+  if constexpr (CONTIG) {
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const float p = __int_as_float(dpp_mov_i<kDppXor1>(__float_as_int(x[k])));
-    x[k] = (lane & 1) ? (x[k] * c[k]) + (p * s[k]) : (x[k] * c[k]) + ((-p) * s[k]);
-  }
-  if (!live) return;
-  if (isq) {
-#pragma unroll
-    for (int k = 0; k < NV; ++k) qkv[c0 + hl + 32 * k] = x[k];
+    for (int k = 0; k < NV; k += 2) {
+      const float xe = x[k], xo = x[k + 1];
+      x[k] = (xe * c[k]) + ((-xo) * s[k]);
+      x[k + 1] = (xo * c[k + 1]) + (xe * s[k + 1]);
+    }
   } else {
-    int8_t* kc = a.kc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD;
-    int8_t* vc = a.vc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int j = hl + 32 * k, ch = g * HD + j;
-      kc[j] = (int8_t)to_i8(x[k] * (a.ch_isk ? a.ch_isk[ch] : a.inv_sk));
-      vc[j] = (int8_t)to_i8(y[k] * (a.ch_isv ? a.ch_isv[ch] : a.inv_sv));
+      const float p = __int_as_float(dpp_mov_i<kDppXor1>(__float_as_int(x[k])));
+      x[k] = (lane & 1) ? (x[k] * c[k]) + (p * s[k]) : (x[k] * c[k]) + ((-p) * s[k]);
     }
+  }
+  // quant_act of a q vector for k_attn_pw (as k_attn_prep_h): each half's maximum over its 32 lanes;
+  // formed while every lane is active (the table's lane exchange reads all 64)
+  float sq = 0.0f, inv = 0.0f;
+  if (a.q8 != nullptr) {
+    uint32_t am = abs_bits(x[0]);
+#pragma unroll
+    for (int k = 1; k < NV; ++k) am = max(am, abs_bits(x[k]));
+    sq = fv(half_max_u32(am, half)) * kInv127;
+    inv = sfu_recip_by(sq, [&](int i) { return make_float2(__shfl(rt.x, i), __shfl(rt.y, i)); });
+  }
+  if (!live) return;
+  auto put8 = [&](int8_t* p, const int (&b)[NV]) {   // the lane's bytes of a vector
+    if constexpr (CONTIG) {
+      *(int*)(p + el(0)) = pack_i8x4(b[0], b[1], b[2], b[3]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) p[el(k)] = (int8_t)b[k];
+    }
+  };
+  if (isq) {
+    if (a.q8 != nullptr) {
+      int b[NV];
+#pragma unroll
+      for (int k = 0; k < NV; ++k) b[k] = to_i8(x[k] * inv);
+      put8(a.q8 + row * a.q8_stride + vi * HD, b);
+      if (hl == 0) a.q8s[row * a.H + vi] = sq;
+    } else if constexpr (CONTIG) {
+      *(v4f_t*)(qkv + c0 + el(0)) = v4f_t{x[0], x[1], x[2], x[3]};
+    } else {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) qkv[c0 + el(k)] = x[k];
+    }
+  } else {
+    int bk[NV], bv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int ch = g * HD + el(k);
+      bk[k] = to_i8(x[k] * (a.ch_isk ? a.ch_isk[ch] : a.inv_sk));
+      bv[k] = to_i8(y[k] * (a.ch_isv ? a.ch_isv[ch] : a.inv_sv));
+    }
+    put8(a.kc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD, bk);
+    put8(a.vc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD, bv);
   }
 }
 
@@ -1527,7 +1625,11 @@ T2R_DEV v2i_t lds_read_tr8(int8_t* p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t*)p);
 }
 
-template <int HD>
+// Q8I: q comes quantized (a.q8 / a.q8s, the prep kernel's quant_act of each head vector): the
+// block's rows are loaded straight into the score MFMA's B operands, and the SFU tables, the P.V sums'
+// zeroing and the row bounds go to LDS after the scores, before the barrier the row maxima need
+// anyway (no barrier before the scores).
+template <int HD, bool Q8I>
 __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArgs a, int M) {
   constexpr int KS = HD / 32, NW = kApWaves, TW = ApCfg<HD>::TW, RING = ApCfg<HD>::RING, NSB = ApCfg<HD>::NSB;
   constexpr int CPR = HD / 16;                    // 16-byte chunks of a K row
@@ -1552,15 +1654,26 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
   const int cap = a.t_cap > 0 && a.t_cap < S ? a.t_cap : S;
   const int kv_dim = a.Hk * HD;
 
-  // ---- the loads that depend on nothing first: q of the wave's rows (rows wave, wave + 8, ...),
-  // the SFU tables; then lane n's row: its position bounds T (rows past M or outside the cache: 0)
+  // ---- the loads that depend on nothing first: q of the wave's rows (rows wave, wave + 8, ...), or
+  // (Q8I) lane n's row's int8 q, straight into the score MFMA's B operands, and its scale; the SFU
+  // tables; then lane n's row: its position bounds T (rows past M or outside the cache: 0)
   float qx[kApRows / NW][NQ];
+  v4i_t qb[KS];
+  float sqn = 0.0f;
+  if constexpr (Q8I) {
+    const int rq = min(r0 + n, M - 1);
+    const int8_t* q8 = a.q8 + (long long)rq * a.q8_stride + (long long)h * HD + 16 * half;
 #pragma unroll
-  for (int k = 0; k < kApRows / NW; ++k) {
-    const int r = min(r0 + wave + NW * k, M - 1);
-    const float* q = a.qkv + (long long)r * a.qkv_stride + (long long)h * HD;
+    for (int ks = 0; ks < KS; ++ks) qb[ks] = *(const v4i_t*)(q8 + 32 * ks);
+    sqn = a.q8s[(long long)rq * a.H + h];
+  } else {
 #pragma unroll
-    for (int e = 0; e < NQ; ++e) qx[k][e] = q[lane + 64 * e];
+    for (int k = 0; k < kApRows / NW; ++k) {
+      const int r = min(r0 + wave + NW * k, M - 1);
+      const float* q = a.qkv + (long long)r * a.qkv_stride + (long long)h * HD;
+#pragma unroll
+      for (int e = 0; e < NQ; ++e) qx[k][e] = q[lane + 64 * e];
+    }
   }
   const v4f_t tv = tid < kSfuWords / 4 ? ((const v4f_t*)a.tab)[tid] : v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
   const float2 ev = tid < kSfuExpPairs ? sfu_exp_pair(tid, a.tab) : make_float2(0.0f, 0.0f);
@@ -1569,6 +1682,7 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
     const int pn = a.pos[min(r0 + n, M - 1)];
     Tn = r0 + n < M && pn >= 0 && pn < S ? min(pn + 1, cap) : 0;
   }
+  if constexpr (Q8I) sqn = Tn > 0 ? sqn : 0.0f;   // an invalid row (its q8 may be stale): scores 0
   const int ntile = ((int)wave_max_u32((uint32_t)Tn) + 31) / 32;   // lanes n cover the 32 rows
   const int nown = ntile > wave ? (ntile - wave + NW - 1) / NW : 0;  // tiles this wave owns
 
@@ -1594,14 +1708,18 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
 #pragma unroll
   for (int j = 0; j < RING - 1; ++j)
     if (j < nown) k_issue(j);
-  for (int k = tid; k < kApRows * OST; k += kApThreads) O[k] = 0;
-  if (wave == 0 && half == 0) s_T[n] = Tn;
+  // the SFU tables, the P.V sums' zeroing and the row bounds (Q8I: after the scores)
+  auto lds_setup = [&]() {
+    for (int k = tid; k < kApRows * OST; k += kApThreads) O[k] = 0;
+    if (wave == 0 && half == 0) s_T[n] = Tn;
+    if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = tv;
+    if (tid < kSfuExpPairs) et[tid] = ev;
+  };
 
   // ---- q of the block's rows to int8, a wave per row; invalid rows 0
-  if (tid < kSfuWords / 4) ((v4f_t*)tab)[tid] = tv;
-  if (tid < kSfuExpPairs) et[tid] = ev;
-  __syncthreads();
-  {
+  if constexpr (!Q8I) {
+    lds_setup();
+    __syncthreads();
     // the four rows' |q| maxima, then s_q = F(max (1/127)) and RECIP once for all four (lane k: row
     // wave + 8 k); an invalid row's multiplier 0 gives q8 = to_i8(0 or NaN) = 0
     uint32_t am[kApRows / NW];
@@ -1625,18 +1743,17 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
       for (int e = 0; e < NQ; ++e) Q8[i][lane + 64 * e] = (int8_t)to_i8(qx[k][e] * inv);
       if (lane == k) s_sq[i] = sq_l;
     }
+    __syncthreads();
+    sqn = s_sq[n];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qb[ks] = *(const v4i_t*)&Q8[n][32 * ks + 16 * half];
   }
-  __syncthreads();
-  const float sqn = s_sq[n];
 
   // ---- scores of the owned tiles: tile j + RING - 1 requested into the slot tile j - 1 left (its
   // fragments were read before its MFMAs), then wait for tile j's DMA (the newer ones may be in
   // flight), its A fragments from the ring and KS MFMAs. Tiles wholly below every valid row's T need
   // no mask.
   const int Tmin = (int)~wave_max_u32(~(Tn > 0 ? (uint32_t)Tn : 0xFFFFFFFFu));
-  v4i_t qb[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) qb[ks] = *(const v4i_t*)&Q8[n][32 * ks + 16 * half];
   float sc[TW][16];
   float rmx = -__builtin_inff();
 #pragma unroll
@@ -1677,6 +1794,7 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
   }
   rmx = smax(rmx, __shfl_xor(rmx, 32));
   if (half == 0) s_mx[n][wave] = rmx;
+  if constexpr (Q8I) lds_setup();
   __syncthreads();
   float mx;
   {
