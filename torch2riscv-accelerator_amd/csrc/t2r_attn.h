@@ -1915,10 +1915,21 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
       pa[j] = v4i_t{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
     };
     if (fast) {
-      // y in [0, 127]: its RNE integer is the low byte of F(y + 1.5 2^23)
+      // y in [0, 127]: v_cvt_pk_u8_f32 converts with round-to-nearest-even (checked on the device
+      // over every half-way point of [0, 128)) and inserts the byte, four to a word
 #pragma unroll
       for (int j = 0; j < TW; ++j)
-        if (j < nown) pack(j, [](float y) { return fb(y + 12582912.0f); });
+        if (j < nown) {
+          uint32_t w4[4];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) w = __builtin_amdgcn_cvt_pk_u8_f32((sc[j][4 * rr + c] * rn) * 127.0f, c, w);
+            w4[rr] = w;
+          }
+          pa[j] = v4i_t{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
+        }
     } else {
 #pragma unroll
       for (int j = 0; j < TW; ++j)
