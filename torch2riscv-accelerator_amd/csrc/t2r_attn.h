@@ -1055,133 +1055,100 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h(AttnArgs a) {
 // kernel, writing the int8 q, 15.5 us against 15.9 writing fp32 q from the strided layout). At head
 // dim 64 lane hl holds elements hl and hl + 32 (the partner one DPP exchange away, byte stores): two
 // consecutive elements a lane, with 16-bit cache stores, took 5.6 us against 5.3 at C4. A wave's
-// halves may hold a q and a k vector (odd H): each half stores what its vector writes.
-template <int HD>
-__global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h2(AttnArgs a) {
+// halves may hold a q and a k vector (odd H): each half stores what its vector writes. R: rows a
+// wave, every row's loads issued before the first row's steps.
+template <int HD, int R = 1>
+__global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h2(AttnArgs a, int rows) {
   constexpr int NV = HD / 32;
   constexpr bool CONTIG = HD == 128;
   static_assert(NV == 2 || NV == 4, "head dims 64 and 128");
   __shared__ __align__(16) float sv[kPrepWaves][2][HD];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5, hl = lane & 31;
-  const int row = blockIdx.y, w2 = 2 * (blockIdx.x * kPrepWaves + wave);
+  const int w2 = 2 * (blockIdx.x * kPrepWaves + wave);
   const int nvec = a.H + a.Hk;
   if (w2 >= nvec) return;                        // (wave-uniform; the kernel has no block barrier)
-  const int pos = a.pos[row];
-  if (pos < 0 || pos >= a.S) {                   // a position outside the cache: nothing is written
-    if (lane == 0) flag_bad_pos(a.status);
-    return;
-  }
   const bool live = w2 + half < nvec;            // the second half of the last wave when nvec is odd
   const int vi = min(w2 + half, nvec - 1);
   const int q_dim = a.H * HD, kv_dim = a.Hk * HD;
-  float* qkv = a.qkv + row * a.qkv_stride;
-  const int32_t* pr = a.part + row * a.qkv_stride;
-  const float sx = a.part_nz > 1 ? a.part_sx[row] : 0.0f;
-  auto el = [&](int k) { return CONTIG ? NV * hl + k : hl + 32 * k; };   // the lane's element k
-  auto cols = [&](int c, float (&o)[NV]) {       // the lane's elements of the vector at column c
-    if (a.part_nz <= 1) {
-      if constexpr (CONTIG) {
-        const v4f_t v = *(const v4f_t*)(qkv + c + el(0));
-        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
-      } else {
-#pragma unroll
-        for (int k = 0; k < NV; ++k) o[k] = qkv[c + el(k)];
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        int acc = 0;
-        for (int z = 0; z < a.part_nz; ++z) acc += pr[z * a.part_zstride + c + el(k)];
-        o[k] = dequant(acc, a.part_sw[c + el(k)], sx);
-      }
-    }
-  };
   const bool isq = vi < a.H;
   const int g = isq ? 0 : vi - a.H;
   const int c0 = isq ? vi * HD : q_dim + g * HD;  // the vector (k for a KV head's half)
   const float* gain = isq ? a.qn : a.kn;
-  const float* cs = a.cos_t + (long long)pos * (HD / 2);
-  const float* sn = a.sin_t + (long long)pos * (HD / 2);
-  float x[NV], y[NV], gv[NV], c[NV], s[NV];
-  cols(c0, x);
-  if (isq) {
+  auto el = [&](int k) { return CONTIG ? NV * hl + k : hl + 32 * k; };   // the lane's element k
+  // the wave's R rows blockIdx.y R + rr (rows past the call or at a position outside the cache: skipped,
+  // the latter flagged; both wave-uniform)
+  int row[R], pos[R];
+  bool ok[R];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) y[k] = 0.0f;
-  } else {
-    cols(q_dim + kv_dim + g * HD, y);
+  for (int rr = 0; rr < R; ++rr) {
+    row[rr] = blockIdx.y * R + rr;
+    pos[rr] = a.pos[min(row[rr], rows - 1)];
+    ok[rr] = row[rr] < rows && pos[rr] >= 0 && pos[rr] < a.S;
+    if (row[rr] < rows && !ok[rr] && lane == 0) flag_bad_pos(a.status);
   }
-  if (gain == nullptr) {
+  // every row's loads first, all of them unconditional (a load under a branch makes the compiler's
+  // wait counts path-dependent, and it then waits for each before the next is issued): rows that are
+  // skipped read row 0 at position 0, q halves read their own vector again for y, a missing gain
+  // reads the row-0 vector; those values are not used
+  float x[R][NV], y[R][NV], c[R][NV], s[R][NV], gv[NV];
+  const int ycol = isq ? c0 : q_dim + kv_dim + g * HD;   // the V vector of a KV head's half
+  int prow[R], ppos[R];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) gv[k] = 0.0f;
-  } else if constexpr (CONTIG) {
-    const v4f_t v = *(const v4f_t*)(gain + el(0));
-    gv[0] = v.x; gv[1] = v.y; gv[2] = v.z; gv[3] = v.w;
-  } else {
-#pragma unroll
-    for (int k = 0; k < NV; ++k) gv[k] = gain[el(k)];
+  for (int rr = 0; rr < R; ++rr) {
+    prow[rr] = ok[rr] ? row[rr] : 0;
+    ppos[rr] = ok[rr] ? pos[rr] : 0;
   }
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {                 // element j's RoPE entry j / 2
-    c[k] = cs[el(k) >> 1];
-    s[k] = sn[el(k) >> 1];
-  }
-  // int8 q (a.q8): RECIP's 64 table pairs, lane i holding pair i, read by lane exchange
-  const float2 rt = a.q8 != nullptr ? sfu_recip_pair(lane, c_sfu) : make_float2(0.0f, 0.0f);
-  if (a.qn != nullptr || a.kn != nullptr) {      // QK-norm of the halves whose vector has a gain
-    float* v = sv[wave][half];
+  auto vec = [&](const float* p, float (&o)[NV]) {       // the lane's elements of the vector at p
     if constexpr (CONTIG) {
-      *(v4f_t*)(v + el(0)) = v4f_t{x[0], x[1], x[2], x[3]};
+      const v4f_t v = *(const v4f_t*)(p + el(0));
+      o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
     } else {
 #pragma unroll
-      for (int k = 0; k < NV; ++k) v[el(k)] = x[k];
+      for (int k = 0; k < NV; ++k) o[k] = p[el(k)];
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
-    float acc = 0.0f;
-    if (hl < a.D) {
-      const int n = HD / a.D;                    // the chain's length (HD a multiple of D)
-      acc = v[hl] * v[hl];
+  };
+  if (a.part_nz <= 1) {
 #pragma unroll
-      for (int m = 1; m < HD / 8; ++m)
-        if (m < n) {
-          const float e = v[hl + m * a.D];
-          acc = acc + e * e;
+    for (int rr = 0; rr < R; ++rr) {
+      const float* qkv = a.qkv + prow[rr] * a.qkv_stride;
+      vec(qkv + c0, x[rr]);
+      vec(qkv + ycol, y[rr]);
+    }
+  } else {                                       // Wqkv's split-K partials summed (the store epilogue)
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      const int32_t* pr = a.part + prow[rr] * a.qkv_stride;
+      const float sx = a.part_sx[prow[rr]];
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        int ax = 0, ay = 0;
+        for (int z = 0; z < a.part_nz; ++z) {
+          ax += pr[z * a.part_zstride + c0 + el(k)];
+          ay += pr[z * a.part_zstride + ycol + el(k)];
         }
-    }
-    acc = lane_tree_rows(acc, a.D, lane);
-    const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
-    const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 32));
-    const float r = sfu_rsqrt((half ? s1 : s0) * a.inv_hd + a.eps);
-    if (gain != nullptr)
-#pragma unroll
-      for (int k = 0; k < NV; ++k) x[k] = (x[k] * r) * gv[k];
-  }
-  // RoPE: even element 2i -> (x c) + ((-x[2i+1]) s), odd 2i+1 -> (x c) + (x[2i] s)
-  if constexpr (CONTIG) {
-#pragma unroll
-    for (int k = 0; k < NV; k += 2) {
-      const float xe = x[k], xo = x[k + 1];
-      x[k] = (xe * c[k]) + ((-xo) * s[k]);
-      x[k + 1] = (xo * c[k + 1]) + (xe * s[k + 1]);
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const float p = __int_as_float(dpp_mov_i<kDppXor1>(__float_as_int(x[k])));
-      x[k] = (lane & 1) ? (x[k] * c[k]) + (p * s[k]) : (x[k] * c[k]) + ((-p) * s[k]);
+        x[rr][k] = dequant(ax, a.part_sw[c0 + el(k)], sx);
+        y[rr][k] = dequant(ay, a.part_sw[ycol + el(k)], sx);
+      }
     }
   }
-  // quant_act of a q vector for k_attn_pw (as k_attn_prep_h): each half's maximum over its 32 lanes;
-  // formed while every lane is active (the table's lane exchange reads all 64)
-  float sq = 0.0f, inv = 0.0f;
-  if (a.q8 != nullptr) {
-    uint32_t am = abs_bits(x[0]);
 #pragma unroll
-    for (int k = 1; k < NV; ++k) am = max(am, abs_bits(x[k]));
-    sq = fv(half_max_u32(am, half)) * kInv127;
-    inv = sfu_recip_by(sq, [&](int i) { return make_float2(__shfl(rt.x, i), __shfl(rt.y, i)); });
+  for (int rr = 0; rr < R; ++rr) {
+    const float* cs = a.cos_t + (long long)ppos[rr] * (HD / 2);
+    const float* sn = a.sin_t + (long long)ppos[rr] * (HD / 2);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {               // element j's RoPE entry j / 2 (CONTIG: k, k + 1 share it)
+      if (CONTIG && (k & 1)) {
+        c[rr][k] = c[rr][k - 1];
+        s[rr][k] = s[rr][k - 1];
+      } else {
+        c[rr][k] = cs[el(k) >> 1];
+        s[rr][k] = sn[el(k) >> 1];
+      }
+    }
   }
-  if (!live) return;
+  vec(gain != nullptr ? gain : a.qkv, gv);
+  // int8 q (a.q8): RECIP's 64 table pairs, lane i holding pair i, read by lane exchange
+  const float2 rt = sfu_recip_pair(lane, c_sfu);
   auto put8 = [&](int8_t* p, const int (&b)[NV]) {   // the lane's bytes of a vector
     if constexpr (CONTIG) {
       *(int*)(p + el(0)) = pack_i8x4(b[0], b[1], b[2], b[3]);
@@ -1190,29 +1157,90 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h2(AttnArgs a) {
       for (int k = 0; k < NV; ++k) p[el(k)] = (int8_t)b[k];
     }
   };
-  if (isq) {
-    if (a.q8 != nullptr) {
-      int b[NV];
 #pragma unroll
-      for (int k = 0; k < NV; ++k) b[k] = to_i8(x[k] * inv);
-      put8(a.q8 + row * a.q8_stride + vi * HD, b);
-      if (hl == 0) a.q8s[row * a.H + vi] = sq;
-    } else if constexpr (CONTIG) {
-      *(v4f_t*)(qkv + c0 + el(0)) = v4f_t{x[0], x[1], x[2], x[3]};
+  for (int rr = 0; rr < R; ++rr) {
+    if (!ok[rr]) continue;
+    float* xr = x[rr];
+    if (a.qn != nullptr || a.kn != nullptr) {    // QK-norm of the halves whose vector has a gain
+      float* v = sv[wave][half];                 // (a wave's LDS operations run in order: the previous
+      if constexpr (CONTIG) {                    //  row's chain reads come before these stores)
+        *(v4f_t*)(v + el(0)) = v4f_t{xr[0], xr[1], xr[2], xr[3]};
+      } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) v[el(k)] = xr[k];
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);        // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
+      float acc = 0.0f;
+      if (hl < a.D) {
+        const int n = HD / a.D;                  // the chain's length (HD a multiple of D)
+        acc = v[hl] * v[hl];
+#pragma unroll
+        for (int m = 1; m < HD / 8; ++m)
+          if (m < n) {
+            const float e = v[hl + m * a.D];
+            acc = acc + e * e;
+          }
+      }
+      acc = lane_tree_rows(acc, a.D, lane);
+      const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+      const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 32));
+      const float r = sfu_rsqrt((half ? s1 : s0) * a.inv_hd + a.eps);
+      if (gain != nullptr)
+#pragma unroll
+        for (int k = 0; k < NV; ++k) xr[k] = (xr[k] * r) * gv[k];
+    }
+    // RoPE: even element 2i -> (x c) + ((-x[2i+1]) s), odd 2i+1 -> (x c) + (x[2i] s)
+    if constexpr (CONTIG) {
+#pragma unroll
+      for (int k = 0; k < NV; k += 2) {
+        const float xe = xr[k], xo = xr[k + 1];
+        xr[k] = (xe * c[rr][k]) + ((-xo) * s[rr][k]);
+        xr[k + 1] = (xo * c[rr][k + 1]) + (xe * s[rr][k + 1]);
+      }
     } else {
 #pragma unroll
-      for (int k = 0; k < NV; ++k) qkv[c0 + el(k)] = x[k];
+      for (int k = 0; k < NV; ++k) {
+        const float p = __int_as_float(dpp_mov_i<kDppXor1>(__float_as_int(xr[k])));
+        xr[k] = (lane & 1) ? (xr[k] * c[rr][k]) + (p * s[rr][k]) : (xr[k] * c[rr][k]) + ((-p) * s[rr][k]);
+      }
     }
-  } else {
-    int bk[NV], bv[NV];
+    // quant_act of a q vector for k_attn_pw (as k_attn_prep_h): each half's maximum over its 32
+    // lanes; formed with every lane active (the table's lane exchange reads all 64)
+    float sq = 0.0f, inv = 0.0f;
+    if (a.q8 != nullptr) {
+      uint32_t am = abs_bits(xr[0]);
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int ch = g * HD + el(k);
-      bk[k] = to_i8(x[k] * (a.ch_isk ? a.ch_isk[ch] : a.inv_sk));
-      bv[k] = to_i8(y[k] * (a.ch_isv ? a.ch_isv[ch] : a.inv_sv));
+      for (int k = 1; k < NV; ++k) am = max(am, abs_bits(xr[k]));
+      sq = fv(half_max_u32(am, half)) * kInv127;
+      inv = sfu_recip_by(sq, [&](int i) { return make_float2(__shfl(rt.x, i), __shfl(rt.y, i)); });
     }
-    put8(a.kc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD, bk);
-    put8(a.vc + row * a.kv_row_stride + (long long)pos * kv_dim + g * HD, bv);
+    if (!live) continue;
+    const int rw = row[rr];
+    if (isq) {
+      if (a.q8 != nullptr) {
+        int b[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) b[k] = to_i8(xr[k] * inv);
+        put8(a.q8 + rw * a.q8_stride + vi * HD, b);
+        if (hl == 0) a.q8s[rw * a.H + vi] = sq;
+      } else if constexpr (CONTIG) {
+        *(v4f_t*)(a.qkv + rw * a.qkv_stride + c0 + el(0)) = v4f_t{xr[0], xr[1], xr[2], xr[3]};
+      } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) a.qkv[rw * a.qkv_stride + c0 + el(k)] = xr[k];
+      }
+    } else {
+      int bk[NV], bv[NV];
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int ch = g * HD + el(k);
+        bk[k] = to_i8(xr[k] * (a.ch_isk ? a.ch_isk[ch] : a.inv_sk));
+        bv[k] = to_i8(y[rr][k] * (a.ch_isv ? a.ch_isv[ch] : a.inv_sv));
+      }
+      put8(a.kc + rw * a.kv_row_stride + (long long)pos[rr] * kv_dim + g * HD, bk);
+      put8(a.vc + rw * a.kv_row_stride + (long long)pos[rr] * kv_dim + g * HD, bv);
+    }
   }
 }
 
