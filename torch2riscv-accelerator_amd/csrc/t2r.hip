@@ -252,8 +252,8 @@ int attn_launch(int mode, const AttnArgs& a, int rows, hipStream_t st) {
     const dim3 pg(cdiv(a.H + a.Hk, kPrepWaves), rows), pb(64 * kPrepWaves);
     // two vectors a wave over many rows (C3 prefill 5.86 -> 5.77 ms, C4 1.85 -> 1.83 ms); a short
     // prompt keeps a wave per vector, for the parallelism (C2's 40 rows: 1.53 against 1.57 ms)
-    // at head dim 64 two rows a wave, all their loads issued first (C4's prep 5.7 -> 5.3 us; at head
-    // dim 128 two rows took 15.8 against 15.5 us)
+    // at head dim 64 two rows a wave, all their loads issued first (C4's prep 5.7 -> 5.4 us; at head
+    // dim 128 two rows took 14.6 against 13.0 us)
     const dim3 pg2(cdiv(a.H + a.Hk, 2 * kPrepWaves), rows), pg2r(cdiv(a.H + a.Hk, 2 * kPrepWaves), cdiv(rows, 2));
     if (a.hd == 128 && rows >= 256) launch((k_attn_prep_h2<128, 1>), pg2, pb, 0, st, a, rows);
     else if (a.hd == 64 && rows >= 256) launch((k_attn_prep_h2<64, 2>), pg2r, pb, 0, st, a, rows);

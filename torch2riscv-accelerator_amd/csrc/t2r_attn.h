@@ -963,35 +963,48 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_attn_prep_h(AttnArgs a) {
   }
   const int q_dim = a.H * HD, kv_dim = a.Hk * HD;
   float* qkv = a.qkv + row * a.qkv_stride;
-  const int32_t* pr = a.part + row * a.qkv_stride;
-  const float sx = a.part_nz > 1 ? a.part_sx[row] : 0.0f;
-  auto col = [&](int c) {                        // column c of the row's [q | k | v]
-    if (a.part_nz <= 1) return qkv[c];
-    int acc = 0;
-    for (int z = 0; z < a.part_nz; ++z) acc += pr[z * a.part_zstride + c];
-    return dequant(acc, a.part_sw[c], sx);
-  };
   const bool isq = vi < a.H;
   const int g = vi - a.H;
   const int c0 = isq ? vi * HD : q_dim + g * HD;    // the vector (k for a KV head's wave)
+  const int ycol = isq ? c0 : q_dim + kv_dim + g * HD;   // its V vector (a q wave: its own, unused)
   const float* gain = isq ? a.qn : a.kn;
+  const float* gsrc = gain != nullptr ? gain : qkv;      // (no gain: any readable vector, unused)
   const float* cs = a.cos_t + (long long)pos * (HD / 2);
   const float* sn = a.sin_t + (long long)pos * (HD / 2);
+  // every load issued before the first wait: unconditional, the split-K sums on a path of their own
+  // (a load under a branch makes the compiler's wait counts path-dependent, and it then waits for
+  // each before the next is issued)
   float x[NV], y[NV], gv[NV], c[NV], s[NV];
+  if (a.part_nz <= 1) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      x[k] = qkv[c0 + lane + 64 * k];
+      y[k] = qkv[ycol + lane + 64 * k];
+    }
+  } else {
+    const int32_t* pr = a.part + row * a.qkv_stride;
+    const float sx = a.part_sx[row];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int j = lane + 64 * k;
+      int ax = 0, ay = 0;
+      for (int z = 0; z < a.part_nz; ++z) {
+        ax += pr[z * a.part_zstride + c0 + j];
+        ay += pr[z * a.part_zstride + ycol + j];
+      }
+      x[k] = dequant(ax, a.part_sw[c0 + j], sx);
+      y[k] = dequant(ay, a.part_sw[ycol + j], sx);
+    }
+  }
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int j = lane + 64 * k;
-    x[k] = col(c0 + j);
-    gv[k] = gain != nullptr ? gain[j] : 0.0f;
+    gv[k] = gsrc[j];
     c[k] = cs[j >> 1];
     s[k] = sn[j >> 1];
   }
-  if (!isq) {
-#pragma unroll
-    for (int k = 0; k < NV; ++k) y[k] = col(q_dim + kv_dim + g * HD + lane + 64 * k);
-  }
   // int8 q (a.q8): RECIP's 64 table pairs, lane i holding pair i, read by lane exchange
-  const float2 rt = isq && a.q8 != nullptr ? sfu_recip_pair(lane, c_sfu) : make_float2(0.0f, 0.0f);
+  const float2 rt = sfu_recip_pair(lane, c_sfu);
   if (gain != nullptr) {
     float* v = sv[wave];
 #pragma unroll
