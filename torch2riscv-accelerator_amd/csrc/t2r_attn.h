@@ -1695,9 +1695,13 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
   const int cap = a.t_cap > 0 && a.t_cap < S ? a.t_cap : S;
   const int kv_dim = a.Hk * HD;
 
-  // ---- the loads that depend on nothing first: q of the wave's rows (rows wave, wave + 8, ...), or
-  // (Q8I) lane n's row's int8 q, straight into the score MFMA's B operands, and its scale; the SFU
-  // tables; then lane n's row: its position bounds T (rows past M or outside the cache: 0)
+  // ---- the loads that depend on nothing first, all unconditional and issued before the first wait
+  // (a load under a branch makes the compiler's wait counts path-dependent, and it then waits for
+  // each before the next is issued): lane n's row's position, which the K tiles' requests wait for;
+  // q of the wave's rows (rows wave, wave + 8, ...), or (Q8I) lane n's row's int8 q, straight into
+  // the score MFMA's B operands, and its scale; the SFU tables. Then the row's position bounds T
+  // (rows past M or outside the cache: 0).
+  const int pn = a.pos[min(r0 + n, M - 1)];
   float qx[kApRows / NW][NQ];
   v4i_t qb[KS];
   float sqn = 0.0f;
@@ -1716,13 +1720,9 @@ __global__ __launch_bounds__(kApThreads, ApCfg<HD>::MINB) void k_attn_pw(AttnArg
       for (int e = 0; e < NQ; ++e) qx[k][e] = q[lane + 64 * e];
     }
   }
-  const v4f_t tv = tid < kSfuWords / 4 ? ((const v4f_t*)a.tab)[tid] : v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const float2 ev = tid < kSfuExpPairs ? sfu_exp_pair(tid, a.tab) : make_float2(0.0f, 0.0f);
-  int Tn;
-  {
-    const int pn = a.pos[min(r0 + n, M - 1)];
-    Tn = r0 + n < M && pn >= 0 && pn < S ? min(pn + 1, cap) : 0;
-  }
+  const v4f_t tv = ((const v4f_t*)a.tab)[tid & (kSfuWords / 4 - 1)];      // (stored by tid < kSfuWords / 4)
+  const float2 ev = sfu_exp_pair(min(tid, kSfuExpPairs - 1), a.tab);      // (stored by tid < kSfuExpPairs)
+  const int Tn = r0 + n < M && pn >= 0 && pn < S ? min(pn + 1, cap) : 0;
   if constexpr (Q8I) sqn = Tn > 0 ? sqn : 0.0f;   // an invalid row (its q8 may be stale): scores 0
   const int ntile = ((int)wave_max_u32((uint32_t)Tn) + 31) / 32;   // lanes n cover the 32 rows
   const int nown = ntile > wave ? (ntile - wave + NW - 1) / NW : 0;  // tiles this wave owns

@@ -197,8 +197,9 @@ T2R_DEV float sfu_exp_np(float xin, const float* tab = c_sfu) {
 // The EXP table as 65 {T, S} pairs: entries 0..63 the table's, entry 64 {F(T[63] + S[63]), 0}.
 constexpr int kSfuExpPairs = 65;
 T2R_DEV float2 sfu_exp_pair(int i, const float* tab) {
-  return i < 64 ? make_float2(tab[kSfuExpT + i], tab[kSfuExpS + i])
-                : make_float2(tab[kSfuExpT + 63] + tab[kSfuExpS + 63], 0.0f);
+  const int j = min(i, 63);                      // (both reads unconditional: no branch around a load)
+  const float t = tab[kSfuExpT + j], s = tab[kSfuExpS + j];
+  return i < 64 ? make_float2(t, s) : make_float2(t + s, 0.0f);
 }
 
 // EXP of a softmax argument x = s - max under a finite maximum: x <= 0 or -inf, never NaN. Equal to
