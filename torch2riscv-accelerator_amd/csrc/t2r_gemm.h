@@ -324,8 +324,30 @@ T2R_DEV void gemm_d_epilogue_vec(const GemmArgs& a, const v16i_t (&acc)[2][2], i
   constexpr int OC = kGT, CS = kEpiCS;                            // output columns of the tile, stride
   int* c1 = (int*)lds;                                            // [64][CS]
   const int lr = lane & 31, kh = lane >> 5;
-  __syncthreads();                                                // every wave is done with the ring
   const int nbase = n0;                                           // first output column of the tile
+  // item k of band b is row 64 b + (tid + NT k) / (OC / 4), columns 4 (tid % (OC / 4)) + 0..3 (the
+  // same four in every item). Their scales and residual rows are requested here, all at once and
+  // from clamped (always readable) addresses, before the staging: loads inside the item loop would
+  // each be waited for before the next is issued.
+  constexpr int IT = 64 * (OC / 4) / NT;
+  static_assert(IT * NT == 64 * (OC / 4) && NT % (OC / 4) == 0, "whole items, fixed columns per thread");
+  const int nct = 4 * (tid % (OC / 4));
+  v4f_t swp = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float sxp[NB][IT];
+  v4f_t rvp[EPI == EPI_RESID ? NB : 1][EPI == EPI_RESID ? IT : 1];
+  if constexpr (!SPLIT) {
+    swp = *(const v4f_t*)&a.s_w[min(nbase + nct, a.N - 4)];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int k = 0; k < IT; ++k) {
+        const int m = min(m0 + 64 * b + (tid + NT * k) / (OC / 4), a.M - 1);
+        sxp[b][k] = a.s_x[m];
+        if constexpr (EPI == EPI_RESID)
+          rvp[b][k] = *(const v4f_t*)&a.res[(long long)m * a.y_stride + min(nbase + nct, a.N - 4)];
+      }
+  }
+  __syncthreads();                                                // every wave is done with the ring
   for (int b = 0; b < NB; ++b) {
     if (wm == b) {
 #pragma unroll
@@ -338,23 +360,21 @@ T2R_DEV void gemm_d_epilogue_vec(const GemmArgs& a, const v16i_t (&acc)[2][2], i
         }
     }
     __syncthreads();
-    for (int e = tid; e < 64 * (OC / 4); e += NT) {
-      const int mr = e / (OC / 4), nc = 4 * (e % (OC / 4));
+#pragma unroll
+    for (int k = 0; k < IT; ++k) {
+      const int mr = (tid + NT * k) / (OC / 4), nc = nct;
       const int m = m0 + 64 * b + mr, n = nbase + nc;
       if (m < a.M && n < a.N) {                                   // (N % 4 == 0: all four columns)
         const v4i_t v = *(const v4i_t*)&c1[mr * CS + nc];
         if constexpr (SPLIT) {
           *(v4i_t*)&a.part[((long long)z * a.M + m) * a.N + n] = v;
         } else {
-          const float sx = a.s_x[m];
-          const v4f_t sw = *(const v4f_t*)&a.s_w[n];
           v4f_t y;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) y[q] = dequant(v[q], sw[q], sx);
+          for (int q = 0; q < 4; ++q) y[q] = dequant(v[q], swp[q], sxp[b][k]);
           if constexpr (EPI == EPI_RESID) {
-            const v4f_t rv = *(const v4f_t*)&a.res[(long long)m * a.y_stride + n];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) y[q] = rv[q] + y[q];
+            for (int q = 0; q < 4; ++q) y[q] = rvp[b][k][q] + y[q];
           }
           *(v4f_t*)&a.y[(long long)m * a.y_stride + n] = y;
         }
@@ -646,6 +666,21 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmArgs a, int ntile) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
   const int lr = lane & 31, kh = lane >> 5;
   auto frag = [&](const int8_t* base, int row, int kc) { return *(const v4i_t*)(base + (row * CPR + (kc ^ swz(row))) * 16); };
+  // the epilogue's scales and residual rows (item k: e = tid + 256 k), requested first, all at once
+  // and from clamped (always readable) addresses: inside the item loop each load would be waited
+  // for before the next is issued. (Older than every slab, they only add to the first slab's wait.)
+  constexpr int IT = TM * (TN / 4) / 256;
+  static_assert(IT * 256 == TM * (TN / 4), "whole items per thread");
+  float sxp[IT];
+  v4f_t swp[IT], rvp[EPI == EPI_RESID ? IT : 1];
+#pragma unroll
+  for (int k = 0; k < IT; ++k) {
+    const int e = tid + 256 * k;
+    const int m = min(m0 + e / (TN / 4), a.M - 1), n = min(n0 + 4 * (e % (TN / 4)), a.N - 4);
+    sxp[k] = a.s_x[m];
+    swp[k] = *(const v4f_t*)&a.s_w[n];
+    if constexpr (EPI == EPI_RESID) rvp[k] = *(const v4f_t*)&a.res[(long long)m * a.y_stride + n];
+  }
 #pragma unroll
   for (int p = 0; p < kGwStages; ++p)
     if (p < nk) issue(p);
@@ -686,22 +721,21 @@ __global__ __launch_bounds__(256) void k_gemm_w(GemmArgs a, int ntile) {
       for (int r = 0; r < 16; ++r) pt[(32 * i + 8 * (r >> 2) + 4 * kh + (r & 3)) * PS + 32 * j + lr] = acc[i][j][r];
   __syncthreads();
   const int* p0 = (const int*)lds;
-  for (int e = tid; e < TM * (TN / 4); e += 256) {
+#pragma unroll
+  for (int k = 0; k < IT; ++k) {
+    const int e = tid + 256 * k;
     const int mr = e / (TN / 4), nc = 4 * (e % (TN / 4));
     const int m = m0 + mr, n = n0 + nc;
     if (m >= a.M || n >= a.N) continue;                           // (N % 4 == 0: all four columns)
     v4i_t v = *(const v4i_t*)(p0 + mr * PS + nc);
 #pragma unroll
     for (int q = 1; q < 4; ++q) v += *(const v4i_t*)(p0 + q * TM * PS + mr * PS + nc);
-    const float sx = a.s_x[m];
-    const v4f_t sw = *(const v4f_t*)&a.s_w[n];
     v4f_t y;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) y[q] = dequant(v[q], sw[q], sx);
+    for (int q = 0; q < 4; ++q) y[q] = dequant(v[q], swp[k][q], sxp[k]);
     if constexpr (EPI == EPI_RESID) {
-      const v4f_t rv = *(const v4f_t*)&a.res[(long long)m * a.y_stride + n];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) y[q] = rv[q] + y[q];
+      for (int q = 0; q < 4; ++q) y[q] = rvp[k][q] + y[q];
     }
     *(v4f_t*)&a.y[(long long)m * a.y_stride + n] = y;
   }
