@@ -447,6 +447,26 @@ __global__ __launch_bounds__(2 * BM, (BKD == 64 && NST == 3) ? 3 : 1) void k_gem
   auto frag = [&](const int8_t* base, int row, int kc) {
     return *(const v4i_t*)(base + (row * CPR + (kc ^ swz(row))) * 16);
   };
+  const int mr0 = m0 + wm * 64 + kh * 4;
+  auto mrow = [&](int i, int r) { return mr0 + 32 * i + 8 * (r >> 2) + (r & 3); };
+  // (SwiGLU on 256-row tiles: one workgroup a CU, registers to spare) the epilogue's row and column
+  // scales and the gate's table pairs requested before the K loop, so that the epilogue does not wait
+  // for them after it
+  constexpr bool EARLY = EPI == EPI_SWIGLU && BM == 2 * kGT;
+  float sx_e[EARLY ? 2 : 1][EARLY ? 16 : 1];
+  float sw1_e = 0.0f, sw3_e = 0.0f;
+  float2 ep_e = make_float2(0.0f, 0.0f), rp_e = make_float2(0.0f, 0.0f);
+  if constexpr (EARLY) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sx_e[i][r] = a.s_x[min(mrow(i, r), a.M - 1)];
+    const int nc = min((n0 >> 1) + wn * 32 + lr, a.N - 1);
+    sw1_e = a.s_w[nc];
+    sw3_e = a.s_w3[nc];
+    ep_e = sfu_exp_pair(min(tid, kSfuExpPairs - 1), a.tab);
+    rp_e = sfu_recip_pair(tid & 63, a.tab);
+  }
 #pragma unroll
   for (int p = 0; p < NST - 1; ++p)
     if (p < nk) {
@@ -517,8 +537,6 @@ __global__ __launch_bounds__(2 * BM, (BKD == 64 && NST == 3) ? 3 : 1) void k_gem
   // + r % 4. Every load it needs (scales, residual, SFU table) is issued before its first store:
   // y may alias the residual, so a load after a store would wait out the store's round trip.
   // (Each element is read and written by its own lane only, so reading all first is the same.)
-  const int mr0 = m0 + wm * 64 + kh * 4;
-  auto mrow = [&](int i, int r) { return mr0 + 32 * i + 8 * (r >> 2) + (r & 3); };
   if constexpr (SPLIT) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -535,15 +553,15 @@ __global__ __launch_bounds__(2 * BM, (BKD == 64 && NST == 3) ? 3 : 1) void k_gem
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sx[i][r] = a.s_x[min(mrow(i, r), a.M - 1)];
+    for (int r = 0; r < 16; ++r) sx[i][r] = EARLY ? sx_e[EARLY ? i : 0][EARLY ? r : 0] : a.s_x[min(mrow(i, r), a.M - 1)];
   if constexpr (EPI == EPI_SWIGLU) {
     const int n = (n0 >> 1) + wn * 32 + lr, nc = min(n, a.N - 1);
-    const float sw1 = a.s_w[nc], sw3 = a.s_w3[nc];
+    const float sw1 = EARLY ? sw1_e : a.s_w[nc], sw3 = EARLY ? sw3_e : a.s_w3[nc];
     float2* ep = (float2*)lds;                    // the gates' pair tables
     float2* rp = ep + kSfuExpPairs;
     __syncthreads();                              // every wave is done with the stage ring
-    if (tid < kSfuExpPairs) ep[tid] = sfu_exp_pair(tid, a.tab);
-    if (tid < 64) rp[tid] = sfu_recip_pair(tid, a.tab);
+    if (tid < kSfuExpPairs) ep[tid] = EARLY ? ep_e : sfu_exp_pair(tid, a.tab);
+    if (tid < 64) rp[tid] = EARLY ? rp_e : sfu_recip_pair(tid, a.tab);
     __syncthreads();
     // A whole tile without an int32 copy: no bounds checks, one gate branch for the tile, and each
     // store at the tile's (uniform) origin plus a 32-bit byte offset: one add per output.
