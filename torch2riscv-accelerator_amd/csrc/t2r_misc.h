@@ -102,7 +102,20 @@ __global__ __launch_bounds__(kGemvThreads) void k_rows_fin_quant(GemvArgs a, Fin
     sw[j] = *(const float4*)(f.s_w + i);
     acc[j] = *(const v4i_t*)(pr + i);
   }
-  for (int z = 1; z < f.nz; ++z)
+  // the other splits' partials (nz is 1, 2 or 4), requested together from clamped splits and added
+  // where they exist (a loop over nz would wait for each split's load before the next)
+  v4i_t pz[3][S::NX];
+#pragma unroll
+  for (int z = 1; z < 4; ++z)
+#pragma unroll
+    for (int j = 0; j < S::NX; ++j)
+      pz[z - 1][j] = *(const v4i_t*)(pr + min(z, f.nz - 1) * f.zstride + min((tid + j * kGemvThreads) * 4, K - 4));
+#pragma unroll
+  for (int z = 1; z < 4; ++z)
+#pragma unroll
+    for (int j = 0; j < S::NX; ++j)
+      if (z < f.nz) acc[j] += pz[z - 1][j];
+  for (int z = 4; z < f.nz; ++z)                   // (more splits than the launcher makes: in order)
 #pragma unroll
     for (int j = 0; j < S::NX; ++j) acc[j] += *(const v4i_t*)(pr + z * f.zstride + min((tid + j * kGemvThreads) * 4, K - 4));
 #pragma unroll
