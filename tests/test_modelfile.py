@@ -215,6 +215,43 @@ def test_llama2c_tokenizer_known_answers(tmp_path):
     assert t.decode([1, tid(b" "), tid(b"\xc3\xa9")]) == "é"
 
 
+def _merge_by_rescan(t, tok):
+    """run.c's merge loop as written there: rescan every adjacent pair at each step, keep the first
+    one with the highest score above -1e10, join it."""
+    while True:
+        best, at, mid = -1e10, -1, -1
+        for k in range(len(tok) - 1):
+            m = t.ids.get(t.pieces[tok[k]] + t.pieces[tok[k + 1]])
+            if m is not None and t.scores[m] > best:
+                best, at, mid = t.scores[m], k, m
+        if at < 0:
+            return tok
+        tok = tok[:at] + [mid] + tok[at + 2:]
+
+
+def test_llama2c_tokenizer_heap_merge_equals_rescan(tmp_path):
+    """The heap-ordered merge picks the same pair as a full rescan at every step: random vocabularies
+    with many equal scores, NaN and sub-floor scores and chains of merges, random texts."""
+    rng = np.random.default_rng(11)
+    alpha = ["a", "b", "c", " ", "é"]
+    for trial in range(40):
+        extra = sorted({"".join(rng.choice(alpha, int(rng.integers(2, 5)))).encode() for _ in range(50)})
+        pieces = PIECES[:259] + [b" ", b"a", b"b", b"c", b"\xc3\xa9"] + extra
+        scores = [float(np.float32(s)) for s in rng.integers(-3, 3, len(pieces))]
+        for q in rng.integers(264, len(pieces), 4):
+            scores[q] = float("nan") if q % 2 else -3e10
+        path = tmp_path / f"t{trial}.bin"
+        with open(path, "wb") as f:
+            f.write(struct.pack("<i", 8))
+            for p, s in zip(pieces, scores):
+                f.write(struct.pack("<fi", s, len(p)) + p)
+        t = MF.Llama2cTokenizer(str(path), len(pieces))
+        for _ in range(10):
+            text = "".join(rng.choice(alpha, int(rng.integers(0, 40))))
+            start = [1] + ([t.ids[b" "]] + t._code_points(text.encode()) if text else [])
+            assert t.encode(text) == _merge_by_rescan(t, start), (trial, text)
+
+
 def test_hf_tokenizer(tmp_path):
     tokenizers = pytest.importorskip("tokenizers")
     from tokenizers import Tokenizer, decoders, models, pre_tokenizers, processors

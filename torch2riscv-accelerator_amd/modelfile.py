@@ -17,6 +17,7 @@
   (compiler/frontend/hf_tokenizer.py:1-20) states it is identical to.
 """
 import dataclasses
+import heapq
 import os
 import re
 import struct
@@ -383,72 +384,109 @@ def write_llama2c(path, cfg, w):
 # ------------------------------------------------------------------ tokenizers
 class Llama2cTokenizer:
     """tokenizer.bin of llama2.c: int32 max_token_length, then per id a float32 score, an int32
-    length and the piece's bytes. encode() follows run.c (llm/tokenizer.py:24-52): BOS, a " " dummy
-    prefix for non-empty text, one piece per UTF-8 code point (else its bytes, id = byte + 3), then
-    repeatedly the adjacent pair whose merged piece has the highest score (the leftmost such pair
-    on ties) is merged, while one scores above -1e10. decode() prints as run.c: the space after BOS dropped, <0xNN> pieces as
-    their byte, other single bytes only when printable or whitespace."""
+    length and the piece's bytes; a piece listed twice maps to its first id.
+
+    encode() gives run.c's ids (llm/tokenizer.py:24-52): BOS, a " " dummy prefix for non-empty
+    text, one piece per UTF-8 code point (at most 4 bytes; an unknown one as its bytes, id = byte
+    + 3), then merges: each step joins the adjacent pair (BOS included) whose joined piece is in
+    the vocabulary with the highest score above -1e10 (a NaN score never qualifies), the leftmost
+    such pair on equal scores, until none is left. Here the pairs wait in a heap keyed by (score,
+    position of the left token) over a linked list of the tokens; a merge keeps the left token's
+    position, so the positions still order the live tokens, and a popped pair is used only if both
+    tokens are still live, adjacent and unchanged. That picks the same pair as a rescan of the list
+    at every step, in O(n log n) rather than O(n^2).
+
+    decode() prints as run.c (llm/tokenizer.py:54-67): after BOS a piece loses one leading space;
+    a piece "<0xHH>" is the byte HH; a single byte that is neither printable ASCII nor C whitespace
+    prints nothing."""
+    _HEX = frozenset(b"0123456789abcdefABCDEF")
+    _SPACE = frozenset(b" \t\n\r\x0b\x0c")
 
     def __init__(self, path, vocab_size):
         with open(path, "rb") as f:
-            data = f.read()
-        (self.max_token_length,) = struct.unpack_from("<i", data, 0)
-        pos = 4
+            blob = memoryview(f.read())
+        (self.max_token_length,) = struct.unpack_from("<i", blob, 0)
         self.pieces, self.scores = [], []
+        at = 4
         for _ in range(vocab_size):
-            score, n = struct.unpack_from("<fi", data, pos)
-            pos += 8
-            self.pieces.append(data[pos:pos + n])
+            score, n = struct.unpack_from("<fi", blob, at)
             self.scores.append(score)
-            pos += n
+            self.pieces.append(bytes(blob[at + 8:at + 8 + n]))
+            at += 8 + n
         self.ids = {}
-        for i, p in enumerate(self.pieces):
-            if p not in self.ids:                # the first id of a repeated piece wins
-                self.ids[p] = i
-        self._hex = re.compile(rb"<0x([0-9A-Fa-f]{2})>")
+        for i in range(vocab_size - 1, -1, -1):    # lowest id last, so it is the one kept
+            self.ids[self.pieces[i]] = i
+        self._shown = {}
+
+    def _code_points(self, data):
+        out, i = [], 0
+        while i < len(data):
+            j = i + 1
+            while j < min(len(data), i + 4) and data[j] >> 6 == 2:   # continuation bytes 10xxxxxx
+                j += 1
+            tid = self.ids.get(data[i:j])
+            if tid is None:
+                out.extend(c + 3 for c in data[i:j])
+            else:
+                out.append(tid)
+            i = j
+        return out
+
+    def _merge(self, tok):
+        n = len(tok)
+        nxt, prv, live = list(range(1, n + 1)), list(range(-1, n - 1)), [True] * n
+        heap = []
+
+        def offer(a):                              # the pair (a, its right neighbour), if it merges
+            b = nxt[a]
+            if b < n:
+                m = self.ids.get(self.pieces[tok[a]] + self.pieces[tok[b]])
+                if m is not None and self.scores[m] > -1e10:
+                    heapq.heappush(heap, (-self.scores[m], a, b, tok[a], tok[b], m))
+
+        for a in range(n - 1):
+            offer(a)
+        while heap:
+            _, a, b, ta, tb, m = heapq.heappop(heap)
+            if not live[a] or nxt[a] != b or tok[a] != ta or tok[b] != tb:
+                continue                           # stale: a neighbour merged since it was offered
+            tok[a], live[b] = m, False
+            nxt[a] = nxt[b]
+            if nxt[a] < n:
+                prv[nxt[a]] = a
+            if prv[a] >= 0:
+                offer(prv[a])
+            offer(a)
+        out, a = [], 0
+        while a < n:
+            out.append(tok[a])
+            a = nxt[a]
+        return out
 
     def encode(self, text, bos=True, eos=False):
         data = text.encode("utf-8")
-        out = [BOS] if bos else []
-        if data:
-            out.append(self.ids[b" "])
-        i = 0
-        while i < len(data):
-            j = i + 1
-            while j < len(data) and j - i < 4 and (data[j] & 0xC0) == 0x80:
-                j += 1
-            cp = data[i:j]
-            tid = self.ids.get(cp)
-            out.extend([tid] if tid is not None else [b + 3 for b in cp])
-            i = j
-        while len(out) > 1:                       # over the whole list, BOS included, as run.c
-            # a merge must score above run.c's floor of -1e10 (a NaN score never does)
-            best = (-1e10, -1, -1)                 # (score, position, id)
-            for k in range(len(out) - 1):
-                tid = self.ids.get(self.pieces[out[k]] + self.pieces[out[k + 1]])
-                if tid is not None and self.scores[tid] > best[0]:
-                    best = (self.scores[tid], k, tid)
-            _, k, tid = best
-            if k < 0:
-                break
-            out[k:k + 2] = [tid]
-        if eos:
-            out.append(EOS)
-        return out
+        tok = ([BOS] if bos else []) + ([self.ids[b" "]] if data else []) + self._code_points(data)
+        tok = self._merge(tok)
+        return tok + [EOS] if eos else tok
 
-    def piece(self, prev, token):
-        p = self.pieces[token]
-        if prev == BOS and p.startswith(b" "):
-            p = p[1:]
-        m = self._hex.fullmatch(p)
-        if m:
-            p = bytes([int(m.group(1), 16)])
-        if len(p) == 1 and not (32 <= p[0] < 127 or p in (b" ", b"\t", b"\n", b"\r", b"\x0b", b"\x0c")):
+    def _printed(self, p):
+        if len(p) == 6 and p[:3] == b"<0x" and p[5:] == b">" and p[3] in self._HEX and p[4] in self._HEX:
+            p = bytes([int(p[3:5].decode(), 16)])
+        if len(p) == 1 and not (32 <= p[0] <= 126 or p[0] in self._SPACE):
             return b""
         return p
 
+    def piece(self, prev, token):
+        """The bytes run.c prints for `token` when `prev` came before it."""
+        p = self.pieces[token]
+        if prev == BOS and p[:1] == b" ":
+            return self._printed(p[1:])
+        if token not in self._shown:
+            self._shown[token] = self._printed(p)
+        return self._shown[token]
+
     def decode(self, tokens):
-        """Text of a token sequence that starts with BOS (run.c's printing of tokens[1:])."""
+        """Text of a token sequence that starts with BOS (what run.c prints for tokens[1:])."""
         return b"".join(self.piece(a, b) for a, b in zip(tokens, tokens[1:])).decode("utf-8", "replace")
 
 

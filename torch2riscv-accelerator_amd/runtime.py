@@ -33,45 +33,70 @@ F = np.float32
 BOS = 1
 
 
-class Sampler:
-    """llama2.c run.c's sampler: temperature 0 = argmax; otherwise softmax(logits / T) and then
-    top-p (nucleus) sampling, or multinomial when topp is not in (0, 1), with run.c's xorshift*
-    random numbers (llm/runtime.py:37-72)."""
-    MASK = (1 << 64) - 1
+class XorShiftStar:
+    """run.c's random numbers: a 64-bit xorshift state (shifts right 12, left 25, right 27) whose
+    output is the high half of its product with 0x2545F4914F6CDD1D; a uniform float in [0, 1) is
+    that output's top 24 bits over 2^24. Seed 0 is replaced by 1 (an all-zero state never moves)."""
+    M64 = (1 << 64) - 1
 
-    def __init__(self, temperature=0.0, topp=0.9, seed=1):
-        self.t, self.topp = temperature, topp
-        self.state = (seed & self.MASK) or 1
+    def __init__(self, seed):
+        self.state = (seed & self.M64) or 1
 
-    def random_u32(self):
+    def u32(self):
         s = self.state
         s ^= s >> 12
-        s ^= (s << 25) & self.MASK
+        s = (s ^ (s << 25)) & self.M64
         s ^= s >> 27
         self.state = s
-        return ((s * 0x2545F4914F6CDD1D) & self.MASK) >> 32
+        return (s * 0x2545F4914F6CDD1D & self.M64) >> 32
 
-    def random_f32(self):
-        return (self.random_u32() >> 8) / 16777216.0
+    def uniform(self):
+        return (self.u32() >> 8) * 2.0 ** -24         # exact: 24 bits scaled by a power of two
+
+
+def _first_above(cdf, x, stop):
+    """The first index i <= stop with cdf[i] > x (x compared as float32), else stop: run.c's
+    "return the first index whose running sum exceeds the coin" with its clamp to the last."""
+    hit = np.flatnonzero(cdf[:stop + 1] > F(x))
+    return int(hit[0]) if hit.size else stop
+
+
+class Sampler:
+    """llama2.c run.c's sampler (llm/runtime.py:37-72): temperature 0 takes the argmax (first on
+    ties). Otherwise the logits over the temperature go through a float32 softmax and one uniform
+    draw picks the token: by the running sum of every probability (multinomial) when topp is not in
+    (0, 1), else from the nucleus. The nucleus holds the tokens whose probability is at least
+    (1 - topp) / (n - 1), by descending probability with the lower id first on ties; it ends at the
+    first token whose running sum passes topp, and the draw is scaled by that sum. `state` is the
+    generator's 64-bit state, which advances once per sampled (non-argmax) token."""
+
+    def __init__(self, temperature=0.0, topp=0.9, seed=1):
+        self.temperature, self.topp = temperature, topp
+        self.rng = XorShiftStar(seed)
+
+    @property
+    def state(self):
+        return self.rng.state
+
+    def probabilities(self, logits):
+        """softmax(logits / temperature) in float32: the maximum subtracted, then exp, then each
+        divided by the (pairwise float32) sum."""
+        x = np.asarray(logits, F) / F(self.temperature)
+        e = np.exp(x - x.max())
+        return e / e.sum(dtype=F)
 
     def __call__(self, logits):
-        if self.t == 0:
+        if self.temperature == 0:
             return int(np.argmax(logits))
-        x = np.asarray(logits, F) / F(self.t)
-        p = np.exp((x - x.max()).astype(F)).astype(F)
-        p /= p.sum(dtype=F)
-        coin = self.random_f32()
-        if self.topp <= 0 or self.topp >= 1:
-            cdf = np.cumsum(p, dtype=F)
-            return int(min(np.searchsorted(cdf, coin, side="right"), p.size - 1))
-        # nucleus: candidates above (1 - topp) / (n - 1), by descending probability (stable)
-        cutoff = (1.0 - self.topp) / (p.size - 1)
-        cand = np.flatnonzero(p >= cutoff)
-        cand = cand[np.argsort(-p[cand], kind="stable")]
-        cdf = np.cumsum(p[cand], dtype=F)
-        last = int(min(np.searchsorted(cdf, F(self.topp), side="right"), cand.size - 1))
-        r = coin * float(cdf[last])
-        return int(cand[int(min(np.searchsorted(cdf[:last + 1], r, side="right"), last))])
+        p = self.probabilities(logits)
+        u = self.rng.uniform()
+        if not 0 < self.topp < 1:
+            return _first_above(np.cumsum(p, dtype=F), u, p.size - 1)
+        ids = np.flatnonzero(p >= (1.0 - self.topp) / (p.size - 1))
+        ids = ids[np.lexsort((ids, -p[ids]))]          # descending probability, then ascending id
+        run = np.cumsum(p[ids], dtype=F)
+        end = _first_above(run, F(self.topp), ids.size - 1)
+        return int(ids[_first_above(run, u * float(run[end]), end)])
 
 
 def _default_tokenizer(model_path):
