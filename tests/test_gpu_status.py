@@ -60,7 +60,7 @@ def test_position_outside_cache_sets_bit2():
     dev = LlamaDevice(cfg)
     m = dev.m
     m.tok.fill_(3)
-    m.pos.fill_(cfg.seq_len)              # one past the cache: the attention kernels end at once
+    m.pos.fill_(cfg.seq_len)              # one past the cache: the attention kernels write nothing
     m.step()
     assert m.status(clear=False) == 4
     assert not m.kc.any().item() and not m.vc.any().item()     # nothing written anywhere

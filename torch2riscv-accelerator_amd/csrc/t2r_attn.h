@@ -397,9 +397,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 // ------------------------------------------------------------------ decode attention
 // Same numerics as k_attn<ATTN_FUSED>, organised around memory latency and instruction count.
 // Every thread owns one 16-byte chunk (slot c of the NCHP slots per row) of R rows
-// t = ts + TS i, for both K and V. The position is the only load the others wait for; right after
-// it the workgroup issues the row's k / v or q, the RoPE inputs, the SFU tables and its K and V
-// chunks. K and V go through buffer loads whose range ends at row pos: rows past it read as zero
+// t = ts + TS i, for both K and V. The position is requested first and with it what does not
+// depend on it (the SFU tables, the row's k / v or q, the norm gains); the RoPE inputs and the K and
+// V chunks follow once it has arrived. K and V go through buffer loads whose range ends at row pos: rows past it read as zero
 // without a memory access, so the loads stay unconditional (exact in-order wait counts) and cost
 // nothing when the sequence is short. Per row, the slot lanes' partial dot products meet by DPP.
 // Each lane exps one row in NCHP; the exps go to the lane-major copy for the D-lane ordered sum,
@@ -408,6 +408,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a) {
 // four rows.
 T2R_DEV __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// the same from wave-uniform inputs, taken from the first lane: a descriptor must sit in scalar
+// registers, and one built from a uniform value that the compiler keeps in vector registers turns
+// every load through it into a waterfall loop
+T2R_DEV __amdgpu_buffer_rsrc_t buffer_rsrc_u(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  return buffer_rsrc((const void*)(((uint64_t)hi << 32) | lo), (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes));
 }
 T2R_DEV v4i_t buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
@@ -466,36 +475,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 
   const int h = blockIdx.x, row = SPLIT ? 0 : blockIdx.y, tid = threadIdx.x;
   const int sj = SPLIT ? blockIdx.y : 0;         // this workgroup's split
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // (uniform: scalar selects by wave)
   const int G = a.H / a.Hk, g = h / G, S = a.S;
   a.kc += row * a.kv_row_stride;                 // this row's sequence cache
   a.vc += row * a.kv_row_stride;
   const long long q_dim = (long long)a.H * HD;
   const int kv_dim = a.Hk * HD;
-  const int pos = a.pos[row];
-  if (pos < 0 || pos >= S) {                     // a position outside the cache: nothing is read or written
-    if (tid == 0) flag_bad_pos(a.status);
-    return;
-  }
-  const int T = pos + 1;
-  // SPLIT: splits past the number of passes end here (all of a launch's workgroups agree on it);
-  // SPLIT 2: with zero sums
-  const int nsp = SPLIT ? min(a.nsplit, (T + TS * R - 1) / (TS * R)) : 1;
-  if (SPLIT && sj >= nsp) {
-    if (SPLIT == 2)
-      for (int j = tid; j < HD; j += kAttnThreads) a.sp_o[(long long)sj * q_dim + (long long)h * HD + j] = 0;
-    if (tid == 0) __hip_atomic_fetch_add(a.sp_sync + 2 * h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
+  // ---- issue: the position, then what does not depend on it (SFU tables, head vectors, gains), then
+  // the RoPE rows and K chunks at the position. The position comes by a vector load, counted in order
+  // with the loads after it, so that waiting for it waits for nothing issued later; the loads before
+  // that wait are unconditional and no branch precedes it in the default kernels (a branch lets the
+  // compiler sink them below the wait). A position outside the cache runs as position 0 and writes
+  // nothing: no cache row, no output, the status bit at the end (the split kernels, whose workgroups
+  // meet, still end at once).
+  const int pos_v = (int)__builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc_u(a.pos + row, 4), 0, 0, 0);
   const float* qkv = a.qkv + row * a.qkv_stride;
-  const int c = tid & (NCHP - 1), ts = tid / NCHP;
-  const bool cok = c < NCH;
-  // cache rows [0, pos): byte range of this KV head's columns up to row pos
-  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.kc + (long long)g * HD, (uint32_t)pos * kv_dim);
-  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc + (long long)g * HD, (uint32_t)pos * kv_dim);
-  auto chunk_off = [&](int t) -> uint32_t { return cok ? (uint32_t)t * kv_dim + 16 * c : 0xFFFFFFF0u; };
-
-  // ---- issue: SFU tables, head vectors, K and V chunks (in this order; waits count in order)
   v4f_t tb[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) tb[k] = ((const v4f_t*)a.tab)[(lane + 64 * k) & (kSfuWords / 4 - 1)];
@@ -526,6 +520,32 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
       xc2[k] = c2[j];
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  const int pos_in = __builtin_amdgcn_readfirstlane(pos_v);
+  const bool pos_ok = pos_in >= 0 && pos_in < S;
+  if constexpr (SPLIT != 0) {
+    if (!pos_ok) {
+      if (tid == 0) flag_bad_pos(a.status);
+      return;
+    }
+  }
+  const int pos = pos_ok ? pos_in : 0;
+  const int T = pos + 1;
+  // SPLIT: splits past the number of passes end here (all of a launch's workgroups agree on it);
+  // SPLIT 2: with zero sums
+  const int nsp = SPLIT ? min(a.nsplit, (T + TS * R - 1) / (TS * R)) : 1;
+  if (SPLIT && sj >= nsp) {
+    if (SPLIT == 2)
+      for (int j = tid; j < HD; j += kAttnThreads) a.sp_o[(long long)sj * q_dim + (long long)h * HD + j] = 0;
+    if (tid == 0) __hip_atomic_fetch_add(a.sp_sync + 2 * h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const int c = tid & (NCHP - 1), ts = tid / NCHP;
+  const bool cok = c < NCH;
+  // cache rows [0, pos): byte range of this KV head's columns up to row pos
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc_u(a.kc + (long long)g * HD, (uint32_t)pos * kv_dim);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc_u(a.vc + (long long)g * HD, (uint32_t)pos * kv_dim);
+  auto chunk_off = [&](int t) -> uint32_t { return cok ? (uint32_t)t * kv_dim + 16 * c : 0xFFFFFFF0u; };
   float cs[NV], sn[NV];                          // RoPE of element j = lane + 64 k: pair j / 2
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -586,7 +606,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
         if (j < HD) {
           kq8[j] = kb;
           vq8[j] = vb8;
-          if (h % G == 0 && sj == 0) {
+          if (h % G == 0 && sj == 0 && pos_ok) {
             a.kc[crow + j] = kb;
             a.vc[crow + j] = vb8;
           }
@@ -863,6 +883,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
                (uint32_t)(nsp - 1);
     __syncthreads();
     if (!s_last) return;
+  }
+  if (!pos_ok) {                                 // (the default kernels only: the split ones ended at once)
+    if (tid == 0) flag_bad_pos(a.status);
+    return;
   }
   for (int j = tid; j < HD; j += kAttnThreads) {
     int ssum = 0;
