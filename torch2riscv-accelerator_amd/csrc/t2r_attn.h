@@ -486,8 +486,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   // with the loads after it, so that waiting for it waits for nothing issued later; the loads before
   // that wait are unconditional and no branch precedes it in the default kernels (a branch lets the
   // compiler sink them below the wait). A position outside the cache runs as position 0 and writes
-  // nothing: no cache row, no output, the status bit at the end (the split kernels, whose workgroups
-  // meet, still end at once).
+  // nothing: no cache row, no output (SPLIT 2: no sums; SPLIT 1 clears its sums as after any launch),
+  // the status bit at the end.
   const int pos_v = (int)__builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc_u(a.pos + row, 4), 0, 0, 0);
   const float* qkv = a.qkv + row * a.qkv_stride;
   v4f_t tb[2];
@@ -523,23 +523,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   const int pos_in = __builtin_amdgcn_readfirstlane(pos_v);
   const bool pos_ok = pos_in >= 0 && pos_in < S;
-  if constexpr (SPLIT != 0) {
-    if (!pos_ok) {
-      if (tid == 0) flag_bad_pos(a.status);
-      return;
-    }
-  }
   const int pos = pos_ok ? pos_in : 0;
   const int T = pos + 1;
-  // SPLIT: splits past the number of passes end here (all of a launch's workgroups agree on it);
-  // SPLIT 2: with zero sums
-  const int nsp = SPLIT ? min(a.nsplit, (T + TS * R - 1) / (TS * R)) : 1;
-  if (SPLIT && sj >= nsp) {
-    if (SPLIT == 2)
-      for (int j = tid; j < HD; j += kAttnThreads) a.sp_o[(long long)sj * q_dim + (long long)h * HD + j] = 0;
-    if (tid == 0) __hip_atomic_fetch_add(a.sp_sync + 2 * h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
+  const int nsp = SPLIT ? min(a.nsplit, (T + TS * R - 1) / (TS * R)) : 1;   // splits with passes
   const int c = tid & (NCHP - 1), ts = tid / NCHP;
   const bool cok = c < NCH;
   // cache rows [0, pos): byte range of this KV head's columns up to row pos
@@ -632,6 +618,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     }
   }
   __syncthreads();
+  // SPLIT: splits past the number of passes end here (all of a launch's workgroups agree on it; not
+  // before the head vectors' first use, so that no branch lets the compiler sink their loads below
+  // the position's wait); SPLIT 2: with zero sums
+  if (SPLIT && sj >= nsp) {
+    if (SPLIT == 2)
+      for (int j = tid; j < HD; j += kAttnThreads) a.sp_o[(long long)sj * q_dim + (long long)h * HD + j] = 0;
+    if (tid == 0) __hip_atomic_fetch_add(a.sp_sync + 2 * h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < R; ++i) vw[i] = buffer_load16(vrs, chunk_off(sj * TS * R + ts + TS * i));
 
@@ -862,8 +857,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
       int ssum = 0;
 #pragma unroll
       for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
-      a.sp_o[(long long)sj * q_dim + (long long)h * HD + j] = ssum;
+      if (pos_ok) a.sp_o[(long long)sj * q_dim + (long long)h * HD + j] = ssum;
     }
+    if (!pos_ok && tid == 0) flag_bad_pos(a.status);
     return;
   }
   if constexpr (SPLIT == 1) {
@@ -884,10 +880,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
     __syncthreads();
     if (!s_last) return;
   }
-  if (!pos_ok) {                                 // (the default kernels only: the split ones ended at once)
-    if (tid == 0) flag_bad_pos(a.status);
-    return;
-  }
+  if (!pos_ok && tid == 0) flag_bad_pos(a.status);   // (SPLIT 1 still clears its sums below)
   for (int j = tid; j < HD; j += kAttnThreads) {
     int ssum = 0;
     if constexpr (SPLIT) {
@@ -898,6 +891,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_dec(AttnArgs a) {
 #pragma unroll
       for (int w = 0; w < kAttnWaves * 4; ++w) ssum += part[w][j];
     }
+    if (!pos_ok) continue;
     if constexpr (OPT) {
       float o = (float)ssum;
       if (a.qsum) o = o * rq;
