@@ -2125,7 +2125,7 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   __shared__ int part[kGqaWaves * 4][GW * HD];
 
   const int row = blockIdx.y, tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6, lr = lane & 31, kh = lane >> 5;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lr = lane & 31, kh = lane >> 5;
   const int G = a.H / a.Hk, S = a.S, D = a.D, P = osum_stride(S, D), SH = D * P + 64;
   const int NSPL = G / GW;                       // workgroups per KV head
   const int g = (int)blockIdx.x / NSPL, spl = (int)blockIdx.x - g * NSPL;
@@ -2137,18 +2137,13 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
   a.vc += row * a.kv_row_stride;
   const long long q_dim = (long long)a.H * HD;
   const int kv_dim = a.Hk * HD;
-  const int pos = a.pos[row];
-  if (pos < 0 || pos >= S) {                     // a position outside the cache: nothing is read or written
-    if (tid == 0) flag_bad_pos(a.status);
-    return;
-  }
-  const int T = pos + 1;
+  // ---- issue: the position (a vector load, so that its wait leaves the later loads in flight), the
+  // SFU tables and this wave's vector job inputs, none of which depend on it; then the RoPE rows and
+  // the first pass of K tiles and V chunks. No branch before the position's wait (it would let the
+  // compiler sink the loads below it): a position outside the cache runs as position 0 and writes
+  // nothing (no cache row, no output; the status bit at the end).
+  const int pos_v = (int)__builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc_u(a.pos + row, 4), 0, 0, 0);
   const float* qkv = a.qkv + row * a.qkv_stride;
-  // cache rows [0, pos) of this KV head's columns: rows past pos - 1 read as zero
-  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(a.kc + (long long)g * HD, (uint32_t)pos * kv_dim);
-  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(a.vc + (long long)g * HD, (uint32_t)pos * kv_dim);
-
-  // ---- issue: SFU tables, this wave's vector job inputs, the first pass of K tiles and V chunks
   v4f_t tb[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) tb[k] = ((const v4f_t*)a.tab)[(lane + 64 * k) & (kSfuWords / 4 - 1)];
@@ -2167,9 +2162,6 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
     xa[k] = va[j];
     xb[k] = vb[j];
     xg[k] = gn[j];
-    const long long ip = (long long)pos * (HD / 2) + (j >> 1);
-    cs[k] = a.cos_t[ip];
-    sn[k] = a.sin_t[ip];
   }
   // OPT: per-channel scales of the KV head (job 0: 1 / s_k, 1 / s_v; query jobs: the q multiplier
   // s_k), loaded unconditionally from a readable address when absent
@@ -2184,6 +2176,20 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
       xc1[k] = c1[j];
       xc2[k] = c2[j];
     }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int pos_in = __builtin_amdgcn_readfirstlane(pos_v);
+  const bool pos_ok = pos_in >= 0 && pos_in < S;
+  const int pos = pos_ok ? pos_in : 0;
+  const int T = pos + 1;
+  // cache rows [0, pos) of this KV head's columns: rows past pos - 1 read as zero
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc_u(a.kc + (long long)g * HD, (uint32_t)pos * kv_dim);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc_u(a.vc + (long long)g * HD, (uint32_t)pos * kv_dim);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const long long ip = (long long)pos * (HD / 2) + (min(lane + 64 * k, HD - 1) >> 1);
+    cs[k] = a.cos_t[ip];
+    sn[k] = a.sin_t[ip];
   }
   __builtin_amdgcn_sched_barrier(0);
   v4i_t kw[kGqaRK][KS];
@@ -2246,7 +2252,7 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
         if (j < HD) {
           s_k8[j] = kb;
           s_v8[j] = vb8;
-          if (spl == 0) {
+          if (spl == 0 && pos_ok) {
             a.kc[crow + j] = kb;
             a.vc[crow + j] = vb8;
           }
@@ -2444,6 +2450,10 @@ __global__ __launch_bounds__(kGqaThreads) void k_attn_gqa(AttnArgs a) {
         for (int b = 0; b < 16; ++b) part[wave * 4 + (lane >> 4)][h * HD + 16 * c + b] = acc[h][b];
   }
   __syncthreads();
+  if (!pos_ok) {
+    if (tid == 0) flag_bad_pos(a.status);
+    return;
+  }
   float* out = a.att + row * a.att_stride;
   for (int idx = tid; idx < GH * HD; idx += kGqaThreads) {
     int ssum = 0;
