@@ -257,7 +257,7 @@ int t2r_decode_batch(void* model, const int32_t* tokens, const int32_t* position
  * outside [0, vocab) was embedded (row 0 read instead); bit 1 a bounded wait between the workgroups of
  * a head's decode attention ran out (its output is then not to be trusted); bit 2 a row's position
  * (device memory: a replayed graph's advancing position, say) was outside the cache, and its attention
- * neither read nor wrote the cache. The bits stay set until cleared. Waits for the device; clear != 0
+ * read no cache row and wrote nothing (no cache row, no output). The bits stay set until cleared. Waits for the device; clear != 0
  * then zeroes the word. */
 int t2r_model_status(void* model, int32_t* out, int clear);
 
