@@ -19,7 +19,32 @@ __global__ __launch_bounds__(256) void k_embed(const int8_t* emb_q, const float*
     t = 0;
   }
   const float s = emb_s[t];
-  for (int i = threadIdx.x; i < dim; i += blockDim.x) x[r * x_stride + i] = (float)emb_q[(long long)t * dim + i] * s;
+  const int8_t* e = emb_q + (long long)t * dim;
+  float* xr = x + r * x_stride;
+  int done = 0;
+  if (dim % 16 == 0 && ((uintptr_t)e & 15) == 0 && ((uintptr_t)xr & 15) == 0) {
+    // 16 bytes a thread and pass, every pass's load issued (from a clamped address) before the first
+    // conversion: one memory round trip for the row instead of one per pass
+    constexpr int NP = 4;
+    const int span = 16 * (int)blockDim.x;
+    v4i_t q[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) q[p] = *(const v4i_t*)(e + min(16 * (int)threadIdx.x + span * p, dim - 16));
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int i = 16 * (int)threadIdx.x + span * p;
+      if (i < dim) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int v = q[p][w];
+          *(float4*)(xr + i + 4 * w) = make_float4((float)(int8_t)v * s, (float)(int8_t)(v >> 8) * s,
+                                                   (float)(int8_t)(v >> 16) * s, (float)(int8_t)(v >> 24) * s);
+        }
+      }
+    }
+    done = min(dim, NP * span);
+  }
+  for (int i = done + threadIdx.x; i < dim; i += blockDim.x) xr[i] = (float)e[i] * s;
   if (keys && r == 0)
     for (int i = threadIdx.x; i < nkeys; i += blockDim.x) keys[i] = 0;
 }
